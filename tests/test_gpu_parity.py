@@ -1,0 +1,294 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle.
+
+Bars (written in each test): int8 codes and int32 accumulators bit-exact;
+W8A32/W8A8 M=1 fp32 outputs bit-exact (the reference's epilogue is a fixed
+sequence of IEEE roundings); M>1 fp32 outputs within relative L2 1e-5;
+W8A16 fp32 outputs within 1e-5, bf16/fp16 outputs within 2e-3; lm_head argmax
+identical.  Sizes are chosen so the oracle finishes in seconds; the largest
+shapes are additionally checked through size-independent properties.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+F = np.float32
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def make(rng, M, N, K):
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    s = rng.uniform(0.002, 0.02, N).astype(F)
+    return x, w, s
+
+
+def bf16_bits(x):
+    u = np.ascontiguousarray(x, F).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bf16_to_f32(b):
+    return (b.astype(np.uint32) << 16).view(F)
+
+
+# ---------------------------------------------------------------------------
+# quantizers
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,cols", [(7, 2048), (3, 6144), (5, 37), (4, 1), (2, 16), (33, 100)])
+def test_quantizers_bit_exact(lin, orc, rows, cols):
+    say(f"quantize rows={rows} cols={cols}")
+    rng = np.random.default_rng(rows * 1000 + cols)
+    w = (rng.standard_normal((rows, cols)) * rng.uniform(1e-3, 10, (rows, 1))).astype(F)
+    w[0, :] = 0.0                                        # absmax 0 -> scale 1
+    if cols >= 16:
+        w[-1, 3] = w[-1, 3] * 0 + np.abs(w[-1]).max() * 1.0  # an exact argmax
+    want_q, want_s = orc.quantize_rows(w)
+    for fn in ("w8a32_quantize", "w8a8_quantize_weights", "w8a8_quantize_activations",
+               "w8a16_quantize_weights"):
+        q, s = lin.quantize(w, fn)
+        np.testing.assert_array_equal(s, want_s, err_msg=fn)
+        np.testing.assert_array_equal(q, want_q, err_msg=fn)
+
+
+def test_quantizer_ties_nan_inf(lin, orc):
+    say("quantize ties/nan/inf")
+    rows = []
+    r = np.zeros(32, F); r[0] = 127; r[1:7] = [2.5, 3.5, -2.5, -3.5, 0.5, -0.5]; rows.append(r)
+    r = np.zeros(32, F); r[0] = 127; r[16:21] = [2.5, -2.5, 0.5, -0.5, 3.5]; rows.append(r)
+    r = np.linspace(-3, 3, 32).astype(F); r[5] = np.nan; rows.append(r)
+    r = np.ones(32, F); r[2] = np.inf; rows.append(r)
+    for i, r in enumerate(rows):
+        q, s = lin.quantize(r[None])
+        wq, ws = orc.quantize_rows(r[None])
+        np.testing.assert_array_equal(q, wq, err_msg=str(i))
+        assert (s[0] == ws[0]) or (np.isinf(s[0]) and np.isinf(ws[0])), i
+    # tail-only case (K=21): codes 16..20 use round-half-away
+    r = np.zeros(21, F); r[0] = 127; r[16:21] = [2.5, -2.5, 0.5, -0.5, 3.5]
+    q, _ = lin.quantize(r[None])
+    assert list(q[0, 16:21]) == [3, -3, 1, -1, 4]
+
+
+# ---------------------------------------------------------------------------
+# M=1 decode GEMV (W8A32 batch==1)
+# ---------------------------------------------------------------------------
+DECODE_SHAPES = [(6144, 2048), (4096, 2048), (2048, 2048), (1024, 2048), (12288, 2048),
+                 (2048, 6144), (37, 50), (100, 1000), (16, 64), (512, 16384), (48, 20000)]
+
+
+@pytest.mark.parametrize("N,K", DECODE_SHAPES)
+def test_gemv_w8a32_bit_exact(lin, orc, N, K):
+    say(f"gemv w8a32 host-ABI N={N} K={K}")
+    rng = np.random.default_rng(N + 7 * K)
+    x, w, s = make(rng, 1, N, K)
+    want, codes, xs, acc = orc.w8a32_linear(x, w, s, detail=True)
+    got = lin.w8a32_linear(x, w, s)
+    np.testing.assert_array_equal(got, want)
+    b = rng.standard_normal(N).astype(F)
+    np.testing.assert_array_equal(lin.w8a32_linear(x, w, s, bias=b), orc.w8a32_linear(x, w, s, bias=b))
+
+
+@pytest.mark.parametrize("N,K", [(6144, 2048), (2048, 6144), (151936 // 16, 2048), (37, 50), (64, 16384)])
+def test_gemv_accumulators_and_scale(lin, orc, dev, N, K):
+    import torch
+    say(f"gemv int32 acc N={N} K={K}")
+    rng = np.random.default_rng(N * 3 + K)
+    x, w, s = make(rng, 1, N, K)
+    _, codes, xs, acc = orc.w8a32_linear(x, w, s, detail=True)
+    W = lin.DeviceWeights.from_codes(w, s)
+    xd = torch.from_numpy(x).to(dev)
+    accd = torch.empty(N, dtype=torch.int32, device=dev)
+    xsd = torch.empty(1, dtype=torch.float32, device=dev)
+    lin.gemv_acc_dev(xd, W, accd, xsd)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(accd.cpu().numpy(), acc)       # exact int32
+    assert xsd.cpu().numpy()[0] == xs
+    W.close()
+
+
+def test_gemv_deterministic_and_fused_equals_concat(lin, orc, dev):
+    """Run-to-run bitwise determinism (split-K counters reset), and the fused
+    QKV / gate_up matrices give the concatenation of the separate GEMVs."""
+    say("gemv determinism + fused==concat")
+    rng = np.random.default_rng(99)
+    x, wq, sq = make(rng, 1, 2048, 2048)
+    _, wk, sk = make(rng, 1, 1024, 2048)
+    _, wv, sv = make(rng, 1, 1024, 2048)
+    y1 = lin.w8a32_linear(x, wq, sq)
+    for _ in range(3):
+        np.testing.assert_array_equal(lin.w8a32_linear(x, wq, sq), y1)
+    wqkv = np.ascontiguousarray(np.concatenate([wq, wk, wv]))
+    sqkv = np.ascontiguousarray(np.concatenate([sq, sk, sv]))
+    fused = lin.w8a32_linear(x, wqkv, sqkv)
+    sep = np.concatenate([y1, lin.w8a32_linear(x, wk, sk), lin.w8a32_linear(x, wv, sv)], axis=1)
+    np.testing.assert_array_equal(fused, sep)
+
+
+def test_lm_head_argmax(lin, orc):
+    say("lm_head N=151936 K=2048")
+    rng = np.random.default_rng(151936)
+    x, w, s = make(rng, 1, 151936, 2048)
+    want = orc.w8a32_linear(x, w, s)
+    got = lin.w8a32_linear(x, w, s)
+    np.testing.assert_array_equal(got, want)
+    assert int(np.argmax(got)) == int(np.argmax(want))
+    # 8 more hidden states: argmax identical on every row
+    for i in range(8):
+        xi = rng.standard_normal((1, 2048), dtype=np.float32)
+        assert int(np.argmax(lin.w8a32_linear(xi, w, s))) == int(np.argmax(orc.w8a32_linear(xi, w, s)))
+
+
+def test_registry_detects_in_place_update(lin, orc):
+    say("registry in-place update")
+    rng = np.random.default_rng(5)
+    x, w, s = make(rng, 1, 256, 512)
+    y0 = lin.w8a32_linear(x, w, s)
+    w[:] = rng.integers(-127, 128, w.shape, dtype=np.int8)   # same pointer, new contents
+    np.testing.assert_array_equal(lin.w8a32_linear(x, w, s), orc.w8a32_linear(x, w, s))
+    assert not np.array_equal(y0, lin.w8a32_linear(x, w, s))
+
+
+# ---------------------------------------------------------------------------
+# W8A32 batch > 1 (fp32 semantics)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("M,N,K", [(2, 2048, 2048), (4, 6144, 2048), (8, 2048, 6144), (3, 100, 70),
+                                   (17, 512, 2048), (64, 1024, 2048), (200, 4096, 2048)])
+def test_w8a32_batch_fp32(lin, orc, M, N, K):
+    say(f"w8a32 batch M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 13 + N + K)
+    x, w, s = make(rng, M, N, K)
+    want = orc.w8a32_linear(x, w, s)
+    got = lin.w8a32_linear(x, w, s)
+    assert rel_l2(got, want) <= 1e-5
+    b = rng.standard_normal(N).astype(F)
+    assert rel_l2(lin.w8a32_linear(x, w, s, bias=b), orc.w8a32_linear(x, w, s, bias=b)) <= 1e-5
+
+
+def test_w8a32_prefill_rows_consistent(lin, orc):
+    """1200-token prefill (fused QKV shape): rows are independent, so a
+    subset computed alone matches the corresponding rows of the full call."""
+    say("w8a32 prefill M=1200 N=4096 K=2048")
+    rng = np.random.default_rng(1200)
+    x, w, s = make(rng, 1200, 4096, 2048)
+    full = lin.w8a32_linear(x, w, s)
+    sub = np.r_[0:5, 597:603, 1195:1200]
+    want = orc.w8a32_linear(np.ascontiguousarray(x[sub]), w, s)
+    assert rel_l2(full[sub], want) <= 1e-5
+
+
+# ---------------------------------------------------------------------------
+# W8A8
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("N,K", [(6144, 2048), (2048, 6144), (37, 50)])
+def test_w8a8_m1_bit_exact(lin, orc, N, K):
+    say(f"w8a8 M=1 N={N} K={K}")
+    rng = np.random.default_rng(N + K + 1)
+    x, w, s = make(rng, 1, N, K)
+    xq, xs = orc.quantize_rows(x)
+    b = rng.standard_normal(N).astype(F)
+    np.testing.assert_array_equal(lin.w8a8_linear(xq, xs, w, s), orc.w8a8_linear(xq, xs, w, s))
+    np.testing.assert_array_equal(lin.w8a8_linear(xq, xs, w, s, bias=b),
+                                  orc.w8a8_linear(xq, xs, w, s, bias=b))
+
+
+@pytest.mark.parametrize("M,N,K", [(2, 512, 2048), (16, 6144, 2048), (100, 2048, 6144), (256, 6144, 2048),
+                                   (45, 130, 300)])
+def test_w8a8_gemm(lin, orc, dev, M, N, K):
+    import torch
+    say(f"w8a8 gemm M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + 3 * N + K)
+    x, w, s = make(rng, M, N, K)
+    xq, xs = orc.quantize_rows(x)
+    # int32 accumulators bit-exact
+    W = lin.DeviceWeights.from_codes(w, s)
+    acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    lin.gemm_acc_dev(torch.from_numpy(xq).to(dev), W, acc)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(acc.cpu().numpy(), orc.int_acc(xq, w))
+    # fp32 outputs through the reference ABI
+    assert rel_l2(lin.w8a8_linear(xq, xs, w, s), orc.w8a8_linear(xq, xs, w, s)) <= 1e-5
+    # prefill path: fp32 X quantized on the GPU, then the int8 GEMM
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    lin.w8a8_linear_f32_dev(torch.from_numpy(x).to(dev), W, y)
+    torch.cuda.synchronize()
+    assert rel_l2(y.cpu().numpy(), orc.w8a8_linear(xq, xs, w, s)) <= 1e-5
+    W.close()
+
+
+def test_w8a8_prefill_full_size(lin, orc, dev):
+    """Config shape M=1024, N=6144, K=2048: codes on a row subset bit-exact,
+    full accumulators bit-exact, fp32 outputs of sampled rows within 1e-5."""
+    import torch
+    say("w8a8 prefill M=1024 N=6144 K=2048")
+    rng = np.random.default_rng(1024)
+    x, w, s = make(rng, 1024, 6144, 2048)
+    xq, xs = orc.quantize_rows(x)
+    xd = torch.from_numpy(x).to(dev)
+    codes = torch.empty((1024, 2048), dtype=torch.int8, device=dev)
+    scales = torch.empty(1024, dtype=torch.float32, device=dev)
+    lin.quantize_rows_dev(xd, codes, scales)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(codes.cpu().numpy(), xq)
+    np.testing.assert_array_equal(scales.cpu().numpy(), xs)
+    W = lin.DeviceWeights.from_codes(w, s)
+    acc = torch.empty((1024, 6144), dtype=torch.int32, device=dev)
+    lin.gemm_acc_dev(codes, W, acc)
+    y = torch.empty((1024, 6144), dtype=torch.float32, device=dev)
+    lin.w8a8_linear_f32_dev(xd, W, y)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(acc.cpu().numpy(), orc.int_acc(xq, w))
+    sub = np.r_[0:4, 500:504, 1020:1024]
+    want = orc.w8a8_linear(np.ascontiguousarray(xq[sub]), xs[sub], w, s)
+    assert rel_l2(y.cpu().numpy()[sub], want) <= 1e-5
+    W.close()
+
+
+# ---------------------------------------------------------------------------
+# W8A16
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("M,N,K", [(1, 2048, 2048), (1, 37, 50), (8, 4096, 2048), (64, 2048, 2048),
+                                   (256, 12288, 2048), (33, 200, 130)])
+def test_w8a16_fp32_out(lin, orc, M, N, K):
+    say(f"w8a16 fp32-out M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + N + K + 16)
+    x, w, s = make(rng, M, N, K)
+    xb = bf16_bits(x)
+    want = orc.w8a16_linear(xb, w, s)
+    assert rel_l2(lin.w8a16_linear(xb, w, s), want) <= 1e-5
+    b = rng.standard_normal(N).astype(F)
+    assert rel_l2(lin.w8a16_linear(xb, w, s, bias=b), orc.w8a16_linear(xb, w, s, bias=b)) <= 1e-5
+
+
+@pytest.mark.parametrize("M,N", [(1, 2048), (8, 4096), (64, 12288), (256, 2048), (1024, 4096)])
+def test_w8a16_bf16_fp16(lin, orc, dev, M, N):
+    import torch
+    K = 2048
+    say(f"w8a16 bf16/fp16 M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 7 + N)
+    x, w, s = make(rng, M, N, K)
+    W = lin.DeviceWeights.from_codes(w, s)
+    rows = np.arange(M) if M <= 64 else np.r_[0:8, M - 8:M]
+    # bf16 X, bf16 out: 2e-3
+    xb = bf16_bits(x)
+    want = orc.w8a16_linear(np.ascontiguousarray(xb[rows]), w, s)
+    xt = torch.from_numpy(x).to(dev).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    lin.w8a16_linear_dev(xt, W, y)
+    torch.cuda.synchronize()
+    assert rel_l2(y.float().cpu().numpy()[rows], want) <= 2e-3
+    # fp16 X, fp16 out: reference math in float64 on the fp16-rounded X
+    xh = x.astype(np.float16)
+    wantf = (xh[rows].astype(np.float64) @ w.astype(np.float64).T) * s.astype(np.float64)
+    yh = torch.empty((M, N), dtype=torch.float16, device=dev)
+    lin.w8a16_linear_dev(torch.from_numpy(xh).to(dev), W, yh)
+    torch.cuda.synchronize()
+    assert rel_l2(yh.float().cpu().numpy()[rows], wantf) <= 2e-3
+    W.close()

@@ -1,0 +1,208 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+Checks: golden vectors computed independently (tests/golden/make_golden.py),
+closed forms and invariants of the quantizer, brute-force integer dots,
+float64 brute force for the dequant-then-SGEMM branch, linearity.  Each check
+is chosen so that a plausible mistake fails it (see the comments).
+"""
+import numpy as np
+import pytest
+
+F = np.float32
+
+
+def _split(flat, lens):
+    out, o = [], 0
+    for n in lens:
+        out.append(flat[o:o + n]); o += n
+    return out
+
+
+@pytest.mark.parametrize("clamp", [1, 0])
+def test_quantizer_golden(orc, golden, clamp):
+    srcs = _split(golden["quant_src"], golden["quant_len"])
+    codes = _split(golden[f"quant_codes_c{clamp}"], golden["quant_len"])
+    for i, (src, want) in enumerate(zip(srcs, codes)):
+        q, s = orc.quantize_rows(src, clamp_main=bool(clamp))
+        assert s[0] == golden[f"quant_scales_c{clamp}"][i], i
+        np.testing.assert_array_equal(q[0], want, err_msg=f"case {i}")
+
+
+def test_quantizer_closed_forms(orc):
+    rng = np.random.default_rng(7)
+    for K in (16, 48, 2048, 6144, 37, 1):
+        x = (rng.standard_normal((5, K)) * rng.uniform(1e-3, 1e3, (5, 1))).astype(F)
+        q, s = orc.quantize_rows(x)
+        for r in range(5):
+            absmax = np.max(np.abs(x[r]))
+            assert s[r] == F(absmax) / F(127)                       # scale formula
+            assert np.all(np.abs(q[r].astype(int)) <= 127)
+            j = int(np.argmax(np.abs(x[r])))
+            assert abs(int(q[r, j])) == 127                          # argmax -> +-127
+            err = np.abs(x[r].astype(np.float64) - q[r].astype(np.float64) * float(s[r]))
+            # round-to-nearest: truncation or floor would break this bound
+            assert np.all(err <= float(s[r]) / 2 * (1 + 2.0 ** -22)), K
+
+
+def test_quantizer_ties(orc):
+    # s == 1 exactly (absmax 127): vector region rounds ties to even ...
+    x = np.zeros(32, F); x[0] = 127
+    x[1:7] = [2.5, 3.5, -2.5, -3.5, 0.5, -0.5]
+    q, s = orc.quantize_rows(x)
+    assert s[0] == 1.0
+    assert list(q[0, 1:7]) == [2, 4, -2, -4, 0, 0]
+    # ... and the scalar tail (k >= K & ~15) rounds ties away from zero (lroundf)
+    x = np.zeros(21, F); x[0] = 127
+    x[16:21] = [2.5, -2.5, 0.5, -0.5, 3.5]
+    q, _ = orc.quantize_rows(x)
+    assert list(q[0, 16:21]) == [3, -3, 1, -1, 4]
+
+
+def test_quantizer_uses_reciprocal_multiply(orc):
+    # code = rne(fl(x * fl(1/s))), not rne(fl(x / s)): find rows where the
+    # two differ (vectorised search) and require the first.
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((400000, 16)).astype(F)
+    s = np.max(np.abs(x), axis=1) / F(127)
+    inv = F(1) / s
+    a = np.rint(x * inv[:, None])
+    b = np.rint(x / s[:, None])
+    rows = np.nonzero(np.any(a != b, axis=1))[0][:64]
+    assert rows.size > 0
+    q, qs = orc.quantize_rows(x[rows])
+    np.testing.assert_array_equal(qs, s[rows])
+    np.testing.assert_array_equal(q, a[rows].astype(np.int8))
+
+
+def test_quantizer_special_rows(orc):
+    q, s = orc.quantize_rows(np.zeros((2, 40), F))
+    assert np.all(s == 1.0) and np.all(q == 0)
+    # NaN in the 16-aligned prefix: absmax is NaN, `absmax > 0` is false, s = 1
+    x = np.linspace(-3, 3, 32).astype(F); x[5] = np.nan
+    q, s = orc.quantize_rows(x)
+    assert s[0] == 1.0 and q[0, 5] == 0 and q[0, 31] == 3
+    # NaN only in the scalar tail is ignored by the `v > absmax` scan
+    x = np.linspace(-3, 3, 20).astype(F); x[18] = np.nan
+    q, s = orc.quantize_rows(x)
+    assert s[0] == F(3) / F(127) and q[0, 18] == 0
+    # Inf: scale Inf, inv 0, every code 0
+    x = np.ones(16, F); x[2] = np.inf
+    q, s = orc.quantize_rows(x)
+    assert np.isinf(s[0]) and np.all(q == 0)
+
+
+def test_activation_quantizer_matches_weight_quantizer(orc):
+    # |x*inv| <= 127 (1 + 3 eps) always rounds into [-127, 127], so the
+    # missing clamp of the activation quantizer never changes a code.
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((64, 2048)).astype(F)
+    a, sa = orc.quantize_rows(x, clamp_main=False)
+    b, sb = orc.quantize_rows(x, clamp_main=True)
+    np.testing.assert_array_equal(a, b)
+    np.testing.assert_array_equal(sa, sb)
+
+
+def test_int_acc_bruteforce(orc):
+    rng = np.random.default_rng(5)
+    xq = rng.integers(-127, 128, (3, 70), dtype=np.int8)
+    w = rng.integers(-127, 128, (9, 70), dtype=np.int8)
+    acc = orc.int_acc(xq, w)
+    for b in range(3):
+        for n in range(9):
+            assert acc[b, n] == sum(int(i) * int(j) for i, j in zip(xq[b], w[n]))
+    # the largest |acc| the reference can produce at K = 6144 still fits int32
+    xq = np.full((1, 6144), -127, np.int8)
+    w = np.full((2, 6144), -127, np.int8)
+    assert orc.int_acc(xq, w)[0, 0] == 127 * 127 * 6144
+
+
+@pytest.mark.parametrize("tag", ["a", "b", "c"])
+def test_gemv_golden(orc, golden, tag):
+    g = {k[len(f"gemv_{tag}_"):]: v for k, v in golden.items() if k.startswith(f"gemv_{tag}_")}
+    y, codes, xs, acc = orc.w8a32_linear(g["x"][None], g["w"], g["ws"], detail=True)
+    np.testing.assert_array_equal(codes, g["codes"])
+    assert xs == g["xs"][0]
+    np.testing.assert_array_equal(acc, g["acc"])
+    np.testing.assert_array_equal(y[0], g["y"])                       # bit-exact
+    yb = orc.w8a32_linear(g["x"][None], g["w"], g["ws"], bias=g["bias"])
+    np.testing.assert_array_equal(yb[0], g["ybias"])
+    y8 = orc.w8a8_linear(codes[None], g["xs"], g["w"], g["ws"], bias=g["bias"])
+    np.testing.assert_array_equal(y8[0], g["y8bias"])                 # fused epilogue
+
+
+def test_gemv_epilogue_order(orc):
+    # fl(fl(acc*ws)*xs) and fl(acc*fl(ws*xs)) differ in many outputs; the
+    # oracle must produce the first (w8a32_kernel.c:239).
+    rng = np.random.default_rng(1234)
+    N, K = 6144, 2048
+    x = rng.standard_normal(K).astype(F)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = rng.uniform(0.002, 0.02, N).astype(F)
+    y, codes, xs, acc = orc.w8a32_linear(x[None], w, ws, detail=True)
+    want = (acc.astype(F) * ws) * F(xs)
+    other = acc.astype(F) * (ws * F(xs))
+    np.testing.assert_array_equal(y[0], want)
+    assert np.count_nonzero(want != other) > 100
+
+
+def test_gemm_golden_and_bruteforce(orc, golden):
+    X, w, ws, Y = golden["gemm_X"], golden["gemm_w"], golden["gemm_ws"], golden["gemm_Y"]
+    y = orc.w8a32_linear(X, w, ws)
+    np.testing.assert_allclose(y, Y, rtol=1e-6, atol=1e-6)
+    # float64 brute force of dequant-then-dot on a larger case
+    rng = np.random.default_rng(9)
+    M, N, K = 5, 64, 2048
+    X = rng.standard_normal((M, K)).astype(F)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = rng.uniform(0.002, 0.02, N).astype(F)
+    wd = (w.astype(F) * ws[:, None]).astype(np.float64)
+    want = (X.astype(np.float64) @ wd.T).astype(F)
+    y = orc.w8a32_linear(X, w, ws)
+    rel = np.linalg.norm(y - want) / np.linalg.norm(want)
+    assert rel < 1e-7
+    # linearity in X (a dropped or transposed term breaks it)
+    y2 = orc.w8a32_linear(2 * X, w, ws)
+    np.testing.assert_allclose(y2, 2 * y, rtol=1e-6, atol=1e-6)
+
+
+def test_gemm_bias_is_separate_rounding(orc):
+    rng = np.random.default_rng(2)
+    M, N, K = 2, 16, 64
+    X = rng.standard_normal((M, K)).astype(F)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = rng.uniform(0.002, 0.02, N).astype(F)
+    b = rng.standard_normal(N).astype(F)
+    np.testing.assert_array_equal(orc.w8a32_linear(X, w, ws, bias=b),
+                                  orc.w8a32_linear(X, w, ws) + b)
+
+
+def test_w8a8_batch_paths(orc):
+    rng = np.random.default_rng(4)
+    M, N, K = 4, 48, 256
+    X = rng.standard_normal((M, K)).astype(F)
+    xq, xs = orc.quantize_rows(X)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = rng.uniform(0.002, 0.02, N).astype(F)
+    y = orc.w8a8_linear(xq, xs, w, ws)
+    acc = orc.int_acc(xq, w).astype(np.float64)
+    exact = acc * ws.astype(np.float64)[None] * xs.astype(np.float64)[:, None]
+    assert np.linalg.norm(y - exact) / np.linalg.norm(exact) < 1e-6
+    # batch == 1 row equals the M=1 epilogue on the same codes
+    y1 = orc.w8a8_linear(xq[:1], xs[:1], w, ws)
+    want = (acc[0].astype(F) * ws) * xs[0]
+    np.testing.assert_array_equal(y1[0], want.astype(F))
+
+
+def test_w8a16_paths(orc):
+    rng = np.random.default_rng(6)
+    M, N, K = 3, 32, 264
+    X = rng.standard_normal((M, K)).astype(F)
+    xb = (X.view(np.uint32) + 0x7fff + ((X.view(np.uint32) >> 16) & 1)) >> 16
+    xb = xb.astype(np.uint16)
+    xf = (xb.astype(np.uint32) << 16).view(F).astype(np.float64)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = rng.uniform(0.002, 0.02, N).astype(F)
+    for m in (1, M):
+        y = orc.w8a16_linear(xb[:m], w, ws)
+        exact = (xf[:m] @ w.astype(np.float64).T) * ws.astype(np.float64)
+        assert np.linalg.norm(y - exact) / np.linalg.norm(exact) < 1e-6

@@ -1,0 +1,845 @@
+// api.cpp -- C ABI of libtyphoon_linear.so (declared in include/typhoon_linear.h).
+//
+// Part 1 keeps the reference's host-pointer entry points
+// (kernel/w8a32_kernel.c:63-68, :355-363; kernel/w8a8_kernel.c:102-114,
+// :270-272; kernel/w8a16_kernel.c:44, :218-219): the arguments are borrowed
+// host memory, the call is synchronous and Y is complete on return.  Each call
+// stages X through pinned memory into HBM, runs the kernels on a library
+// stream, and copies Y back.  Quantized weights stay resident in HBM as 16x64
+// tiles: a registry keyed by (weight pointer, scale pointer, rows, cols,
+// device) and validated with a sampled content fingerprint uploads and packs
+// a weight matrix the first time it is used (the reference keeps the same
+// host arrays alive for the model's lifetime: decoder.py:215, :259).
+//
+// Part 2 exposes the same kernels on device pointers and caller streams.
+// Split-reduction work-space (partials + arrival counters, counters zero at
+// rest) is owned per (device, stream).
+#include "../../include/typhoon_linear.h"
+#include "tl_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+#include <vector>
+
+using namespace tl;
+
+struct tl_weights {
+  int dev = -1;
+  int rows = 0, cols = 0;
+  int KB = 0, NG = 0;
+  uint8_t* tiles = nullptr;   // NG * KB * 1024 bytes
+  float* scales = nullptr;    // NG * 16 floats, zero padded
+  size_t bytes = 0;
+};
+
+namespace {
+
+// --------------------------------------------------------------------------
+// errors
+// --------------------------------------------------------------------------
+thread_local std::string t_err;
+thread_local bool t_has_err = false;
+
+struct Fail {
+  std::string msg;
+};
+
+void record_error(const char* fn, const std::string& msg) {
+  t_err = std::string(fn) + ": " + msg;
+  t_has_err = true;
+  std::fprintf(stderr, "[typhoon_linear] %s\n", t_err.c_str());
+}
+
+#define HIP_OK(expr)                                                                     \
+  do {                                                                                   \
+    hipError_t _e = (expr);                                                              \
+    if (_e != hipSuccess) throw Fail{std::string(#expr) + " -> " + hipGetErrorString(_e)}; \
+  } while (0)
+#define REQUIRE(cond, msg) \
+  do {                     \
+    if (!(cond)) throw Fail{msg}; \
+  } while (0)
+
+template <class F>
+int guarded(const char* fn, F&& f) {
+  t_has_err = false;
+  try {
+    f();
+    return 0;
+  } catch (const Fail& e) {
+    record_error(fn, e.msg);
+  } catch (const std::exception& e) {
+    record_error(fn, e.what());
+  } catch (...) {
+    record_error(fn, "unknown error");
+  }
+  return -1;
+}
+
+int current_device() {
+  int d = -1;
+  HIP_OK(hipGetDevice(&d));
+  return d;
+}
+
+// --------------------------------------------------------------------------
+// buffers
+// --------------------------------------------------------------------------
+struct DevBuf {
+  void* p = nullptr;
+  size_t n = 0;
+  // grows to at least `bytes`; `st` is synchronized before an old buffer is freed
+  void ensure(size_t bytes, hipStream_t st) {
+    if (bytes <= n) return;
+    if (p) {
+      HIP_OK(hipStreamSynchronize(st));
+      HIP_OK(hipFree(p));
+      p = nullptr;
+      n = 0;
+    }
+    size_t want = bytes < 256 ? 256 : bytes;
+    HIP_OK(hipMalloc(&p, want));
+    n = want;
+  }
+};
+
+struct PinnedBuf {
+  void* p = nullptr;
+  size_t n = 0;
+  void ensure(size_t bytes) {
+    if (bytes <= n) return;
+    if (p) {
+      HIP_OK(hipHostFree(p));
+      p = nullptr;
+      n = 0;
+    }
+    size_t want = bytes < 4096 ? 4096 : bytes;
+    HIP_OK(hipHostMalloc(&p, want, hipHostMallocDefault));
+    n = want;
+  }
+};
+
+// --------------------------------------------------------------------------
+// per (device, stream) work-space
+// --------------------------------------------------------------------------
+struct Workspace {
+  DevBuf part;        // split partial sums
+  DevBuf cnt;         // arrival counters (zero at rest)
+  size_t cnt_n = 0;
+  DevBuf act;         // activation codes (tiles or padded rows)
+  DevBuf act_s;       // activation scales
+};
+
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, Workspace*> g_ws;
+
+Workspace& workspace(int dev, hipStream_t st) {
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  auto key = std::make_pair(dev, st);
+  auto it = g_ws.find(key);
+  if (it != g_ws.end()) return *it->second;
+  Workspace* w = new Workspace();
+  g_ws[key] = w;
+  return *w;
+}
+
+uint32_t* ensure_counters(Workspace& w, size_t n, hipStream_t st) {
+  if (n > w.cnt_n) {
+    size_t want = n < 65536 ? 65536 : n;
+    w.cnt.ensure(want * sizeof(uint32_t), st);
+    HIP_OK(hipMemsetAsync(w.cnt.p, 0, want * sizeof(uint32_t), st));
+    HIP_OK(hipStreamSynchronize(st));
+    w.cnt_n = want;
+  }
+  return static_cast<uint32_t*>(w.cnt.p);
+}
+
+// --------------------------------------------------------------------------
+// weights
+// --------------------------------------------------------------------------
+tl_weights* weights_alloc(int rows, int cols) {
+  REQUIRE(rows > 0 && cols > 0, "rows and cols must be positive");
+  tl_weights* W = new tl_weights();
+  W->dev = current_device();
+  W->rows = rows;
+  W->cols = cols;
+  W->KB = cdiv(cols, 64);
+  W->NG = cdiv(rows, 16);
+  const size_t tb = (size_t)W->NG * W->KB * 1024;
+  const size_t sb = (size_t)W->NG * 16 * sizeof(float);
+  if (hipMalloc(&W->tiles, tb) != hipSuccess) {
+    delete W;
+    throw Fail{"out of device memory for weight tiles"};
+  }
+  if (hipMalloc(&W->scales, sb) != hipSuccess) {
+    (void)hipFree(W->tiles);
+    delete W;
+    throw Fail{"out of device memory for weight scales"};
+  }
+  W->bytes = tb + sb;
+  return W;
+}
+
+void weights_free(tl_weights* W) {
+  if (!W) return;
+  if (W->tiles) (void)hipFree(W->tiles);
+  if (W->scales) (void)hipFree(W->scales);
+  delete W;
+}
+
+// pack row-major int8 (host or device) + scales into a new tl_weights
+tl_weights* weights_from_codes(const int8_t* w, const float* s, int rows, int cols, bool on_device,
+                               hipStream_t st) {
+  tl_weights* W = weights_alloc(rows, cols);
+  try {
+    const size_t wb = (size_t)rows * cols;
+    HIP_OK(hipMemsetAsync(W->scales, 0, (size_t)W->NG * 16 * sizeof(float), st));
+    HIP_OK(hipMemcpyAsync(W->scales, s, (size_t)rows * sizeof(float),
+                          on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st));
+    if (on_device) {
+      HIP_OK(launch_pack_tiles(w, rows, cols, W->tiles, st));
+      HIP_OK(hipStreamSynchronize(st));
+    } else {
+      void* tmp = nullptr;
+      HIP_OK(hipMalloc(&tmp, wb));
+      hipError_t e = hipMemcpyAsync(tmp, w, wb, hipMemcpyHostToDevice, st);
+      if (e == hipSuccess) e = launch_pack_tiles(static_cast<const int8_t*>(tmp), rows, cols, W->tiles, st);
+      hipError_t e2 = hipStreamSynchronize(st);
+      (void)hipFree(tmp);
+      HIP_OK(e);
+      HIP_OK(e2);
+    }
+  } catch (...) {
+    weights_free(W);
+    throw;
+  }
+  return W;
+}
+
+// --------------------------------------------------------------------------
+// host-weight registry
+// --------------------------------------------------------------------------
+struct RegKey {
+  const void* w;
+  const void* s;
+  int rows, cols, dev;
+  bool operator<(const RegKey& o) const {
+    if (w != o.w) return w < o.w;
+    if (s != o.s) return s < o.s;
+    if (rows != o.rows) return rows < o.rows;
+    if (cols != o.cols) return cols < o.cols;
+    return dev < o.dev;
+  }
+};
+struct RegEntry {
+  tl_weights* W = nullptr;
+  uint64_t fp = 0;
+  uint64_t tick = 0;
+};
+
+std::mutex g_reg_mu;
+std::map<RegKey, RegEntry> g_reg;
+uint64_t g_tick = 0;
+size_t g_reg_bytes = 0;
+
+size_t registry_cap() {
+  static size_t cap = [] {
+    const char* e = std::getenv("TL_REGISTRY_MAX_BYTES");
+    if (e && *e) return (size_t)std::strtoull(e, nullptr, 10);
+    return (size_t)96 << 30;  // HBM budget for cached weights (288 GB per GPU)
+  }();
+  return cap;
+}
+
+inline uint64_t mix64(uint64_t h, uint64_t v) {
+  h ^= v + 0x9e3779b97f4a7c15ull + (h << 6) + (h >> 2);
+  h ^= h >> 31;
+  h *= 0xbf58476d1ce4e5b9ull;
+  return h ^ (h >> 29);
+}
+
+// sampled content fingerprint: 64 eight-byte windows of W, 32 scales, shape
+uint64_t fingerprint(const int8_t* w, const float* s, int rows, int cols) {
+  uint64_t h = mix64((uint64_t)rows, (uint64_t)cols);
+  const size_t n = (size_t)rows * cols;
+  if (n >= 8) {
+    for (int i = 0; i < 64; i++) {
+      size_t off = (size_t)(((unsigned __int128)(n - 8) * (unsigned)i) / 63);
+      uint64_t v;
+      std::memcpy(&v, w + off, 8);
+      h = mix64(h, v);
+    }
+  } else {
+    for (size_t i = 0; i < n; i++) h = mix64(h, (uint64_t)(uint8_t)w[i]);
+  }
+  for (int i = 0; i < 32; i++) {
+    size_t r = (size_t)(((unsigned long long)(rows - 1) * (unsigned)i) / 31);
+    uint32_t v;
+    std::memcpy(&v, s + r, 4);
+    h = mix64(h, v);
+  }
+  return h;
+}
+
+void registry_evict_lru_locked(size_t need) {
+  while (!g_reg.empty() && g_reg_bytes + need > registry_cap()) {
+    auto victim = g_reg.begin();
+    for (auto it = g_reg.begin(); it != g_reg.end(); ++it)
+      if (it->second.tick < victim->second.tick) victim = it;
+    g_reg_bytes -= victim->second.W->bytes;
+    weights_free(victim->second.W);
+    g_reg.erase(victim);
+  }
+}
+
+const tl_weights* registry_get(const int8_t* w, const float* s, int rows, int cols, hipStream_t st) {
+  REQUIRE(w && s, "weight and scale pointers must be non-NULL");
+  const int dev = current_device();
+  const uint64_t fp = fingerprint(w, s, rows, cols);
+  std::lock_guard<std::mutex> lk(g_reg_mu);
+  RegKey key{w, s, rows, cols, dev};
+  auto it = g_reg.find(key);
+  if (it != g_reg.end()) {
+    if (it->second.fp == fp) {
+      it->second.tick = ++g_tick;
+      return it->second.W;
+    }
+    g_reg_bytes -= it->second.W->bytes;  // contents changed in place: re-upload
+    weights_free(it->second.W);
+    g_reg.erase(it);
+  }
+  const size_t need = (size_t)cdiv(rows, 16) * 16 * (size_t)cdiv(cols, 64) * 64 + (size_t)rows * 4;
+  registry_evict_lru_locked(need);
+  tl_weights* W = weights_from_codes(w, s, rows, cols, false, st);
+  g_reg[key] = RegEntry{W, fp, ++g_tick};
+  g_reg_bytes += W->bytes;
+  return W;
+}
+
+// --------------------------------------------------------------------------
+// host-call context (Part 1): one per device, calls serialized
+// --------------------------------------------------------------------------
+struct HostCtx {
+  hipStream_t st = nullptr;
+  DevBuf x, y, bias, xs;
+  PinnedBuf hin, hout;
+};
+std::mutex g_host_mu;
+std::map<int, HostCtx*> g_host;
+
+HostCtx& host_ctx(int dev) {
+  auto it = g_host.find(dev);
+  if (it != g_host.end()) return *it->second;
+  HostCtx* c = new HostCtx();
+  HIP_OK(hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking));
+  g_host[dev] = c;
+  return *c;
+}
+
+void h2d(HostCtx& c, DevBuf& d, const void* src, size_t bytes) {
+  c.hin.ensure(bytes);
+  d.ensure(bytes, c.st);
+  HIP_OK(hipStreamSynchronize(c.st));  // hin may still be the source of an earlier copy
+  std::memcpy(c.hin.p, src, bytes);
+  HIP_OK(hipMemcpyAsync(d.p, c.hin.p, bytes, hipMemcpyHostToDevice, c.st));
+}
+
+void d2h(HostCtx& c, void* dst, const void* src, size_t bytes) {
+  c.hout.ensure(bytes);
+  HIP_OK(hipMemcpyAsync(c.hout.p, src, bytes, hipMemcpyDeviceToHost, c.st));
+  HIP_OK(hipStreamSynchronize(c.st));
+  std::memcpy(dst, c.hout.p, bytes);
+}
+
+void check_shape(int batch, int M, int K) {
+  REQUIRE(batch >= 1, "batch must be >= 1");
+  REQUIRE(M >= 1, "M (output features) must be >= 1");
+  REQUIRE(K >= 1, "K (input features) must be >= 1");
+}
+
+// --------------------------------------------------------------------------
+// device-level operations shared by Part 1 and Part 2
+// --------------------------------------------------------------------------
+void check_weights(const tl_weights* W) {
+  REQUIRE(W != nullptr, "weights handle is NULL");
+  REQUIRE(W->dev == current_device(), "weights live on another device");
+}
+
+// precomputed codes for the GEMV: row-major, zero padded to KB*64
+uint8_t* quantize_padded(Workspace& ws, const float* x, int K, float** xs_dev, hipStream_t st) {
+  const int kpad = cdiv(K, 64) * 64;
+  ws.act.ensure((size_t)kpad, st);
+  ws.act_s.ensure(sizeof(float), st);
+  HIP_OK(hipMemsetAsync(ws.act.p, 0, (size_t)kpad, st));
+  HIP_OK(launch_quantize_rows(x, static_cast<int8_t*>(ws.act.p), static_cast<float*>(ws.act_s.p), 1, K,
+                              false, st));
+  *xs_dev = static_cast<float*>(ws.act_s.p);
+  return static_cast<uint8_t*>(ws.act.p);
+}
+
+void run_gemv(Workspace& ws, GemvLaunch& L, hipStream_t st) {
+  GemvPlan p = gemv_plan(L.N, L.K);
+  if (p.split > 1) {
+    ws.part.ensure(gemv_workspace_bytes(L.N, L.K), st);
+    L.part = static_cast<int32_t*>(ws.part.p);
+    L.cnt = ensure_counters(ws, (size_t)cdiv(L.N, 16), st);
+  }
+  HIP_OK(launch_gemv_i8(L, st));
+}
+
+void run_gemm(Workspace& ws, GemmLaunch& L, hipStream_t st) {
+  GemmPlan p = gemm_plan(L.amode, L.M, L.N, L.K);
+  if (p.split > 1) {
+    ws.part.ensure(gemm_workspace_bytes(L.amode, L.M, L.N, L.K), st);
+    L.part = ws.part.p;
+    L.cnt = ensure_counters(ws, gemm_counter_count(L.amode, L.M, L.N, L.K), st);
+  }
+  HIP_OK(launch_gemm(L, st));
+}
+
+void op_w8a32(const float* X, const tl_weights* W, const float* bias, float* Y, int batch,
+              hipStream_t st) {
+  Workspace& ws = workspace(W->dev, st);
+  if (batch == 1) {
+    GemvLaunch L;
+    L.wt = W->tiles;
+    L.ws = W->scales;
+    L.bias = bias;
+    L.y = Y;
+    L.N = W->rows;
+    L.K = W->cols;
+    L.epi = EPI_W8A32;
+    if (gemv_fused_xv(W->cols) > 0) {
+      L.x = X;
+    } else {
+      float* xs = nullptr;
+      L.xq = quantize_padded(ws, X, W->cols, &xs, st);
+      L.xs_in = xs;
+    }
+    run_gemv(ws, L, st);
+  } else {
+    GemmLaunch L;
+    L.amode = A_F32X3;
+    L.A = X;
+    L.lda = W->cols;
+    L.Bt = W->tiles;
+    L.ws = W->scales;
+    L.bias = bias;
+    L.Y = Y;
+    L.ldy = W->rows;
+    L.M = batch;
+    L.N = W->rows;
+    L.K = W->cols;
+    L.ep = EP_SCALE;
+    L.out = OUT_F32;
+    run_gemm(ws, L, st);
+  }
+}
+
+// W8A8 on row-major device codes
+void op_w8a8_codes(const int8_t* xq, const float* xs, const tl_weights* W, const float* bias,
+                   void* Y, int out, int batch, hipStream_t st) {
+  Workspace& ws = workspace(W->dev, st);
+  const int K = W->cols, KB = W->KB;
+  if (batch == 1 && out != OUT_I32) {
+    // codes must be zero padded to KB*64 for the GEMV
+    const int kpad = KB * 64;
+    ws.act.ensure((size_t)kpad, st);
+    if (kpad != K) HIP_OK(hipMemsetAsync(ws.act.p, 0, (size_t)kpad, st));
+    HIP_OK(hipMemcpyAsync(ws.act.p, xq, (size_t)K, hipMemcpyDeviceToDevice, st));
+    GemvLaunch L;
+    L.xq = static_cast<const uint8_t*>(ws.act.p);
+    L.xs_in = xs;
+    L.wt = W->tiles;
+    L.ws = W->scales;
+    L.bias = bias;
+    L.y = static_cast<float*>(Y);
+    L.N = W->rows;
+    L.K = K;
+    L.epi = EPI_W8A8;
+    run_gemv(ws, L, st);
+    return;
+  }
+  const size_t tb = (size_t)cdiv(batch, 16) * KB * 1024;
+  ws.act.ensure(tb, st);
+  HIP_OK(launch_pack_tiles(xq, batch, K, static_cast<uint8_t*>(ws.act.p), st));
+  GemmLaunch L;
+  L.amode = A_I8;
+  L.A = ws.act.p;
+  L.Bt = W->tiles;
+  L.ws = W->scales;
+  L.xs = xs;
+  L.bias = bias;
+  L.Y = Y;
+  L.ldy = W->rows;
+  L.M = batch;
+  L.N = W->rows;
+  L.K = K;
+  L.out = out;
+  run_gemm(ws, L, st);
+}
+
+void op_w8a16(const void* X, int x_type, const tl_weights* W, const float* bias, void* Y,
+              int y_type, int batch, hipStream_t st) {
+  REQUIRE(x_type == TL_BF16 || x_type == TL_F16, "x_type must be TL_BF16 or TL_F16");
+  REQUIRE(y_type == TL_F32 || y_type == TL_BF16 || y_type == TL_F16, "bad y_type");
+  Workspace& ws = workspace(W->dev, st);
+  GemmLaunch L;
+  L.amode = (x_type == TL_BF16) ? A_BF16 : A_F16;
+  L.A = X;
+  L.lda = W->cols;
+  L.Bt = W->tiles;
+  L.ws = W->scales;
+  L.bias = bias;
+  L.Y = Y;
+  L.ldy = W->rows;
+  L.M = batch;
+  L.N = W->rows;
+  L.K = W->cols;
+  // batch==1 fuses the bias into one fma (kernel/w8a16_kernel.c:134); batch>1
+  // adds it after the product (:193-200)
+  L.ep = (batch == 1) ? EP_SCALE_FMA : EP_SCALE;
+  L.out = (y_type == TL_F32) ? OUT_F32 : (y_type == TL_BF16 ? OUT_BF16 : OUT_F16);
+  run_gemm(ws, L, st);
+}
+
+void host_quantize(const char* fn, const float* src, int8_t* dst, float* scales, int rows,
+                   int cols, bool clamp127) {
+  (void)fn;
+  REQUIRE(src && dst && scales, "NULL pointer");
+  REQUIRE(rows >= 1 && cols >= 1, "rows and cols must be >= 1");
+  std::lock_guard<std::mutex> lk(g_host_mu);
+  HostCtx& c = host_ctx(current_device());
+  // chunks of at most 64 MiB of fp32 input
+  int chunk = (int)std::max<size_t>(1, ((size_t)64 << 20) / ((size_t)cols * 4));
+  if (chunk > rows) chunk = rows;
+  c.y.ensure((size_t)chunk * cols, c.st);
+  c.xs.ensure((size_t)chunk * sizeof(float), c.st);
+  for (int r0 = 0; r0 < rows; r0 += chunk) {
+    const int nr = std::min(chunk, rows - r0);
+    h2d(c, c.x, src + (size_t)r0 * cols, (size_t)nr * cols * sizeof(float));
+    HIP_OK(launch_quantize_rows(static_cast<const float*>(c.x.p), static_cast<int8_t*>(c.y.p),
+                                static_cast<float*>(c.xs.p), nr, cols, clamp127, c.st));
+    d2h(c, dst + (size_t)r0 * cols, c.y.p, (size_t)nr * cols);
+    d2h(c, scales + r0, c.xs.p, (size_t)nr * sizeof(float));
+  }
+}
+
+}  // namespace
+
+// ==========================================================================
+// Part 1 -- reference entry points
+// ==========================================================================
+extern "C" {
+
+void w8a32_quantize(const float* w_fp32, int8_t* w_int8, float* scales, int rows, int cols) {
+  guarded("w8a32_quantize", [&] { host_quantize("w8a32_quantize", w_fp32, w_int8, scales, rows, cols, true); });
+}
+
+void w8a8_quantize_weights(const float* w_fp32, int8_t* w_int8, float* w_scales, int rows, int cols) {
+  guarded("w8a8_quantize_weights",
+          [&] { host_quantize("w8a8_quantize_weights", w_fp32, w_int8, w_scales, rows, cols, true); });
+}
+
+void w8a8_quantize_activations(const float* x_fp32, int8_t* x_int8, float* x_scales, int batch, int K) {
+  guarded("w8a8_quantize_activations",
+          [&] { host_quantize("w8a8_quantize_activations", x_fp32, x_int8, x_scales, batch, K, true); });
+}
+
+void w8a16_quantize_weights(const float* w_fp32, int8_t* w_int8, float* scales, int rows, int cols) {
+  guarded("w8a16_quantize_weights",
+          [&] { host_quantize("w8a16_quantize_weights", w_fp32, w_int8, scales, rows, cols, true); });
+}
+
+void w8a32_linear(const float* X, const int8_t* w_int8, const float* scales, const float* bias,
+                  float* Y, float* scratch, int batch, int M, int K) {
+  (void)scratch;  // unused, as in the reference (kernel/w8a32_kernel.c:364)
+  guarded("w8a32_linear", [&] {
+    check_shape(batch, M, K);
+    REQUIRE(X && Y, "X and Y must be non-NULL");
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    HostCtx& c = host_ctx(current_device());
+    const tl_weights* W = registry_get(w_int8, scales, M, K, c.st);
+    h2d(c, c.x, X, (size_t)batch * K * sizeof(float));
+    const float* b = nullptr;
+    if (bias) {
+      c.bias.ensure((size_t)M * sizeof(float), c.st);
+      HIP_OK(hipMemcpyAsync(c.bias.p, bias, (size_t)M * sizeof(float), hipMemcpyHostToDevice, c.st));
+      b = static_cast<const float*>(c.bias.p);
+    }
+    c.y.ensure((size_t)batch * M * sizeof(float), c.st);
+    op_w8a32(static_cast<const float*>(c.x.p), W, b, static_cast<float*>(c.y.p), batch, c.st);
+    d2h(c, Y, c.y.p, (size_t)batch * M * sizeof(float));
+  });
+}
+
+void w8a8_linear(const int8_t* x_int8, const float* x_scales, const int8_t* w_int8,
+                 const float* w_scales, const float* bias, float* Y, int batch, int M, int K) {
+  guarded("w8a8_linear", [&] {
+    check_shape(batch, M, K);
+    REQUIRE(x_int8 && x_scales && Y, "x_int8, x_scales and Y must be non-NULL");
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    HostCtx& c = host_ctx(current_device());
+    const tl_weights* W = registry_get(w_int8, w_scales, M, K, c.st);
+    h2d(c, c.x, x_int8, (size_t)batch * K);
+    c.xs.ensure((size_t)batch * sizeof(float), c.st);
+    HIP_OK(hipMemcpyAsync(c.xs.p, x_scales, (size_t)batch * sizeof(float), hipMemcpyHostToDevice, c.st));
+    const float* b = nullptr;
+    if (bias) {
+      c.bias.ensure((size_t)M * sizeof(float), c.st);
+      HIP_OK(hipMemcpyAsync(c.bias.p, bias, (size_t)M * sizeof(float), hipMemcpyHostToDevice, c.st));
+      b = static_cast<const float*>(c.bias.p);
+    }
+    c.y.ensure((size_t)batch * M * sizeof(float), c.st);
+    op_w8a8_codes(static_cast<const int8_t*>(c.x.p), static_cast<const float*>(c.xs.p), W, b, c.y.p,
+                  OUT_F32, batch, c.st);
+    d2h(c, Y, c.y.p, (size_t)batch * M * sizeof(float));
+  });
+}
+
+void w8a16_linear(const uint16_t* x_bf16_raw, const int8_t* w_int8, const float* w_scales,
+                  const float* bias, float* Y, int batch, int M, int K) {
+  guarded("w8a16_linear", [&] {
+    check_shape(batch, M, K);
+    REQUIRE(x_bf16_raw && Y, "x and Y must be non-NULL");
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    HostCtx& c = host_ctx(current_device());
+    const tl_weights* W = registry_get(w_int8, w_scales, M, K, c.st);
+    h2d(c, c.x, x_bf16_raw, (size_t)batch * K * sizeof(uint16_t));
+    const float* b = nullptr;
+    if (bias) {
+      c.bias.ensure((size_t)M * sizeof(float), c.st);
+      HIP_OK(hipMemcpyAsync(c.bias.p, bias, (size_t)M * sizeof(float), hipMemcpyHostToDevice, c.st));
+      b = static_cast<const float*>(c.bias.p);
+    }
+    c.y.ensure((size_t)batch * M * sizeof(float), c.st);
+    op_w8a16(c.x.p, TL_BF16, W, b, c.y.p, TL_F32, batch, c.st);
+    d2h(c, Y, c.y.p, (size_t)batch * M * sizeof(float));
+  });
+}
+
+// ==========================================================================
+// Part 2 -- extensions
+// ==========================================================================
+const char* tl_last_error(void) { return t_has_err ? t_err.c_str() : nullptr; }
+void tl_clear_error(void) { t_has_err = false; }
+const char* tl_version(void) { return "typhoon_linear 0.1 gfx950"; }
+
+int tl_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+int tl_register_weights(const int8_t* w_int8, const float* scales, int rows, int cols) {
+  return guarded("tl_register_weights", [&] {
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    HostCtx& c = host_ctx(current_device());
+    (void)registry_get(w_int8, scales, rows, cols, c.st);
+  });
+}
+
+int tl_evict_weights(const int8_t* w_int8) {
+  return guarded("tl_evict_weights", [&] {
+    std::lock_guard<std::mutex> lk(g_reg_mu);
+    for (auto it = g_reg.begin(); it != g_reg.end();) {
+      if (it->first.w == (const void*)w_int8) {
+        g_reg_bytes -= it->second.W->bytes;
+        weights_free(it->second.W);
+        it = g_reg.erase(it);
+      } else {
+        ++it;
+      }
+    }
+  });
+}
+
+void tl_registry_clear(void) {
+  std::lock_guard<std::mutex> lk(g_reg_mu);
+  for (auto& kv : g_reg) weights_free(kv.second.W);
+  g_reg.clear();
+  g_reg_bytes = 0;
+}
+
+size_t tl_registry_bytes(void) {
+  std::lock_guard<std::mutex> lk(g_reg_mu);
+  return g_reg_bytes;
+}
+
+int tl_registry_entries(void) {
+  std::lock_guard<std::mutex> lk(g_reg_mu);
+  return (int)g_reg.size();
+}
+
+tl_weights* tl_weights_create(const int8_t* w_int8, const float* scales, int rows, int cols,
+                              int src_on_device) {
+  tl_weights* out = nullptr;
+  guarded("tl_weights_create", [&] {
+    REQUIRE(w_int8 && scales, "NULL pointer");
+    hipStream_t st = nullptr;
+    out = weights_from_codes(w_int8, scales, rows, cols, src_on_device != 0, st);
+  });
+  return out;
+}
+
+tl_weights* tl_weights_quantize_dev(const float* w_fp32, int rows, int cols, int8_t* codes_out,
+                                    float* scales_out, void* stream) {
+  tl_weights* out = nullptr;
+  guarded("tl_weights_quantize_dev", [&] {
+    REQUIRE(w_fp32, "NULL pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    tl_weights* W = weights_alloc(rows, cols);
+    hipError_t e = hipMemsetAsync(W->scales, 0, (size_t)W->NG * 16 * sizeof(float), st);
+    if (e == hipSuccess) e = launch_quantize_rows_tiled(w_fp32, rows, cols, W->tiles, W->scales, true, st);
+    if (e == hipSuccess && codes_out) {
+      float* s2 = scales_out;
+      DevBuf tmp;
+      if (!s2) {
+        tmp.ensure((size_t)rows * sizeof(float), st);
+        s2 = static_cast<float*>(tmp.p);
+      }
+      e = launch_quantize_rows(w_fp32, codes_out, s2, rows, cols, true, st);
+      if (e == hipSuccess) e = hipStreamSynchronize(st);
+      if (tmp.p) (void)hipFree(tmp.p);
+    } else if (e == hipSuccess && scales_out) {
+      e = hipMemcpyAsync(scales_out, W->scales, (size_t)rows * sizeof(float), hipMemcpyDeviceToDevice, st);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) {
+      weights_free(W);
+      throw Fail{std::string("quantize: ") + hipGetErrorString(e)};
+    }
+    out = W;
+  });
+  return out;
+}
+
+void tl_weights_destroy(tl_weights* w) { weights_free(w); }
+int tl_weights_rows(const tl_weights* w) { return w ? w->rows : -1; }
+int tl_weights_cols(const tl_weights* w) { return w ? w->cols : -1; }
+size_t tl_weights_bytes(const tl_weights* w) { return w ? w->bytes : 0; }
+
+int tl_w8a32_linear_dev(const float* X, const tl_weights* W, const float* bias, float* Y, int batch,
+                        void* stream) {
+  return guarded("tl_w8a32_linear_dev", [&] {
+    check_weights(W);
+    REQUIRE(batch >= 1 && X && Y, "bad arguments");
+    op_w8a32(X, W, bias, Y, batch, static_cast<hipStream_t>(stream));
+  });
+}
+
+int tl_quantize_rows_dev(const float* src, int8_t* codes, float* scales, int rows, int cols,
+                         int clamp127, void* stream) {
+  return guarded("tl_quantize_rows_dev", [&] {
+    REQUIRE(src && codes && scales && rows >= 1 && cols >= 1, "bad arguments");
+    HIP_OK(launch_quantize_rows(src, codes, scales, rows, cols, clamp127 != 0,
+                                static_cast<hipStream_t>(stream)));
+  });
+}
+
+int tl_w8a8_linear_dev(const int8_t* x_int8, const float* x_scales, const tl_weights* W,
+                       const float* bias, float* Y, int batch, void* stream) {
+  return guarded("tl_w8a8_linear_dev", [&] {
+    check_weights(W);
+    REQUIRE(batch >= 1 && x_int8 && x_scales && Y, "bad arguments");
+    op_w8a8_codes(x_int8, x_scales, W, bias, Y, OUT_F32, batch, static_cast<hipStream_t>(stream));
+  });
+}
+
+int tl_w8a8_linear_f32_dev(const float* X, const tl_weights* W, const float* bias, float* Y, int batch,
+                           void* stream) {
+  return guarded("tl_w8a8_linear_f32_dev", [&] {
+    check_weights(W);
+    REQUIRE(batch >= 1 && X && Y, "bad arguments");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    Workspace& ws = workspace(W->dev, st);
+    if (batch == 1) {
+      GemvLaunch L;
+      L.wt = W->tiles;
+      L.ws = W->scales;
+      L.bias = bias;
+      L.y = Y;
+      L.N = W->rows;
+      L.K = W->cols;
+      L.epi = EPI_W8A8;
+      if (gemv_fused_xv(W->cols) > 0) {
+        L.x = X;
+      } else {
+        float* xs = nullptr;
+        L.xq = quantize_padded(ws, X, W->cols, &xs, st);
+        L.xs_in = xs;
+      }
+      run_gemv(ws, L, st);
+      return;
+    }
+    const int MG = cdiv(batch, 16);
+    ws.act.ensure((size_t)MG * W->KB * 1024, st);
+    ws.act_s.ensure((size_t)MG * 16 * sizeof(float), st);
+    HIP_OK(launch_quantize_rows_tiled(X, batch, W->cols, static_cast<uint8_t*>(ws.act.p),
+                                      static_cast<float*>(ws.act_s.p), true, st));
+    GemmLaunch L;
+    L.amode = A_I8;
+    L.A = ws.act.p;
+    L.Bt = W->tiles;
+    L.ws = W->scales;
+    L.xs = static_cast<const float*>(ws.act_s.p);
+    L.bias = bias;
+    L.Y = Y;
+    L.ldy = W->rows;
+    L.M = batch;
+    L.N = W->rows;
+    L.K = W->cols;
+    L.out = OUT_F32;
+    run_gemm(ws, L, st);
+  });
+}
+
+int tl_w8a16_linear_dev(const void* X, int x_type, const tl_weights* W, const float* bias, void* Y,
+                        int y_type, int batch, void* stream) {
+  return guarded("tl_w8a16_linear_dev", [&] {
+    check_weights(W);
+    REQUIRE(batch >= 1 && X && Y, "bad arguments");
+    op_w8a16(X, x_type, W, bias, Y, y_type, batch, static_cast<hipStream_t>(stream));
+  });
+}
+
+int tl_w8a32_gemv_acc_dev(const float* x, const tl_weights* W, int32_t* acc, float* x_scale,
+                          void* stream) {
+  return guarded("tl_w8a32_gemv_acc_dev", [&] {
+    check_weights(W);
+    REQUIRE(x && acc, "bad arguments");
+    REQUIRE(gemv_fused_xv(W->cols) > 0, "K too large for the fused GEMV");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    Workspace& ws = workspace(W->dev, st);
+    GemvLaunch L;
+    L.x = x;
+    L.wt = W->tiles;
+    L.ws = W->scales;
+    L.acc_out = acc;
+    L.xs_out = x_scale;
+    L.N = W->rows;
+    L.K = W->cols;
+    L.epi = EPI_ACC;
+    run_gemv(ws, L, st);
+  });
+}
+
+int tl_w8a8_gemm_acc_dev(const int8_t* x_int8, const tl_weights* W, int32_t* acc, int batch,
+                         void* stream) {
+  return guarded("tl_w8a8_gemm_acc_dev", [&] {
+    check_weights(W);
+    REQUIRE(batch >= 1 && x_int8 && acc, "bad arguments");
+    op_w8a8_codes(x_int8, nullptr, W, nullptr, acc, OUT_I32, batch, static_cast<hipStream_t>(stream));
+  });
+}
+
+}  // extern "C"

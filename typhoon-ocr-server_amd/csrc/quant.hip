@@ -1,0 +1,223 @@
+// quant.hip -- per-row symmetric int8 quantization and weight tile packing.
+//
+// quantize_rows_kernel restates the reference quantizers on the GPU, bit for
+// bit (kernel/w8a32_kernel.c:63-108 w8a32_quantize, :139-178
+// _quantize_activation_i8; kernel/w8a8_kernel.c:54-100 _quantize_rows;
+// kernel/w8a16_kernel.c:44-65 w8a16_quantize_weights):
+//   absmax = max|x|     (NaN-propagating over the 16-aligned prefix, a
+//                        NaN-ignoring scan over the K%16 tail)
+//   scale  = absmax > 0 ? fl(absmax/127) : 1,   inv = fl(1/scale)
+//   code   = k < K&~15 ? rne(fl(x*inv)) : round-half-away(fl(x*inv)),
+//            clamped to [-127,127] (the activation quantizer of the M=1 GEMV
+//            only saturates to [-128,127]; |x*inv| <= 127(1+3 eps) makes the
+//            two identical)
+// One work-group of 256 threads per row: pass 1 reduces the absmax, pass 2
+// re-reads the (L2-resident) row and writes codes.
+//
+// quantize_rows_tiled_kernel does the same for 16 rows at once and writes the
+// codes straight into the 16x64 tile layout used as the int8 MFMA A operand.
+//
+// pack_tiles_kernel re-lays a row-major int8 matrix into 16x64 tiles.
+#include "tl_common.h"
+#include "tl_kernels.h"
+
+namespace tl {
+
+__global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restrict__ src,
+                                                            int8_t* __restrict__ dst,
+                                                            float* __restrict__ scales, int cols,
+                                                            int clamp127) {
+  __shared__ uint32_t s_mx[4];
+  __shared__ float s_tail[4];
+  const int r = blockIdx.x;
+  const float* row = src + (size_t)r * cols;
+  int8_t* out = dst + (size_t)r * cols;
+  const int main_end = cols & ~15;
+  const bool vec = ((cols & 3) == 0) && ((((uintptr_t)row) & 15) == 0);
+
+  uint32_t mx = 0;
+  float tail = 0.0f;
+  if (vec) {
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+    for (int i = threadIdx.x; i < (main_end >> 2); i += 256) {
+      float4 v = r4[i];
+      uint32_t a = max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w)));
+      mx = a > mx ? a : mx;
+    }
+  } else {
+    for (int k = threadIdx.x; k < main_end; k += 256) {
+      uint32_t a = abs_bits(row[k]);
+      mx = a > mx ? a : mx;
+    }
+  }
+  for (int k = main_end + threadIdx.x; k < cols; k += 256) {
+    float a = fabsf(row[k]);
+    tail = (a > tail) ? a : tail;
+  }
+  const float absmax = block_absmax_256(mx, tail, s_mx, s_tail);
+  const float scale = quant_scale(absmax);
+  const float inv = quant_inv(scale);
+  if (threadIdx.x == 0) scales[r] = scale;
+
+  const bool c127 = clamp127 != 0;
+  if (vec && ((((uintptr_t)out) & 3) == 0)) {
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+    uint32_t* o4 = reinterpret_cast<uint32_t*>(out);
+    for (int i = threadIdx.x; i < (cols >> 2); i += 256) {
+      float4 v = r4[i];
+      int k = i << 2;
+      o4[i] = pack4(code_at(v.x, inv, k, cols, c127), code_at(v.y, inv, k + 1, cols, c127),
+                    code_at(v.z, inv, k + 2, cols, c127), code_at(v.w, inv, k + 3, cols, c127));
+    }
+  } else {
+    for (int k = threadIdx.x; k < cols; k += 256)
+      out[k] = (int8_t)code_at(row[k], inv, k, cols, c127);
+  }
+}
+
+// 16 rows per work-group, codes written as 16x64 tiles (zero padded).
+__global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(const float* __restrict__ src,
+                                                                  int rows, int cols, int KB,
+                                                                  uint8_t* __restrict__ tiles,
+                                                                  float* __restrict__ scales,
+                                                                  int clamp127) {
+  __shared__ float s_inv[16];
+  const int g = blockIdx.x;
+  const int w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int main_end = cols & ~15;
+  const bool vec = ((cols & 3) == 0) && ((((uintptr_t)src) & 15) == 0);
+
+  // pass 1: wave w reduces rows 4w .. 4w+3 of this row group
+  for (int rr = 0; rr < 4; rr++) {
+    const int r = g * 16 + w * 4 + rr;
+    float inv = 1.0f;
+    if (r < rows) {
+      const float* row = src + (size_t)r * cols;
+      uint32_t mx = 0;
+      float tail = 0.0f;
+      if (vec) {
+        const float4* r4 = reinterpret_cast<const float4*>(row);
+        for (int i = lane; i < (main_end >> 2); i += 64) {
+          float4 v = r4[i];
+          uint32_t a = max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w)));
+          mx = a > mx ? a : mx;
+        }
+      } else {
+        for (int k = lane; k < main_end; k += 64) {
+          uint32_t a = abs_bits(row[k]);
+          mx = a > mx ? a : mx;
+        }
+      }
+      for (int k = main_end + lane; k < cols; k += 64) {
+        float a = fabsf(row[k]);
+        tail = (a > tail) ? a : tail;
+      }
+      mx = wave_max_u32(mx);
+      tail = wave_maxf_nonnan(tail);
+      float vmax = __uint_as_float(mx);
+      float absmax = (tail > vmax) ? tail : vmax;
+      float scale = quant_scale(absmax);
+      inv = quant_inv(scale);
+      if (lane == 0) scales[r] = scale;
+    }
+    if (lane == 0) s_inv[w * 4 + rr] = inv;
+  }
+  __syncthreads();
+
+  // pass 2: each lane writes the 16 codes of one tile lane; a wave writes one
+  // whole 1 KiB tile per iteration
+  const int rl = lane & 15;
+  const int r = g * 16 + rl;
+  const float inv = s_inv[rl];
+  const bool c127 = clamp127 != 0;
+  for (int kb = w; kb < KB; kb += 4) {
+    const int k0 = kb * 64 + (lane >> 4) * 16;
+    uint4 q = make_uint4(0, 0, 0, 0);
+    if (r < rows) {
+      const float* row = src + (size_t)r * cols;
+      float x[16];
+      if (vec && k0 + 16 <= cols) {
+        const float4* p = reinterpret_cast<const float4*>(row + k0);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          float4 v = p[j];
+          x[4 * j] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; j++) x[j] = (k0 + j < cols) ? row[k0 + j] : 0.0f;
+      }
+      int c[16];
+#pragma unroll
+      for (int j = 0; j < 16; j++) c[j] = (k0 + j < cols) ? code_at(x[j], inv, k0 + j, cols, c127) : 0;
+      q.x = pack4(c[0], c[1], c[2], c[3]);
+      q.y = pack4(c[4], c[5], c[6], c[7]);
+      q.z = pack4(c[8], c[9], c[10], c[11]);
+      q.w = pack4(c[12], c[13], c[14], c[15]);
+    }
+    reinterpret_cast<uint4*>(tiles)[((size_t)g * KB + kb) * 64 + lane] = q;
+  }
+}
+
+// one thread per (tile, lane): 16 bytes of W[16g + (l&15)][64kb + 16(l>>4) ..]
+__global__ __launch_bounds__(256) void pack_tiles_kernel(const int8_t* __restrict__ w, int rows,
+                                                         int cols, int KB, long long total,
+                                                         uint8_t* __restrict__ tiles) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= total) return;
+  const int lane = (int)(t & 63);
+  const long long tile = t >> 6;
+  const int kb = (int)(tile % KB);
+  const int g = (int)(tile / KB);
+  const int r = g * 16 + (lane & 15);
+  const int k0 = kb * 64 + (lane >> 4) * 16;
+  uint4 q = make_uint4(0, 0, 0, 0);
+  if (r < rows) {
+    const int8_t* p = w + (size_t)r * cols + k0;
+    if (k0 + 16 <= cols && ((((uintptr_t)p) & 15) == 0)) {
+      q = *reinterpret_cast<const uint4*>(p);
+    } else {
+      uint8_t b[16];
+#pragma unroll
+      for (int j = 0; j < 16; j++) b[j] = (k0 + j < cols) ? (uint8_t)p[j] : 0;
+      q.x = b[0] | (b[1] << 8) | (b[2] << 16) | ((uint32_t)b[3] << 24);
+      q.y = b[4] | (b[5] << 8) | (b[6] << 16) | ((uint32_t)b[7] << 24);
+      q.z = b[8] | (b[9] << 8) | (b[10] << 16) | ((uint32_t)b[11] << 24);
+      q.w = b[12] | (b[13] << 8) | (b[14] << 16) | ((uint32_t)b[15] << 24);
+    }
+  }
+  reinterpret_cast<uint4*>(tiles)[t] = q;
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+hipError_t launch_quantize_rows(const float* src, int8_t* dst, float* scales, int rows, int cols,
+                                bool clamp127, hipStream_t st) {
+  if (rows <= 0 || cols <= 0) return hipSuccess;
+  hipLaunchKernelGGL(quantize_rows_kernel, dim3(rows), dim3(256), 0, st, src, dst, scales, cols,
+                     clamp127 ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize_rows_tiled(const float* src, int rows, int cols, uint8_t* tiles,
+                                      float* scales, bool clamp127, hipStream_t st) {
+  if (rows <= 0 || cols <= 0) return hipSuccess;
+  const int KB = cdiv(cols, 64);
+  hipLaunchKernelGGL(quantize_rows_tiled_kernel, dim3(cdiv(rows, 16)), dim3(256), 0, st, src, rows,
+                     cols, KB, tiles, scales, clamp127 ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_tiles(const int8_t* w, int rows, int cols, uint8_t* tiles, hipStream_t st) {
+  if (rows <= 0 || cols <= 0) return hipSuccess;
+  const int KB = cdiv(cols, 64);
+  const long long total = (long long)cdiv(rows, 16) * KB * 64;
+  const long long blocks = (total + 255) / 256;
+  hipLaunchKernelGGL(pack_tiles_kernel, dim3((unsigned)blocks), dim3(256), 0, st, w, rows, cols, KB,
+                     total, tiles);
+  return hipGetLastError();
+}
+
+}  // namespace tl

@@ -1,0 +1,162 @@
+// tl_common.h -- device-side building blocks shared by the INT8 linear kernels
+// (gfx950 / CDNA4, wave64).
+//
+// Weight tile layout ("16x64 tiles"), used for every weight matrix held in
+// HBM and for the int8 activation codes fed to the int8 MFMA:
+//
+//   tile (g, kb) covers rows 16g .. 16g+15 and columns 64kb .. 64kb+63; it is
+//   1 KiB, lane-major: byte b of lane l holds  W[16g + (l & 15)][64kb + 16(l >> 4) + b].
+//   tiles are stored g-major: offset(g, kb) = (g * KB + kb) * 1024, KB = Kpad/64.
+//
+// One 16-byte load per lane reads a whole tile, perfectly coalesced.  The
+// layout is the operand layout of v_mfma_i32_16x16x64_i8 (A or B): lane l
+// supplies row (l & 15), lane group (l >> 4) supplies a 16-wide slice of K.
+// An MFMA only needs A and B to agree on which K index sits in which (lane
+// group, byte) slot, and they do because both are packed this way.  For the
+// bf16 MFMA (v_mfma_f32_16x16x32_bf16, 8 values per lane) bytes 0-7 and 8-15
+// of a lane become two bf16 operands for two MFMAs over K halves.
+//
+// Rows beyond N and columns beyond K are zero in the packed buffer, so a
+// padded K contributes exactly 0 to every integer or float dot product.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tl_kernels.h"
+
+#define TL_TILE_ROWS 16
+#define TL_TILE_K 64
+#define TL_TILE_BYTES 1024
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+
+namespace tl {
+
+// ---------------------------------------------------------------------------
+// quantizer primitives (reference: kernel/w8a32_kernel.c:63-108, :139-178)
+// ---------------------------------------------------------------------------
+
+// |v| as raw bits; for non-negative floats the unsigned order of the bits is
+// the numeric order and every NaN sorts above +Inf, so an unsigned max of
+// these is the NaN-propagating vmaxq_f32/vmaxvq_f32 max of the reference's
+// 16-aligned prefix.
+__device__ inline uint32_t abs_bits(float v) { return __float_as_uint(v) & 0x7fffffffu; }
+
+// scale = absmax > 0 ? fl(absmax / 127) : 1  (NaN > 0 is false -> 1)
+__device__ inline float quant_scale(float absmax) {
+  return (absmax > 0.0f) ? __fdiv_rn(absmax, 127.0f) : 1.0f;
+}
+__device__ inline float quant_inv(float scale) { return __fdiv_rn(1.0f, scale); }
+
+// FCVTNS + saturating narrow to int8 (vector region): round half to even,
+// NaN -> 0.  clamp127 additionally limits to [-127, 127] (weight quantizers).
+__device__ inline int code_rne(float v, bool clamp127) {
+  float r = __builtin_rintf(v);
+  r = (v != v) ? 0.0f : r;
+  r = __builtin_fminf(__builtin_fmaxf(r, clamp127 ? -127.0f : -128.0f), 127.0f);
+  return (int)r;
+}
+
+// lroundf + clamp to [-127, 127] (scalar tail k >= K & ~15): half away from 0.
+__device__ inline int code_tail(float v) {
+  float r = __builtin_roundf(v);
+  r = (v != v) ? 0.0f : r;
+  r = __builtin_fminf(__builtin_fmaxf(r, -127.0f), 127.0f);
+  return (int)r;
+}
+
+// code for element k of a row of length K with reciprocal scale inv
+__device__ inline int code_at(float x, float inv, int k, int K, bool clamp127) {
+  float v = x * inv;
+  return (k < (K & ~15)) ? code_rne(v, clamp127) : code_tail(v);
+}
+
+__device__ inline uint32_t pack4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+         ((uint32_t)(d & 0xff) << 24);
+}
+
+// ---------------------------------------------------------------------------
+// wave reductions (wave64)
+// ---------------------------------------------------------------------------
+__device__ inline uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint32_t t = (uint32_t)__shfl_xor((int)v, o, 64);
+    v = v > t ? v : t;
+  }
+  return v;
+}
+
+__device__ inline float wave_maxf_nonnan(float v) {  // max ignoring NaN (tail scan)
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float t = __shfl_xor(v, o, 64);
+    v = (t > v) ? t : v;
+  }
+  return v;
+}
+
+// block-wide absmax of a 256-thread block with the reference's NaN semantics:
+// mx = max |x| bits over the 16-aligned prefix (NaN-propagating), tail = max
+// over the K%16 tail ignoring NaN; the tail is compared against the prefix max
+// the way `if (v > absmax) absmax = v` does (kernel/w8a32_kernel.c:153).
+__device__ inline float block_absmax_256(uint32_t mx, float tail, uint32_t* s_mx, float* s_tail) {
+  mx = wave_max_u32(mx);
+  tail = wave_maxf_nonnan(tail);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    s_mx[w] = mx;
+    s_tail[w] = tail;
+  }
+  __syncthreads();
+  uint32_t m = s_mx[0];
+  float t = s_tail[0];
+#pragma unroll
+  for (int i = 1; i < 4; i++) {
+    m = s_mx[i] > m ? s_mx[i] : m;
+    t = s_tail[i] > t ? s_tail[i] : t;
+  }
+  const float vec = __uint_as_float(m);
+  return (t > vec) ? t : vec;
+}
+
+// ---------------------------------------------------------------------------
+// int8 dot products
+// ---------------------------------------------------------------------------
+__device__ inline int dot16(uint4 w, uint4 x, int acc) {
+  acc = __builtin_amdgcn_sdot4((int)w.x, (int)x.x, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)w.y, (int)x.y, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)w.z, (int)x.z, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)w.w, (int)x.w, acc, false);
+  return acc;
+}
+
+// ---------------------------------------------------------------------------
+// bf16 helpers
+// ---------------------------------------------------------------------------
+// fp32 -> bf16 bits, round to nearest even (finite inputs; NaN kept quiet)
+__device__ inline uint32_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ inline float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// 4 signed int8 (one dword) -> 4 bf16 (two dwords), exact for |w| <= 128
+__device__ inline uint2 i8x4_to_bf16x4(uint32_t w) {
+  float f0 = (float)(int8_t)(w & 0xff);
+  float f1 = (float)(int8_t)((w >> 8) & 0xff);
+  float f2 = (float)(int8_t)((w >> 16) & 0xff);
+  float f3 = (float)(int8_t)(w >> 24);
+  // integers |v| <= 128 are exact in bf16: the high halves of the floats
+  uint2 r;
+  r.x = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
+  r.y = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
+  return r;
+}
+
+}  // namespace tl

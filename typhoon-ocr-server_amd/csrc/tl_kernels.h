@@ -1,0 +1,76 @@
+// tl_kernels.h -- host-side launchers of the INT8 linear kernels (namespace tl).
+// All pointers are device pointers; every launcher is asynchronous on `st`.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace tl {
+
+__host__ __device__ inline int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+// GEMV epilogues (gemv.hip)
+enum { EPI_W8A32 = 0, EPI_W8A8 = 1, EPI_ACC = 2 };
+// GEMM A-operand modes and output types (gemm.hip)
+enum { A_I8 = 0, A_BF16 = 1, A_F16 = 2, A_F32X3 = 3 };
+enum { OUT_F32 = 0, OUT_BF16 = 1, OUT_F16 = 2, OUT_I32 = 3 };
+// GEMM float epilogues: fl(acc*ws) then + bias, or fma(acc, ws, bias|0)
+enum { EP_SCALE = 0, EP_SCALE_FMA = 1 };
+
+// ---- quantization / packing (quant.hip) ----------------------------------
+hipError_t launch_quantize_rows(const float* src, int8_t* dst, float* scales, int rows, int cols,
+                                bool clamp127, hipStream_t st);
+hipError_t launch_quantize_rows_tiled(const float* src, int rows, int cols, uint8_t* tiles,
+                                      float* scales, bool clamp127, hipStream_t st);
+hipError_t launch_pack_tiles(const int8_t* w, int rows, int cols, uint8_t* tiles, hipStream_t st);
+
+// ---- M=1 GEMV (gemv.hip) --------------------------------------------------
+struct GemvPlan {
+  int rpw = 1, split = 1, blocks = 0;
+};
+struct GemvLaunch {
+  const float* x = nullptr;       // fp32 activation (fused quantization) or null
+  const uint8_t* xq = nullptr;    // precomputed codes, zero padded to ceil(K/64)*64
+  const float* xs_in = nullptr;   // precomputed activation scale (device scalar)
+  const uint8_t* wt = nullptr;    // weight tiles
+  const float* ws = nullptr;
+  const float* bias = nullptr;
+  float* y = nullptr;
+  int32_t* acc_out = nullptr;
+  float* xs_out = nullptr;
+  int32_t* part = nullptr;        // split workspace (gemv_workspace_bytes)
+  uint32_t* cnt = nullptr;        // ceil(N/16) zeroed counters
+  int N = 0, K = 0, epi = EPI_W8A32;
+  int force_split = 0;
+};
+GemvPlan gemv_plan(int N, int K);
+int gemv_fused_xv(int K);
+size_t gemv_workspace_bytes(int N, int K);
+hipError_t launch_gemv_i8(const GemvLaunch& L, hipStream_t st);
+
+// ---- MFMA GEMM (gemm.hip) -------------------------------------------------
+struct GemmPlan {
+  int cfg = 0, ntm = 1, ntn = 1, split = 1, blocks = 0;
+};
+struct GemmLaunch {
+  int amode = A_I8;
+  const void* A = nullptr;        // A_I8: code tiles; else row-major [M][lda]
+  int lda = 0;
+  const uint8_t* Bt = nullptr;    // weight tiles
+  const float* ws = nullptr;
+  const float* xs = nullptr;      // per-token scales (A_I8)
+  const float* bias = nullptr;
+  void* Y = nullptr;
+  int ldy = 0;
+  int M = 0, N = 0, K = 0;
+  int ep = EP_SCALE, out = OUT_F32;
+  void* part = nullptr;           // split workspace (gemm_workspace_bytes)
+  uint32_t* cnt = nullptr;        // gemm_counter_count zeroed counters
+  int force_split = 0;
+};
+GemmPlan gemm_plan(int amode, int M, int N, int K);
+size_t gemm_workspace_bytes(int amode, int M, int N, int K);
+size_t gemm_counter_count(int amode, int M, int N, int K);
+hipError_t launch_gemm(const GemmLaunch& L, hipStream_t st);
+
+}  // namespace tl

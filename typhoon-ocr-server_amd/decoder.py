@@ -1,0 +1,185 @@
+"""Linear-path mirror of the reference's decoder.py on libtyphoon_linear.so.
+
+The reference's Decoder (decoder.py:182-523) quantizes every projection at
+load with the library's w8a32_quantize (:248-260), keeps the int8/scale arrays
+alive (:215, :259), concatenates Q||K||V and gate||up for prefill (:290-302),
+registers the pointers with the C decoder (:304-317), and per generated token
+computes the lm_head logits with w8a32_linear(batch=1) after a numpy final
+RMSNorm (:443-460), then samples (:462-477).
+
+This module keeps those steps with the same names, argument meaning and
+error behaviour, on the MI355X library:
+  * load_decoder_lib() binds w8a32_quantize / w8a32_linear with the
+    reference's argtypes (decoder.py:145-157) plus tl_last_error;
+  * Decoder quantizes on the GPU, packs the fused matrices, and registers
+    every quantized matrix with tl_register_weights, which uploads it once
+    into HBM tiles (the step the reference's decoder_set_layer_weights_v32
+    performs by pointer);
+  * project() runs one projection through w8a32_linear with the reference's
+    batch-dependent numerics; get_logits() / sample() are _get_logits and the
+    greedy branch of _sample.
+
+The 28-layer loop itself (norms, M-RoPE, attention, KV cache:
+kernel/decoder.c:33-314) is not part of this library.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Dict, List, Mapping, Optional
+
+import numpy as np
+
+from . import linear as _lin
+
+# Qwen3-VL 2B constants (reference decoder.py:28-38)
+HIDDEN_DIM = 2048
+KV_DIM = 1024
+FFN_DIM = 6144
+NUM_Q_HEADS = 16
+NUM_KV_HEADS = 8
+HEAD_DIM = 128
+NUM_LAYERS = 28
+MAX_SEQ_LEN = 2048
+TILE_M = 128
+QKV_DIM = HIDDEN_DIM + 2 * KV_DIM      # 4096
+GATE_UP_DIM = 2 * FFN_DIM              # 12288
+VOCAB = 151936
+RMS_EPS = 1e-6
+
+PROJECTIONS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+
+def _np_ptr(arr: np.ndarray, ctype=ctypes.c_float):
+    return arr.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+def load_decoder_lib() -> ctypes.CDLL:
+    """Load the MI355X library with the reference's linear-path argtypes."""
+    lib = _lin.load_library()
+    _i8p = ctypes.POINTER(ctypes.c_int8)
+    _f32p = ctypes.POINTER(ctypes.c_float)
+    lib.w8a32_quantize.restype = None
+    lib.w8a32_quantize.argtypes = [_f32p, _i8p, _f32p, ctypes.c_int, ctypes.c_int]
+    lib.w8a32_linear.restype = None
+    lib.w8a32_linear.argtypes = [_f32p, _i8p, _f32p, _f32p, _f32p, _f32p,
+                                 ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    return lib
+
+
+def qwen3vl_shapes(num_layers: int = NUM_LAYERS, vocab: int = VOCAB) -> Dict[str, tuple]:
+    """(rows, cols) of every linear weight of the Qwen3-VL-2B text decoder."""
+    per_layer = {"q_proj": (HIDDEN_DIM, HIDDEN_DIM), "k_proj": (KV_DIM, HIDDEN_DIM),
+                 "v_proj": (KV_DIM, HIDDEN_DIM), "o_proj": (HIDDEN_DIM, HIDDEN_DIM),
+                 "gate_proj": (FFN_DIM, HIDDEN_DIM), "up_proj": (FFN_DIM, HIDDEN_DIM),
+                 "down_proj": (HIDDEN_DIM, FFN_DIM)}
+    out = {f"layers.{l}.{k}": v for l in range(num_layers) for k, v in per_layer.items()}
+    out["lm_head"] = (vocab, HIDDEN_DIM)
+    return out
+
+
+def random_layer_weights(rng: np.random.Generator, hidden: int = HIDDEN_DIM, kv: int = KV_DIM,
+                         ffn: int = FFN_DIM, std: float = 0.02) -> Dict[str, np.ndarray]:
+    """Random-init fp32 weights of one layer's seven projections."""
+    shapes = {"q_proj": (hidden, hidden), "k_proj": (kv, hidden), "v_proj": (kv, hidden),
+              "o_proj": (hidden, hidden), "gate_proj": (ffn, hidden), "up_proj": (ffn, hidden),
+              "down_proj": (hidden, ffn)}
+    return {k: (rng.standard_normal(s, dtype=np.float32) * np.float32(std)) for k, s in shapes.items()}
+
+
+class Decoder:
+    """Quantized linear layers of the text decoder, resident in HBM.
+
+    layers:      sequence of mappings name -> fp32 [out, in] array for the seven
+                 projections of each layer (PROJECTIONS)
+    lm_head:     fp32 [vocab, hidden] (optional)
+    final_norm:  fp32 [hidden] RMSNorm weight (optional)
+    """
+
+    def __init__(self, layers: List[Mapping[str, np.ndarray]], lib: Optional[ctypes.CDLL] = None,
+                 lm_head: Optional[np.ndarray] = None, final_norm: Optional[np.ndarray] = None,
+                 verbose: bool = False):
+        self._lib = lib or load_decoder_lib()
+        self._weight_store: list = []          # keep numpy arrays alive (reference :215)
+        self.layers: List[Dict[str, tuple]] = []
+        for l_idx, layer in enumerate(layers):
+            self._register_layer(l_idx, layer)
+            if verbose and ((l_idx + 1) % 7 == 0 or l_idx == len(layers) - 1):
+                print(f"\r[Decoder] Layer {l_idx + 1}/{len(layers)} ...", end="", flush=True)
+        if verbose:
+            print("\n[Decoder] Weights loaded.", flush=True)
+        self._final_norm_w = None if final_norm is None else np.ascontiguousarray(final_norm, np.float32)
+        self._lm_head_w = None
+        if lm_head is not None:
+            q, s = self._quantize_and_keep(lm_head)
+            self._lm_head_w, self._lm_head_s = q, s
+            self._lm_head_M, self._lm_head_K = q.shape
+            self._lm_head_scratch = np.empty((TILE_M, self._lm_head_K), dtype=np.float32)
+            self._weight_store.append(self._lm_head_scratch)
+            self._register(q, s)
+            self._logits_buf = np.empty(self._lm_head_M, dtype=np.float32)
+
+    # -- weight quantization helpers (reference :248-317) -------------------
+    def _quantize_and_keep(self, w_fp32: np.ndarray):
+        M, K = w_fp32.shape
+        w_packed = np.empty((M, K), dtype=np.int8)
+        scales = np.empty(M, dtype=np.float32)
+        w_fp32_c = np.ascontiguousarray(w_fp32, dtype=np.float32)
+        self._lib.w8a32_quantize(_np_ptr(w_fp32_c), _np_ptr(w_packed, ctypes.c_int8), _np_ptr(scales),
+                                 ctypes.c_int(M), ctypes.c_int(K))
+        _lin.check(self._lib, "w8a32_quantize")
+        self._weight_store.extend([w_packed, scales])
+        return w_packed, scales
+
+    def _register(self, w: np.ndarray, s: np.ndarray) -> None:
+        rc = self._lib.tl_register_weights(_np_ptr(w, ctypes.c_int8), _np_ptr(s), w.shape[0], w.shape[1])
+        if rc != 0:
+            _lin.check(self._lib, "tl_register_weights")
+
+    def _register_layer(self, l_idx: int, layer: Mapping[str, np.ndarray]) -> None:
+        q = {name: self._quantize_and_keep(layer[name]) for name in PROJECTIONS}
+        # fused Q||K||V [4096 x 2048] and gate||up [12288 x 2048] (reference :290-302)
+        qkv_w = np.ascontiguousarray(np.concatenate([q["q_proj"][0], q["k_proj"][0], q["v_proj"][0]], axis=0))
+        qkv_s = np.ascontiguousarray(np.concatenate([q["q_proj"][1], q["k_proj"][1], q["v_proj"][1]]))
+        gu_w = np.ascontiguousarray(np.concatenate([q["gate_proj"][0], q["up_proj"][0]], axis=0))
+        gu_s = np.ascontiguousarray(np.concatenate([q["gate_proj"][1], q["up_proj"][1]]))
+        self._weight_store.extend([qkv_w, qkv_s, gu_w, gu_s])
+        entry = dict(q)
+        entry["qkv_proj"] = (qkv_w, qkv_s)
+        entry["gate_up_proj"] = (gu_w, gu_s)
+        for w, s in entry.values():
+            self._register(w, s)
+        self.layers.append(entry)
+
+    # -- core operations ------------------------------------------------------
+    def project(self, l_idx: int, name: str, x: np.ndarray, out: Optional[np.ndarray] = None) -> np.ndarray:
+        """y = w8a32_linear(x, W[name]) with the reference's call convention
+        (bias NULL, scratch ignored): batch==1 rows take the int8 GEMV."""
+        w, s = self.layers[l_idx][name]
+        x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+        batch, K = x.shape
+        M = w.shape[0]
+        y = out if out is not None else np.empty((batch, M), np.float32)
+        self._lib.w8a32_linear(_np_ptr(x), _np_ptr(w, ctypes.c_int8), _np_ptr(s), None, _np_ptr(y), None,
+                               ctypes.c_int(batch), ctypes.c_int(M), ctypes.c_int(K))
+        _lin.check(self._lib, "w8a32_linear")
+        return y
+
+    def get_logits(self, h_np: np.ndarray) -> np.ndarray:
+        """Final RMSNorm of the last row (numpy, as reference :444-448), then the
+        lm_head GEMV w8a32_linear(batch=1, N=vocab) (:449-459)."""
+        if self._lm_head_w is None:
+            raise RuntimeError("Decoder has no lm_head")
+        h = np.atleast_2d(h_np)[-1]
+        rms = np.sqrt(np.mean(h * h) + RMS_EPS)
+        h_normed = (h / rms) * self._final_norm_w if self._final_norm_w is not None else h / rms
+        x = np.ascontiguousarray(h_normed.reshape(1, self._lm_head_K), dtype=np.float32)
+        self._lib.w8a32_linear(_np_ptr(x), _np_ptr(self._lm_head_w, ctypes.c_int8), _np_ptr(self._lm_head_s),
+                               None, _np_ptr(self._logits_buf), _np_ptr(self._lm_head_scratch),
+                               ctypes.c_int(1), ctypes.c_int(self._lm_head_M), ctypes.c_int(self._lm_head_K))
+        _lin.check(self._lib, "w8a32_linear")
+        return self._logits_buf
+
+    @staticmethod
+    def sample(logits_1d: np.ndarray) -> int:
+        """Greedy branch of _sample (reference :463-464): first index of the max."""
+        return int(np.argmax(logits_1d))

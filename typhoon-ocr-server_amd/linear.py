@@ -1,0 +1,267 @@
+"""ctypes bindings of libtyphoon_linear.so (include/typhoon_linear.h).
+
+Part 1 functions keep the reference's signatures and host-pointer semantics
+(kernel/w8a32_kernel.c:63-68, :355-363; kernel/w8a8_kernel.c:102-114,
+:270-272; kernel/w8a16_kernel.c:44, :218-219).  The numpy wrappers below check
+tl_last_error() after each call and raise RuntimeError, since the C functions
+return void as in the reference.  There is no fallback: if the library is
+missing or the GPU call fails, the wrapper raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import numpy as np
+
+from . import LIB_PATH
+
+_i8p = ctypes.POINTER(ctypes.c_int8)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_vp = ctypes.c_void_p
+_int = ctypes.c_int
+
+TL_F32, TL_BF16, TL_F16 = 0, 1, 2
+
+# name -> (restype, argtypes); Part 1 first, then Part 2
+SIGNATURES = {
+    "w8a32_quantize": (None, [_f32p, _i8p, _f32p, _int, _int]),
+    "w8a32_linear": (None, [_f32p, _i8p, _f32p, _f32p, _f32p, _f32p, _int, _int, _int]),
+    "w8a8_quantize_weights": (None, [_f32p, _i8p, _f32p, _int, _int]),
+    "w8a8_quantize_activations": (None, [_f32p, _i8p, _f32p, _int, _int]),
+    "w8a8_linear": (None, [_i8p, _f32p, _i8p, _f32p, _f32p, _f32p, _int, _int, _int]),
+    "w8a16_quantize_weights": (None, [_f32p, _i8p, _f32p, _int, _int]),
+    "w8a16_linear": (None, [_u16p, _i8p, _f32p, _f32p, _f32p, _int, _int, _int]),
+    "tl_last_error": (ctypes.c_char_p, []),
+    "tl_clear_error": (None, []),
+    "tl_version": (ctypes.c_char_p, []),
+    "tl_device_count": (_int, []),
+    "tl_register_weights": (_int, [_i8p, _f32p, _int, _int]),
+    "tl_evict_weights": (_int, [_i8p]),
+    "tl_registry_clear": (None, []),
+    "tl_registry_bytes": (ctypes.c_size_t, []),
+    "tl_registry_entries": (_int, []),
+    "tl_weights_create": (_vp, [_vp, _vp, _int, _int, _int]),
+    "tl_weights_quantize_dev": (_vp, [_vp, _int, _int, _vp, _vp, _vp]),
+    "tl_weights_destroy": (None, [_vp]),
+    "tl_weights_rows": (_int, [_vp]),
+    "tl_weights_cols": (_int, [_vp]),
+    "tl_weights_bytes": (ctypes.c_size_t, [_vp]),
+    "tl_w8a32_linear_dev": (_int, [_vp, _vp, _vp, _vp, _int, _vp]),
+    "tl_quantize_rows_dev": (_int, [_vp, _vp, _vp, _int, _int, _int, _vp]),
+    "tl_w8a8_linear_dev": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _vp]),
+    "tl_w8a8_linear_f32_dev": (_int, [_vp, _vp, _vp, _vp, _int, _vp]),
+    "tl_w8a16_linear_dev": (_int, [_vp, _int, _vp, _vp, _vp, _int, _int, _vp]),
+    "tl_w8a32_gemv_acc_dev": (_int, [_vp, _vp, _vp, _vp, _vp]),
+    "tl_w8a8_gemm_acc_dev": (_int, [_vp, _vp, _vp, _int, _vp]),
+}
+
+_LIB: Optional[ctypes.CDLL] = None
+
+
+def load_library(path=None) -> ctypes.CDLL:
+    """Load libtyphoon_linear.so and declare every exported signature."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    p = path or LIB_PATH
+    if not p.exists():
+        raise RuntimeError(f"{p} is missing: build it first (make -C {p.parent})")
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _LIB = lib
+    return lib
+
+
+def check(lib: ctypes.CDLL, what: str) -> None:
+    msg = lib.tl_last_error()
+    if msg:
+        raise RuntimeError(f"{what}: {msg.decode()}")
+
+
+def _p(a: Optional[np.ndarray], ct):
+    if a is None:
+        return None
+    if not a.flags["C_CONTIGUOUS"]:
+        raise ValueError("array must be C-contiguous")
+    return a.ctypes.data_as(ctypes.POINTER(ct))
+
+
+# ---------------------------------------------------------------------------
+# numpy wrappers over Part 1 (host pointers)
+# ---------------------------------------------------------------------------
+def quantize(w: np.ndarray, which: str = "w8a32_quantize"):
+    """Per-row quantization via one of the four reference quantizers."""
+    lib = load_library()
+    w = np.ascontiguousarray(np.atleast_2d(w), dtype=np.float32)
+    rows, cols = w.shape
+    q = np.empty((rows, cols), np.int8)
+    s = np.empty(rows, np.float32)
+    getattr(lib, which)(_p(w, ctypes.c_float), _p(q, ctypes.c_int8), _p(s, ctypes.c_float), rows, cols)
+    check(lib, which)
+    return q, s
+
+
+def w8a32_linear(x: np.ndarray, w: np.ndarray, scales: np.ndarray, bias=None,
+                 out: Optional[np.ndarray] = None) -> np.ndarray:
+    lib = load_library()
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    batch, K = x.shape
+    M = w.shape[0]
+    y = out if out is not None else np.empty((batch, M), np.float32)
+    lib.w8a32_linear(_p(x, ctypes.c_float), _p(w, ctypes.c_int8), _p(scales, ctypes.c_float),
+                     _p(bias, ctypes.c_float), _p(y, ctypes.c_float), None, batch, M, K)
+    check(lib, "w8a32_linear")
+    return y
+
+
+def w8a8_linear(x_q: np.ndarray, x_scales: np.ndarray, w: np.ndarray, w_scales: np.ndarray,
+                bias=None) -> np.ndarray:
+    lib = load_library()
+    x_q = np.ascontiguousarray(np.atleast_2d(x_q), dtype=np.int8)
+    x_scales = np.ascontiguousarray(np.atleast_1d(x_scales), dtype=np.float32)
+    batch, K = x_q.shape
+    M = w.shape[0]
+    y = np.empty((batch, M), np.float32)
+    lib.w8a8_linear(_p(x_q, ctypes.c_int8), _p(x_scales, ctypes.c_float), _p(w, ctypes.c_int8),
+                    _p(w_scales, ctypes.c_float), _p(bias, ctypes.c_float), _p(y, ctypes.c_float),
+                    batch, M, K)
+    check(lib, "w8a8_linear")
+    return y
+
+
+def w8a16_linear(x_bf16: np.ndarray, w: np.ndarray, w_scales: np.ndarray, bias=None) -> np.ndarray:
+    lib = load_library()
+    x_bf16 = np.ascontiguousarray(np.atleast_2d(x_bf16), dtype=np.uint16)
+    batch, K = x_bf16.shape
+    M = w.shape[0]
+    y = np.empty((batch, M), np.float32)
+    lib.w8a16_linear(_p(x_bf16, ctypes.c_uint16), _p(w, ctypes.c_int8), _p(w_scales, ctypes.c_float),
+                     _p(bias, ctypes.c_float), _p(y, ctypes.c_float), batch, M, K)
+    check(lib, "w8a16_linear")
+    return y
+
+
+# ---------------------------------------------------------------------------
+# Part 2 helpers over torch device tensors (torch is only the allocator here)
+# ---------------------------------------------------------------------------
+def _ptr(t) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> Optional[int]:
+    if stream is None:
+        import torch
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
+
+
+class DeviceWeights:
+    """Packed int8 tiles + fp32 scales resident in HBM (tl_weights)."""
+
+    def __init__(self, handle: int, rows: int, cols: int):
+        self.handle = handle
+        self.rows = rows
+        self.cols = cols
+
+    @classmethod
+    def from_codes(cls, w_int8, scales) -> "DeviceWeights":
+        """w_int8/scales: torch device tensors or numpy host arrays."""
+        lib = load_library()
+        if isinstance(w_int8, np.ndarray):
+            w_int8 = np.ascontiguousarray(w_int8, dtype=np.int8)
+            scales = np.ascontiguousarray(scales, dtype=np.float32)
+            rows, cols = w_int8.shape
+            h = lib.tl_weights_create(w_int8.ctypes.data, scales.ctypes.data, rows, cols, 0)
+        else:
+            w_int8 = w_int8.contiguous()
+            scales = scales.contiguous()
+            rows, cols = w_int8.shape
+            h = lib.tl_weights_create(w_int8.data_ptr(), scales.data_ptr(), rows, cols, 1)
+        if not h:
+            check(lib, "tl_weights_create")
+            raise RuntimeError("tl_weights_create failed")
+        return cls(h, rows, cols)
+
+    @classmethod
+    def quantize(cls, w_fp32, codes_out=None, scales_out=None, stream=None) -> "DeviceWeights":
+        lib = load_library()
+        rows, cols = w_fp32.shape
+        h = lib.tl_weights_quantize_dev(w_fp32.data_ptr(), rows, cols, _ptr(codes_out), _ptr(scales_out),
+                                        _stream(stream))
+        if not h:
+            check(lib, "tl_weights_quantize_dev")
+            raise RuntimeError("tl_weights_quantize_dev failed")
+        return cls(h, rows, cols)
+
+    def bytes(self) -> int:
+        return load_library().tl_weights_bytes(self.handle)
+
+    def close(self):
+        if self.handle:
+            load_library().tl_weights_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _rc(lib, rc, what):
+    if rc != 0:
+        check(lib, what)
+        raise RuntimeError(f"{what} failed")
+
+
+def w8a32_linear_dev(x, W: DeviceWeights, y, bias=None, stream=None):
+    lib = load_library()
+    _rc(lib, lib.tl_w8a32_linear_dev(x.data_ptr(), W.handle, _ptr(bias), y.data_ptr(), x.shape[0],
+                                     _stream(stream)), "tl_w8a32_linear_dev")
+
+
+def w8a8_linear_f32_dev(x, W: DeviceWeights, y, bias=None, stream=None):
+    lib = load_library()
+    _rc(lib, lib.tl_w8a8_linear_f32_dev(x.data_ptr(), W.handle, _ptr(bias), y.data_ptr(), x.shape[0],
+                                        _stream(stream)), "tl_w8a8_linear_f32_dev")
+
+
+def w8a8_linear_dev(x_q, x_scales, W: DeviceWeights, y, bias=None, stream=None):
+    lib = load_library()
+    _rc(lib, lib.tl_w8a8_linear_dev(x_q.data_ptr(), x_scales.data_ptr(), W.handle, _ptr(bias),
+                                    y.data_ptr(), x_q.shape[0], _stream(stream)), "tl_w8a8_linear_dev")
+
+
+def w8a16_linear_dev(x, W: DeviceWeights, y, bias=None, stream=None):
+    import torch
+    lib = load_library()
+    xt = TL_BF16 if x.dtype == torch.bfloat16 else TL_F16
+    yt = {torch.float32: TL_F32, torch.bfloat16: TL_BF16, torch.float16: TL_F16}[y.dtype]
+    _rc(lib, lib.tl_w8a16_linear_dev(x.data_ptr(), xt, W.handle, _ptr(bias), y.data_ptr(), yt,
+                                     x.shape[0], _stream(stream)), "tl_w8a16_linear_dev")
+
+
+def quantize_rows_dev(src, codes, scales, clamp127=True, stream=None):
+    lib = load_library()
+    rows, cols = src.shape
+    _rc(lib, lib.tl_quantize_rows_dev(src.data_ptr(), codes.data_ptr(), scales.data_ptr(), rows, cols,
+                                      1 if clamp127 else 0, _stream(stream)), "tl_quantize_rows_dev")
+
+
+def gemv_acc_dev(x, W: DeviceWeights, acc, x_scale=None, stream=None):
+    lib = load_library()
+    _rc(lib, lib.tl_w8a32_gemv_acc_dev(x.data_ptr(), W.handle, acc.data_ptr(), _ptr(x_scale),
+                                       _stream(stream)), "tl_w8a32_gemv_acc_dev")
+
+
+def gemm_acc_dev(x_q, W: DeviceWeights, acc, stream=None):
+    lib = load_library()
+    _rc(lib, lib.tl_w8a8_gemm_acc_dev(x_q.data_ptr(), W.handle, acc.data_ptr(), x_q.shape[0],
+                                      _stream(stream)), "tl_w8a8_gemm_acc_dev")
