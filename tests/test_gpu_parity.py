@@ -40,6 +40,16 @@ def bf16_to_f32(b):
     return (b.astype(np.uint32) << 16).view(F)
 
 
+def test_single_hip_runtime(lin):
+    """The library and torch must share one HIP runtime in the process."""
+    lin.load_library()
+    import torch
+    assert torch.cuda.is_available()
+    maps = open("/proc/self/maps").read().split("\n")
+    hip = {ln.split()[-1] for ln in maps if "libamdhip64" in ln}
+    assert len(hip) == 1, hip
+
+
 # ---------------------------------------------------------------------------
 # quantizers
 # ---------------------------------------------------------------------------

@@ -67,6 +67,14 @@ def load_library(path=None) -> ctypes.CDLL:
     if _LIB is not None and path is None:
         return _LIB
     p = path or LIB_PATH
+    # torch ships its own HIP/HSA runtime (same SONAME libamdhip64.so.7 as
+    # /opt/rocm's).  Loading torch first makes this library bind to that one
+    # runtime; loading it first would make a later `import torch` bring a
+    # second runtime into the process, which then sees no GPU.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     if not p.exists():
         raise RuntimeError(f"{p} is missing: build it first (make -C {p.parent})")
     lib = ctypes.CDLL(str(p))
