@@ -97,6 +97,12 @@ void tl_registry_clear(void);
 size_t tl_registry_bytes(void);
 int tl_registry_entries(void);
 
+/* Tuning override of the M=1 GEMV decomposition for every later call in the
+ * process: waves per 16-row group in a work-group (1, 2, 4), K split across
+ * work-groups (>= 1), tiles per load batch (2, 4, 8).  Zeros restore the
+ * built-in planner. */
+int tl_gemv_set_plan(int ksw, int split, int u);
+
 /* ---- device-resident weights ------------------------------------------- */
 typedef struct tl_weights tl_weights;
 

@@ -640,6 +640,15 @@ int tl_device_count(void) {
   return n;
 }
 
+int tl_gemv_set_plan(int ksw, int split, int u) {
+  return guarded("tl_gemv_set_plan", [&] {
+    REQUIRE(ksw == 0 || ksw == 1 || ksw == 2 || ksw == 4, "ksw must be 0, 1, 2 or 4");
+    REQUIRE(u == 0 || u == 2 || u == 4 || u == 8, "u must be 0, 2, 4 or 8");
+    REQUIRE(split >= 0, "split must be >= 0");
+    gemv_set_plan(ksw, split, u);
+  });
+}
+
 int tl_register_weights(const int8_t* w_int8, const float* scales, int rows, int cols) {
   return guarded("tl_register_weights", [&] {
     std::lock_guard<std::mutex> lk(g_host_mu);
@@ -699,6 +708,7 @@ tl_weights* tl_weights_quantize_dev(const float* w_fp32, int rows, int cols, int
     hipStream_t st = static_cast<hipStream_t>(stream);
     tl_weights* W = weights_alloc(rows, cols);
     hipError_t e = hipMemsetAsync(W->scales, 0, (size_t)W->NG * 16 * sizeof(float), st);
+    if (e == hipSuccess) e = hipMemsetAsync(W->tiles, 0, (size_t)W->NG * W->KB * 1024, st);
     if (e == hipSuccess) e = launch_quantize_rows_tiled(w_fp32, rows, cols, W->tiles, W->scales, true, st);
     if (e == hipSuccess && codes_out) {
       float* s2 = scales_out;

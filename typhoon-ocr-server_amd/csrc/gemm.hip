@@ -427,6 +427,7 @@ hipError_t launch_gemm(const GemmLaunch& L, hipStream_t st) {
   a.cnt = L.cnt;
   if (p.split > 1 && (!L.part || !L.cnt)) return hipErrorInvalidValue;
   if (L.amode == A_I8 && L.out != OUT_I32 && !L.xs) return hipErrorInvalidValue;
+  if (L.amode == A_I8 && L.M > 16) return launch_gemm_i8(L, st);
   switch (L.amode) {
     case A_I8: return launch_mode<A_I8>(a, p.cfg, p.blocks, st);
     case A_BF16: return launch_mode<A_BF16>(a, p.cfg, p.blocks, st);

@@ -11,18 +11,21 @@
 //   * weights are 16x64 tiles (tl_common.h); a wave streams the tiles of one
 //     16-row group over a contiguous range of k-blocks with one 16-byte load
 //     per lane per tile (1 KiB per wave-load, fully coalesced) and keeps two
-//     batches of 8 tiles in flight (software pipeline);
+//     batches of U tiles in flight (software pipeline, U in {2, 4, 8} picked
+//     so that the wave's tiles form whole batches); the loop body is
+//     branch-free, tail tiles are read from a clamped address and masked;
 //   * lane l accumulates row (l & 15) over the k slice of its lane group with
 //     v_dot4_i32_i8; two xor-shuffles finish the row sums;
-//   * a work-group has 4 waves = RPW row groups x (4/RPW) k-slices, reduced
+//   * a work-group has 4 waves = (4/KSW) row groups x KSW k-slices, reduced
 //     through LDS; small N additionally splits K over S work-groups, whose
 //     int32 partials are summed in a fixed order by the last work-group to
 //     arrive (arrival counter in device memory, reset by that work-group, so
 //     the counters are zero again when the kernel ends).  Integer sums make
 //     every split bit-identical to the unsplit sum.
 //
-// Fused activation quantization (XV > 0): every work-group first issues its
-// first batch of weight loads, then reads all of x (XV float4 per thread),
+// Fused activation quantization (XV > 0): every work-group first issues the
+// loads of x and of its first two batches of weight tiles, then reduces all of
+// x (XV float4 per thread),
 // reduces absmax, derives scale/inverse exactly as the reference
 // (w8a32_kernel.c:145-158) and writes the int8 codes into LDS; the weight
 // loads are in flight meanwhile.  XV == 0 takes precomputed codes from
@@ -45,6 +48,8 @@ struct GemvArgs {
   int32_t* part;       // [S][NG*16] partial sums (S > 1)
   uint32_t* cnt;       // [NG] arrival counters, zero at rest
   int N, K, KB, NG, S, epi;
+  int ksw;             // waves per row group in a work-group (1, 2, 4)
+  int x_vec;           // 2: K == 1024*XV and x 16-byte aligned (unguarded loads)
 };
 
 __device__ inline void gemv_epilogue(const GemvArgs& a, int n, int acc, float xs) {
@@ -61,17 +66,49 @@ __device__ inline void gemv_epilogue(const GemvArgs& a, int n, int acc, float xs
   }
 }
 
-template <int RPW, int XV>
+// acc += dot(tile, codes) for U tiles starting at wave-local tile index t0;
+// tiles at or beyond n_t were loaded from a clamped address and are dropped.
+template <int XV, int U>
+__device__ inline int consume_batch(const uint4 (&b)[U], const uint4 (&c)[XV == 0 ? U : 1],
+                                    const uint4* s_codes, int kb0, int t0, int n_t, int lg, int acc) {
+  uint4 cv[U];
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    if constexpr (XV > 0) cv[u] = s_codes[(kb0 + min(t0 + u, n_t - 1)) * 4 + lg];
+    else cv[u] = c[u];
+  }
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const int d = dot16(b[u], cv[u], 0);
+    acc += (t0 + u < n_t) ? d : 0;
+  }
+  return acc;
+}
+
+template <int XV, int U>
+__device__ inline void load_batch(uint4 (&b)[U], uint4 (&c)[XV == 0 ? U : 1], const uint4* wp,
+                                  const uint4* cg, int kb0, int t0, int n_t, int lg) {
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const int t = min(t0 + u, n_t - 1);
+    b[u] = wp[(size_t)t * 64];
+    if constexpr (XV == 0) c[u] = cg[(kb0 + t) * 4 + lg];
+  }
+  // keep the batch issued here, ahead of the consumption that follows
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int XV, int U>
 __global__ __launch_bounds__(256) void gemv_i8_kernel(GemvArgs a) {
-  constexpr int U = 8;           // tiles per batch
-  constexpr int KSW = 4 / RPW;   // waves per row group inside the work-group
   __shared__ uint4 s_codes[XV > 0 ? XV * 64 : 1];
   __shared__ uint32_t s_mx[4];
   __shared__ float s_tail[4];
   __shared__ int s_red[4][16];
 
+  const int KSW = a.ksw;                  // waves per row group (1, 2 or 4)
+  const int RPW = 4 / KSW;
   const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
   const int lg = lane >> 4;
   const int blk = blockIdx.x / a.S;
   const int s = blockIdx.x - blk * a.S;
@@ -82,58 +119,59 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(GemvArgs a) {
   const int kb0 = (int)(((long long)j * a.KB) / T);
   const int kb1 = (int)(((long long)(j + 1) * a.KB) / T);
   const bool g_ok = g < a.NG;
-  const int n_t = g_ok ? (kb1 - kb0) : 0;
+  const int n_t = kb1 - kb0;              // >= 1 (host keeps T <= KB)
+  const int gl = g_ok ? g : a.NG - 1;     // out-of-range row groups re-read a valid one
 
-  const uint4* wp = reinterpret_cast<const uint4*>(a.wt) + ((size_t)(g_ok ? g : 0) * a.KB + kb0) * 64 + lane;
+  const uint4* wp = reinterpret_cast<const uint4*>(a.wt) + ((size_t)gl * a.KB + kb0) * 64 + lane;
   const uint4* cg = reinterpret_cast<const uint4*>(a.xq);
 
   uint4 b0[U], b1[U];
   uint4 c0[XV == 0 ? U : 1], c1[XV == 0 ? U : 1];
+
+  // x is read before the first weight batch is issued, so the wait for x
+  // never waits for weights
+  float4 xv[XV > 0 ? XV : 1];
+  if constexpr (XV > 0) {
+    const int K = a.K;
+    if (a.x_vec == 2) {
+      // K == 1024 * XV and x 16-byte aligned: XV unconditional float4 loads
 #pragma unroll
-  for (int u = 0; u < U; u++)
-    if (u < n_t) {
-      b0[u] = wp[(size_t)u * 64];
-      if constexpr (XV == 0) c0[u] = cg[(kb0 + u) * 4 + lg];
+      for (int i = 0; i < XV; i++) xv[i] = *reinterpret_cast<const float4*>(a.x + 4 * (threadIdx.x + 256 * i));
+    } else {
+#pragma unroll
+      for (int i = 0; i < XV; i++) {
+        const int k0 = 4 * (threadIdx.x + 256 * i);
+        float4 v;
+        v.x = (k0 < K) ? a.x[k0] : 0.f;
+        v.y = (k0 + 1 < K) ? a.x[k0 + 1] : 0.f;
+        v.z = (k0 + 2 < K) ? a.x[k0 + 2] : 0.f;
+        v.w = (k0 + 3 < K) ? a.x[k0 + 3] : 0.f;
+        xv[i] = v;
+      }
     }
+  }
+  load_batch<XV, U>(b0, c0, wp, cg, kb0, 0, n_t, lg);
+  load_batch<XV, U>(b1, c1, wp, cg, kb0, U, n_t, lg);
 
   float xs;
   if constexpr (XV > 0) {
     // ---- fused per-token activation quantization --------------------------
     const int K = a.K;
     const int main_end = K & ~15;
-    const bool vec = ((K & 3) == 0) && ((((uintptr_t)a.x) & 15) == 0);
-    float4 xv[XV];
     uint32_t mx = 0;
     float tail = 0.0f;
 #pragma unroll
     for (int i = 0; i < XV; i++) {
       const int k0 = 4 * (threadIdx.x + 256 * i);
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (vec && k0 + 3 < K) {
-        v = *reinterpret_cast<const float4*>(a.x + k0);
-      } else if (k0 < K) {
-        v.x = a.x[k0];
-        v.y = (k0 + 1 < K) ? a.x[k0 + 1] : 0.f;
-        v.z = (k0 + 2 < K) ? a.x[k0 + 2] : 0.f;
-        v.w = (k0 + 3 < K) ? a.x[k0 + 3] : 0.f;
-      }
-      xv[i] = v;
-      if (k0 + 3 < main_end) {
-        uint32_t m4 = max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w)));
-        mx = m4 > mx ? m4 : mx;
-      } else {
-        const float e[4] = {v.x, v.y, v.z, v.w};
+      const float4 v = xv[i];
+      const float e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const int k = k0 + q;
-          if (k < main_end) {
-            uint32_t m1 = abs_bits(e[q]);
-            mx = m1 > mx ? m1 : mx;
-          } else if (k < K) {
-            float t = fabsf(e[q]);
-            tail = (t > tail) ? t : tail;
-          }
-        }
+      for (int q = 0; q < 4; q++) {
+        const int k = k0 + q;
+        const uint32_t m1 = (k < main_end) ? abs_bits(e[q]) : 0u;
+        mx = m1 > mx ? m1 : mx;
+        const float t1 = (k >= main_end && k < K) ? fabsf(e[q]) : 0.0f;
+        tail = (t1 > tail) ? t1 : tail;
       }
     }
     const float absmax = block_absmax_256(mx, tail, s_mx, s_tail);
@@ -154,46 +192,27 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(GemvArgs a) {
   }
 
   // ---- main loop: two batches of U tiles in flight ---------------------------
+  // Both batches were issued before the prologue.  The loop body is
+  // straight-line code that enters and leaves with the 2U loads of b0 and b1
+  // outstanding, so the compiler keeps the wait counts exact.
   int acc = 0;
-  for (int i = 0; i < n_t; i += 2 * U) {
-#pragma unroll
-    for (int u = 0; u < U; u++)
-      if (i + U + u < n_t) {
-        b1[u] = wp[(size_t)(i + U + u) * 64];
-        if constexpr (XV == 0) c1[u] = cg[(kb0 + i + U + u) * 4 + lg];
-      }
-#pragma unroll
-    for (int u = 0; u < U; u++)
-      if (i + u < n_t) {
-        uint4 c;
-        if constexpr (XV > 0) c = s_codes[(kb0 + i + u) * 4 + lg];
-        else c = c0[u];
-        acc = dot16(b0[u], c, acc);
-      }
-#pragma unroll
-    for (int u = 0; u < U; u++)
-      if (i + 2 * U + u < n_t) {
-        b0[u] = wp[(size_t)(i + 2 * U + u) * 64];
-        if constexpr (XV == 0) c0[u] = cg[(kb0 + i + 2 * U + u) * 4 + lg];
-      }
-#pragma unroll
-    for (int u = 0; u < U; u++)
-      if (i + U + u < n_t) {
-        uint4 c;
-        if constexpr (XV > 0) c = s_codes[(kb0 + i + U + u) * 4 + lg];
-        else c = c1[u];
-        acc = dot16(b1[u], c, acc);
-      }
+  int t = 0;
+  for (; t + 2 * U < n_t; t += 2 * U) {
+    acc = consume_batch<XV, U>(b0, c0, s_codes, kb0, t, n_t, lg, acc);
+    load_batch<XV, U>(b0, c0, wp, cg, kb0, t + 2 * U, n_t, lg);
+    acc = consume_batch<XV, U>(b1, c1, s_codes, kb0, t + U, n_t, lg, acc);
+    load_batch<XV, U>(b1, c1, wp, cg, kb0, t + 3 * U, n_t, lg);
   }
+  acc = consume_batch<XV, U>(b0, c0, s_codes, kb0, t, n_t, lg, acc);
+  acc = consume_batch<XV, U>(b1, c1, s_codes, kb0, t + U, n_t, lg, acc);
 
   // ---- reductions ------------------------------------------------------------
   acc += __shfl_xor(acc, 16, 64);
   acc += __shfl_xor(acc, 32, 64);
-  if constexpr (KSW > 1) {
+  if (KSW > 1) {
     if (lane < 16) s_red[wv][lane] = acc;
     __syncthreads();
     if (ks == 0) {
-#pragma unroll
       for (int q = 1; q < KSW; q++) acc += s_red[wv + q][lane & 15];
     }
   }
@@ -225,20 +244,17 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(GemvArgs a) {
 // ---------------------------------------------------------------------------
 // launcher
 // ---------------------------------------------------------------------------
-template <int RPW, int XV>
-static void launch_rpw_xv(const GemvArgs& a, int blocks, hipStream_t st) {
-  hipLaunchKernelGGL((gemv_i8_kernel<RPW, XV>), dim3(blocks), dim3(256), 0, st, a);
+template <int XV, int U>
+static void launch_xv_u(const GemvArgs& a, int blocks, hipStream_t st) {
+  hipLaunchKernelGGL((gemv_i8_kernel<XV, U>), dim3(blocks), dim3(256), 0, st, a);
 }
 
-template <int RPW>
-static hipError_t launch_rpw(const GemvArgs& a, int xv, int blocks, hipStream_t st) {
-  switch (xv) {
-    case 0: launch_rpw_xv<RPW, 0>(a, blocks, st); break;
-    case 2: launch_rpw_xv<RPW, 2>(a, blocks, st); break;
-    case 4: launch_rpw_xv<RPW, 4>(a, blocks, st); break;
-    case 6: launch_rpw_xv<RPW, 6>(a, blocks, st); break;
-    case 8: launch_rpw_xv<RPW, 8>(a, blocks, st); break;
-    case 16: launch_rpw_xv<RPW, 16>(a, blocks, st); break;
+template <int XV>
+static hipError_t launch_xv(const GemvArgs& a, int u, int blocks, hipStream_t st) {
+  switch (u) {
+    case 2: launch_xv_u<XV, 2>(a, blocks, st); break;
+    case 4: launch_xv_u<XV, 4>(a, blocks, st); break;
+    case 8: launch_xv_u<XV, 8>(a, blocks, st); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -256,28 +272,63 @@ int gemv_fused_xv(int K) {
   return 0;
 }
 
+// batch depth: the largest of {8, 4, 2} that splits the wave's tiles into an
+// even number of whole batches (no redundant loads), else the smallest waste
+static int pick_u(int n_t) {
+  for (int u : {8, 4, 2})
+    if (n_t % (2 * u) == 0) return u;
+  int best = 2, waste = 1 << 30;
+  for (int u : {8, 4, 2}) {
+    int w = (2 * u - n_t % (2 * u)) % (2 * u);
+    if (w < waste) { waste = w; best = u; }
+  }
+  return best;
+}
+
+static int g_force_ksw = 0, g_force_split = 0, g_force_u = 0;
+
+void gemv_set_plan(int ksw, int split, int u) {
+  g_force_ksw = ksw;
+  g_force_split = split;
+  g_force_u = u;
+}
+
+static GemvPlan planner(int N, int K);
+
+// the planner's choice with the process-wide tuning override applied
 GemvPlan gemv_plan(int N, int K) {
+  GemvPlan p = planner(N, K);
+  const int NG = cdiv(N, 16), KB = cdiv(K, 64);
+  if (g_force_ksw > 0 || g_force_split > 0) {
+    const int ksw = g_force_ksw > 0 ? g_force_ksw : p.ksw;
+    const int split = g_force_split > 0 ? g_force_split : p.split;
+    if (ksw * split <= KB) {
+      p.ksw = ksw;
+      p.split = split;
+      p.blocks = cdiv(NG, 4 / ksw) * split;
+      p.u = pick_u(cdiv(KB, ksw * split));
+    }
+  }
+  if (g_force_u > 0) p.u = g_force_u;
+  return p;
+}
+
+// Measured on MI355X (graph-replayed launches over > 512 MB of rotating
+// weights): one 16-row group per work-group with K split over its 4 waves is
+// fastest for every decode shape, including the 151936-row lm_head; splitting
+// K across work-groups (fence + counter reduction) was 1.5-2.5x slower for
+// N <= 4096.  U = 4: both batches (8 tiles per wave at K = 2048) are in
+// flight before the activation prologue; at K = 6144 the 24 tiles form 3
+// exact double batches.
+static GemvPlan planner(int N, int K) {
   GemvPlan p;
   const int NG = cdiv(N, 16);
   const int KB = cdiv(K, 64);
-  const int target_waves = 2048;  // 8 per CU on 256 CUs
-  if (NG >= 2048) {
-    p.rpw = 4;
-    p.split = 1;
-  } else if (NG >= 512) {
-    p.rpw = 2;
-    p.split = 1;
-  } else {
-    p.rpw = 1;
-    int waves = NG * 4;
-    int s = cdiv(target_waves, waves);
-    int max_s = KB / 4;            // at least one tile per wave
-    if (max_s < 1) max_s = 1;
-    if (s > max_s) s = max_s;
-    if (s < 1) s = 1;
-    p.split = s;
-  }
-  p.blocks = cdiv(NG, p.rpw) * p.split;
+  p.ksw = KB >= 4 ? 4 : (KB >= 2 ? 2 : 1);
+  p.split = 1;
+  p.blocks = cdiv(NG, 4 / p.ksw);
+  const int n_t = cdiv(KB, p.ksw);
+  p.u = n_t >= 4 ? 4 : 2;
   return p;
 }
 
@@ -304,22 +355,32 @@ hipError_t launch_gemv_i8(const GemvLaunch& L, hipStream_t st) {
   a.KB = cdiv(L.K, 64);
   a.NG = cdiv(L.N, 16);
   a.epi = L.epi;
+  a.x_vec = 0;
   GemvPlan p = gemv_plan(L.N, L.K);
-  if (L.force_split > 0) {
-    p.split = L.force_split;
-    p.blocks = cdiv(a.NG, p.rpw) * p.split;
+  if (L.force_ksw > 0) p.ksw = L.force_ksw;
+  if (L.force_split > 0) p.split = L.force_split;
+  if (L.force_ksw > 0 || L.force_split > 0) {
+    if (p.ksw * p.split > a.KB) return hipErrorInvalidValue;
+    p.blocks = cdiv(a.NG, 4 / p.ksw) * p.split;
+    p.u = pick_u(cdiv(a.KB, p.ksw * p.split));
   }
+  if (L.force_u > 0) p.u = L.force_u;
+  a.ksw = p.ksw;
   a.S = p.split;
   a.part = L.part;
   a.cnt = L.cnt;
   if (p.split > 1 && (!L.part || !L.cnt)) return hipErrorInvalidValue;
   const int xv = L.x ? gemv_fused_xv(L.K) : 0;
   if (L.x && xv == 0) return hipErrorInvalidValue;  // caller must quantize first
+  if (L.x && L.K == 1024 * xv && (((uintptr_t)L.x) & 15) == 0) a.x_vec = 2;
   if (!L.x && !L.xq) return hipErrorInvalidValue;
-  switch (p.rpw) {
-    case 1: return launch_rpw<1>(a, xv, p.blocks, st);
-    case 2: return launch_rpw<2>(a, xv, p.blocks, st);
-    case 4: return launch_rpw<4>(a, xv, p.blocks, st);
+  switch (xv) {
+    case 0: return launch_xv<0>(a, p.u, p.blocks, st);
+    case 2: return launch_xv<2>(a, p.u, p.blocks, st);
+    case 4: return launch_xv<4>(a, p.u, p.blocks, st);
+    case 6: return launch_xv<6>(a, p.u, p.blocks, st);
+    case 8: return launch_xv<8>(a, p.u, p.blocks, st);
+    case 16: return launch_xv<16>(a, p.u, p.blocks, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -14,8 +14,9 @@
 // One work-group of 256 threads per row: pass 1 reduces the absmax, pass 2
 // re-reads the (L2-resident) row and writes codes.
 //
-// quantize_rows_tiled_kernel does the same for 16 rows at once and writes the
-// codes straight into the 16x64 tile layout used as the int8 MFMA A operand.
+// quantize_rows_tiled_kernel does the same with one wave per row and writes
+// the codes straight into the 16x64 tile layout used as the int8 MFMA A
+// operand.
 //
 // pack_tiles_kernel re-lays a row-major int8 matrix into 16x64 tiles.
 #include "tl_common.h"
@@ -75,88 +76,72 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restr
   }
 }
 
-// 16 rows per work-group, codes written as 16x64 tiles (zero padded).
+// One wave per row, 4 rows per work-group; codes are written straight into
+// the 16x64 tile layout (row r -> tile lanes (r & 15) + 16 lg), zero beyond K.
 __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(const float* __restrict__ src,
                                                                   int rows, int cols, int KB,
                                                                   uint8_t* __restrict__ tiles,
                                                                   float* __restrict__ scales,
                                                                   int clamp127) {
-  __shared__ float s_inv[16];
-  const int g = blockIdx.x;
-  const int w = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float* row = src + (size_t)r * cols;
   const int main_end = cols & ~15;
   const bool vec = ((cols & 3) == 0) && ((((uintptr_t)src) & 15) == 0);
 
-  // pass 1: wave w reduces rows 4w .. 4w+3 of this row group
-  for (int rr = 0; rr < 4; rr++) {
-    const int r = g * 16 + w * 4 + rr;
-    float inv = 1.0f;
-    if (r < rows) {
-      const float* row = src + (size_t)r * cols;
-      uint32_t mx = 0;
-      float tail = 0.0f;
-      if (vec) {
-        const float4* r4 = reinterpret_cast<const float4*>(row);
-        for (int i = lane; i < (main_end >> 2); i += 64) {
-          float4 v = r4[i];
-          uint32_t a = max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w)));
-          mx = a > mx ? a : mx;
-        }
-      } else {
-        for (int k = lane; k < main_end; k += 64) {
-          uint32_t a = abs_bits(row[k]);
-          mx = a > mx ? a : mx;
-        }
-      }
-      for (int k = main_end + lane; k < cols; k += 64) {
-        float a = fabsf(row[k]);
-        tail = (a > tail) ? a : tail;
-      }
-      mx = wave_max_u32(mx);
-      tail = wave_maxf_nonnan(tail);
-      float vmax = __uint_as_float(mx);
-      float absmax = (tail > vmax) ? tail : vmax;
-      float scale = quant_scale(absmax);
-      inv = quant_inv(scale);
-      if (lane == 0) scales[r] = scale;
+  uint32_t mx = 0;
+  float tail = 0.0f;
+  if (vec) {
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+    for (int i = lane; i < (main_end >> 2); i += 64) {
+      float4 v = r4[i];
+      uint32_t a = max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w)));
+      mx = a > mx ? a : mx;
     }
-    if (lane == 0) s_inv[w * 4 + rr] = inv;
+  } else {
+    for (int k = lane; k < main_end; k += 64) {
+      uint32_t a = abs_bits(row[k]);
+      mx = a > mx ? a : mx;
+    }
   }
-  __syncthreads();
+  for (int k = main_end + lane; k < cols; k += 64) {
+    float a = fabsf(row[k]);
+    tail = (a > tail) ? a : tail;
+  }
+  mx = wave_max_u32(mx);
+  tail = wave_maxf_nonnan(tail);
+  const float vmax = __uint_as_float(mx);
+  const float absmax = (tail > vmax) ? tail : vmax;
+  const float scale = quant_scale(absmax);
+  const float inv = quant_inv(scale);
+  if (lane == 0) scales[r] = scale;
 
-  // pass 2: each lane writes the 16 codes of one tile lane; a wave writes one
-  // whole 1 KiB tile per iteration
-  const int rl = lane & 15;
-  const int r = g * 16 + rl;
-  const float inv = s_inv[rl];
   const bool c127 = clamp127 != 0;
-  for (int kb = w; kb < KB; kb += 4) {
-    const int k0 = kb * 64 + (lane >> 4) * 16;
-    uint4 q = make_uint4(0, 0, 0, 0);
-    if (r < rows) {
-      const float* row = src + (size_t)r * cols;
-      float x[16];
-      if (vec && k0 + 16 <= cols) {
-        const float4* p = reinterpret_cast<const float4*>(row + k0);
+  uint4* t4 = reinterpret_cast<uint4*>(tiles) + ((size_t)(r >> 4) * KB) * 64 + (r & 15);
+  for (int c = lane; c < KB * 4; c += 64) {   // 16-wide chunk c = (kb, lg)
+    const int k0 = c * 16;
+    float x[16];
+    if (vec && k0 + 16 <= cols) {
+      const float4* p = reinterpret_cast<const float4*>(row + k0);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          float4 v = p[j];
-          x[4 * j] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 16; j++) x[j] = (k0 + j < cols) ? row[k0 + j] : 0.0f;
+      for (int j = 0; j < 4; j++) {
+        float4 v = p[j];
+        x[4 * j] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
       }
-      int c[16];
+    } else {
 #pragma unroll
-      for (int j = 0; j < 16; j++) c[j] = (k0 + j < cols) ? code_at(x[j], inv, k0 + j, cols, c127) : 0;
-      q.x = pack4(c[0], c[1], c[2], c[3]);
-      q.y = pack4(c[4], c[5], c[6], c[7]);
-      q.z = pack4(c[8], c[9], c[10], c[11]);
-      q.w = pack4(c[12], c[13], c[14], c[15]);
+      for (int j = 0; j < 16; j++) x[j] = (k0 + j < cols) ? row[k0 + j] : 0.0f;
     }
-    reinterpret_cast<uint4*>(tiles)[((size_t)g * KB + kb) * 64 + lane] = q;
+    int q[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) q[j] = (k0 + j < cols) ? code_at(x[j], inv, k0 + j, cols, c127) : 0;
+    uint4 o;
+    o.x = pack4(q[0], q[1], q[2], q[3]);
+    o.y = pack4(q[4], q[5], q[6], q[7]);
+    o.z = pack4(q[8], q[9], q[10], q[11]);
+    o.w = pack4(q[12], q[13], q[14], q[15]);
+    t4[(size_t)(c >> 2) * 64 + 16 * (c & 3)] = o;
   }
 }
 
@@ -205,7 +190,7 @@ hipError_t launch_quantize_rows_tiled(const float* src, int rows, int cols, uint
                                       float* scales, bool clamp127, hipStream_t st) {
   if (rows <= 0 || cols <= 0) return hipSuccess;
   const int KB = cdiv(cols, 64);
-  hipLaunchKernelGGL(quantize_rows_tiled_kernel, dim3(cdiv(rows, 16)), dim3(256), 0, st, src, rows,
+  hipLaunchKernelGGL(quantize_rows_tiled_kernel, dim3(cdiv(rows, 4)), dim3(256), 0, st, src, rows,
                      cols, KB, tiles, scales, clamp127 ? 1 : 0);
   return hipGetLastError();
 }

@@ -26,7 +26,7 @@ hipError_t launch_pack_tiles(const int8_t* w, int rows, int cols, uint8_t* tiles
 
 // ---- M=1 GEMV (gemv.hip) --------------------------------------------------
 struct GemvPlan {
-  int rpw = 1, split = 1, blocks = 0;
+  int ksw = 4, split = 1, blocks = 0, u = 8;
 };
 struct GemvLaunch {
   const float* x = nullptr;       // fp32 activation (fused quantization) or null
@@ -41,12 +41,14 @@ struct GemvLaunch {
   int32_t* part = nullptr;        // split workspace (gemv_workspace_bytes)
   uint32_t* cnt = nullptr;        // ceil(N/16) zeroed counters
   int N = 0, K = 0, epi = EPI_W8A32;
-  int force_split = 0;
+  int force_split = 0, force_ksw = 0, force_u = 0;   // tuning overrides (0 = planner)
 };
 GemvPlan gemv_plan(int N, int K);
 int gemv_fused_xv(int K);
 size_t gemv_workspace_bytes(int N, int K);
 hipError_t launch_gemv_i8(const GemvLaunch& L, hipStream_t st);
+// process-wide override of the GEMV plan for tuning (0 = planner's choice)
+void gemv_set_plan(int ksw, int split, int u);
 
 // ---- MFMA GEMM (gemm.hip) -------------------------------------------------
 struct GemmPlan {
@@ -72,5 +74,10 @@ GemmPlan gemm_plan(int amode, int M, int N, int K);
 size_t gemm_workspace_bytes(int amode, int M, int N, int K);
 size_t gemm_counter_count(int amode, int M, int N, int K);
 hipError_t launch_gemm(const GemmLaunch& L, hipStream_t st);
+
+// ---- W8A8 LDS-staged int8 MFMA GEMM (gemm_i8.hip), used for M > 16 ------
+hipError_t launch_gemm_i8(const GemmLaunch& L, hipStream_t st);
+int gemm_i8_pick_cfg(int M, int N, int K);
+void gemm_i8_set_cfg(int cfg);   // tuning override (-1 = planner)
 
 }  // namespace tl
