@@ -396,7 +396,25 @@ void run_gemv(Workspace& ws, GemvLaunch& L, hipStream_t st) {
   HIP_OK(launch_gemv_i8(L, st));
 }
 
+// 1 KiB of zeros per device: the int8 GEMM copies it in place of k-blocks
+// past K
+std::mutex g_zero_mu;
+std::map<int, uint8_t*> g_zero;
+
+const uint8_t* zero_tile(int dev) {
+  std::lock_guard<std::mutex> lk(g_zero_mu);
+  auto it = g_zero.find(dev);
+  if (it != g_zero.end()) return it->second;
+  void* p = nullptr;
+  HIP_OK(hipMalloc(&p, 1024));
+  HIP_OK(hipMemset(p, 0, 1024));
+  HIP_OK(hipDeviceSynchronize());
+  g_zero[dev] = static_cast<uint8_t*>(p);
+  return static_cast<uint8_t*>(p);
+}
+
 void run_gemm(Workspace& ws, GemmLaunch& L, hipStream_t st) {
+  L.zero_tile = zero_tile(current_device());
   GemmPlan p = gemm_plan(L.amode, L.M, L.N, L.K);
   if (p.split > 1) {
     ws.part.ensure(gemm_workspace_bytes(L.amode, L.M, L.N, L.K), st);

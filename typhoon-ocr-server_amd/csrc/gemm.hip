@@ -213,7 +213,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < TN; j++) {
       const int ng = ng0 + j;
-      bw[j] = (ng < a.NG) ? Bt4[((size_t)ng * a.KB + kb) * 64 + lane] : make_uint4(0, 0, 0, 0);
+      bw[j] = (ng < a.NG) ? Bt4[((size_t)kb * a.NG + ng) * 64 + lane] : make_uint4(0, 0, 0, 0);
     }
     if constexpr (AMODE == A_I8) {
       const uint4* At4 = reinterpret_cast<const uint4*>(a.A);
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int i = 0; i < TM; i++) {
         const int mg = mg0 + i;
-        aw[i] = (mg < a.MG) ? At4[((size_t)mg * a.KB + kb) * 64 + lane] : make_uint4(0, 0, 0, 0);
+        aw[i] = (mg < a.MG) ? At4[((size_t)kb * a.MG + mg) * 64 + lane] : make_uint4(0, 0, 0, 0);
       }
 #pragma unroll
       for (int i = 0; i < TM; i++)
@@ -427,7 +427,9 @@ hipError_t launch_gemm(const GemmLaunch& L, hipStream_t st) {
   a.cnt = L.cnt;
   if (p.split > 1 && (!L.part || !L.cnt)) return hipErrorInvalidValue;
   if (L.amode == A_I8 && L.out != OUT_I32 && !L.xs) return hipErrorInvalidValue;
+  if (L.M <= 16 && gemm_small_supported(L)) return launch_gemm_small(L, st);
   if (L.amode == A_I8 && L.M > 16) return launch_gemm_i8(L, st);
+  if (L.amode != A_I8 && L.M > 16 && gemm_b16_supported(L)) return launch_gemm_b16(L, st);
   switch (L.amode) {
     case A_I8: return launch_mode<A_I8>(a, p.cfg, p.blocks, st);
     case A_BF16: return launch_mode<A_BF16>(a, p.cfg, p.blocks, st);

@@ -1,0 +1,368 @@
+// gemm_b16.hip -- prefill GEMMs with 16-bit MFMAs over int8 weight tiles:
+//   A_BF16  W8A16 (kernel/w8a16_kernel.c:203-216): bf16 X x int8 W (exact in
+//           bf16) on v_mfma_f32_16x16x32_bf16, fp32 accumulation, fp32 scale
+//           after the sum, fp32 / bf16 (RNE) / fp16 output.
+//   A_F16   the same with fp16 X on v_mfma_f32_16x16x32_f16.
+//   A_F32X3 W8A32 batch > 1 (kernel/w8a32_kernel.c:297-350): fp32 X split
+//           exactly into three bf16 terms (x0 = bf16(x), x1 = bf16(x - x0),
+//           x2 = bf16(x - x0 - x1)); three bf16 MFMAs per fragment give the
+//           fp32 product sum with exact products.
+//
+// Same skeleton as gemm_i8.hip: a ring of NST LDS stage buffers filled by
+// direct global -> LDS copies (one 16-byte piece per lane per copy), one
+// barrier per 64-wide K stage, transposed accumulators (weights as the MFMA's
+// first operand) so each lane stores 4 consecutive output columns.
+//
+// A copies land directly in MFMA operand layout.  Within a 64-wide K block the
+// int8 weight tile gives lane l row (l & 15) and k = 16 (l >> 4) + 0..15; the
+// bf16 MFMA consumes 8 k per lane, so the block is two MFMAs, half h taking
+// k = 16 (l >> 4) + 8 h + 0..7.  Each A copy therefore reads, for lane l,
+//   16-bit X: 8 elements X[row][64 kb + 16 (l >> 4) + 8 h ..]      (2 copies)
+//   fp32  X : 4 elements X[row][64 kb + 16 (l >> 4) + 4 j ..]      (4 copies)
+// and a wave reads its operand with one ds_read_b128 per copy.  Weight tiles
+// stay int8 in LDS and are widened to bf16/fp16 in registers after the read.
+// Lanes whose row is past M or whose k is past K copy 16 bytes of zeros.
+#include "tl_common.h"
+#include "tl_kernels.h"
+
+typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
+
+namespace tl {
+
+struct GemmB16Args {
+  const void* X;         // row-major [M][lda], element type per AMODE
+  int lda;
+  const uint8_t* Bt;     // weight tiles [KB][NG]
+  const float* ws;       // [N]
+  const float* bias;     // [N] or null
+  void* Y;
+  int ldy;
+  int M, N, K, KB, MG, NG;
+  int ntm, ntn;
+  int ep, out;
+  const uint8_t* zero_tile;
+};
+
+__device__ inline v8bf as_bf(uint4 u) { return __builtin_bit_cast(v8bf, u); }
+__device__ inline v8h_t as_h(uint4 u) { return __builtin_bit_cast(v8h_t, u); }
+
+// int8 weight lane (16 values) -> two 8-wide 16-bit operands (exact)
+template <int AMODE>
+__device__ inline void widen(uint4 w, uint4& h0, uint4& h1) {
+  const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+  uint32_t o[8];
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const float f0 = (float)(int8_t)(d[q] & 0xff), f1 = (float)(int8_t)((d[q] >> 8) & 0xff);
+    const float f2 = (float)(int8_t)((d[q] >> 16) & 0xff), f3 = (float)(int8_t)(d[q] >> 24);
+    if constexpr (AMODE == A_F16) {
+      const _Float16 h0f = (_Float16)f0, h1f = (_Float16)f1, h2f = (_Float16)f2, h3f = (_Float16)f3;
+      o[2 * q] = (uint32_t)__builtin_bit_cast(uint16_t, h0f) | ((uint32_t)__builtin_bit_cast(uint16_t, h1f) << 16);
+      o[2 * q + 1] = (uint32_t)__builtin_bit_cast(uint16_t, h2f) | ((uint32_t)__builtin_bit_cast(uint16_t, h3f) << 16);
+    } else {
+      // |w| <= 127 is exact in bf16: the high halves of the floats
+      o[2 * q] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
+      o[2 * q + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
+    }
+  }
+  h0 = make_uint4(o[0], o[1], o[2], o[3]);
+  h1 = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
+// 8 fp32 -> three bf16 terms t0 + t1 + t2 (exact decomposition)
+__device__ inline void split3x8(const float* x, uint4& t0, uint4& t1, uint4& t2) {
+  uint32_t a[8], b[8], c[8];
+#pragma unroll
+  for (int q = 0; q < 8; q++) {
+    a[q] = f32_to_bf16_rne(x[q]);
+    const float r1 = x[q] - bf16_to_f32(a[q]);
+    b[q] = f32_to_bf16_rne(r1);
+    const float r2 = r1 - bf16_to_f32(b[q]);
+    c[q] = f32_to_bf16_rne(r2);
+  }
+  t0 = make_uint4(a[0] | (a[1] << 16), a[2] | (a[3] << 16), a[4] | (a[5] << 16), a[6] | (a[7] << 16));
+  t1 = make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16));
+  t2 = make_uint4(c[0] | (c[1] << 16), c[2] | (c[3] << 16), c[4] | (c[5] << 16), c[6] | (c[7] << 16));
+}
+
+template <int AMODE>
+__device__ inline v4f mfma16(uint4 w, uint4 x, v4f c) {
+  if constexpr (AMODE == A_F16) return __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h(w), as_h(x), c, 0, 0, 0);
+  else return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(w), as_bf(x), c, 0, 0, 0);
+}
+
+template <int AMODE, int MT, int NT, int NST, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args a) {
+  constexpr int NW = WM * WN;
+  constexpr int AP = (AMODE == A_F32X3) ? 4 : 2;       // A copies per (row group, K block)
+  constexpr int ESZ = (AMODE == A_F32X3) ? 4 : 2;      // bytes per X element
+  constexpr int EPC = 16 / ESZ;                        // X elements per copy per lane
+  constexpr int TA = MT * AP, TB = NT, TS = TA + TB;
+  static_assert(TS % NW == 0, "stage copies must divide evenly over the waves");
+  constexpr int PW = TS / NW;
+  constexpr int FM = MT / WM, FN = NT / WN;
+  static_assert(MT % WM == 0 && NT % WN == 0, "wave grid must divide the tile");
+  static_assert(NST >= 2 && NST <= 8, "2..8 stage buffers");
+  static_assert(PW * (NST - 2) < 64, "vmcnt range");
+
+  __shared__ uint4 s0[TS * 64];
+  __shared__ uint4 s1[TS * 64];
+  __shared__ uint4 s2[NST > 2 ? TS * 64 : 1];
+  __shared__ uint4 s3[NST > 3 ? TS * 64 : 1];
+  __shared__ uint4 s4[NST > 4 ? TS * 64 : 1];
+  __shared__ uint4 s5[NST > 5 ? TS * 64 : 1];
+  __shared__ uint4 s6[NST > 6 ? TS * 64 : 1];
+  __shared__ uint4 s7[NST > 7 ? TS * 64 : 1];
+  uint4* const ring[8] = {s0, s1, s2, s3, s4, s5, s6, s7};
+
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wv / WN, wn = wv % WN;
+
+  const int ntiles = a.ntm * a.ntn;
+  int t = blockIdx.x;
+  if (ntiles % 8 == 0) t = (blockIdx.x % 8) * (ntiles / 8) + blockIdx.x / 8;
+  const int tn = t / a.ntm, tm = t - (t / a.ntm) * a.ntm;
+  const int mg0 = tm * MT, ng0 = tn * NT;
+
+  const uint4* B4 = reinterpret_cast<const uint4*>(a.Bt) + lane;
+  const uint4* Z4 = reinterpret_cast<const uint4*>(a.zero_tile);   // any 16 zero bytes
+  const char* Xb = static_cast<const char*>(a.X);
+  const int KB = a.KB;
+  const int nst = KB;
+
+  // per copy: source for stage 0 and its advance per stage
+  const char* qsrc[PW];
+  int qkoff[PW];                // X column of this lane's piece at stage 0 (A copies), -1 for B
+  bool qrow_ok[PW];
+  uint32_t qlds[PW];
+#pragma unroll
+  for (int p = 0; p < PW; p++) {
+    const int q = wv + NW * p;
+    qlds[p] = (uint32_t)q * 1024u;
+    if (q < TA) {
+      const int i = q / AP, j = q % AP;
+      const int row = (mg0 + i) * 16 + (lane & 15);
+      const int koff = 16 * (lane >> 4) + EPC * j;
+      qrow_ok[p] = row < a.M;
+      qkoff[p] = koff;
+      qsrc[p] = Xb + ((size_t)min(row, a.M - 1) * a.lda + koff) * ESZ;
+    } else {
+      const int ng = min(ng0 + (q - TA), a.NG - 1);
+      qrow_ok[p] = true;
+      qkoff[p] = -1;
+      qsrc[p] = reinterpret_cast<const char*>(B4 + (size_t)ng * 64);
+    }
+  }
+  const size_t bstride = (size_t)a.NG * 1024;   // bytes between K blocks of the weights
+  auto issue = [&](int st, uint4* buf) {
+    if (st >= nst) return;
+    const uint32_t base = lds_addr(buf);
+#pragma unroll
+    for (int p = 0; p < PW; p++) {
+      const uint4* g;
+      if (qkoff[p] >= 0) {
+        const int k = st * 64 + qkoff[p];
+        g = (qrow_ok[p] && k < a.K) ? reinterpret_cast<const uint4*>(qsrc[p] + (size_t)st * 64 * ESZ) : Z4;
+      } else {
+        g = reinterpret_cast<const uint4*>(qsrc[p] + (size_t)st * bstride);
+      }
+      dma_tile(g, base + qlds[p]);
+    }
+  };
+
+  // epilogue operands (transposed accumulators: lane holds row m, cols n..n+3)
+  const int mrow = lane & 15;
+  const int ncol = (lane >> 4) * 4;
+  float e_ws[FN][4], e_b[FN][4];
+#pragma unroll
+  for (int j = 0; j < FN; j++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int n = min((ng0 + wn * FN + j) * 16 + ncol + r, a.N - 1);
+      e_ws[j][r] = a.ws[n];
+      e_b[j][r] = a.bias ? a.bias[n] : 0.0f;
+    }
+  wait_vm<0>();
+
+  v4f acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](const uint4* buf) {
+    uint4 wb[FN][2];
+#pragma unroll
+    for (int j = 0; j < FN; j++) widen<AMODE>(buf[(TA + wn * FN + j) * 64 + lane], wb[j][0], wb[j][1]);
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+      const int ab = (wm * FM + i) * AP;
+      if constexpr (AMODE == A_F32X3) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const uint4 u0 = buf[(ab + 2 * h) * 64 + lane], u1 = buf[(ab + 2 * h + 1) * 64 + lane];
+          const float x[8] = {__uint_as_float(u0.x), __uint_as_float(u0.y), __uint_as_float(u0.z), __uint_as_float(u0.w),
+                              __uint_as_float(u1.x), __uint_as_float(u1.y), __uint_as_float(u1.z), __uint_as_float(u1.w)};
+          uint4 t0, t1, t2;
+          split3x8(x, t0, t1, t2);
+#pragma unroll
+          for (int j = 0; j < FN; j++) {
+            acc[i][j] = mfma16<A_BF16>(wb[j][h], t2, acc[i][j]);
+            acc[i][j] = mfma16<A_BF16>(wb[j][h], t1, acc[i][j]);
+            acc[i][j] = mfma16<A_BF16>(wb[j][h], t0, acc[i][j]);
+          }
+        }
+      } else {
+        const uint4 x0 = buf[ab * 64 + lane], x1 = buf[(ab + 1) * 64 + lane];
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+          acc[i][j] = mfma16<AMODE>(wb[j][0], x0, acc[i][j]);
+          acc[i][j] = mfma16<AMODE>(wb[j][1], x1, acc[i][j]);
+        }
+      }
+    }
+  };
+
+  auto step = [&](int st, const uint4* cur, uint4* nxt) {
+    wait_vm<PW * (NST - 2)>();
+    wait_lgkm0();
+    stage_barrier();
+    issue(st + NST - 1, nxt);
+    if (st < nst) compute(cur);
+  };
+
+#pragma unroll
+  for (int b = 0; b < NST - 1; b++) issue(b, ring[b]);
+  for (int st = 0; st < nst; st += NST) {
+#pragma unroll
+    for (int b = 0; b < NST; b++) step(st + b, ring[b], ring[(b + NST - 1) % NST]);
+  }
+  wait_vm<0>();   // no copy may still be landing in LDS when the work-group exits
+
+  const bool vec_ok = ((a.ldy & 3) == 0) &&
+                      ((((uintptr_t)a.Y) & (a.out == OUT_F32 ? 15 : 7)) == 0);
+#pragma unroll
+  for (int i = 0; i < FM; i++) {
+    const int m = (mg0 + wm * FM + i) * 16 + mrow;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+      const int n = (ng0 + wn * FN + j) * 16 + ncol;
+      if (n >= a.N) continue;
+      float y[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float c = acc[i][j][r];
+        if (a.ep == EP_SCALE_FMA) {
+          y[r] = __fmaf_rn(c, e_ws[j][r], e_b[j][r]);
+        } else {
+          y[r] = __fmul_rn(c, e_ws[j][r]);
+          if (a.bias) y[r] = __fadd_rn(y[r], e_b[j][r]);
+        }
+      }
+      const size_t o = (size_t)m * a.ldy + n;
+      const bool full = vec_ok && n + 4 <= a.N;
+      if (a.out == OUT_F32) {
+        float* yp = reinterpret_cast<float*>(a.Y) + o;
+        if (full) *reinterpret_cast<float4*>(yp) = make_float4(y[0], y[1], y[2], y[3]);
+        else for (int r = 0; r < 4 && n + r < a.N; r++) yp[r] = y[r];
+      } else {
+        uint16_t hv[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          if (a.out == OUT_BF16) {
+            hv[r] = (uint16_t)f32_to_bf16_rne(y[r]);
+          } else {
+            const _Float16 h = (_Float16)y[r];
+            hv[r] = __builtin_bit_cast(uint16_t, h);
+          }
+        }
+        uint16_t* yp = reinterpret_cast<uint16_t*>(a.Y) + o;
+        if (full) *reinterpret_cast<uint2*>(yp) = make_uint2(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16));
+        else for (int r = 0; r < 4 && n + r < a.N; r++) yp[r] = hv[r];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// planning and launch
+// ---------------------------------------------------------------------------
+// 16-bit X:  cfg 0  128 x 192 tiles, 4-deep ring (112 KiB)
+//            cfg 1   64 x 128 tiles, 8-deep ring (128 KiB)
+// fp32 X:    cfg 0   64 x 128 tiles, 4-deep ring (96 KiB)
+//            cfg 1   64 x  64 tiles, 6-deep ring (96 KiB)
+static void b16_cfg(int amode, int cfg, int& mt, int& nt) {
+  if (amode == A_F32X3) {
+    mt = 4;
+    nt = (cfg == 0) ? 8 : 4;
+  } else {
+    mt = (cfg == 0) ? 8 : 4;
+    nt = (cfg == 0) ? 12 : 8;
+  }
+}
+
+bool gemm_b16_supported(const GemmLaunch& L) {
+  if (L.amode != A_BF16 && L.amode != A_F16 && L.amode != A_F32X3) return false;
+  const int align = (L.amode == A_F32X3) ? 4 : 8;   // elements per 16-byte copy
+  if (L.K % align != 0 || L.lda % align != 0) return false;
+  if ((((uintptr_t)L.A) & 15) != 0) return false;
+  return L.zero_tile != nullptr;
+}
+
+hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st) {
+  if (!gemm_b16_supported(L)) return hipErrorInvalidValue;
+  GemmB16Args a;
+  a.X = L.A;
+  a.lda = L.lda;
+  a.Bt = L.Bt;
+  a.ws = L.ws;
+  a.bias = L.bias;
+  a.Y = L.Y;
+  a.ldy = L.ldy;
+  a.M = L.M;
+  a.N = L.N;
+  a.K = L.K;
+  a.KB = cdiv(L.K, 64);
+  a.MG = cdiv(L.M, 16);
+  a.NG = cdiv(L.N, 16);
+  a.ep = L.ep;
+  a.out = L.out;
+  a.zero_tile = L.zero_tile;
+  // the configuration whose tile count best fills 256 CUs
+  int best = 0;
+  double best_eff = -1.0;
+  for (int cfg : {0, 1}) {
+    int mt, nt;
+    b16_cfg(L.amode, cfg, mt, nt);
+    const int tiles = cdiv(a.MG, mt) * cdiv(a.NG, nt);
+    const double eff = (double)tiles / (cdiv(tiles, 256) * 256);
+    if (eff > best_eff + 1e-9) {
+      best_eff = eff;
+      best = cfg;
+    }
+  }
+  int mt, nt;
+  b16_cfg(L.amode, best, mt, nt);
+  a.ntm = cdiv(a.MG, mt);
+  a.ntn = cdiv(a.NG, nt);
+  const int blocks = a.ntm * a.ntn;
+  switch (L.amode) {
+    case A_BF16:
+      if (best == 0) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_BF16, 8, 12, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
+      else hipLaunchKernelGGL((gemm_b16_lds_kernel<A_BF16, 4, 8, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
+      break;
+    case A_F16:
+      if (best == 0) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F16, 8, 12, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
+      else hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F16, 4, 8, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
+      break;
+    default:
+      if (best == 0) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F32X3, 4, 8, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
+      else hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F32X3, 4, 4, 6, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
+      break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace tl

@@ -1,0 +1,286 @@
+// gemm_small.hip -- M <= 16 token rows over int8 weight tiles (decode rows
+// M = 2..8 of w8a32_linear, W8A16 at M = 1..16, W8A8 batches of 2..16).
+//
+// HBM-bound like the M = 1 GEMV, and organised the same way: a work-group
+// owns one 16-row weight group, its 4 waves split K, each wave streams its
+// 1 KiB weight tiles with two batches of U tiles in flight (branch-free,
+// clamped tail tiles get their activations zeroed), and the token rows ride along
+// as the second MFMA operand (L2-resident: 16 rows x K).  Each wave keeps one
+// 16x16 accumulator D[n][m] (weights as the first MFMA operand, so a lane
+// holds 4 consecutive n of one token row m); the 4 partial accumulators are
+// summed through LDS in a fixed order and wave 0 applies the epilogue.
+//
+//   A_I8    codes as 16x64 tiles (one row group), v_mfma_i32_16x16x64_i8
+//   A_BF16  bf16 rows, v_mfma_f32_16x16x32_bf16 (two per 64-wide K block)
+//   A_F16   fp16 rows, v_mfma_f32_16x16x32_f16
+//   A_F32X3 fp32 rows split exactly into three bf16 terms (six MFMAs per block)
+// Token rows >= M read row M-1 (their output columns are never stored); K
+// positions >= K are zero in the weight tiles and are zeroed in X as well.
+#include "tl_common.h"
+#include "tl_kernels.h"
+
+typedef _Float16 v8h_s __attribute__((ext_vector_type(8)));
+
+namespace tl {
+
+struct GemmSmallArgs {
+  const void* A;        // A_I8: code tiles [KB][1]; else row-major [M][lda]
+  int lda;
+  const uint8_t* Bt;    // weight tiles [KB][NG]
+  const float* ws;
+  const float* xs;      // per-token scales (A_I8)
+  const float* bias;
+  void* Y;
+  int ldy;
+  int M, N, K, KB, NG;
+  int ep, out;
+};
+
+template <int AMODE>
+struct AFrag {
+  // A_I8: 1 x uint4; 16-bit: 2 x uint4 (K halves); fp32: 4 x uint4 (16 floats)
+  uint4 v[AMODE == A_I8 ? 1 : (AMODE == A_F32X3 ? 4 : 2)];
+};
+
+template <int AMODE>
+__device__ inline AFrag<AMODE> load_a(const GemmSmallArgs& a, int kb, int lane) {
+  AFrag<AMODE> f;
+  if constexpr (AMODE == A_I8) {
+    f.v[0] = reinterpret_cast<const uint4*>(a.A)[(size_t)kb * 64 + lane];
+  } else {
+    constexpr int ESZ = (AMODE == A_F32X3) ? 4 : 2;
+    constexpr int NV = (AMODE == A_F32X3) ? 4 : 2;
+    constexpr int EPV = 16 / ESZ;                     // elements per uint4
+    const int row = min(lane & 15, a.M - 1);
+    const int k0 = kb * 64 + 16 * (lane >> 4);
+    const char* base = static_cast<const char*>(a.A) + (size_t)row * a.lda * ESZ;
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+      const int k = k0 + EPV * v;
+      const int kc = min(k, a.K - EPV);               // in-bounds address
+      uint4 u = *reinterpret_cast<const uint4*>(base + (size_t)kc * ESZ);
+      f.v[v] = (k < a.K) ? u : make_uint4(0, 0, 0, 0);
+    }
+  }
+  return f;
+}
+
+__device__ inline void widen_bf16(uint4 w, uint4& h0, uint4& h1) {
+  uint2 p0 = i8x4_to_bf16x4(w.x), p1 = i8x4_to_bf16x4(w.y);
+  uint2 p2 = i8x4_to_bf16x4(w.z), p3 = i8x4_to_bf16x4(w.w);
+  h0 = make_uint4(p0.x, p0.y, p1.x, p1.y);
+  h1 = make_uint4(p2.x, p2.y, p3.x, p3.y);
+}
+
+__device__ inline uint32_t f16x2(float a, float b) {
+  const _Float16 ha = (_Float16)a, hb = (_Float16)b;
+  return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+}
+__device__ inline void widen_f16(uint4 w, uint4& h0, uint4& h1) {
+  const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+  uint32_t o[8];
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    o[2 * q] = f16x2((float)(int8_t)(d[q] & 0xff), (float)(int8_t)((d[q] >> 8) & 0xff));
+    o[2 * q + 1] = f16x2((float)(int8_t)((d[q] >> 16) & 0xff), (float)(int8_t)(d[q] >> 24));
+  }
+  h0 = make_uint4(o[0], o[1], o[2], o[3]);
+  h1 = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
+__device__ inline void split3_8(const float* x, uint4& t0, uint4& t1, uint4& t2) {
+  uint32_t a[8], b[8], c[8];
+#pragma unroll
+  for (int q = 0; q < 8; q++) {
+    a[q] = f32_to_bf16_rne(x[q]);
+    const float r1 = x[q] - bf16_to_f32(a[q]);
+    b[q] = f32_to_bf16_rne(r1);
+    const float r2 = r1 - bf16_to_f32(b[q]);
+    c[q] = f32_to_bf16_rne(r2);
+  }
+  t0 = make_uint4(a[0] | (a[1] << 16), a[2] | (a[3] << 16), a[4] | (a[5] << 16), a[6] | (a[7] << 16));
+  t1 = make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16));
+  t2 = make_uint4(c[0] | (c[1] << 16), c[2] | (c[3] << 16), c[4] | (c[5] << 16), c[6] | (c[7] << 16));
+}
+
+template <int AMODE>
+using acc_small_t = typename std::conditional<AMODE == A_I8, v4i, v4f>::type;
+
+template <int AMODE>
+__device__ inline acc_small_t<AMODE> mma(uint4 w, const AFrag<AMODE>& x, acc_small_t<AMODE> c) {
+  if constexpr (AMODE == A_I8) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, w), __builtin_bit_cast(v4i, x.v[0]), c, 0, 0, 0);
+  } else if constexpr (AMODE == A_BF16) {
+    uint4 h0, h1;
+    widen_bf16(w, h0, h1);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h0), __builtin_bit_cast(v8bf, x.v[0]), c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h1), __builtin_bit_cast(v8bf, x.v[1]), c, 0, 0, 0);
+  } else if constexpr (AMODE == A_F16) {
+    uint4 h0, h1;
+    widen_f16(w, h0, h1);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h_s, h0), __builtin_bit_cast(v8h_s, x.v[0]), c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h_s, h1), __builtin_bit_cast(v8h_s, x.v[1]), c, 0, 0, 0);
+  } else {
+    uint4 h[2];
+    widen_bf16(w, h[0], h[1]);
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+      const uint4 u0 = x.v[2 * hh], u1 = x.v[2 * hh + 1];
+      const float f[8] = {__uint_as_float(u0.x), __uint_as_float(u0.y), __uint_as_float(u0.z), __uint_as_float(u0.w),
+                          __uint_as_float(u1.x), __uint_as_float(u1.y), __uint_as_float(u1.z), __uint_as_float(u1.w)};
+      uint4 t0, t1, t2;
+      split3_8(f, t0, t1, t2);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h[hh]), __builtin_bit_cast(v8bf, t2), c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h[hh]), __builtin_bit_cast(v8bf, t1), c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h[hh]), __builtin_bit_cast(v8bf, t0), c, 0, 0, 0);
+    }
+    return c;
+  }
+}
+
+template <int AMODE, int U>
+__global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
+  using acc_t = acc_small_t<AMODE>;
+  __shared__ acc_t s_part[4][64];
+
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = blockIdx.x;                            // weight row group
+  const int kb0 = (wv * a.KB) / 4, kb1 = ((wv + 1) * a.KB) / 4;
+  const int n_t = kb1 - kb0;                           // may be 0 when KB < 4
+  const int last = max(n_t - 1, 0);
+  const uint4* wp = reinterpret_cast<const uint4*>(a.Bt) + ((size_t)kb0 * a.NG + g) * 64 + lane;
+  const size_t tstride = (size_t)a.NG * 64;
+
+  acc_t acc = acc_t{0, 0, 0, 0};
+  uint4 b0[U], b1[U];
+  AFrag<AMODE> x0[U], x1[U];
+  auto load = [&](uint4 (&b)[U], AFrag<AMODE> (&x)[U], int t0) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int t = min(t0 + u, last);
+      b[u] = wp[(size_t)t * tstride];
+      x[u] = load_a<AMODE>(a, min(kb0 + t, a.KB - 1), lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto consume = [&](const uint4 (&b)[U], const AFrag<AMODE> (&x)[U], int t0) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      // clamped repeats add exactly 0: their activations are zeroed (the
+      // weights are finite int8, so 0 * w == 0 even when X holds Inf/NaN)
+      AFrag<AMODE> xv = x[u];
+      if (!(t0 + u < n_t)) {
+#pragma unroll
+        for (int q = 0; q < (int)(sizeof(xv.v) / sizeof(uint4)); q++) xv.v[q] = make_uint4(0, 0, 0, 0);
+      }
+      acc = mma<AMODE>(b[u], xv, acc);
+    }
+  };
+
+  load(b0, x0, 0);
+  load(b1, x1, U);
+  int t = 0;
+  for (; t + 2 * U < n_t; t += 2 * U) {
+    consume(b0, x0, t);
+    load(b0, x0, t + 2 * U);
+    consume(b1, x1, t + U);
+    load(b1, x1, t + 3 * U);
+  }
+  consume(b0, x0, t);
+  consume(b1, x1, t + U);
+
+  s_part[wv][lane] = acc;
+  __syncthreads();
+  if (wv != 0) return;
+  acc_t tot = s_part[0][lane];
+#pragma unroll
+  for (int w = 1; w < 4; w++) {
+    const acc_t p = s_part[w][lane];
+#pragma unroll
+    for (int r = 0; r < 4; r++) tot[r] += p[r];
+  }
+
+  // lane holds D[n .. n+3][m]: m = lane & 15, n = 16 g + 4 (lane >> 4)
+  const int m = lane & 15;
+  const int n0 = g * 16 + 4 * (lane >> 4);
+  if (m >= a.M) return;
+  for (int r = 0; r < 4; r++) {
+    const int n = n0 + r;
+    if (n >= a.N) break;
+    const size_t o = (size_t)m * a.ldy + n;
+    float y;
+    if constexpr (AMODE == A_I8) {
+      if (a.out == OUT_I32) {
+        reinterpret_cast<int32_t*>(a.Y)[o] = tot[r];
+        continue;
+      }
+      y = __fmul_rn(__fmul_rn((float)tot[r], a.ws[n]), a.xs[m]);
+      if (a.bias) y = __fadd_rn(y, a.bias[n]);
+    } else {
+      if (a.ep == EP_SCALE_FMA) {
+        y = __fmaf_rn(tot[r], a.ws[n], a.bias ? a.bias[n] : 0.0f);
+      } else {
+        y = __fmul_rn(tot[r], a.ws[n]);
+        if (a.bias) y = __fadd_rn(y, a.bias[n]);
+      }
+    }
+    if (a.out == OUT_F32) {
+      reinterpret_cast<float*>(a.Y)[o] = y;
+    } else if (a.out == OUT_BF16) {
+      reinterpret_cast<uint16_t*>(a.Y)[o] = (uint16_t)f32_to_bf16_rne(y);
+    } else {
+      const _Float16 h = (_Float16)y;
+      reinterpret_cast<uint16_t*>(a.Y)[o] = __builtin_bit_cast(uint16_t, h);
+    }
+  }
+}
+
+bool gemm_small_supported(const GemmLaunch& L) {
+  if (L.M < 1 || L.M > 16) return false;
+  if (L.amode == A_I8) return true;                    // code tiles, any K
+  const int epv = (L.amode == A_F32X3) ? 4 : 8;        // elements per 16 bytes
+  if (L.K % epv != 0 || L.lda % epv != 0) return false;
+  return (((uintptr_t)L.A) & 15) == 0;
+}
+
+template <int AMODE>
+static void launch_small_mode(const GemmSmallArgs& a, int u, hipStream_t st) {
+  const dim3 grid(a.NG), block(256);
+  if (u == 8) hipLaunchKernelGGL((gemm_small_kernel<AMODE, 8>), grid, block, 0, st, a);
+  else if (u == 4) hipLaunchKernelGGL((gemm_small_kernel<AMODE, 4>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((gemm_small_kernel<AMODE, 2>), grid, block, 0, st, a);
+}
+
+hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st) {
+  if (!gemm_small_supported(L)) return hipErrorInvalidValue;
+  GemmSmallArgs a;
+  a.A = L.A;
+  a.lda = L.lda;
+  a.Bt = L.Bt;
+  a.ws = L.ws;
+  a.xs = L.xs;
+  a.bias = L.bias;
+  a.Y = L.Y;
+  a.ldy = L.ldy;
+  a.M = L.M;
+  a.N = L.N;
+  a.K = L.K;
+  a.KB = cdiv(L.K, 64);
+  a.NG = cdiv(L.N, 16);
+  a.ep = L.ep;
+  a.out = L.out;
+  if (L.amode == A_I8 && L.out != OUT_I32 && !L.xs) return hipErrorInvalidValue;
+  const int n_t = cdiv(a.KB, 4);
+  // the fp32 split carries 4 uint4 of X per tile: its batches stay at 2
+  const int u = (L.amode != A_F32X3 && n_t >= 4) ? 4 : 2;
+  switch (L.amode) {
+    case A_I8: launch_small_mode<A_I8>(a, u, st); break;
+    case A_BF16: launch_small_mode<A_BF16>(a, u, st); break;
+    case A_F16: launch_small_mode<A_F16>(a, u, st); break;
+    default: launch_small_mode<A_F32X3>(a, u, st); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace tl

@@ -87,11 +87,11 @@ __device__ inline int consume_batch(const uint4 (&b)[U], const uint4 (&c)[XV == 
 
 template <int XV, int U>
 __device__ inline void load_batch(uint4 (&b)[U], uint4 (&c)[XV == 0 ? U : 1], const uint4* wp,
-                                  const uint4* cg, int kb0, int t0, int n_t, int lg) {
+                                  size_t tstride, const uint4* cg, int kb0, int t0, int n_t, int lg) {
 #pragma unroll
   for (int u = 0; u < U; u++) {
     const int t = min(t0 + u, n_t - 1);
-    b[u] = wp[(size_t)t * 64];
+    b[u] = wp[(size_t)t * tstride];
     if constexpr (XV == 0) c[u] = cg[(kb0 + t) * 4 + lg];
   }
   // keep the batch issued here, ahead of the consumption that follows
@@ -122,7 +122,8 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(GemvArgs a) {
   const int n_t = kb1 - kb0;              // >= 1 (host keeps T <= KB)
   const int gl = g_ok ? g : a.NG - 1;     // out-of-range row groups re-read a valid one
 
-  const uint4* wp = reinterpret_cast<const uint4*>(a.wt) + ((size_t)gl * a.KB + kb0) * 64 + lane;
+  const uint4* wp = reinterpret_cast<const uint4*>(a.wt) + ((size_t)kb0 * a.NG + gl) * 64 + lane;
+  const size_t tstride = (size_t)a.NG * 64;   // uint4 between consecutive k-blocks
   const uint4* cg = reinterpret_cast<const uint4*>(a.xq);
 
   uint4 b0[U], b1[U];
@@ -150,8 +151,8 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(GemvArgs a) {
       }
     }
   }
-  load_batch<XV, U>(b0, c0, wp, cg, kb0, 0, n_t, lg);
-  load_batch<XV, U>(b1, c1, wp, cg, kb0, U, n_t, lg);
+  load_batch<XV, U>(b0, c0, wp, tstride, cg, kb0, 0, n_t, lg);
+  load_batch<XV, U>(b1, c1, wp, tstride, cg, kb0, U, n_t, lg);
 
   float xs;
   if constexpr (XV > 0) {
@@ -199,9 +200,9 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(GemvArgs a) {
   int t = 0;
   for (; t + 2 * U < n_t; t += 2 * U) {
     acc = consume_batch<XV, U>(b0, c0, s_codes, kb0, t, n_t, lg, acc);
-    load_batch<XV, U>(b0, c0, wp, cg, kb0, t + 2 * U, n_t, lg);
+    load_batch<XV, U>(b0, c0, wp, tstride, cg, kb0, t + 2 * U, n_t, lg);
     acc = consume_batch<XV, U>(b1, c1, s_codes, kb0, t + U, n_t, lg, acc);
-    load_batch<XV, U>(b1, c1, wp, cg, kb0, t + 3 * U, n_t, lg);
+    load_batch<XV, U>(b1, c1, wp, tstride, cg, kb0, t + 3 * U, n_t, lg);
   }
   acc = consume_batch<XV, U>(b0, c0, s_codes, kb0, t, n_t, lg, acc);
   acc = consume_batch<XV, U>(b1, c1, s_codes, kb0, t + U, n_t, lg, acc);

@@ -78,6 +78,10 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restr
 
 // One wave per row, 4 rows per work-group; codes are written straight into
 // the 16x64 tile layout (row r -> tile lanes (r & 15) + 16 lg), zero beyond K.
+// Lane l owns the 16-wide chunks c = l + 64 j of the row (64 contiguous bytes
+// of x each): with CH > 0 all CH chunks are loaded at once and kept in
+// registers, so the row is read once; CH == 0 is the generic two-pass loop.
+template <int CH>
 __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(const float* __restrict__ src,
                                                                   int rows, int cols, int KB,
                                                                   uint8_t* __restrict__ tiles,
@@ -85,54 +89,15 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(const float* _
                                                                   int clamp127) {
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int MG = cdiv(rows, 16);
   if (r >= rows) return;
   const float* row = src + (size_t)r * cols;
   const int main_end = cols & ~15;
-  const bool vec = ((cols & 3) == 0) && ((((uintptr_t)src) & 15) == 0);
-
-  uint32_t mx = 0;
-  float tail = 0.0f;
-  if (vec) {
-    const float4* r4 = reinterpret_cast<const float4*>(row);
-    for (int i = lane; i < (main_end >> 2); i += 64) {
-      float4 v = r4[i];
-      uint32_t a = max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w)));
-      mx = a > mx ? a : mx;
-    }
-  } else {
-    for (int k = lane; k < main_end; k += 64) {
-      uint32_t a = abs_bits(row[k]);
-      mx = a > mx ? a : mx;
-    }
-  }
-  for (int k = main_end + lane; k < cols; k += 64) {
-    float a = fabsf(row[k]);
-    tail = (a > tail) ? a : tail;
-  }
-  mx = wave_max_u32(mx);
-  tail = wave_maxf_nonnan(tail);
-  const float vmax = __uint_as_float(mx);
-  const float absmax = (tail > vmax) ? tail : vmax;
-  const float scale = quant_scale(absmax);
-  const float inv = quant_inv(scale);
-  if (lane == 0) scales[r] = scale;
-
   const bool c127 = clamp127 != 0;
-  uint4* t4 = reinterpret_cast<uint4*>(tiles) + ((size_t)(r >> 4) * KB) * 64 + (r & 15);
-  for (int c = lane; c < KB * 4; c += 64) {   // 16-wide chunk c = (kb, lg)
+  uint4* t4 = reinterpret_cast<uint4*>(tiles) + (size_t)(r >> 4) * 64 + (r & 15);
+
+  auto store_chunk = [&](int c, const float* x, float inv) {
     const int k0 = c * 16;
-    float x[16];
-    if (vec && k0 + 16 <= cols) {
-      const float4* p = reinterpret_cast<const float4*>(row + k0);
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        float4 v = p[j];
-        x[4 * j] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 16; j++) x[j] = (k0 + j < cols) ? row[k0 + j] : 0.0f;
-    }
     int q[16];
 #pragma unroll
     for (int j = 0; j < 16; j++) q[j] = (k0 + j < cols) ? code_at(x[j], inv, k0 + j, cols, c127) : 0;
@@ -141,7 +106,63 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(const float* _
     o.y = pack4(q[4], q[5], q[6], q[7]);
     o.z = pack4(q[8], q[9], q[10], q[11]);
     o.w = pack4(q[12], q[13], q[14], q[15]);
-    t4[(size_t)(c >> 2) * 64 + 16 * (c & 3)] = o;
+    t4[(size_t)(c >> 2) * MG * 64 + 16 * (c & 3)] = o;
+  };
+
+  if constexpr (CH > 0) {
+    // cols == 1024 * CH, row 16-byte aligned
+    float4 v[CH][4];
+#pragma unroll
+    for (int j = 0; j < CH; j++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[j][e] = reinterpret_cast<const float4*>(row)[(lane + 64 * j) * 4 + e];
+    uint32_t mx = 0;
+#pragma unroll
+    for (int j = 0; j < CH; j++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float4 f = v[j][e];
+        const uint32_t m4 = max(max(abs_bits(f.x), abs_bits(f.y)), max(abs_bits(f.z), abs_bits(f.w)));
+        mx = m4 > mx ? m4 : mx;
+      }
+    mx = wave_max_u32(mx);
+    const float scale = quant_scale(__uint_as_float(mx));
+    const float inv = quant_inv(scale);
+    if (lane == 0) scales[r] = scale;
+#pragma unroll
+    for (int j = 0; j < CH; j++) {
+      float x[16];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        x[4 * e] = v[j][e].x; x[4 * e + 1] = v[j][e].y; x[4 * e + 2] = v[j][e].z; x[4 * e + 3] = v[j][e].w;
+      }
+      store_chunk(lane + 64 * j, x, inv);
+    }
+  } else {
+    uint32_t mx = 0;
+    float tail = 0.0f;
+    for (int k = lane; k < main_end; k += 64) {
+      const uint32_t a = abs_bits(row[k]);
+      mx = a > mx ? a : mx;
+    }
+    for (int k = main_end + lane; k < cols; k += 64) {
+      const float a = fabsf(row[k]);
+      tail = (a > tail) ? a : tail;
+    }
+    mx = wave_max_u32(mx);
+    tail = wave_maxf_nonnan(tail);
+    const float vmax = __uint_as_float(mx);
+    const float absmax = (tail > vmax) ? tail : vmax;
+    const float scale = quant_scale(absmax);
+    const float inv = quant_inv(scale);
+    if (lane == 0) scales[r] = scale;
+    for (int c = lane; c < KB * 4; c += 64) {
+      const int k0 = c * 16;
+      float x[16];
+#pragma unroll
+      for (int j = 0; j < 16; j++) x[j] = (k0 + j < cols) ? row[k0 + j] : 0.0f;
+      store_chunk(c, x, inv);
+    }
   }
 }
 
@@ -152,9 +173,10 @@ __global__ __launch_bounds__(256) void pack_tiles_kernel(const int8_t* __restric
   const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
   if (t >= total) return;
   const int lane = (int)(t & 63);
-  const long long tile = t >> 6;
-  const int kb = (int)(tile % KB);
-  const int g = (int)(tile / KB);
+  const long long tile = t >> 6;               // k-block-major: tile = kb * NG + g
+  const int NG = (rows + 15) / 16;
+  const int g = (int)(tile % NG);
+  const int kb = (int)(tile / NG);
   const int r = g * 16 + (lane & 15);
   const int k0 = kb * 64 + (lane >> 4) * 16;
   uint4 q = make_uint4(0, 0, 0, 0);
@@ -190,8 +212,20 @@ hipError_t launch_quantize_rows_tiled(const float* src, int rows, int cols, uint
                                       float* scales, bool clamp127, hipStream_t st) {
   if (rows <= 0 || cols <= 0) return hipSuccess;
   const int KB = cdiv(cols, 64);
-  hipLaunchKernelGGL(quantize_rows_tiled_kernel, dim3(cdiv(rows, 4)), dim3(256), 0, st, src, rows,
-                     cols, KB, tiles, scales, clamp127 ? 1 : 0);
+  const dim3 grid(cdiv(rows, 4)), block(256);
+  const int c = clamp127 ? 1 : 0;
+  const bool aligned = (((uintptr_t)src) & 15) == 0;
+  // the register-resident path needs cols == 1024 * CH (then K % 16 == 0, no tail)
+  if (aligned && cols == 2048)
+    hipLaunchKernelGGL(quantize_rows_tiled_kernel<2>, grid, block, 0, st, src, rows, cols, KB, tiles, scales, c);
+  else if (aligned && cols == 6144)
+    hipLaunchKernelGGL(quantize_rows_tiled_kernel<6>, grid, block, 0, st, src, rows, cols, KB, tiles, scales, c);
+  else if (aligned && cols == 1024)
+    hipLaunchKernelGGL(quantize_rows_tiled_kernel<1>, grid, block, 0, st, src, rows, cols, KB, tiles, scales, c);
+  else if (aligned && cols == 4096)
+    hipLaunchKernelGGL(quantize_rows_tiled_kernel<4>, grid, block, 0, st, src, rows, cols, KB, tiles, scales, c);
+  else
+    hipLaunchKernelGGL(quantize_rows_tiled_kernel<0>, grid, block, 0, st, src, rows, cols, KB, tiles, scales, c);
   return hipGetLastError();
 }
 

@@ -6,7 +6,10 @@
 //
 //   tile (g, kb) covers rows 16g .. 16g+15 and columns 64kb .. 64kb+63; it is
 //   1 KiB, lane-major: byte b of lane l holds  W[16g + (l & 15)][64kb + 16(l >> 4) + b].
-//   tiles are stored g-major: offset(g, kb) = (g * KB + kb) * 1024, KB = Kpad/64.
+//   tiles are stored k-block-major: offset(g, kb) = (kb * NG + g) * 1024,
+//   NG = ceil(rows/16).  One K slice of all row groups is then contiguous, so
+//   the tiles a GEMM stage reads spread over all L2 channels (with g-major
+//   order they sat KB KiB apart and fell on the same few channels).
 //
 // One 16-byte load per lane reads a whole tile, perfectly coalesced.  The
 // layout is the operand layout of v_mfma_i32_16x16x64_i8 (A or B): lane l
@@ -157,6 +160,35 @@ __device__ inline uint2 i8x4_to_bf16x4(uint32_t w) {
   r.x = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
   r.y = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
   return r;
+}
+
+// ---------------------------------------------------------------------------
+// global -> LDS tile copies and explicit waits (LDS-staged GEMMs)
+// ---------------------------------------------------------------------------
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0]+[15:14], expcnt[6:4],
+// lgkmcnt[11:8]); unnamed counters at their maximum
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | (((N >> 4) & 3) << 14));
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x3 << 14)); }
+
+// One 1 KiB tile global -> LDS: lane l's 16 bytes land at lds_base + 16 l.
+// Issued as volatile asm with a memory clobber so the compiler neither moves
+// it across the stage barrier nor adds its own (conservative) vmcnt waits in
+// front of LDS reads; every wait on these copies is explicit.
+__device__ __forceinline__ void dma_tile(const uint4* gsrc, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds_base), "v"(gsrc)
+               : "memory");
+}
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) void*)p));
 }
 
 }  // namespace tl

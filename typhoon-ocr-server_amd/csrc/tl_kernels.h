@@ -69,6 +69,7 @@ struct GemmLaunch {
   void* part = nullptr;           // split workspace (gemm_workspace_bytes)
   uint32_t* cnt = nullptr;        // gemm_counter_count zeroed counters
   int force_split = 0;
+  const uint8_t* zero_tile = nullptr;   // 1 KiB of device zeros (LDS-staged int8 GEMM)
 };
 GemmPlan gemm_plan(int amode, int M, int N, int K);
 size_t gemm_workspace_bytes(int amode, int M, int N, int K);
@@ -79,5 +80,13 @@ hipError_t launch_gemm(const GemmLaunch& L, hipStream_t st);
 hipError_t launch_gemm_i8(const GemmLaunch& L, hipStream_t st);
 int gemm_i8_pick_cfg(int M, int N, int K);
 void gemm_i8_set_cfg(int cfg);   // tuning override (-1 = planner)
+
+// ---- LDS-staged 16-bit MFMA GEMM (gemm_b16.hip): A_BF16 / A_F16 / A_F32X3,
+//      used for M > 16 when X rows are 16-byte aligned pieces --------------
+bool gemm_b16_supported(const GemmLaunch& L);
+// ---- M <= 16 rows (gemm_small.hip): GEMV-shaped MFMA kernel ---------------
+bool gemm_small_supported(const GemmLaunch& L);
+hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st);
+hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st);
 
 }  // namespace tl
