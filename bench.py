@@ -9,9 +9,10 @@ The step is captured once in a HIP graph (113 GEMV launches) and replayed.
 
 value   = algorithmic bytes of one step / step time (GB/s); bytes per GEMV
           launch are N*K + 4N + 4K + 4N (weights, scales, x, y).
-roofline: the GEMV kernel family, bytes per launch over its average launch
-          duration (HIP events around each launch on the launch stream),
-          against the 8 TB/s HBM peak.
+roofline: the GEMV kernel family (every launch of the step is a GEMV),
+          average bytes per launch over its average launch duration (HIP
+          events on the replay stream around the timed replays, divided by
+          the 113 launches each), against the 8 TB/s HBM peak.
 Also: W8A8 prefill TOPS (M=1024; N=6144,K=2048 and N=2048,K=6144; includes
 the per-token quantization kernel), and the CPU baseline (the oracle's M=1
 GEMV, OpenMP on the host cores) on a bounded sample.
@@ -32,6 +33,22 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
+COPY_PROBE_BYTES = 512 << 20
+TRAFFIC_SUMMARY = ROOT / "profiles" / "gemv_decode_step_traffic.md"
+
+
+def measured_traffic():
+    """HBM bytes per GEMV launch measured with rocprofv3 --pmc FETCH_SIZE and
+    WRITE_SIZE on `bench.py --traffic-probe` (counters scaled by what they
+    read for a 512 MiB copy), recorded in the profile summary; None if absent."""
+    try:
+        for line in TRAFFIC_SUMMARY.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
 LAYERS = 28
 LAYER_SHAPES = [("qkv", 4096, 2048), ("o", 2048, 2048), ("gate_up", 12288, 2048), ("down", 2048, 6144)]
 LM_HEAD = ("lm_head", 151936, 2048)
@@ -67,20 +84,30 @@ def run_step(lin, items, stream):
         lin.w8a32_linear_dev(x, W, y, stream=stream)
 
 
-def time_kernels(lin, torch, items, stream, reps):
-    """Average duration of each GEMV launch, HIP events on the launch stream."""
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in items]
-    tot = np.zeros(len(items))
-    with torch.cuda.stream(stream):
-        for _ in range(reps):
-            for i, (_, _, _, W, x, y) in enumerate(items):
-                ev[i][0].record(stream)
+def time_shapes(lin, torch, items, stream, reps):
+    """Average launch duration per decode shape: the launches of one shape in
+    a step (28 distinct matrices, or the lm_head) captured back-to-back in a
+    HIP graph and replayed; HIP events on the replay stream."""
+    by = {}
+    for it in items:
+        by.setdefault(it[0].split(".")[-1], []).append(it)
+    out = {}
+    for key, its in by.items():
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for (_, _, _, W, x, y) in its:
                 lin.w8a32_linear_dev(x, W, y, stream=stream)
-                ev[i][1].record(stream)
-            stream.synchronize()
-            for i in range(len(items)):
-                tot[i] += ev[i][0].elapsed_time(ev[i][1])
-    return tot / reps * 1e-3  # seconds per launch
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        out[key] = (its[0][1], its[0][2], e0.elapsed_time(e1) * 1e-3 / (reps * len(its)))
+        del g
+    return out
 
 
 def bench_w8a8_prefill(lin, torch, dev, reps=20):
@@ -120,9 +147,12 @@ def bench_w8a8_prefill(lin, torch, dev, reps=20):
     return out
 
 
-def cpu_baseline(seconds=12.0):
-    """The oracle's M=1 GEMV (same formula as the reference's w8a32_gemv) on the
-    host cores; the per-token time is 28 x the layer set + lm_head."""
+def cpu_baseline(seconds=10.0):
+    """The oracle's M=1 GEMV (same formula as the reference's w8a32_gemv,
+    OpenMP over row chunks like its GCD fan-out) on the host cores, over the
+    same decode step as the GPU: 28 distinct layer sets + lm_head (1.72 GB of
+    int8 weights, so no cache holds them).  Whole steps are timed until the
+    time budget is spent; the median step time gives GB/s and tok/s."""
     from oracle import oracle as orc
     native = True
     try:
@@ -135,29 +165,155 @@ def cpu_baseline(seconds=12.0):
         cores = os.cpu_count() or 1
     cores = max(1, min(cores, 16))
     rng = np.random.default_rng(0)
-    shapes = [(n, N, K) for (n, N, K) in LAYER_SHAPES] + [LM_HEAD]
-    per = {}
-    budget = seconds / len(shapes)
+    shapes = [(f"l{l}.{n}", N, K) for l in range(LAYERS) for (n, N, K) in LAYER_SHAPES] + [LM_HEAD]
+    mats = []
     for (name, N, K) in shapes:
         w = rng.integers(-127, 128, (N, K), dtype=np.int8)
         s = rng.uniform(0.002, 0.02, N).astype(np.float32)
         x = rng.standard_normal(K, dtype=np.float32)
-        y = np.empty(N, np.float32)
-        orc.w8a32_gemv_timed(x, w, s, y, cores, native=native)   # warm-up
-        times = []
-        t_end = time.perf_counter() + budget
-        while time.perf_counter() < t_end or len(times) < 3:
-            t0 = time.perf_counter()
+        mats.append((w, s, x, np.empty(N, np.float32)))
+    for (w, s, x, y) in mats[:4]:
+        orc.w8a32_gemv_timed(x, w, s, y, cores, native=native)        # warm-up
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 2:
+        t0 = time.perf_counter()
+        for (w, s, x, y) in mats:
             orc.w8a32_gemv_timed(x, w, s, y, cores, native=native)
-            times.append(time.perf_counter() - t0)
-        per[name] = float(np.median(times))
-    t_tok = LAYERS * sum(per[n] for (n, _, _) in LAYER_SHAPES) + per["lm_head"]
-    step_bytes = LAYERS * sum(gemv_bytes(N, K) for (_, N, K) in LAYER_SHAPES) + gemv_bytes(*LM_HEAD[1:])
+        times.append(time.perf_counter() - t0)
+    t_tok = float(np.median(times))
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    step_bytes = sum(gemv_bytes(N, K) for (_, N, K) in shapes)
     return {"value": round(step_bytes / t_tok / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
-            "tok_s": round(1.0 / t_tok, 2),
-            "sample": f"oracle M=1 GEMV ({'-march=native' if native else 'x86-64-v3'}, OpenMP) timed on "
-                      f"one layer set + lm_head (median of repeats, ~{seconds:.0f}s); per-token time = "
-                      f"28 x layer set + lm_head"}
+            "tok_s": round(1.0 / t_tok, 2), "steps_timed": len(times),
+            "host_cpu": model, "nproc": os.cpu_count(),
+            "sample": f"oracle M=1 GEMV ({'-march=native' if native else 'x86-64-v3'}, OpenMP, "
+                      f"{cores} threads) over whole decode steps (28 distinct layer sets + lm_head, "
+                      f"1.72 GB int8), median of {len(times)} steps in ~{seconds:.0f} s"}
+
+
+def rotating(lin, torch, dev, N, K, min_bytes=600e6):
+    copies = max(2, int(np.ceil(min_bytes / (N * K))))
+    Ws = []
+    for _ in range(copies):
+        w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev)
+        s = torch.rand(N, device=dev) * 0.018 + 0.002
+        Ws.append(lin.DeviceWeights.from_codes(w, s))
+    return Ws
+
+
+def time_calls(torch, fn, n_w, reps=20):
+    st = torch.cuda.current_stream()
+    for i in range(3):
+        fn(i % n_w, st)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for i in range(reps):
+        fn(i % n_w, st)
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / reps
+
+
+def bench_decode_rows(lin, torch, dev):
+    """W8A32 decode rows M = 1, 2, 4, 8 (M = 1: int8 GEMV; M > 1: fp32
+    semantics on the MFMA small-M kernel) per decode shape, HBM GB/s."""
+    out = {}
+    for (name, N, K) in LAYER_SHAPES + [LM_HEAD]:
+        Ws = rotating(lin, torch, dev, N, K)
+        row = {}
+        for M in (1, 2, 4, 8):
+            x = torch.randn((M, K), device=dev)
+            y = torch.empty((M, N), device=dev)
+            t = time_calls(torch, lambda i, st: lin.w8a32_linear_dev(x, Ws[i], y, stream=st), len(Ws))
+            b = N * K + 4 * N + 4 * M * K + 4 * M * N
+            row[f"M{M}"] = {"us": round(t * 1e6, 2), "GBps": round(b / t / 1e9, 1),
+                            "frac_hbm": round(b / t / 1e9 / HBM_PEAK_GBS, 4)}
+        out[f"{name}_{N}x{K}"] = row
+        for W in Ws:
+            W.close()
+    return out
+
+
+def bench_w8a16_sweep(lin, torch, dev):
+    """W8A16 sweep: bf16 X [M, 2048], int8 W [N, 2048], bf16 out."""
+    out = {}
+    K = 2048
+    for N in (2048, 4096, 12288):
+        Ws = rotating(lin, torch, dev, N, K)
+        for M in (1, 8, 64, 256, 1024):
+            x = torch.randn((M, K), device=dev).to(torch.bfloat16)
+            y = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
+            t = time_calls(torch, lambda i, st: lin.w8a16_linear_dev(x, Ws[i], y, stream=st), len(Ws))
+            ops = 2.0 * M * N * K
+            b = N * K + 4 * N + 2 * M * K + 2 * M * N
+            hbm = M <= 64
+            frac = (b / t / 1e9 / HBM_PEAK_GBS) if hbm else (ops / t / 1e12 / BF16_PEAK_TFLOPS)
+            out[f"M{M}_N{N}"] = {"us": round(t * 1e6, 2), "TFLOPs": round(ops / t / 1e12, 1),
+                                 "GBps": round(b / t / 1e9, 1), "bound": "hbm" if hbm else "mfma",
+                                 "frac": round(frac, 4)}
+        for W in Ws:
+            W.close()
+    return out
+
+
+def bench_w8a32_prefill(lin, torch, dev, M=1200):
+    """The reference decoder's prefill linear path, w8a32_linear(batch=S)
+    (fp32 X times dequantized weights), at S = 1200 on the fused layer shapes;
+    computed as three bf16 MFMA passes (fp32-accurate)."""
+    out = {}
+    tot_f, tot_t = 0.0, 0.0
+    for (name, N, K) in LAYER_SHAPES:
+        Ws = rotating(lin, torch, dev, N, K, min_bytes=300e6)
+        x = torch.randn((M, K), device=dev)
+        y = torch.empty((M, N), device=dev)
+        t = time_calls(torch, lambda i, st: lin.w8a32_linear_dev(x, Ws[i], y, stream=st), len(Ws), reps=10)
+        f = 2.0 * M * N * K
+        out[name] = {"us": round(t * 1e6, 1), "TFLOPs_fp32_equiv": round(f / t / 1e12, 1)}
+        tot_f += f
+        tot_t += t
+        for W in Ws:
+            W.close()
+    out["layer_ms"] = round(tot_t * 1e3, 3)
+    out["prefill_tok_s_linear_only"] = round(M / (LAYERS * tot_t), 1)
+    return out
+
+
+def bench_host_abi(lin, reps=200):
+    """The reference's own entry point, w8a32_linear(batch=1) on host
+    pointers: registered weights, x copied in and y copied out through pinned
+    staging on every call, stream synchronised before return.  Wall-clock per
+    call (PCIe and synchronisation included)."""
+    lib = lin.load_library()
+    rng = np.random.default_rng(1)
+    out = {}
+    for (name, N, K) in [("qkv", 4096, 2048), ("lm_head", 151936, 2048)]:
+        w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+        s = rng.uniform(0.002, 0.02, N).astype(np.float32)
+        x = rng.standard_normal((1, K), dtype=np.float32)
+        y = np.empty((1, N), np.float32)
+        if lib.tl_register_weights(lin._p(w, lin.ctypes.c_int8), lin._p(s, lin.ctypes.c_float), N, K) != 0:
+            lin.check(lib, "tl_register_weights")
+        n = reps if N < 100000 else max(20, reps // 10)
+        for _ in range(5):
+            lin.w8a32_linear(x, w, s, out=y)
+        t0 = time.perf_counter()
+        for _ in range(n):
+            lin.w8a32_linear(x, w, s, out=y)
+        t = (time.perf_counter() - t0) / n
+        b = gemv_bytes(N, K)
+        out[f"{name}_{N}x{K}"] = {"us": round(t * 1e6, 2), "GBps": round(b / t / 1e9, 1)}
+        lib.tl_evict_weights(lin._p(w, lin.ctypes.c_int8))
+    out["includes"] = "host x -> HBM, GEMV, HBM -> host y, stream sync; weights already resident"
+    return out
 
 
 def main():
@@ -168,6 +324,13 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the W8A8 prefill timing")
     ap.add_argument("--kernel-reps", type=int, default=5)
+    ap.add_argument("--quick", action="store_true",
+                    help="decode set only (no prefill, sweeps or CPU baseline)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the W8A8 prefill timing (for counter runs)")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run a 512 MiB device copy (counter calibration) and one eager decode "
+                         "step, then exit; used under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1"}))
@@ -184,8 +347,22 @@ def main():
         raise SystemExit("bench.py needs a GPU")
     dev = torch.device("cuda:0")
 
+    if args.prefill_only:
+        print(json.dumps({"w8a8_prefill": bench_w8a8_prefill(lin, torch, dev)}), flush=True)
+        return
     log("building the decode set (1.72 GB of int8 weights)")
     items = build_decode_set(lin, torch, dev)
+    if args.traffic_probe:
+        src = torch.empty(COPY_PROBE_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        st = torch.cuda.current_stream()
+        run_step(lin, items, st)
+        torch.cuda.synchronize()
+        log("traffic probe done")
+        return
     step_bytes = sum(gemv_bytes(N, K) for (_, N, K, *_r) in items)
     stream = torch.cuda.Stream()
 
@@ -215,35 +392,48 @@ def main():
     t_step = e0.elapsed_time(e1) * 1e-3 / args.steps
     value = step_bytes / t_step / 1e9
 
-    log("per-launch kernel timing (events)")
-    kt = time_kernels(lin, torch, items, stream, args.kernel_reps)
-    shapes = {}
-    for (name, N, K, *_r), t in zip(items, kt):
-        key = name.split(".")[-1]
-        d = shapes.setdefault(key, {"N": N, "K": K, "bytes": gemv_bytes(N, K), "t": []})
-        d["t"].append(t)
+    log("per-shape launch timing (graph replay)")
+    per = time_shapes(lin, torch, items, stream, max(5, args.kernel_reps))
     per_shape = {}
-    for key, d in shapes.items():
-        t = float(np.mean(d["t"]))
-        per_shape[key] = {"N": d["N"], "K": d["K"], "us": round(t * 1e6, 2),
-                          "GBps": round(d["bytes"] / t / 1e9, 1),
-                          "frac_hbm": round(d["bytes"] / t / 1e9 / HBM_PEAK_GBS, 4)}
+    for key, (N, K, t) in per.items():
+        b = gemv_bytes(N, K)
+        per_shape[key] = {"N": N, "K": K, "us": round(t * 1e6, 2), "GBps": round(b / t / 1e9, 1),
+                          "frac_hbm": round(b / t / 1e9 / HBM_PEAK_GBS, 4)}
+    # every launch of the step is the GEMV kernel and graph replay runs them
+    # back to back, so its average launch duration is the step time over the
+    # launch count
     avg_bytes = step_bytes / len(items)
-    avg_t = float(np.mean(kt))
+    avg_t = t_step / len(items)
     achieved = avg_bytes / avg_t / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                 "kernel": "gemv_i8_kernel (all 113 launches of a step)",
-                "bytes_per_launch": round(avg_bytes), "avg_launch_us": round(avg_t * 1e6, 2),
+                "bytes_per_launch": round(avg_bytes), "avg_launch_us": round(avg_t * 1e6, 3),
                 "per_shape": per_shape}
 
-    prefill = None
-    if not args.no_prefill:
+    # the decode set's 1.72 GB is no longer needed
+    n_launch = len(items)
+    del graph
+    for it in items:
+        it[3].close()
+    del items
+
+    prefill = rows = sweep = pre32 = host = None
+    if not args.quick:
+        log("host-pointer ABI (PCIe-inclusive)")
+        host = bench_host_abi(lin)
+    if not args.no_prefill and not args.quick:
         log("W8A8 prefill timing")
         prefill = bench_w8a8_prefill(lin, torch, dev)
+        log("W8A32 decode rows M=1..8")
+        rows = bench_decode_rows(lin, torch, dev)
+        log("W8A16 sweep")
+        sweep = bench_w8a16_sweep(lin, torch, dev)
+        log("W8A32 prefill (fp32 semantics)")
+        pre32 = bench_w8a32_prefill(lin, torch, dev)
 
     cpu = None
-    if not args.no_cpu and rank == 0:
+    if not args.no_cpu and not args.quick and rank == 0:
         log("CPU baseline")
         cpu = cpu_baseline()
 
@@ -263,11 +453,15 @@ def main():
         "config": {"workload": "decode projection set of the Qwen3-VL-2B text decoder, W8A32 batch=1: "
                                "28 x (QKV 4096x2048, O 2048x2048, gate_up 12288x2048, down 2048x6144) "
                                "+ lm_head 151936x2048, distinct weights, HIP-graph replay",
-                   "step_bytes": step_bytes, "launches_per_step": len(items)},
+                   "step_bytes": step_bytes, "launches_per_step": n_launch},
         "decode_tok_s": round(1.0 / t_step, 1),
         "wall_s": round(wall, 3),
         "roofline": roofline,
         "w8a8_prefill": prefill,
+        "w8a32_decode_rows": rows,
+        "w8a16_sweep": sweep,
+        "w8a32_prefill": pre32,
+        "host_abi": host,
         "cpu_baseline": cpu,
     }
     if rank == 0:

@@ -82,21 +82,6 @@ __device__ inline void w_to_f16(uint4 w, uint4& h0, uint4& h1) {
   h1 = make_uint4(o[4], o[5], o[6], o[7]);
 }
 
-// split 8 floats into three bf16 terms (exact decomposition, see header)
-__device__ inline void split3(const float* x, uint4& t0, uint4& t1, uint4& t2) {
-  uint32_t a[8], b[8], c[8];
-#pragma unroll
-  for (int q = 0; q < 8; q++) {
-    a[q] = f32_to_bf16_rne(x[q]);
-    float r1 = x[q] - bf16_to_f32(a[q]);
-    b[q] = f32_to_bf16_rne(r1);
-    float r2 = r1 - bf16_to_f32(b[q]);
-    c[q] = f32_to_bf16_rne(r2);
-  }
-  t0 = make_uint4(a[0] | (a[1] << 16), a[2] | (a[3] << 16), a[4] | (a[5] << 16), a[6] | (a[7] << 16));
-  t1 = make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16));
-  t2 = make_uint4(c[0] | (c[1] << 16), c[2] | (c[3] << 16), c[4] | (c[5] << 16), c[6] | (c[7] << 16));
-}
 
 // 16 consecutive 16-bit values of row m starting at k0 (zero outside [0,K))
 __device__ inline void load_row16_b16(const uint16_t* A, int lda, int M, int K, int m, int k0,
@@ -259,8 +244,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
         float x[16];
         load_row16_f32(reinterpret_cast<const float*>(a.A), a.lda, a.M, a.K, (mg0 + i) * 16 + row,
                        kb * 64 + kl, x);
-        split3(x, t[i][0][0], t[i][0][1], t[i][0][2]);
-        split3(x + 8, t[i][1][0], t[i][1][1], t[i][1][2]);
+        split3x8(x, t[i][0][0], t[i][0][1], t[i][0][2]);
+        split3x8(x + 8, t[i][1][0], t[i][1][1], t[i][1][2]);
       }
 #pragma unroll
       for (int j = 0; j < TN; j++) {

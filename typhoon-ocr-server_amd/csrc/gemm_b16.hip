@@ -69,21 +69,6 @@ __device__ inline void widen(uint4 w, uint4& h0, uint4& h1) {
   h1 = make_uint4(o[4], o[5], o[6], o[7]);
 }
 
-// 8 fp32 -> three bf16 terms t0 + t1 + t2 (exact decomposition)
-__device__ inline void split3x8(const float* x, uint4& t0, uint4& t1, uint4& t2) {
-  uint32_t a[8], b[8], c[8];
-#pragma unroll
-  for (int q = 0; q < 8; q++) {
-    a[q] = f32_to_bf16_rne(x[q]);
-    const float r1 = x[q] - bf16_to_f32(a[q]);
-    b[q] = f32_to_bf16_rne(r1);
-    const float r2 = r1 - bf16_to_f32(b[q]);
-    c[q] = f32_to_bf16_rne(r2);
-  }
-  t0 = make_uint4(a[0] | (a[1] << 16), a[2] | (a[3] << 16), a[4] | (a[5] << 16), a[6] | (a[7] << 16));
-  t1 = make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16));
-  t2 = make_uint4(c[0] | (c[1] << 16), c[2] | (c[3] << 16), c[4] | (c[5] << 16), c[6] | (c[7] << 16));
-}
 
 template <int AMODE>
 __device__ inline v4f mfma16(uint4 w, uint4 x, v4f c) {

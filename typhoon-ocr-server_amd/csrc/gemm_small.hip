@@ -88,20 +88,6 @@ __device__ inline void widen_f16(uint4 w, uint4& h0, uint4& h1) {
   h1 = make_uint4(o[4], o[5], o[6], o[7]);
 }
 
-__device__ inline void split3_8(const float* x, uint4& t0, uint4& t1, uint4& t2) {
-  uint32_t a[8], b[8], c[8];
-#pragma unroll
-  for (int q = 0; q < 8; q++) {
-    a[q] = f32_to_bf16_rne(x[q]);
-    const float r1 = x[q] - bf16_to_f32(a[q]);
-    b[q] = f32_to_bf16_rne(r1);
-    const float r2 = r1 - bf16_to_f32(b[q]);
-    c[q] = f32_to_bf16_rne(r2);
-  }
-  t0 = make_uint4(a[0] | (a[1] << 16), a[2] | (a[3] << 16), a[4] | (a[5] << 16), a[6] | (a[7] << 16));
-  t1 = make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16));
-  t2 = make_uint4(c[0] | (c[1] << 16), c[2] | (c[3] << 16), c[4] | (c[5] << 16), c[6] | (c[7] << 16));
-}
 
 template <int AMODE>
 using acc_small_t = typename std::conditional<AMODE == A_I8, v4i, v4f>::type;
@@ -129,7 +115,7 @@ __device__ inline acc_small_t<AMODE> mma(uint4 w, const AFrag<AMODE>& x, acc_sma
       const float f[8] = {__uint_as_float(u0.x), __uint_as_float(u0.y), __uint_as_float(u0.z), __uint_as_float(u0.w),
                           __uint_as_float(u1.x), __uint_as_float(u1.y), __uint_as_float(u1.z), __uint_as_float(u1.w)};
       uint4 t0, t1, t2;
-      split3_8(f, t0, t1, t2);
+      split3x8(f, t0, t1, t2);
       c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h[hh]), __builtin_bit_cast(v8bf, t2), c, 0, 0, 0);
       c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h[hh]), __builtin_bit_cast(v8bf, t1), c, 0, 0, 0);
       c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h[hh]), __builtin_bit_cast(v8bf, t0), c, 0, 0, 0);

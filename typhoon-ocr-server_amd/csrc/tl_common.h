@@ -141,13 +141,35 @@ __device__ inline int dot16(uint4 w, uint4 x, int acc) {
 // ---------------------------------------------------------------------------
 // bf16 helpers
 // ---------------------------------------------------------------------------
-// fp32 -> bf16 bits, round to nearest even (finite inputs; NaN kept quiet)
-__device__ inline uint32_t f32_to_bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// two fp32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32)
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
+// fp32 -> bf16 bits, round to nearest even
+__device__ inline uint32_t f32_to_bf16_rne(float f) { return pack_bf16x2(f, 0.0f) & 0xffffu; }
 __device__ inline float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// 8 fp32 -> three packed bf16 terms with x == t0 + t1 + t2 to within 2^-24 |x|:
+// t0 = bf16(x), t1 = bf16(x - t0), t2 = bf16(x - t0 - t1); both differences
+// are exact in fp32 (each term holds the leading bits of the remainder).
+__device__ inline void split3x8(const float* x, uint4& t0, uint4& t1, uint4& t2) {
+  uint32_t a[4], b[4], c[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const float x0 = x[2 * q], x1 = x[2 * q + 1];
+    a[q] = pack_bf16x2(x0, x1);
+    const float r0 = x0 - __uint_as_float(a[q] << 16), r1 = x1 - __uint_as_float(a[q] & 0xffff0000u);
+    b[q] = pack_bf16x2(r0, r1);
+    const float s0 = r0 - __uint_as_float(b[q] << 16), s1 = r1 - __uint_as_float(b[q] & 0xffff0000u);
+    c[q] = pack_bf16x2(s0, s1);
+  }
+  t0 = make_uint4(a[0], a[1], a[2], a[3]);
+  t1 = make_uint4(b[0], b[1], b[2], b[3]);
+  t2 = make_uint4(c[0], c[1], c[2], c[3]);
+}
 
 // 4 signed int8 (one dword) -> 4 bf16 (two dwords), exact for |w| <= 128
 __device__ inline uint2 i8x4_to_bf16x4(uint32_t w) {
