@@ -98,10 +98,11 @@ size_t tl_registry_bytes(void);
 int tl_registry_entries(void);
 
 /* Tuning override of the M=1 GEMV decomposition for every later call in the
- * process: waves per 16-row group in a work-group (1, 2, 4), K split across
- * work-groups (>= 1), tiles per load batch (2, 4, 8).  Zeros restore the
- * built-in planner. */
-int tl_gemv_set_plan(int ksw, int split, int u);
+ * process: mode 1 = one 16-row group per work-group, 2 = persistent grid
+ * walking the row groups; grid = persistent work-groups; u = weight tiles
+ * per load batch (2, 4, 8, 12; 4 in mode 2).  Zeros restore the built-in
+ * planner. */
+int tl_gemv_set_plan(int mode, int grid, int u);
 
 /* ---- device-resident weights ------------------------------------------- */
 typedef struct tl_weights tl_weights;

@@ -124,6 +124,30 @@ def test_gemv_accumulators_and_scale(lin, orc, dev, N, K):
     W.close()
 
 
+@pytest.mark.parametrize("mode,grid,u", [(1, 0, 2), (1, 0, 4), (1, 0, 8), (1, 0, 12),
+                                         (2, 7, 0), (2, 64, 0), (2, 1, 0)])
+@pytest.mark.parametrize("N,K", [(1000, 2048), (4100, 2040), (300, 6144), (37, 50), (129, 16384)])
+def test_gemv_plans_bit_exact(lin, orc, mode, grid, u, N, K):
+    """Every GEMV decomposition the planner can pick (one row group per
+    work-group with each batch depth, or a persistent grid that walks the row
+    groups, here with few work-groups so each one loops) gives the oracle's
+    bits, for W8A32 (fused activation quantization) and W8A8 (given codes)."""
+    say(f"gemv plan mode={mode} grid={grid} u={u} N={N} K={K}")
+    lib = lin.load_library()
+    rng = np.random.default_rng(N * 31 + K + 7 * mode + u + grid)
+    x, w, s = make(rng, 1, N, K)
+    b = rng.standard_normal(N).astype(F)
+    xq, xsc = orc.quantize_rows(x, clamp_main=False)
+    assert lib.tl_gemv_set_plan(mode, grid, u) == 0
+    try:
+        np.testing.assert_array_equal(lin.w8a32_linear(x, w, s), orc.w8a32_linear(x, w, s))
+        np.testing.assert_array_equal(lin.w8a32_linear(x, w, s, bias=b), orc.w8a32_linear(x, w, s, bias=b))
+        np.testing.assert_array_equal(lin.w8a8_linear(xq, xsc, w, s, bias=b),
+                                      orc.w8a8_linear(xq, xsc, w, s, bias=b))
+    finally:
+        lib.tl_gemv_set_plan(0, 0, 0)
+
+
 def test_gemv_deterministic_and_fused_equals_concat(lin, orc, dev):
     """Run-to-run bitwise determinism (split-K counters reset), and the fused
     QKV / gate_up matrices give the concatenation of the separate GEMVs."""

@@ -386,15 +386,7 @@ uint8_t* quantize_padded(Workspace& ws, const float* x, int K, float** xs_dev, h
   return static_cast<uint8_t*>(ws.act.p);
 }
 
-void run_gemv(Workspace& ws, GemvLaunch& L, hipStream_t st) {
-  GemvPlan p = gemv_plan(L.N, L.K);
-  if (p.split > 1) {
-    ws.part.ensure(gemv_workspace_bytes(L.N, L.K), st);
-    L.part = static_cast<int32_t*>(ws.part.p);
-    L.cnt = ensure_counters(ws, (size_t)cdiv(L.N, 16), st);
-  }
-  HIP_OK(launch_gemv_i8(L, st));
-}
+void run_gemv(Workspace&, GemvLaunch& L, hipStream_t st) { HIP_OK(launch_gemv_i8(L, st)); }
 
 // 1 KiB of zeros per device: the int8 GEMM copies it in place of k-blocks
 // past K
@@ -658,12 +650,13 @@ int tl_device_count(void) {
   return n;
 }
 
-int tl_gemv_set_plan(int ksw, int split, int u) {
+int tl_gemv_set_plan(int mode, int grid, int u) {
   return guarded("tl_gemv_set_plan", [&] {
-    REQUIRE(ksw == 0 || ksw == 1 || ksw == 2 || ksw == 4, "ksw must be 0, 1, 2 or 4");
-    REQUIRE(u == 0 || u == 2 || u == 4 || u == 8, "u must be 0, 2, 4 or 8");
-    REQUIRE(split >= 0, "split must be >= 0");
-    gemv_set_plan(ksw, split, u);
+    REQUIRE(mode >= 0 && mode <= 2, "mode must be 0, 1 or 2");
+    REQUIRE(grid >= 0, "grid must be >= 0");
+    REQUIRE(u == 0 || u == 2 || u == 4 || u == 8 || u == 12, "u must be 0, 2, 4, 8 or 12");
+    REQUIRE(mode != 2 || u == 0 || u == 4, "the persistent GEMV runs with u = 4");
+    gemv_set_plan(mode, grid, u);
   });
 }
 

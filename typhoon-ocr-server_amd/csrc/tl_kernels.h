@@ -26,7 +26,8 @@ hipError_t launch_pack_tiles(const int8_t* w, int rows, int cols, uint8_t* tiles
 
 // ---- M=1 GEMV (gemv.hip) --------------------------------------------------
 struct GemvPlan {
-  int ksw = 4, split = 1, blocks = 0, u = 8;
+  bool loop = false;   // persistent grid walking the row groups
+  int blocks = 0, u = 4;
 };
 struct GemvLaunch {
   const float* x = nullptr;       // fp32 activation (fused quantization) or null
@@ -38,17 +39,15 @@ struct GemvLaunch {
   float* y = nullptr;
   int32_t* acc_out = nullptr;
   float* xs_out = nullptr;
-  int32_t* part = nullptr;        // split workspace (gemv_workspace_bytes)
-  uint32_t* cnt = nullptr;        // ceil(N/16) zeroed counters
   int N = 0, K = 0, epi = EPI_W8A32;
-  int force_split = 0, force_ksw = 0, force_u = 0;   // tuning overrides (0 = planner)
 };
 GemvPlan gemv_plan(int N, int K);
 int gemv_fused_xv(int K);
-size_t gemv_workspace_bytes(int N, int K);
 hipError_t launch_gemv_i8(const GemvLaunch& L, hipStream_t st);
-// process-wide override of the GEMV plan for tuning (0 = planner's choice)
-void gemv_set_plan(int ksw, int split, int u);
+// process-wide override of the GEMV plan for tuning: mode 0 = planner,
+// 1 = one row group per work-group, 2 = persistent grid; grid = persistent
+// work-groups (0 = planner); u = tiles per load batch (0 = planner)
+void gemv_set_plan(int mode, int grid, int u);
 
 // ---- MFMA GEMM (gemm.hip) -------------------------------------------------
 struct GemmPlan {
