@@ -98,11 +98,10 @@ size_t tl_registry_bytes(void);
 int tl_registry_entries(void);
 
 /* Tuning override of the M=1 GEMV decomposition for every later call in the
- * process: mode 1 = one 16-row group per work-group, 2 = persistent grid
- * walking the row groups; grid = persistent work-groups; u = weight tiles
- * per load batch (2, 4, 8, 12; 4 in mode 2).  Zeros restore the built-in
- * planner. */
-int tl_gemv_set_plan(int mode, int grid, int u);
+ * process: rows per work-group (16, or 8 = half of a 16-row tile group) and
+ * weight load instructions per batch (2, 4, 8, 12 with 16 rows; 2, 4, 6, 8
+ * with 8 rows).  Zeros restore the built-in planner. */
+int tl_gemv_set_plan(int rows, int u);
 
 /* ---- device-resident weights ------------------------------------------- */
 typedef struct tl_weights tl_weights;

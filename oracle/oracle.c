@@ -22,6 +22,10 @@
  *       exact-tie cases (ties-to-even in the vector region, ties-away in the
  *       K%16 tail), x*fl(1/s) vs x/s discriminating cases, all-zero rows,
  *       NaN/Inf rows, and golden vectors computed independently in Python.
+ *       One case is left unpinned: a row whose absmax is so small that
+ *       absmax/127 underflows to 0 has inv = +inf, and its K%16 tail then
+ *       evaluates (int)lroundf(+-inf), which C leaves unspecified (here:
+ *       glibc's lroundf, 0 after the clamp; an AArch64 build may differ).
  *   orc_int_acc        -- pinned: brute-force Python integer dot products.
  *   orc_w8a32_linear   -- batch==1 pinned: closed form
  *       fl(fl(fl(acc)*ws)*xs) (+ bias as its own rounding) recomputed in

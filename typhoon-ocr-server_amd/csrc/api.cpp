@@ -650,13 +650,12 @@ int tl_device_count(void) {
   return n;
 }
 
-int tl_gemv_set_plan(int mode, int grid, int u) {
+int tl_gemv_set_plan(int rows, int u) {
   return guarded("tl_gemv_set_plan", [&] {
-    REQUIRE(mode >= 0 && mode <= 2, "mode must be 0, 1 or 2");
-    REQUIRE(grid >= 0, "grid must be >= 0");
-    REQUIRE(u == 0 || u == 2 || u == 4 || u == 8 || u == 12, "u must be 0, 2, 4, 8 or 12");
-    REQUIRE(mode != 2 || u == 0 || u == 4, "the persistent GEMV runs with u = 4");
-    gemv_set_plan(mode, grid, u);
+    REQUIRE(rows == 0 || rows == 8 || rows == 16, "rows must be 0, 8 or 16");
+    REQUIRE(u == 0 || u == 2 || u == 4 || u == 6 || u == 8 || u == 12, "u must be 0, 2, 4, 6, 8 or 12");
+    REQUIRE(u == 0 || rows == 0 || (rows == 16 ? u != 6 : u != 12), "u = 6 needs rows 8, u = 12 rows 16");
+    gemv_set_plan(rows, u);
   });
 }
 

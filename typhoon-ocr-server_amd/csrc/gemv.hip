@@ -8,24 +8,20 @@
 //   W8A8 : y[n] = fma(fl(fl(acc) * ws[n]), xs, bias ? bias[n] : 0)
 //
 // Work decomposition (HBM-bound: 1 weight byte per 2 ops):
-//   * weights are 16x64 tiles (tl_common.h).  A work-group (4 waves) owns
-//     one 16-row group at a time; wave w streams the tiles of k-blocks
-//     [w*KB/4, (w+1)*KB/4) with one 16-byte load per lane per tile (1 KiB per
-//     wave-load, fully coalesced), two batches of U tiles in flight; the loop
-//     body is branch-free, tail tiles are read from a clamped address and
-//     masked;
-//   * lane l accumulates row (l & 15) over the k slice of its lane group
-//     (l >> 4) with v_dot4_i32_i8; the 16 partial sums of a row (4 lane
-//     groups x 4 waves) meet in LDS and are added in a fixed order.  Integer
-//     sums make every decomposition bit-identical to the sequential sum.
-//   * LOOP = false: one row group per work-group (NG work-groups).  Used for
-//     the decode shapes, which are latency-bound: everything a wave needs is
-//     issued in its first instructions (U is chosen so that the two batches
-//     hold all of the wave's tiles whenever that fits).
-//   * LOOP = true: a persistent grid walks the row groups (g += gridDim.x)
-//     and issues the first tiles of its next row group before reducing the
-//     current one, so the activation prologue runs once per work-group
-//     instead of once per row group (large N: the 151936-row lm_head).
+//   * weights are 16x64 tiles (tl_common.h).  A work-group (4 waves) owns RH
+//     rows (16, or 8 = half a tile's rows); wave w streams k-blocks
+//     [w*KB/4, (w+1)*KB/4) with one 16-byte load per lane per instruction
+//     (1 KiB per wave-load, whole 128-byte lines), two batches of U load
+//     instructions in flight; the loop body is branch-free, tail k-blocks are
+//     read from a clamped address and masked;
+//   * each lane accumulates one row over a 16-wide k sub-slice of a k-block
+//     with v_dot4_i32_i8; the partial sums of a row (lane slots x 4 waves)
+//     meet in LDS and are added in a fixed order.  Integer sums make every
+//     decomposition bit-identical to the sequential sum.
+//   * the decode shapes are latency-bound: U is chosen so that both batches
+//     hold all of a wave's loads whenever that fits, so every weight load is
+//     issued in the wave's first instructions; 8-row work-groups put every CU
+//     to work when N has fewer than 256 tile rows.
 //
 // Fused activation quantization (XV > 0): every work-group first issues the
 // loads of x (XV float4 per thread) and of its first two batches of weight
@@ -109,59 +105,121 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, int n, int acc,
   }
 }
 
-// acc += dot(tile, codes) for U tiles starting at wave-local tile index t0;
-// tiles at or beyond n_t were loaded from a clamped address and are dropped.
-template <int XV, int U>
+// Four int8 codes of fl(v * inv) rounded to nearest even, packed: adding
+// 1.5 * 2^23 leaves rint(p) in the low mantissa bits of the (exact for
+// |p| < 2^22) sum, so the low byte of the sum's bits is the two's-complement
+// code; v_perm_b32 gathers the four low bytes.  Valid when inv is finite and
+// every |v| <= absmax (then |p| <= 127 (1 + 2^-22)).
+__device__ __forceinline__ uint32_t codes4_rne(float4 v, float inv) {
+  const float M = 12582912.0f;
+  const uint32_t a = __float_as_uint(__fadd_rn(__fmul_rn(v.x, inv), M));
+  const uint32_t b = __float_as_uint(__fadd_rn(__fmul_rn(v.y, inv), M));
+  const uint32_t c = __float_as_uint(__fadd_rn(__fmul_rn(v.z, inv), M));
+  const uint32_t d = __float_as_uint(__fadd_rn(__fmul_rn(v.w, inv), M));
+  const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);   // a.b0, b.b0, 0, 0
+  const uint32_t hi = __builtin_amdgcn_perm(d, c, 0x04000c0cu);   // 0, 0, c.b0, d.b0
+  return lo | hi;
+}
+
+// Per-lane view of the weight stream.  RH rows per work-group:
+//   RH == 16: one 16x64 tile per load instruction, lane l = tile lane l;
+//   RH == 8 : rows 8h..8h+7 of two consecutive k-blocks per load instruction
+//             (lanes 0-31: k-block kb, lanes 32-63: kb + 1); within a k-block
+//             lane j reads tile lane 16 (j >> 3 & 3) + 8h + (j & 7), so each 8
+//             consecutive lanes read one 128-byte line.
+template <int RH>
+struct WStream {
+  static constexpr int KPI = 16 / RH;   // k-blocks per load instruction
+  const uint4* base;                    // tile lane of this lane in k-block 0
+  size_t tstride;                       // uint4 between consecutive k-blocks
+  int kb0, kb1, kbmax, sub;
+  __device__ __forceinline__ int kb_of(int i) const { return kb0 + i * KPI + sub; }
+  __device__ __forceinline__ int kb_clamped(int i) const { return min(kb_of(i), kbmax); }
+};
+
+// acc += dot(tiles, codes) for U load instructions starting at i0; k-blocks at
+// or beyond kb1 were loaded from a clamped address and are dropped.
+template <int XV, int U, int RH>
 __device__ __forceinline__ int consume_batch(const uint4 (&b)[U], const uint4 (&c)[XV == 0 ? U : 1],
-                                             const uint4* s_codes, int kb0, int t0, int tmax, int n_t,
-                                             int lg, int acc) {
+                                             const uint4* s_codes, const WStream<RH>& ws, int i0, int lg,
+                                             int acc) {
   uint4 cv[U];
 #pragma unroll
   for (int u = 0; u < U; u++) {
-    if constexpr (XV > 0) cv[u] = s_codes[(kb0 + min(t0 + u, tmax)) * 4 + lg];
+    if constexpr (XV > 0) cv[u] = s_codes[ws.kb_clamped(i0 + u) * 4 + lg];
     else cv[u] = c[u];
   }
 #pragma unroll
   for (int u = 0; u < U; u++) {
     const int d = dot16(b[u], cv[u], 0);
-    acc += (t0 + u < n_t) ? d : 0;
+    acc += (ws.kb_of(i0 + u) < ws.kb1) ? d : 0;
   }
   return acc;
 }
 
-template <int XV, int U>
-__device__ __forceinline__ void load_batch(uint4 (&b)[U], uint4 (&c)[XV == 0 ? U : 1], const uint4* wp,
-                                           size_t tstride, const uint4* cg, int kb0, int t0, int tmax,
-                                           int lg) {
+template <int XV, int U, int RH>
+__device__ __forceinline__ void load_batch(uint4 (&b)[U], uint4 (&c)[XV == 0 ? U : 1], const WStream<RH>& ws,
+                                           const uint4* cg, int i0, int lg) {
 #pragma unroll
   for (int u = 0; u < U; u++) {
-    const int t = min(t0 + u, tmax);
-    b[u] = wp[(size_t)t * tstride];
-    if constexpr (XV == 0) c[u] = cg[(kb0 + t) * 4 + lg];
+    const int kb = ws.kb_clamped(i0 + u);
+    b[u] = ws.base[(size_t)kb * ws.tstride];
+    if constexpr (XV == 0) c[u] = cg[kb * 4 + lg];
   }
   // keep the batch issued here, ahead of the consumption that follows
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int XV, int U, bool LOOP>
-__global__ __launch_bounds__(256) void gemv_i8_kernel(GemvArgs a) {
+// Arguments are scalars so that the leading ones (through `flags`) are
+// preloaded into SGPRs at wave launch (kernarg preload, -amdgpu-kernarg-
+// preload-count in the build): the first loads need no kernarg fetch.
+// flags: bits 0-1 x_vec, bits 2-3 epilogue, bit 4 bias present.
+template <int XV, int U, int RH>
+__global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint8_t* wt, const float* ws,
+                                                      float* y, int N, int K, int NG, int KB, int flags,
+                                                      const uint8_t* xq, const float* xs_in, const float* bias,
+                                                      int32_t* acc_out, float* xs_out) {
+  constexpr int SL = 64 / RH;           // lanes per row within a wave
+  GemvArgs a;
+  a.x = x;
+  a.xq = xq;
+  a.xs_in = xs_in;
+  a.wt = wt;
+  a.ws = ws;
+  a.bias = (flags & 16) ? bias : nullptr;
+  a.y = y;
+  a.acc_out = acc_out;
+  a.xs_out = xs_out;
+  a.N = N;
+  a.K = K;
+  a.KB = KB;
+  a.NG = NG;
+  a.epi = (flags >> 2) & 3;
+  a.x_vec = flags & 3;
   __shared__ uint4 s_codes[XV > 0 ? XV * 64 : 1];
   __shared__ uint32_t s_mx[4];
   __shared__ float s_tail[4];
-  __shared__ int s_red[LOOP ? 2 : 1][16 * 16];
+  __shared__ int s_red[RH * 4 * SL];
 
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // k slice of this wave
-  const int lg = lane >> 4;
-  const int KB = a.KB, NG = a.NG;
-  const int kb0 = (wv * KB) >> 2;
-  const int n_t = ((wv + 1) * KB >> 2) - kb0;   // 0 for some waves when KB < 4
-  const int tmax = n_t > 0 ? n_t - 1 : 0;        // kb0 + tmax < KB always
-  const size_t tstride = (size_t)NG * 64;       // uint4 between consecutive k-blocks
-  const uint4* wbase = reinterpret_cast<const uint4*>(a.wt) + (size_t)kb0 * tstride + lane;
+  const int r = lane % RH;              // row of this lane within the work-group
+  const int slot = lane / RH;           // 0 .. SL-1
+  const int lg = slot & 3;              // 16-wide k sub-slice of the tile
+  const int row0 = blockIdx.x * RH;
+  WStream<RH> st;
+  {
+    const int g16 = row0 >> 4, h = (row0 >> 3) & 1;
+    const int lane_off = (RH == 16) ? lane : (lg * 16 + 8 * h + r);
+    st.kb0 = (wv * KB) >> 2;
+    st.kb1 = ((wv + 1) * KB) >> 2;
+    st.kbmax = st.kb1 > st.kb0 ? st.kb1 - 1 : st.kb0;   // < KB always
+    st.sub = slot >> 2;
+    st.tstride = (size_t)NG * 64;
+    st.base = reinterpret_cast<const uint4*>(wt) + (size_t)g16 * 64 + lane_off;
+  }
+  const int n_i = (st.kb1 - st.kb0 + WStream<RH>::KPI - 1) / WStream<RH>::KPI;
   const uint4* cg = reinterpret_cast<const uint4*>(a.xq);
-  int g = blockIdx.x;
-  const uint4* wp = wbase + (size_t)g * 64;
 
   uint4 b0[U], b1[U];
   uint4 c0[XV == 0 ? U : 1], c1[XV == 0 ? U : 1];
@@ -170,7 +228,6 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(GemvArgs a) {
   // never waits for weights
   float4 xv[XV > 0 ? XV : 1];
   if constexpr (XV > 0) {
-    const int K = a.K;
     if (a.x_vec == 2) {
 #pragma unroll
       for (int i = 0; i < XV; i++) xv[i] = *reinterpret_cast<const float4*>(a.x + 4 * (threadIdx.x + 256 * i));
@@ -187,17 +244,16 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(GemvArgs a) {
       }
     }
   }
-  load_batch<XV, U>(b0, c0, wp, tstride, cg, kb0, 0, tmax, lg);
-  load_batch<XV, U>(b1, c1, wp, tstride, cg, kb0, U, tmax, lg);
-  // epilogue operands of this work-group's first row group
-  const int r16 = lane & 15;
-  float wsv = a.ws[min(g * 16 + r16, a.N - 1)];
-  float bv = a.bias ? a.bias[min(g * 16 + r16, a.N - 1)] : 0.0f;
+  load_batch<XV, U, RH>(b0, c0, st, cg, 0, lg);
+  load_batch<XV, U, RH>(b1, c1, st, cg, U, lg);
+  // epilogue operands (lanes < RH use them)
+  const int nr = min(row0 + r, N - 1);
+  const float wsv = a.ws[nr];
+  const float bv = a.bias ? a.bias[nr] : 0.0f;
 
   float xs;
   if constexpr (XV > 0) {
     // ---- fused per-token activation quantization --------------------------
-    const int K = a.K;
     uint32_t* sc = reinterpret_cast<uint32_t*>(s_codes);
     if ((K & 15) == 0) {
       // every element is in the 16-aligned prefix: RNE codes; elements past
@@ -215,11 +271,18 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(GemvArgs a) {
       const uint32_t m = max(max(s_mx[0], s_mx[1]), max(s_mx[2], s_mx[3]));
       xs = quant_scale(__uint_as_float(m));
       const float inv = quant_inv(xs);
+      if (m < 0x7f800000u && (__float_as_uint(inv) & 0x7f800000u) != 0x7f800000u) {
+        // finite absmax and reciprocal (the usual case): |x * inv| <= 127.x
 #pragma unroll
-      for (int i = 0; i < XV; i++) {
-        const float4 v = xv[i];
-        sc[threadIdx.x + 256 * i] = pack4(code_rne(v.x * inv, false), code_rne(v.y * inv, false),
-                                          code_rne(v.z * inv, false), code_rne(v.w * inv, false));
+        for (int i = 0; i < XV; i++) sc[threadIdx.x + 256 * i] = codes4_rne(xv[i], inv);
+      } else {
+        // NaN / Inf in x, or a reciprocal that overflows
+#pragma unroll
+        for (int i = 0; i < XV; i++) {
+          const float4 v = xv[i];
+          sc[threadIdx.x + 256 * i] = pack4(code_rne(v.x * inv, false), code_rne(v.y * inv, false),
+                                            code_rne(v.z * inv, false), code_rne(v.w * inv, false));
+        }
       }
     } else {
       // K % 16 != 0: the last K % 16 elements are the reference's scalar tail
@@ -269,80 +332,68 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(GemvArgs a) {
     xs = a.xs_in ? *a.xs_in : 1.0f;
   }
 
-  int it = 0;
-  while (true) {
-    // ---- main loop: two batches of U tiles in flight -------------------------
-    // Both batches were issued before this point.  The loop body is
-    // straight-line code that enters and leaves with the 2U loads of b0 and
-    // b1 outstanding, so the compiler keeps the wait counts exact.
-    int acc = 0;
-    int t = 0;
-    for (; t + 2 * U < n_t; t += 2 * U) {
-      acc = consume_batch<XV, U>(b0, c0, s_codes, kb0, t, tmax, n_t, lg, acc);
-      load_batch<XV, U>(b0, c0, wp, tstride, cg, kb0, t + 2 * U, tmax, lg);
-      acc = consume_batch<XV, U>(b1, c1, s_codes, kb0, t + U, tmax, n_t, lg, acc);
-      load_batch<XV, U>(b1, c1, wp, tstride, cg, kb0, t + 3 * U, tmax, lg);
-    }
-    const int gcur = g;
-    const float wcur = wsv, bcur = bv;
-    if constexpr (LOOP) {
-      // the last double batch of this row group: the loads that follow go
-      // to the first tiles of the next one (clamped to a valid row group when
-      // there is none; those loads are never consumed)
-      g += gridDim.x;
-      const int gn = min(g, NG - 1);
-      wp = wbase + (size_t)gn * 64;
-      acc = consume_batch<XV, U>(b0, c0, s_codes, kb0, t, tmax, n_t, lg, acc);
-      load_batch<XV, U>(b0, c0, wp, tstride, cg, kb0, 0, tmax, lg);
-      acc = consume_batch<XV, U>(b1, c1, s_codes, kb0, t + U, tmax, n_t, lg, acc);
-      load_batch<XV, U>(b1, c1, wp, tstride, cg, kb0, U, tmax, lg);
-      wsv = a.ws[min(gn * 16 + r16, a.N - 1)];
-      bv = a.bias ? a.bias[min(gn * 16 + r16, a.N - 1)] : 0.0f;
-    } else {
-      acc = consume_batch<XV, U>(b0, c0, s_codes, kb0, t, tmax, n_t, lg, acc);
-      acc = consume_batch<XV, U>(b1, c1, s_codes, kb0, t + U, tmax, n_t, lg, acc);
-    }
+  // ---- main loop: two batches of U load instructions in flight --------------
+  // Both batches were issued before the prologue.  The loop body is
+  // straight-line code that enters and leaves with the 2U loads of b0 and b1
+  // outstanding, so the compiler keeps the wait counts exact.
+  int acc = 0;
+  int i = 0;
+  for (; i + 2 * U < n_i; i += 2 * U) {
+    acc = consume_batch<XV, U, RH>(b0, c0, s_codes, st, i, lg, acc);
+    load_batch<XV, U, RH>(b0, c0, st, cg, i + 2 * U, lg);
+    acc = consume_batch<XV, U, RH>(b1, c1, s_codes, st, i + U, lg, acc);
+    load_batch<XV, U, RH>(b1, c1, st, cg, i + 3 * U, lg);
+  }
+  acc = consume_batch<XV, U, RH>(b0, c0, s_codes, st, i, lg, acc);
+  acc = consume_batch<XV, U, RH>(b1, c1, s_codes, st, i + U, lg, acc);
 
-    // ---- reduction: row r's 16 partials (wave w, lane group q) at
-    //      s_red[r*16 + w*4 + q], summed in that order by wave 0 ------------
-    int* red = s_red[LOOP ? (it & 1) : 0];
-    red[r16 * 16 + wv * 4 + lg] = acc;
-    __syncthreads();
-    if (wv == 0 && lane < 16) {
-      const int4* p = reinterpret_cast<const int4*>(red + lane * 16);
-      const int4 q0 = p[0], q1 = p[1], q2 = p[2], q3 = p[3];
-      const int tot = ((q0.x + q0.y) + (q0.z + q0.w)) + ((q1.x + q1.y) + (q1.z + q1.w)) +
-                      ((q2.x + q2.y) + (q2.z + q2.w)) + ((q3.x + q3.y) + (q3.z + q3.w));
-      const int n = gcur * 16 + lane;
-      if (n < a.N) gemv_epilogue(a, n, tot, xs, wcur, bcur);
+  // ---- reduction: row r's 4*SL partials (wave w, lane slot q) at
+  //      s_red[r*4*SL + w*SL + q], summed in that order by wave 0 ------------
+  s_red[r * 4 * SL + wv * SL + slot] = acc;
+  __syncthreads();
+  if (wv == 0 && lane < RH) {
+    const int4* p = reinterpret_cast<const int4*>(s_red + lane * 4 * SL);
+    int tot = 0;
+#pragma unroll
+    for (int q = 0; q < SL; q++) {
+      const int4 v = p[q];
+      tot += (v.x + v.y) + (v.z + v.w);
     }
-    if constexpr (!LOOP) break;
-    if (g >= NG) break;
-    ++it;
+    const int n = row0 + lane;
+    if (n < a.N) gemv_epilogue(a, n, tot, xs, wsv, bv);
   }
 }
 
 // ---------------------------------------------------------------------------
 // launcher
 // ---------------------------------------------------------------------------
-template <int XV, int U, bool LOOP>
+template <int XV, int U, int RH>
 static void launch_one(const GemvArgs& a, int blocks, hipStream_t st) {
-  hipLaunchKernelGGL((gemv_i8_kernel<XV, U, LOOP>), dim3(blocks), dim3(256), 0, st, a);
+  const int flags = (a.x_vec & 3) | ((a.epi & 3) << 2) | (a.bias ? 16 : 0);
+  hipLaunchKernelGGL((gemv_i8_kernel<XV, U, RH>), dim3(blocks), dim3(256), 0, st, a.x, a.wt, a.ws, a.y,
+                     a.N, a.K, a.NG, a.KB, flags, a.xq, a.xs_in, a.bias, a.acc_out, a.xs_out);
 }
 
 template <int XV>
 static hipError_t launch_xv(const GemvArgs& a, const GemvPlan& p, hipStream_t st) {
-  if (p.loop) {
-    if (p.u != 4) return hipErrorInvalidValue;
-    launch_one<XV, 4, true>(a, p.blocks, st);
-  } else {
+  if (p.rows == 16) {
     switch (p.u) {
-      case 2: launch_one<XV, 2, false>(a, p.blocks, st); break;
-      case 4: launch_one<XV, 4, false>(a, p.blocks, st); break;
-      case 8: launch_one<XV, 8, false>(a, p.blocks, st); break;
-      case 12: launch_one<XV, 12, false>(a, p.blocks, st); break;
+      case 2: launch_one<XV, 2, 16>(a, p.blocks, st); break;
+      case 4: launch_one<XV, 4, 16>(a, p.blocks, st); break;
+      case 8: launch_one<XV, 8, 16>(a, p.blocks, st); break;
+      case 12: launch_one<XV, 12, 16>(a, p.blocks, st); break;
       default: return hipErrorInvalidValue;
     }
+  } else if (p.rows == 8) {
+    switch (p.u) {
+      case 2: launch_one<XV, 2, 8>(a, p.blocks, st); break;
+      case 4: launch_one<XV, 4, 8>(a, p.blocks, st); break;
+      case 6: launch_one<XV, 6, 8>(a, p.blocks, st); break;
+      case 8: launch_one<XV, 8, 8>(a, p.blocks, st); break;
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
@@ -359,43 +410,42 @@ int gemv_fused_xv(int K) {
   return 0;
 }
 
-static int g_force_mode = 0, g_force_grid = 0, g_force_u = 0;
+static int g_force_rows = 0, g_force_u = 0;
 
-void gemv_set_plan(int mode, int grid, int u) {
-  g_force_mode = mode;
-  g_force_grid = grid;
+void gemv_set_plan(int rows, int u) {
+  g_force_rows = rows;
   g_force_u = u;
 }
 
-// Persistent grid: work-groups resident per CU x 256 CUs.
-static constexpr int kLoopWgPerCu = 4;
-static constexpr int kNumCu = 256;
+// batch depths built for each row mode
+static bool u_ok(int rows, int u) {
+  return rows == 16 ? (u == 2 || u == 4 || u == 8 || u == 12) : (u == 2 || u == 4 || u == 6 || u == 8);
+}
 
 // Measured on MI355X (graph-replayed launches over > 512 MB of rotating
-// weights).  Decode shapes (NG <= 768) are latency-bound: one row group per
-// work-group, with both batches holding all of a wave's tiles when that is at
-// most 24 (K <= 6144), so every weight load is issued before the activation
-// prologue.  Large N (the lm_head) streams on a persistent grid.
+// weights).  The decode shapes are latency-bound and limited by the memory
+// requests a CU can keep in flight, so every CU should stream: with fewer
+// than 256 sixteen-row groups (N < 4096) a work-group takes 8 rows, which
+// doubles the work-groups at the same bytes per wave.  U is the smallest
+// depth whose two batches hold all of a wave's load instructions, so every
+// weight load is issued before the activation prologue; longer K loops over
+// batches of 8.
 GemvPlan gemv_plan(int N, int K) {
   GemvPlan p;
   const int NG = cdiv(N, 16);
   const int KB = cdiv(K, 64);
-  const int n_t = cdiv(KB, 4);
-  p.loop = NG > 4 * kNumCu * kLoopWgPerCu;
-  if (g_force_mode == 1) p.loop = false;
-  if (g_force_mode == 2) p.loop = true;
-  if (p.loop) {
-    p.u = 4;
-    p.blocks = std::min(NG, g_force_grid > 0 ? g_force_grid : kNumCu * kLoopWgPerCu);
-  } else {
-    p.blocks = NG;
-    if (n_t <= 4) p.u = 2;
-    else if (n_t <= 8) p.u = 4;
-    else if (n_t <= 16) p.u = 8;
-    else if (n_t <= 24) p.u = 12;
-    else p.u = 8;
-    if (g_force_u > 0) p.u = g_force_u;
-  }
+  p.rows = NG < 256 ? 8 : 16;
+  if (g_force_rows == 8 || g_force_rows == 16) p.rows = g_force_rows;
+  p.blocks = cdiv(N, p.rows);
+  const int n_kb = cdiv(KB, 4);
+  const int n_i = p.rows == 16 ? n_kb : cdiv(n_kb, 2);
+  p.u = 8;
+  for (int u : {2, 4, 6, 8, 12})
+    if (u_ok(p.rows, u) && 2 * u >= n_i) {
+      p.u = u;
+      break;
+    }
+  if (g_force_u > 0 && u_ok(p.rows, g_force_u)) p.u = g_force_u;
   return p;
 }
 

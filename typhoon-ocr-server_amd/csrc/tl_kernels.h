@@ -26,7 +26,7 @@ hipError_t launch_pack_tiles(const int8_t* w, int rows, int cols, uint8_t* tiles
 
 // ---- M=1 GEMV (gemv.hip) --------------------------------------------------
 struct GemvPlan {
-  bool loop = false;   // persistent grid walking the row groups
+  int rows = 16;       // rows per work-group (16 or 8)
   int blocks = 0, u = 4;
 };
 struct GemvLaunch {
@@ -44,10 +44,9 @@ struct GemvLaunch {
 GemvPlan gemv_plan(int N, int K);
 int gemv_fused_xv(int K);
 hipError_t launch_gemv_i8(const GemvLaunch& L, hipStream_t st);
-// process-wide override of the GEMV plan for tuning: mode 0 = planner,
-// 1 = one row group per work-group, 2 = persistent grid; grid = persistent
-// work-groups (0 = planner); u = tiles per load batch (0 = planner)
-void gemv_set_plan(int mode, int grid, int u);
+// process-wide override of the GEMV plan for tuning: rows per work-group
+// (16 or 8) and load instructions per batch (0 = planner's choice)
+void gemv_set_plan(int rows, int u);
 
 // ---- MFMA GEMM (gemm.hip) -------------------------------------------------
 struct GemmPlan {
