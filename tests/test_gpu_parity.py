@@ -31,6 +31,13 @@ def make(rng, M, N, K):
     return x, w, s
 
 
+def exact_epilogue(acc, ws, xs):
+    """fl(fl(fl(acc) * ws[n]) * xs[m]) in float32 (numpy rounds every
+    float32 product to nearest even)."""
+    a = np.asarray(acc).astype(F)
+    return (a * ws[None, :].astype(F)).astype(F) * xs[:, None].astype(F)
+
+
 def bf16_bits(x):
     u = np.ascontiguousarray(x, F).view(np.uint32).astype(np.uint64)
     return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
@@ -301,6 +308,9 @@ def test_w8a8_gemm(lin, orc, dev, M, N, K):
     lin.w8a8_linear_f32_dev(torch.from_numpy(x).to(dev), W, y)
     torch.cuda.synchronize()
     assert rel_l2(y.cpu().numpy(), orc.w8a8_linear(xq, xs, w, s)) <= 1e-5
+    # and bit-exact against the exact-integer epilogue fl(fl(fl(acc) * ws) * xs):
+    # pins the codes the GPU quantizer wrote into the tiles
+    np.testing.assert_array_equal(y.cpu().numpy(), exact_epilogue(orc.int_acc(xq, w), s, xs))
     W.close()
 
 
@@ -329,6 +339,7 @@ def test_w8a8_prefill_full_size(lin, orc, dev):
     sub = np.r_[0:4, 500:504, 1020:1024]
     want = orc.w8a8_linear(np.ascontiguousarray(xq[sub]), xs[sub], w, s)
     assert rel_l2(y.cpu().numpy()[sub], want) <= 1e-5
+    np.testing.assert_array_equal(y.cpu().numpy(), exact_epilogue(acc.cpu().numpy(), s, xs))
     W.close()
 
 

@@ -51,46 +51,6 @@ struct GemvArgs {
   int x_vec;           // 2: K == 1024*XV and x 16-byte aligned (unguarded loads)
 };
 
-// DPP row operations (gfx9 encodings): quad permutations, mirrors
-enum : int { DPP_QP_1032 = 0xB1, DPP_QP_2301 = 0x4E, DPP_ROW_HALF_MIRROR = 0x141, DPP_ROW_MIRROR = 0x140 };
-
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
-}
-
-// wave-wide unsigned max, returned wave-uniform: max within each row of 16
-// lanes through DPP, then the 4 row results through readlane
-__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
-  uint32_t t;
-  t = dpp_u32<DPP_QP_1032>(v);         v = v > t ? v : t;
-  t = dpp_u32<DPP_QP_2301>(v);         v = v > t ? v : t;
-  t = dpp_u32<DPP_ROW_HALF_MIRROR>(v); v = v > t ? v : t;
-  t = dpp_u32<DPP_ROW_MIRROR>(v);      v = v > t ? v : t;
-  uint32_t m = __builtin_amdgcn_readlane(v, 0);
-  uint32_t r1 = __builtin_amdgcn_readlane(v, 16), r2 = __builtin_amdgcn_readlane(v, 32),
-           r3 = __builtin_amdgcn_readlane(v, 48);
-  m = m > r1 ? m : r1;
-  m = m > r2 ? m : r2;
-  return m > r3 ? m : r3;
-}
-
-// max ignoring NaN (the tail scan), for non-negative inputs
-__device__ __forceinline__ float wave_fmax_nonnan(float v) {
-  float t;
-  t = __uint_as_float(dpp_u32<DPP_QP_1032>(__float_as_uint(v)));         v = (t > v) ? t : v;
-  t = __uint_as_float(dpp_u32<DPP_QP_2301>(__float_as_uint(v)));         v = (t > v) ? t : v;
-  t = __uint_as_float(dpp_u32<DPP_ROW_HALF_MIRROR>(__float_as_uint(v))); v = (t > v) ? t : v;
-  t = __uint_as_float(dpp_u32<DPP_ROW_MIRROR>(__float_as_uint(v)));      v = (t > v) ? t : v;
-  float m = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
-#pragma unroll
-  for (int r = 16; r < 64; r += 16) {
-    const float o = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), r));
-    m = (o > m) ? o : m;
-  }
-  return m;
-}
-
 __device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, int n, int acc, float xs,
                                               float wsv, float bv) {
   if (a.epi == EPI_ACC) {
@@ -103,22 +63,6 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, int n, int acc,
     const float t = __fmul_rn((float)acc, wsv);
     a.y[n] = __fmaf_rn(t, xs, bv);
   }
-}
-
-// Four int8 codes of fl(v * inv) rounded to nearest even, packed: adding
-// 1.5 * 2^23 leaves rint(p) in the low mantissa bits of the (exact for
-// |p| < 2^22) sum, so the low byte of the sum's bits is the two's-complement
-// code; v_perm_b32 gathers the four low bytes.  Valid when inv is finite and
-// every |v| <= absmax (then |p| <= 127 (1 + 2^-22)).
-__device__ __forceinline__ uint32_t codes4_rne(float4 v, float inv) {
-  const float M = 12582912.0f;
-  const uint32_t a = __float_as_uint(__fadd_rn(__fmul_rn(v.x, inv), M));
-  const uint32_t b = __float_as_uint(__fadd_rn(__fmul_rn(v.y, inv), M));
-  const uint32_t c = __float_as_uint(__fadd_rn(__fmul_rn(v.z, inv), M));
-  const uint32_t d = __float_as_uint(__fadd_rn(__fmul_rn(v.w, inv), M));
-  const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);   // a.b0, b.b0, 0, 0
-  const uint32_t hi = __builtin_amdgcn_perm(d, c, 0x04000c0cu);   // 0, 0, c.b0, d.b0
-  return lo | hi;
 }
 
 // Per-lane view of the weight stream.  RH rows per work-group:

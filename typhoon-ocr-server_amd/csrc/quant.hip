@@ -166,6 +166,48 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(const float* _
   }
 }
 
+// One wave per row, 4 rows per work-group, for rows of cols == 256 NV floats
+// (16-byte aligned): lane l loads float4 l + 64 j (every load instruction
+// reads 1 KiB contiguous), the absmax is reduced with DPP, and each lane
+// writes the 4 codes of each of its float4 as one dword at its place in the
+// 16x64 tile layout (4 consecutive lanes fill one 16-byte tile lane).
+template <int NV>
+__global__ __launch_bounds__(256) void quantize_rows_tiled_vec_kernel(const float* __restrict__ src, int rows,
+                                                                      int cols, int MG,
+                                                                      uint8_t* __restrict__ tiles,
+                                                                      float* __restrict__ scales, int clamp127) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float4* row = reinterpret_cast<const float4*>(src + (size_t)r * cols);
+  float4 v[NV];
+#pragma unroll
+  for (int j = 0; j < NV; j++) v[j] = row[lane + 64 * j];
+  uint32_t mx = 0;
+#pragma unroll
+  for (int j = 0; j < NV; j++)
+    mx = max(mx, max(max(abs_bits(v[j].x), abs_bits(v[j].y)), max(abs_bits(v[j].z), abs_bits(v[j].w))));
+  mx = wave_umax(mx);
+  const float scale = quant_scale(__uint_as_float(mx));
+  const float inv = quant_inv(scale);
+  if (lane == 0) scales[r] = scale;
+  const bool fast = mx < 0x7f800000u && (__float_as_uint(inv) & 0x7f800000u) != 0x7f800000u;
+  const bool c127 = clamp127 != 0;
+  uint32_t* t32 = reinterpret_cast<uint32_t*>(tiles) + ((size_t)(r >> 4) * 64 + (r & 15)) * 4;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int f = lane + 64 * j;          // float4 index: k = 4f .. 4f+3
+    // finite absmax and reciprocal: |x * inv| <= 127 (1 + 2^-22), so the
+    // codes lie in [-127, 127] and the weight clamp changes nothing
+    const uint32_t code = fast ? codes4_rne(v[j], inv)
+                               : pack4(code_rne(v[j].x * inv, c127), code_rne(v[j].y * inv, c127),
+                                       code_rne(v[j].z * inv, c127), code_rne(v[j].w * inv, c127));
+    // chunk c = f >> 2 (16 k): tile kb = f >> 4, lane group (f >> 2) & 3,
+    // dword f & 3 of that tile lane
+    t32[((size_t)(f >> 4) * MG) * 256 + ((f >> 2) & 3) * 64 + (f & 3)] = code;
+  }
+}
+
 // one thread per (tile, lane): 16 bytes of W[16g + (l&15)][64kb + 16(l>>4) ..]
 __global__ __launch_bounds__(256) void pack_tiles_kernel(const int8_t* __restrict__ w, int rows,
                                                          int cols, int KB, long long total,
@@ -215,15 +257,15 @@ hipError_t launch_quantize_rows_tiled(const float* src, int rows, int cols, uint
   const dim3 grid(cdiv(rows, 4)), block(256);
   const int c = clamp127 ? 1 : 0;
   const bool aligned = (((uintptr_t)src) & 15) == 0;
-  // the register-resident path needs cols == 1024 * CH (then K % 16 == 0, no tail)
+  const int MG = cdiv(rows, 16);
   if (aligned && cols == 2048)
-    hipLaunchKernelGGL(quantize_rows_tiled_kernel<2>, grid, block, 0, st, src, rows, cols, KB, tiles, scales, c);
+    hipLaunchKernelGGL(quantize_rows_tiled_vec_kernel<8>, grid, block, 0, st, src, rows, cols, MG, tiles, scales, c);
   else if (aligned && cols == 6144)
-    hipLaunchKernelGGL(quantize_rows_tiled_kernel<6>, grid, block, 0, st, src, rows, cols, KB, tiles, scales, c);
+    hipLaunchKernelGGL(quantize_rows_tiled_vec_kernel<24>, grid, block, 0, st, src, rows, cols, MG, tiles, scales, c);
   else if (aligned && cols == 1024)
-    hipLaunchKernelGGL(quantize_rows_tiled_kernel<1>, grid, block, 0, st, src, rows, cols, KB, tiles, scales, c);
+    hipLaunchKernelGGL(quantize_rows_tiled_vec_kernel<4>, grid, block, 0, st, src, rows, cols, MG, tiles, scales, c);
   else if (aligned && cols == 4096)
-    hipLaunchKernelGGL(quantize_rows_tiled_kernel<4>, grid, block, 0, st, src, rows, cols, KB, tiles, scales, c);
+    hipLaunchKernelGGL(quantize_rows_tiled_vec_kernel<16>, grid, block, 0, st, src, rows, cols, MG, tiles, scales, c);
   else
     hipLaunchKernelGGL(quantize_rows_tiled_kernel<0>, grid, block, 0, st, src, rows, cols, KB, tiles, scales, c);
   return hipGetLastError();
