@@ -44,12 +44,8 @@ struct GemmI8Args {
 // copied global -> LDS by one wave with one global_load_lds_dwordx4 (lane l
 // writes bytes 16l..16l+15 of the tile, i.e. the tile layout itself).  Stage s
 // lives in buffer s % NST; the ring is unrolled so every buffer is a distinct
-// LDS object and the compiler keeps only the explicit waits below:
-//   wait until this wave's copies of stage s landed (vmcnt <= later stages),
-//   wait until this wave's LDS reads of stage s-1 finished (lgkmcnt 0),
-//   barrier (stage s visible to all waves, buffer of stage s-1 free),
-//   issue the copies of stage s+NST-1 into the freed buffer,
-//   MFMAs of stage s.
+// LDS object and the compiler keeps only the explicit waits in `step`.  The
+// MFMA fragments of a stage are read from LDS one step before its MFMAs run.
 template <int MT, int NT, int KT, int NST, int WM, int WN>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds_kernel(GemmI8Args a) {
   constexpr int NW = WM * WN;
@@ -58,8 +54,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds_kernel(GemmI8Args a)
   constexpr int PW = TS / NW;                              // tiles copied per wave per stage
   constexpr int FM = MT / WM, FN = NT / WN;                // 16x16 accumulators per wave
   static_assert(MT % WM == 0 && NT % WN == 0, "wave grid must divide the tile");
-  static_assert(NST >= 2 && NST <= 8, "2..8 stage buffers");
-  static_assert(PW * (NST - 2) < 64, "vmcnt range");
+  static_assert(NST >= 2 && NST <= 8 && NST % 2 == 0, "2, 4, 6 or 8 stage buffers");
+  static_assert(KT == 1, "one k-block per stage");
+  static_assert(PW * (NST - 1) < 64, "vmcnt range");
 
   // one distinct LDS object per ring slot (unused slots are 16 bytes)
   __shared__ uint4 s0[TS * 64];
@@ -112,20 +109,24 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds_kernel(GemmI8Args a)
       qstride[p] = (size_t)KT * a.NG * 64;
     }
   }
+  // copy p (of PW) of stage st into ring buffer buf; stages past the end of K
+  // copy the zero tile, so every step issues exactly PW copies and the
+  // explicit wait counts stay exact
+  auto copy = [&](int st, uint32_t base, int p) {
+    const uint4* g = (st * KT + qk[p] < KB) ? qsrc[p] + (size_t)st * qstride[p] : Z4;
+    dma_tile(g, base + qlds[p]);
+  };
   auto issue = [&](int st, uint4* buf) {
-    if (st >= nst) return;            // fewer copies only makes later waits stricter
     const uint32_t base = lds_addr(buf);
 #pragma unroll
-    for (int p = 0; p < PW; p++) {
-      const uint4* g = (st * KT + qk[p] < KB) ? qsrc[p] + (size_t)st * qstride[p] : Z4;
-      dma_tile(g, base + qlds[p]);
-    }
+    for (int p = 0; p < PW; p++) copy(st, base, p);
   };
 
   // Accumulator tile (i, j) is computed transposed (B fragment as the MFMA's
   // first operand): lane l holds Y[m][n .. n+3] with m = 16 mg + (l & 15) and
   // n = 16 ng + 4 (l >> 4), so the epilogue stores 16 contiguous bytes per lane.
-  // Its operands are loaded now so their latency hides behind the K loop.
+  // Its operands are loaded first: they are older than every tile copy, so
+  // the first copy wait below also covers them.
   const int mrow = lane & 15;
   const int ncol = (lane >> 4) * 4;
   float4 e_ws[FN], e_b[FN];
@@ -148,7 +149,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds_kernel(GemmI8Args a)
     const int m = min((mg0 + wm * FM + i) * 16 + mrow, a.M - 1);
     e_xs[i] = (a.out == OUT_I32) ? 0.0f : a.xs[m];
   }
-  wait_vm<0>();   // the explicit waits below count only the tile copies
 
   v4i acc[FM][FN];
 #pragma unroll
@@ -156,49 +156,65 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds_kernel(GemmI8Args a)
 #pragma unroll
     for (int j = 0; j < FN; j++) acc[i][j] = v4i{0, 0, 0, 0};
 
-  // MFMAs of one stage; the fragments of k-block kk+1 are read from LDS while
-  // the MFMAs of k-block kk run
-  auto compute = [&](const uint4* buf) {
-    uint4 fa[2][FM], fb[2][FN];
+  // Fragments of a stage are read one step ahead of their MFMAs (two
+  // register sets), so LDS latency hides behind the previous stage's MFMAs.
+  uint4 fa[2][FM], fb[2][FN];
+  auto read_frags = [&](const uint4* buf, int c) {
 #pragma unroll
-    for (int i = 0; i < FM; i++) fa[0][i] = buf[((wm * FM + i) * KT) * 64 + lane];
+    for (int i = 0; i < FM; i++) fa[c][i] = buf[(wm * FM + i) * 64 + lane];
 #pragma unroll
-    for (int j = 0; j < FN; j++) fb[0][j] = buf[(TA + (wn * FN + j) * KT) * 64 + lane];
-#pragma unroll
-    for (int kk = 0; kk < KT; kk++) {
-      const int c = kk & 1;
-      if (kk + 1 < KT) {
-#pragma unroll
-        for (int i = 0; i < FM; i++) fa[c ^ 1][i] = buf[((wm * FM + i) * KT + kk + 1) * 64 + lane];
-#pragma unroll
-        for (int j = 0; j < FN; j++) fb[c ^ 1][j] = buf[(TA + (wn * FN + j) * KT + kk + 1) * 64 + lane];
-      }
-#pragma unroll
-      for (int i = 0; i < FM; i++)
-#pragma unroll
-        for (int j = 0; j < FN; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, fb[c][j]),
-                                                            __builtin_bit_cast(v4i, fa[c][i]), acc[i][j], 0, 0, 0);
-    }
+    for (int j = 0; j < FN; j++) fb[c][j] = buf[(TA + wn * FN + j) * 64 + lane];
   };
 
-  // one ring step: stage st is in `cur`; stage st+NST-1 goes into `nxt`
-  auto step = [&](int st, const uint4* cur, uint4* nxt) {
+
+  // Step s: stage s's fragments are in registers (set s & 1).
+  //   wait until this wave's copies of stage s+1 landed (later stages may
+  //   still be in flight), and until its reads of stage s completed;
+  //   barrier: stage s+1 is visible, every wave is done reading stage s;
+  //   MFMAs of stage s, with the reads of stage s+1's fragments and the
+  //   copies of stage s+NST (into stage s's buffer) interleaved one after
+  //   each MFMA, so LDS, copy and matrix pipes work at the same time.
+  auto step = [&](int st, uint4* cur, const uint4* nxt, int c) {
     wait_vm<PW * (NST - 2)>();
     wait_lgkm0();
     stage_barrier();
-    issue(st + NST - 1, nxt);
-    if (st < nst) compute(cur);
+    const uint32_t cbase = lds_addr(cur);
+    constexpr int NMEM = FM + FN + PW;
+    auto mem_op = [&](int q) {
+      if (q < FM) fa[c ^ 1][q] = nxt[(wm * FM + q) * 64 + lane];
+      else if (q < FM + FN) fb[c ^ 1][q - FM] = nxt[(TA + wn * FN + q - FM) * 64 + lane];
+      else copy(st + NST, cbase, q - FM - FN);
+    };
+    // (steps past the last stage multiply fragments of zero-tile stages and
+    // add nothing)
+#pragma unroll
+    for (int m = 0; m < FM * FN; m++) {
+      {
+        const int i = m / FN, j = m % FN;
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, fb[c][j]),
+                                                          __builtin_bit_cast(v4i, fa[c][i]), acc[i][j], 0, 0, 0);
+      }
+      // keep the source order: one MFMA, then one memory operation
+      __builtin_amdgcn_sched_barrier(0);
+      if (m < NMEM) mem_op(m);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int q = FM * FN; q < NMEM; q++) mem_op(q);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
-  // prologue: stages 0 .. NST-2 in flight
+  // prologue: stages 0 .. NST-1 in flight, stage 0's fragments read
 #pragma unroll
-  for (int b = 0; b < NST - 1; b++) issue(b, ring[b]);
-  // ring unrolled NST times: every buffer index below is a compile-time
-  // constant, so each access names one LDS object
+  for (int b = 0; b < NST; b++) issue(b, ring[b]);
+  wait_vm<PW * (NST - 1)>();
+  stage_barrier();
+  read_frags(ring[0], 0);
+  // ring unrolled NST times (NST even, so the fragment set of every step is
+  // a compile-time constant too)
   for (int st = 0; st < nst; st += NST) {
 #pragma unroll
-    for (int b = 0; b < NST; b++) step(st + b, ring[b], ring[(b + NST - 1) % NST]);
+    for (int b = 0; b < NST; b++) step(st + b, ring[b], ring[(b + 1) % NST], b & 1);
   }
 
   wait_vm<0>();   // no copy may still be landing in LDS when the work-group exits
