@@ -260,6 +260,21 @@ def test_w8a32_batch_fp32(lin, orc, M, N, K):
     assert rel_l2(lin.w8a32_linear(x, w, s, bias=b), orc.w8a32_linear(x, w, s, bias=b)) <= 1e-5
 
 
+@pytest.mark.parametrize("M,N,K", [(3, 32776, 200), (8, 40000, 2048), (16, 33000, 130)])
+def test_small_m_wide_n(lin, orc, M, N, K):
+    """M <= 16 token rows over N >= 32768 outputs (the lm_head's regime, where
+    a work-group covers several 16-row groups): W8A32 fp32 within 1e-5,
+    W8A16 fp32 out within 1e-5, W8A8 exact accumulator epilogue."""
+    say(f"small-M wide-N M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 7 + N + K)
+    x, w, s = make(rng, M, N, K)
+    assert rel_l2(lin.w8a32_linear(x, w, s), orc.w8a32_linear(x, w, s)) <= 1e-5
+    xb = bf16_bits(x)
+    assert rel_l2(lin.w8a16_linear(xb, w, s), orc.w8a16_linear(xb, w, s)) <= 1e-5
+    xq, xs = orc.quantize_rows(x)
+    assert rel_l2(lin.w8a8_linear(xq, xs, w, s), orc.w8a8_linear(xq, xs, w, s)) <= 1e-5
+
+
 def test_w8a32_prefill_rows_consistent(lin, orc):
     """1200-token prefill (fused QKV shape): rows are independent, so a
     subset computed alone matches the corresponding rows of the full call."""

@@ -92,8 +92,36 @@ __device__ inline void widen_f16(uint4 w, uint4& h0, uint4& h1) {
 template <int AMODE>
 using acc_small_t = typename std::conditional<AMODE == A_I8, v4i, v4f>::type;
 
+// MFMA operands of one activation fragment (for fp32 activations: the
+// three bf16 terms of each K half)
 template <int AMODE>
-__device__ inline acc_small_t<AMODE> mma(uint4 w, const AFrag<AMODE>& x, acc_small_t<AMODE> c) {
+struct XOps {
+  // A_I8: 1 operand; 16-bit: 2 (K halves); fp32: 6 (3 terms x 2 K halves)
+  static constexpr int NX = AMODE == A_I8 ? 1 : (AMODE == A_F32X3 ? 6 : 2);
+  uint4 v[NX];
+};
+
+template <int AMODE>
+__device__ inline XOps<AMODE> prepare_x(const AFrag<AMODE>& x) {
+  XOps<AMODE> o;
+  if constexpr (AMODE == A_F32X3) {
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+      const uint4 u0 = x.v[2 * hh], u1 = x.v[2 * hh + 1];
+      const float f[8] = {__uint_as_float(u0.x), __uint_as_float(u0.y), __uint_as_float(u0.z), __uint_as_float(u0.w),
+                          __uint_as_float(u1.x), __uint_as_float(u1.y), __uint_as_float(u1.z), __uint_as_float(u1.w)};
+      split3x8(f, o.v[3 * hh], o.v[3 * hh + 1], o.v[3 * hh + 2]);
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < XOps<AMODE>::NX; q++) o.v[q] = x.v[q];
+  }
+  return o;
+}
+
+// the weights of one row group against a prepared activation fragment
+template <int AMODE>
+__device__ inline acc_small_t<AMODE> mma_x(uint4 w, const XOps<AMODE>& x, acc_small_t<AMODE> c) {
   if constexpr (AMODE == A_I8) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, w), __builtin_bit_cast(v4i, x.v[0]), c, 0, 0, 0);
   } else if constexpr (AMODE == A_BF16) {
@@ -109,48 +137,54 @@ __device__ inline acc_small_t<AMODE> mma(uint4 w, const AFrag<AMODE>& x, acc_sma
   } else {
     uint4 h[2];
     widen_bf16(w, h[0], h[1]);
+    // smallest term first: the three products of a K half are added to the
+    // fp32 accumulator in increasing magnitude
 #pragma unroll
     for (int hh = 0; hh < 2; hh++) {
-      const uint4 u0 = x.v[2 * hh], u1 = x.v[2 * hh + 1];
-      const float f[8] = {__uint_as_float(u0.x), __uint_as_float(u0.y), __uint_as_float(u0.z), __uint_as_float(u0.w),
-                          __uint_as_float(u1.x), __uint_as_float(u1.y), __uint_as_float(u1.z), __uint_as_float(u1.w)};
-      uint4 t0, t1, t2;
-      split3x8(f, t0, t1, t2);
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h[hh]), __builtin_bit_cast(v8bf, t2), c, 0, 0, 0);
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h[hh]), __builtin_bit_cast(v8bf, t1), c, 0, 0, 0);
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h[hh]), __builtin_bit_cast(v8bf, t0), c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h[hh]), __builtin_bit_cast(v8bf, x.v[3 * hh + 2]), c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h[hh]), __builtin_bit_cast(v8bf, x.v[3 * hh + 1]), c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h[hh]), __builtin_bit_cast(v8bf, x.v[3 * hh]), c, 0, 0, 0);
     }
     return c;
   }
 }
 
-template <int AMODE, int U>
+// R row groups per work-group share every activation fragment (loaded and,
+// for fp32 activations, split into bf16 terms once per k-block), so the
+// activation work per weight byte falls by R for large N.
+template <int AMODE, int U, int R>
 __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
   using acc_t = acc_small_t<AMODE>;
-  __shared__ acc_t s_part[4][64];
+  __shared__ acc_t s_part[R][4][64];
 
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g = blockIdx.x;                            // weight row group
+  const int g0 = blockIdx.x * R;                       // first weight row group
   const int kb0 = (wv * a.KB) / 4, kb1 = ((wv + 1) * a.KB) / 4;
   const int n_t = kb1 - kb0;                           // may be 0 when KB < 4
   const int last = max(n_t - 1, 0);
-  const uint4* wp = reinterpret_cast<const uint4*>(a.Bt) + ((size_t)kb0 * a.NG + g) * 64 + lane;
   const size_t tstride = (size_t)a.NG * 64;
+  const uint4* wbase = reinterpret_cast<const uint4*>(a.Bt) + (size_t)kb0 * tstride + lane;
+  int goff[R];                                         // row groups past NG re-read a valid one
+#pragma unroll
+  for (int r = 0; r < R; r++) goff[r] = min(g0 + r, a.NG - 1) * 64;
 
-  acc_t acc = acc_t{0, 0, 0, 0};
-  uint4 b0[U], b1[U];
+  acc_t acc[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) acc[r] = acc_t{0, 0, 0, 0};
+  uint4 b0[U][R], b1[U][R];
   AFrag<AMODE> x0[U], x1[U];
-  auto load = [&](uint4 (&b)[U], AFrag<AMODE> (&x)[U], int t0) {
+  auto load = [&](uint4 (&b)[U][R], AFrag<AMODE> (&x)[U], int t0) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int t = min(t0 + u, last);
-      b[u] = wp[(size_t)t * tstride];
+#pragma unroll
+      for (int r = 0; r < R; r++) b[u][r] = wbase[(size_t)t * tstride + goff[r]];
       x[u] = load_a<AMODE>(a, min(kb0 + t, a.KB - 1), lane);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  auto consume = [&](const uint4 (&b)[U], const AFrag<AMODE> (&x)[U], int t0) {
+  auto consume = [&](const uint4 (&b)[U][R], const AFrag<AMODE> (&x)[U], int t0) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
       // clamped repeats add exactly 0: their activations are zeroed (the
@@ -160,7 +194,9 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
 #pragma unroll
         for (int q = 0; q < (int)(sizeof(xv.v) / sizeof(uint4)); q++) xv.v[q] = make_uint4(0, 0, 0, 0);
       }
-      acc = mma<AMODE>(b[u], xv, acc);
+      const XOps<AMODE> xo = prepare_x<AMODE>(xv);
+#pragma unroll
+      for (int r = 0; r < R; r++) acc[r] = mma_x<AMODE>(b[u][r], xo, acc[r]);
     }
   };
 
@@ -176,48 +212,51 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
   consume(b0, x0, t);
   consume(b1, x1, t + U);
 
-  s_part[wv][lane] = acc;
+#pragma unroll
+  for (int r = 0; r < R; r++) s_part[r][wv][lane] = acc[r];
   __syncthreads();
   if (wv != 0) return;
-  acc_t tot = s_part[0][lane];
-#pragma unroll
-  for (int w = 1; w < 4; w++) {
-    const acc_t p = s_part[w][lane];
-#pragma unroll
-    for (int r = 0; r < 4; r++) tot[r] += p[r];
-  }
-
   // lane holds D[n .. n+3][m]: m = lane & 15, n = 16 g + 4 (lane >> 4)
   const int m = lane & 15;
-  const int n0 = g * 16 + 4 * (lane >> 4);
   if (m >= a.M) return;
-  for (int r = 0; r < 4; r++) {
-    const int n = n0 + r;
-    if (n >= a.N) break;
-    const size_t o = (size_t)m * a.ldy + n;
-    float y;
-    if constexpr (AMODE == A_I8) {
-      if (a.out == OUT_I32) {
-        reinterpret_cast<int32_t*>(a.Y)[o] = tot[r];
-        continue;
-      }
-      y = __fmul_rn(__fmul_rn((float)tot[r], a.ws[n]), a.xs[m]);
-      if (a.bias) y = __fadd_rn(y, a.bias[n]);
-    } else {
-      if (a.ep == EP_SCALE_FMA) {
-        y = __fmaf_rn(tot[r], a.ws[n], a.bias ? a.bias[n] : 0.0f);
-      } else {
-        y = __fmul_rn(tot[r], a.ws[n]);
-        if (a.bias) y = __fadd_rn(y, a.bias[n]);
-      }
+#pragma unroll
+  for (int rg = 0; rg < R; rg++) {
+    acc_t tot = s_part[rg][0][lane];
+#pragma unroll
+    for (int w = 1; w < 4; w++) {
+      const acc_t p = s_part[rg][w][lane];
+#pragma unroll
+      for (int q = 0; q < 4; q++) tot[q] += p[q];
     }
-    if (a.out == OUT_F32) {
-      reinterpret_cast<float*>(a.Y)[o] = y;
-    } else if (a.out == OUT_BF16) {
-      reinterpret_cast<uint16_t*>(a.Y)[o] = (uint16_t)f32_to_bf16_rne(y);
-    } else {
-      const _Float16 h = (_Float16)y;
-      reinterpret_cast<uint16_t*>(a.Y)[o] = __builtin_bit_cast(uint16_t, h);
+    const int n0 = (g0 + rg) * 16 + 4 * (lane >> 4);
+    for (int q = 0; q < 4; q++) {
+      const int n = n0 + q;
+      if (n >= a.N) break;
+      const size_t o = (size_t)m * a.ldy + n;
+      float y;
+      if constexpr (AMODE == A_I8) {
+        if (a.out == OUT_I32) {
+          reinterpret_cast<int32_t*>(a.Y)[o] = tot[q];
+          continue;
+        }
+        y = __fmul_rn(__fmul_rn((float)tot[q], a.ws[n]), a.xs[m]);
+        if (a.bias) y = __fadd_rn(y, a.bias[n]);
+      } else {
+        if (a.ep == EP_SCALE_FMA) {
+          y = __fmaf_rn(tot[q], a.ws[n], a.bias ? a.bias[n] : 0.0f);
+        } else {
+          y = __fmul_rn(tot[q], a.ws[n]);
+          if (a.bias) y = __fadd_rn(y, a.bias[n]);
+        }
+      }
+      if (a.out == OUT_F32) {
+        reinterpret_cast<float*>(a.Y)[o] = y;
+      } else if (a.out == OUT_BF16) {
+        reinterpret_cast<uint16_t*>(a.Y)[o] = (uint16_t)f32_to_bf16_rne(y);
+      } else {
+        const _Float16 h = (_Float16)y;
+        reinterpret_cast<uint16_t*>(a.Y)[o] = __builtin_bit_cast(uint16_t, h);
+      }
     }
   }
 }
@@ -230,12 +269,17 @@ bool gemm_small_supported(const GemmLaunch& L) {
   return (((uintptr_t)L.A) & 15) == 0;
 }
 
+template <int AMODE, int R>
+static void launch_small_r(const GemmSmallArgs& a, int u, hipStream_t st) {
+  const dim3 grid(cdiv(a.NG, R)), block(256);
+  if (u == 4) hipLaunchKernelGGL((gemm_small_kernel<AMODE, 4, R>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((gemm_small_kernel<AMODE, 2, R>), grid, block, 0, st, a);
+}
+
 template <int AMODE>
-static void launch_small_mode(const GemmSmallArgs& a, int u, hipStream_t st) {
-  const dim3 grid(a.NG), block(256);
-  if (u == 8) hipLaunchKernelGGL((gemm_small_kernel<AMODE, 8>), grid, block, 0, st, a);
-  else if (u == 4) hipLaunchKernelGGL((gemm_small_kernel<AMODE, 4>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((gemm_small_kernel<AMODE, 2>), grid, block, 0, st, a);
+static void launch_small_mode(const GemmSmallArgs& a, int u, int r, hipStream_t st) {
+  if (r == 4) launch_small_r<AMODE, 4>(a, u, st);
+  else launch_small_r<AMODE, 1>(a, u, st);
 }
 
 hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st) {
@@ -258,13 +302,15 @@ hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st) {
   a.out = L.out;
   if (L.amode == A_I8 && L.out != OUT_I32 && !L.xs) return hipErrorInvalidValue;
   const int n_t = cdiv(a.KB, 4);
-  // the fp32 split carries 4 uint4 of X per tile: its batches stay at 2
-  const int u = (L.amode != A_F32X3 && n_t >= 4) ? 4 : 2;
+  // four row groups per work-group once there are work-groups to spare
+  // (>= 2048 row groups: the lm_head), else one
+  const int r = a.NG >= 2048 ? 4 : 1;
+  const int u = (r == 1 && n_t >= 8) ? 4 : 2;
   switch (L.amode) {
-    case A_I8: launch_small_mode<A_I8>(a, u, st); break;
-    case A_BF16: launch_small_mode<A_BF16>(a, u, st); break;
-    case A_F16: launch_small_mode<A_F16>(a, u, st); break;
-    default: launch_small_mode<A_F32X3>(a, u, st); break;
+    case A_I8: launch_small_mode<A_I8>(a, u, r, st); break;
+    case A_BF16: launch_small_mode<A_BF16>(a, u, r, st); break;
+    case A_F16: launch_small_mode<A_F16>(a, u, r, st); break;
+    default: launch_small_mode<A_F32X3>(a, u, r, st); break;
   }
   return hipGetLastError();
 }
