@@ -112,19 +112,22 @@ struct DevBuf {
   }
 };
 
+// pinned host staging, mapped into the device address space (dp)
 struct PinnedBuf {
   void* p = nullptr;
+  void* dp = nullptr;
   size_t n = 0;
   void ensure(size_t bytes) {
     if (bytes <= n) return;
     if (p) {
       HIP_OK(hipHostFree(p));
-      p = nullptr;
+      p = dp = nullptr;
       n = 0;
     }
     size_t want = bytes < 4096 ? 4096 : bytes;
     HIP_OK(hipHostMalloc(&p, want, hipHostMallocDefault));
     n = want;
+    HIP_OK(hipHostGetDevicePointer(&dp, p, 0));
   }
 };
 
@@ -579,13 +582,29 @@ void w8a32_linear(const float* X, const int8_t* w_int8, const float* scales, con
     std::lock_guard<std::mutex> lk(g_host_mu);
     HostCtx& c = host_ctx(current_device());
     const tl_weights* W = registry_get(w_int8, scales, M, K, c.st);
-    h2d(c, c.x, X, (size_t)batch * K * sizeof(float));
     const float* b = nullptr;
     if (bias) {
       c.bias.ensure((size_t)M * sizeof(float), c.st);
       HIP_OK(hipMemcpyAsync(c.bias.p, bias, (size_t)M * sizeof(float), hipMemcpyHostToDevice, c.st));
       b = static_cast<const float*>(c.bias.p);
     }
+    if (batch == 1) {
+      // decode: x comes in through mapped pinned memory by a copy kernel and
+      // the GEMV writes y straight into mapped pinned memory, so the call is
+      // two kernels and one synchronisation (no DMA transfers)
+      const size_t xb = (size_t)K * sizeof(float), yb = (size_t)M * sizeof(float);
+      c.hin.ensure(xb);
+      c.hout.ensure(yb);
+      c.x.ensure(xb, c.st);
+      HIP_OK(hipStreamSynchronize(c.st));  // staging buffers idle
+      std::memcpy(c.hin.p, X, xb);
+      HIP_OK(launch_copy_words(c.hin.dp, c.x.p, xb, c.st));
+      op_w8a32(static_cast<const float*>(c.x.p), W, b, static_cast<float*>(c.hout.dp), 1, c.st);
+      HIP_OK(hipStreamSynchronize(c.st));
+      std::memcpy(Y, c.hout.p, yb);
+      return;
+    }
+    h2d(c, c.x, X, (size_t)batch * K * sizeof(float));
     c.y.ensure((size_t)batch * M * sizeof(float), c.st);
     op_w8a32(static_cast<const float*>(c.x.p), W, b, static_cast<float*>(c.y.p), batch, c.st);
     d2h(c, Y, c.y.p, (size_t)batch * M * sizeof(float));

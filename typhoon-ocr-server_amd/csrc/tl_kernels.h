@@ -23,6 +23,8 @@ hipError_t launch_quantize_rows(const float* src, int8_t* dst, float* scales, in
 hipError_t launch_quantize_rows_tiled(const float* src, int rows, int cols, uint8_t* tiles,
                                       float* scales, bool clamp127, hipStream_t st);
 hipError_t launch_pack_tiles(const int8_t* w, int rows, int cols, uint8_t* tiles, hipStream_t st);
+// 4-byte-word copy by a kernel (bytes % 4 == 0), e.g. from mapped pinned host memory
+hipError_t launch_copy_words(const void* src, void* dst, size_t bytes, hipStream_t st);
 
 // ---- M=1 GEMV (gemv.hip) --------------------------------------------------
 struct GemvPlan {
