@@ -110,6 +110,51 @@ def time_shapes(lin, torch, items, stream, reps):
     return out
 
 
+def bench_lm_head_greedy(lin, torch, W, K, dev, stream, reps=20):
+    """The fused greedy step (final RMSNorm, lm_head GEMV with per-work-group
+    argmax keys, key reduction: three launches) against the plain lm_head
+    GEMV, each captured in a HIP graph and replayed, alternating between two
+    distinct lm_head matrices (622 MB, beyond the 256 MB Infinity Cache)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    w2 = torch.randint(-127, 128, (W.rows, K), dtype=torch.int8, device=dev, generator=g)
+    s2 = torch.rand(W.rows, device=dev, generator=g) * 0.018 + 0.002
+    W2 = lin.DeviceWeights.from_codes(w2, s2)
+    del w2
+    Ws = (W, W2)
+    h = torch.randn(K, device=dev, generator=g)
+    nw = 1.0 + 0.1 * torch.randn(K, device=dev, generator=g)
+    tok = torch.empty(1, dtype=torch.int32, device=dev)
+    x = torch.randn((1, K), device=dev, generator=g)
+    y = torch.empty((1, W.rows), device=dev)
+    out = {}
+    for name, fn in (("fused_rmsnorm_gemv_argmax", lambda Wi: lin.lm_head_argmax_dev(h, nw, Wi, tok, stream=stream)),
+                     ("gemv_logits_only", lambda Wi: lin.w8a32_linear_dev(x, Wi, y, stream=stream))):
+        with torch.cuda.stream(stream):
+            fn(W)
+            fn(W2)
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(reps):
+                fn(Ws[i & 1])
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(3):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / (3 * reps)
+        b = gemv_bytes(W.rows, K)
+        out[name] = {"us": round(t * 1e6, 2), "GBps": round(b / t / 1e9, 1)}
+        del graph
+    W2.close()
+    out["returns"] = "int32 token id (fused) vs 151936 fp32 logits (GEMV only)"
+    return out
+
+
 def bench_w8a8_prefill(lin, torch, dev, reps=20):
     out = {}
     tot_ops, tot_t = 0.0, 0.0
@@ -411,6 +456,9 @@ def main():
                 "bytes_per_launch": round(avg_bytes), "avg_launch_us": round(avg_t * 1e6, 3),
                 "per_shape": per_shape}
 
+    log("fused greedy lm_head step")
+    greedy = bench_lm_head_greedy(lin, torch, items[-1][3], items[-1][2], dev, stream)
+
     # the decode set's 1.72 GB is no longer needed
     n_launch = len(items)
     del graph
@@ -457,6 +505,7 @@ def main():
         "decode_tok_s": round(1.0 / t_step, 1),
         "wall_s": round(wall, 3),
         "roofline": roofline,
+        "lm_head_greedy": greedy,
         "w8a8_prefill": prefill,
         "w8a32_decode_rows": rows,
         "w8a16_sweep": sweep,

@@ -145,6 +145,23 @@ int tl_w8a8_linear_f32_dev(const float *X, const tl_weights *W, const float *bia
 int tl_w8a16_linear_dev(const void *X, int x_type, const tl_weights *W, const float *bias,
                         void *Y, int y_type, int batch, void *stream);
 
+/* Greedy next token from the last hidden row, the steps of decoder.py:443-464
+ * (_get_logits, then the greedy branch of _sample) in one stream-ordered
+ * call: x = (h / sqrt(mean(h*h) + 1e-6)) * norm_w in numpy's float32 order
+ * (norm_w may be NULL: no weight), lm_head logits = w8a32_linear(x, W)
+ * (stored only if logits != NULL), *token = first index of the largest
+ * logit, *max_logit = that logit (may be NULL).  K = W's columns must be a
+ * power of two in [128, 16384].  No reference counterpart: the reference
+ * returns all 151936 logits to Python and takes the argmax there. */
+int tl_lm_head_argmax_dev(const float *h, const float *norm_w, const tl_weights *W, float *logits,
+                          int32_t *token, float *max_logit, void *stream);
+/* The same on host pointers (weights through the registry, like
+ * w8a32_linear); returns the token in *token, logits optional. */
+int tl_lm_head_argmax(const float *h, const float *norm_w, const int8_t *w_int8, const float *scales,
+                      int N, int K, float *logits, int32_t *token);
+/* Test hook: the normalised row alone (device pointers). */
+int tl_rmsnorm_np_dev(const float *h, const float *norm_w, float *out, int K, void *stream);
+
 /* Test hooks: the exact int32 accumulators of the fused M=1 GEMV (and the
  * activation scale it derived), and of the int8 MFMA GEMM on row-major
  * codes. */

@@ -206,3 +206,41 @@ def test_w8a16_paths(orc):
         y = orc.w8a16_linear(xb[:m], w, ws)
         exact = (xf[:m] @ w.astype(np.float64).T) * ws.astype(np.float64)
         assert np.linalg.norm(y - exact) / np.linalg.norm(exact) < 1e-6
+
+
+def _pairwise_model(x):
+    """The summation order the GPU final-RMSNorm kernel uses for K = 128*2^j:
+    per 128-block 8 interleaved accumulators, ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)),
+    then a balanced tree over the blocks (float32 throughout)."""
+    f = np.float32
+    nb = len(x) // 128
+    blk = []
+    for b in range(nb):
+        r = []
+        for j in range(8):
+            acc = f(x[128 * b + j] * x[128 * b + j])
+            for i in range(1, 16):
+                v = x[128 * b + 8 * i + j]
+                acc = f(acc + f(v * v))
+            r.append(acc)
+        blk.append(f(f(f(r[0] + r[1]) + f(r[2] + r[3])) + f(f(r[4] + r[5]) + f(r[6] + r[7]))))
+    w = 1
+    while w < nb:
+        for i in range(0, nb, 2 * w):
+            blk[i] = f(blk[i] + blk[i + w])
+        w *= 2
+    return blk[0]
+
+
+@pytest.mark.parametrize("K", [128, 256, 1024, 2048, 4096])
+def test_numpy_mean_order_matches_kernel_model(K):
+    """decoder.py:444 computes np.mean(h * h) in float32; numpy sums with its
+    pairwise algorithm.  The GPU kernel follows the model above; this pins
+    that the installed numpy sums in exactly that order (and divides by K in
+    float32), on vectors of very different scales."""
+    rng = np.random.default_rng(K)
+    for t in range(40):
+        h = (rng.standard_normal(K) * 10.0 ** rng.uniform(-4, 4)).astype(np.float32)
+        s = _pairwise_model(h)
+        assert s == np.add.reduce((h * h).astype(np.float32))
+        assert np.mean(h * h) == np.float32(s / np.float32(K))

@@ -140,6 +140,8 @@ struct Workspace {
   size_t cnt_n = 0;
   DevBuf act;         // activation codes (tiles or padded rows)
   DevBuf act_s;       // activation scales
+  DevBuf xn;          // normalised hidden row (lm_head argmax)
+  DevBuf keys;        // per-work-group argmax keys
 };
 
 std::mutex g_ws_mu;
@@ -334,7 +336,7 @@ const tl_weights* registry_get(const int8_t* w, const float* s, int rows, int co
 struct HostCtx {
   hipStream_t st = nullptr;
   DevBuf x, y, bias, xs;
-  PinnedBuf hin, hout;
+  PinnedBuf hin, hout, htok;
 };
 std::mutex g_host_mu;
 std::map<int, HostCtx*> g_host;
@@ -869,6 +871,90 @@ int tl_w8a32_gemv_acc_dev(const float* x, const tl_weights* W, int32_t* acc, flo
     L.K = W->cols;
     L.epi = EPI_ACC;
     run_gemv(ws, L, st);
+  });
+}
+
+int tl_rmsnorm_np_dev(const float* h, const float* norm_w, float* out, int K, void* stream) {
+  return guarded("tl_rmsnorm_np_dev", [&] {
+    REQUIRE(h && out, "h and out must be non-NULL");
+    REQUIRE(K >= 128 && K <= 16384 && (K & (K - 1)) == 0, "K must be a power of two in [128, 16384]");
+    HIP_OK(launch_rmsnorm_np(h, norm_w, out, K, 1e-6f, static_cast<hipStream_t>(stream)));
+  });
+}
+
+// final RMSNorm, lm_head GEMV with per-work-group argmax keys, key reduction
+void op_lm_head_argmax(const float* h, const float* norm_w, const tl_weights* W, float* logits,
+                       int32_t* token, float* max_logit, hipStream_t st) {
+  const int K = W->cols;
+  REQUIRE(K >= 128 && K <= 16384 && (K & (K - 1)) == 0, "K must be a power of two in [128, 16384]");
+  Workspace& ws = workspace(W->dev, st);
+  const GemvPlan p = gemv_plan(W->rows, K);
+  ws.keys.ensure((size_t)p.blocks * sizeof(uint64_t), st);
+  GemvLaunch L;
+  if (gemv_fused_norm_ok(K, h, norm_w)) {
+    // every GEMV work-group normalises the row itself: one launch fewer
+    L.x = h;
+    L.norm = true;
+    L.norm_w = norm_w;
+  } else {
+    ws.xn.ensure((size_t)K * sizeof(float), st);
+    float* xn = static_cast<float*>(ws.xn.p);
+    HIP_OK(launch_rmsnorm_np(h, norm_w, xn, K, 1e-6f, st));
+    L.x = xn;
+  }
+  L.wt = W->tiles;
+  L.ws = W->scales;
+  L.y = logits;
+  L.keys = static_cast<uint64_t*>(ws.keys.p);
+  L.N = W->rows;
+  L.K = K;
+  L.epi = EPI_ARGMAX;
+  HIP_OK(launch_gemv_i8(L, st));
+  HIP_OK(launch_argmax_keys(L.keys, p.blocks, token, max_logit, st));
+}
+
+int tl_lm_head_argmax_dev(const float* h, const float* norm_w, const tl_weights* W, float* logits,
+                          int32_t* token, float* max_logit, void* stream) {
+  return guarded("tl_lm_head_argmax_dev", [&] {
+    check_weights(W);
+    REQUIRE(h && token, "h and token must be non-NULL");
+    op_lm_head_argmax(h, norm_w, W, logits, token, max_logit, static_cast<hipStream_t>(stream));
+  });
+}
+
+int tl_lm_head_argmax(const float* h, const float* norm_w, const int8_t* w_int8, const float* scales,
+                      int N, int K, float* logits, int32_t* token) {
+  return guarded("tl_lm_head_argmax", [&] {
+    check_shape(1, N, K);
+    REQUIRE(h && token, "h and token must be non-NULL");
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    HostCtx& c = host_ctx(current_device());
+    const tl_weights* W = registry_get(w_int8, scales, N, K, c.st);
+    // h and the norm weights in one staging copy: [h | norm_w]
+    const size_t kb = (size_t)K * sizeof(float);
+    const size_t inb = norm_w ? 2 * kb : kb;
+    c.hin.ensure(inb);
+    c.htok.ensure(16);
+    c.x.ensure(inb, c.st);
+    HIP_OK(hipStreamSynchronize(c.st));
+    std::memcpy(c.hin.p, h, kb);
+    if (norm_w) std::memcpy(static_cast<char*>(c.hin.p) + kb, norm_w, kb);
+    HIP_OK(launch_copy_words(c.hin.dp, c.x.p, inb, c.st));
+    const float* hd = static_cast<const float*>(c.x.p);
+    const float* wd = norm_w ? hd + K : nullptr;
+    float* ld = nullptr;
+    if (logits) {
+      c.y.ensure(kb > (size_t)N * 4 ? kb : (size_t)N * 4, c.st);
+      ld = static_cast<float*>(c.y.p);
+    }
+    int32_t* td = static_cast<int32_t*>(c.htok.dp);
+    op_lm_head_argmax(hd, wd, W, ld, td, nullptr, c.st);
+    if (logits) {
+      d2h(c, logits, ld, (size_t)N * sizeof(float));
+    } else {
+      HIP_OK(hipStreamSynchronize(c.st));
+    }
+    *token = *static_cast<const int32_t*>(c.htok.p);
   });
 }
 

@@ -47,6 +47,10 @@ struct GemvArgs {
   float* y;            // [N]
   int32_t* acc_out;    // [N] (EPI_ACC)
   float* xs_out;       // optional activation scale output
+  uint64_t* keys;      // EPI_ARGMAX: per-work-group keys
+  const float* norm_w; // final RMSNorm weights (norm)
+  float norm_eps;
+  bool norm;
   int N, K, KB, NG, epi;
   int x_vec;           // 2: K == 1024*XV and x 16-byte aligned (unguarded loads)
 };
@@ -114,15 +118,78 @@ __device__ __forceinline__ void load_batch(uint4 (&b)[U], uint4 (&c)[XV == 0 ? U
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// Final RMSNorm of the hidden row held in xv (K == 1024 XV, a power of two),
+// in numpy's float32 order (the same arithmetic as rmsnorm_np_kernel in
+// lmhead.hip, decoder.py:444-446): squares through LDS, accumulator j of
+// 128-block b folds x[128b + 8i + j]^2 over i in order, xor butterflies
+// combine the 8 accumulators of a block and the 8 blocks of a wave, every
+// thread finishes the balanced tree over the groups of 8 blocks itself.
+// Then x = fl(fl(x / rms) * w).  Uses the dynamic LDS of the launch (4K bytes).
+template <int XV>
+__device__ void final_rmsnorm(float4 (&xv)[XV], const float4 (&nwv)[XV], bool has_w, int K, float eps) {
+  extern __shared__ float s_sq[];
+  __shared__ float s_grp[16];
+#pragma unroll
+  for (int i = 0; i < XV; i++) {
+    const float4 v = xv[i];
+    reinterpret_cast<float4*>(s_sq)[threadIdx.x + 256 * i] =
+        make_float4(__fmul_rn(v.x, v.x), __fmul_rn(v.y, v.y), __fmul_rn(v.z, v.z), __fmul_rn(v.w, v.w));
+  }
+  __syncthreads();
+  const int nb = K >> 7, ngrp = nb >> 3;     // K >= 1024 here: whole groups of 8 blocks
+  for (int base = 0; base < 64 * ngrp; base += 256) {
+    const int p = base + threadIdx.x;
+    const int b = p >> 3, j = p & 7;
+    float r = 0.0f;
+    if (b < nb) {
+      const float* src = s_sq + 128 * b + j;
+      r = src[0];
+#pragma unroll
+      for (int i = 1; i < 16; i++) r = __fadd_rn(r, src[8 * i]);
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) r = __fadd_rn(r, __shfl_xor(r, o, 64));
+    if ((threadIdx.x & 63) == 0 && (p >> 6) < ngrp) s_grp[p >> 6] = r;
+  }
+  __syncthreads();
+  float gsum[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) gsum[i] = i < ngrp ? s_grp[i] : 0.0f;
+#pragma unroll
+  for (int wdt = 1; wdt < 16; wdt <<= 1)
+#pragma unroll
+    for (int i = 0; i < 16; i += 2 * wdt)
+      if (i + wdt < ngrp) gsum[i] = __fadd_rn(gsum[i], gsum[i + wdt]);
+  const float mean = __fdiv_rn(gsum[0], (float)K);
+  const float rms = sqrtf(__fadd_rn(mean, eps));   // correctly rounded (see lmhead.hip)
+#pragma unroll
+  for (int i = 0; i < XV; i++) {
+    float4 v = xv[i];
+    v.x = __fdiv_rn(v.x, rms);
+    v.y = __fdiv_rn(v.y, rms);
+    v.z = __fdiv_rn(v.z, rms);
+    v.w = __fdiv_rn(v.w, rms);
+    if (has_w) {
+      v.x = __fmul_rn(v.x, nwv[i].x);
+      v.y = __fmul_rn(v.y, nwv[i].y);
+      v.z = __fmul_rn(v.z, nwv[i].z);
+      v.w = __fmul_rn(v.w, nwv[i].w);
+    }
+    xv[i] = v;
+  }
+}
+
 // Arguments are scalars so that the leading ones (through `flags`) are
 // preloaded into SGPRs at wave launch (kernarg preload, -amdgpu-kernarg-
 // preload-count in the build): the first loads need no kernarg fetch.
-// flags: bits 0-1 x_vec, bits 2-3 epilogue, bit 4 bias present.
+// flags: bits 0-1 x_vec, bits 2-3 epilogue, bit 4 bias present, bit 5 final
+// RMSNorm of x first (K == 1024 XV a power of two, x_vec 2).
 template <int XV, int U, int RH>
 __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint8_t* wt, const float* ws,
                                                       float* y, int N, int K, int NG, int KB, int flags,
                                                       const uint8_t* xq, const float* xs_in, const float* bias,
-                                                      int32_t* acc_out, float* xs_out) {
+                                                      int32_t* acc_out, float* xs_out, uint64_t* keys,
+                                                      const float* norm_w, float norm_eps) {
   constexpr int SL = 64 / RH;           // lanes per row within a wave
   GemvArgs a;
   a.x = x;
@@ -134,6 +201,10 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
   a.y = y;
   a.acc_out = acc_out;
   a.xs_out = xs_out;
+  a.keys = keys;
+  a.norm_w = norm_w;
+  a.norm_eps = norm_eps;
+  a.norm = (flags & 32) != 0;
   a.N = N;
   a.K = K;
   a.KB = KB;
@@ -171,10 +242,18 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
   // x is read before the first weight batch is issued, so the wait for x
   // never waits for weights
   float4 xv[XV > 0 ? XV : 1];
+  float4 nwv[XV > 0 ? XV : 1];
+  const bool norm = (flags & 32) != 0;   // x is a hidden row to normalise first
   if constexpr (XV > 0) {
     if (a.x_vec == 2) {
 #pragma unroll
       for (int i = 0; i < XV; i++) xv[i] = *reinterpret_cast<const float4*>(a.x + 4 * (threadIdx.x + 256 * i));
+      if (norm) {
+#pragma unroll
+        for (int i = 0; i < XV; i++)
+          nwv[i] = norm_w ? *reinterpret_cast<const float4*>(norm_w + 4 * (threadIdx.x + 256 * i))
+                          : make_float4(1.f, 1.f, 1.f, 1.f);
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < XV; i++) {
@@ -197,6 +276,7 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
 
   float xs;
   if constexpr (XV > 0) {
+    if (norm) final_rmsnorm<XV>(xv, nwv, norm_w != nullptr, K, norm_eps);
     // ---- fused per-token activation quantization --------------------------
     uint32_t* sc = reinterpret_cast<uint32_t*>(s_codes);
     if ((K & 15) == 0) {
@@ -295,7 +375,9 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
   //      s_red[r*4*SL + w*SL + q], summed in that order by wave 0 ------------
   s_red[r * 4 * SL + wv * SL + slot] = acc;
   __syncthreads();
-  if (wv == 0 && lane < RH) {
+  if (wv != 0) return;
+  uint64_t key = 0;
+  if (lane < RH) {
     const int4* p = reinterpret_cast<const int4*>(s_red + lane * 4 * SL);
     int tot = 0;
 #pragma unroll
@@ -304,7 +386,28 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
       tot += (v.x + v.y) + (v.z + v.w);
     }
     const int n = row0 + lane;
-    if (n < a.N) gemv_epilogue(a, n, tot, xs, wsv, bv);
+    if (n < a.N) {
+      if (a.epi == EPI_ARGMAX) {
+        float r = __fmul_rn(__fmul_rn((float)tot, wsv), xs);
+        if (a.bias) r = __fadd_rn(r, bv);
+        if (a.y) a.y[n] = r;
+        key = argmax_key(r, n);
+      } else {
+        gemv_epilogue(a, n, tot, xs, wsv, bv);
+      }
+    }
+  }
+  if (a.epi == EPI_ARGMAX) {
+    // largest key of the work-group's rows (lanes >= RH hold 0); the keys of
+    // all work-groups are reduced by a second kernel (a last-work-group
+    // reduction needs a device-scope fence per work-group, measured 10x
+    // slower on the lm_head)
+#pragma unroll
+    for (int o = 1; o < RH; o <<= 1) {
+      const uint64_t t = __shfl_xor(key, o, 64);
+      key = t > key ? t : key;
+    }
+    if (lane == 0) keys[blockIdx.x] = key;
   }
 }
 
@@ -313,9 +416,11 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
 // ---------------------------------------------------------------------------
 template <int XV, int U, int RH>
 static void launch_one(const GemvArgs& a, int blocks, hipStream_t st) {
-  const int flags = (a.x_vec & 3) | ((a.epi & 3) << 2) | (a.bias ? 16 : 0);
-  hipLaunchKernelGGL((gemv_i8_kernel<XV, U, RH>), dim3(blocks), dim3(256), 0, st, a.x, a.wt, a.ws, a.y,
-                     a.N, a.K, a.NG, a.KB, flags, a.xq, a.xs_in, a.bias, a.acc_out, a.xs_out);
+  const int flags = (a.x_vec & 3) | ((a.epi & 3) << 2) | (a.bias ? 16 : 0) | (a.norm ? 32 : 0);
+  const size_t dyn = a.norm ? (size_t)a.K * sizeof(float) : 0;
+  hipLaunchKernelGGL((gemv_i8_kernel<XV, U, RH>), dim3(blocks), dim3(256), dyn, st, a.x, a.wt, a.ws, a.y,
+                     a.N, a.K, a.NG, a.KB, flags, a.xq, a.xs_in, a.bias, a.acc_out, a.xs_out, a.keys,
+                     a.norm_w, a.norm_eps);
 }
 
 template <int XV>
@@ -352,6 +457,15 @@ int gemv_fused_xv(int K) {
   if (kpad <= 8192) return 8;
   if (kpad <= 16384) return 16;
   return 0;
+}
+
+// The in-GEMV final RMSNorm needs all of x in registers (K == 1024 XV, both
+// vectors 16-byte aligned) and a power-of-two K (numpy's pairwise tree is
+// then balanced).
+bool gemv_fused_norm_ok(int K, const float* x, const float* norm_w) {
+  const int xv = gemv_fused_xv(K);
+  if (xv == 0 || K != 1024 * xv || (K & (K - 1)) != 0) return false;
+  return ((((uintptr_t)x) | ((uintptr_t)norm_w)) & 15) == 0;
 }
 
 static int g_force_rows = 0, g_force_u = 0;
@@ -404,6 +518,11 @@ hipError_t launch_gemv_i8(const GemvLaunch& L, hipStream_t st) {
   a.y = L.y;
   a.acc_out = L.acc_out;
   a.xs_out = L.xs_out;
+  a.keys = L.keys;
+  a.norm_w = L.norm_w;
+  a.norm_eps = L.norm_eps;
+  a.norm = L.norm;
+  if (L.epi == EPI_ARGMAX && !L.keys) return hipErrorInvalidValue;
   a.N = L.N;
   a.K = L.K;
   a.KB = cdiv(L.K, 64);
@@ -415,6 +534,7 @@ hipError_t launch_gemv_i8(const GemvLaunch& L, hipStream_t st) {
   const int xv = L.x ? gemv_fused_xv(L.K) : 0;
   if (L.x && xv == 0) return hipErrorInvalidValue;  // caller must quantize first
   if (L.x && L.K == 1024 * xv && (((uintptr_t)L.x) & 15) == 0) a.x_vec = 2;
+  if (L.norm && (!gemv_fused_norm_ok(L.K, L.x, L.norm_w) || a.x_vec != 2)) return hipErrorInvalidValue;
   if (!L.x && !L.xq) return hipErrorInvalidValue;
   switch (xv) {
     case 0: return launch_xv<0>(a, p, st);

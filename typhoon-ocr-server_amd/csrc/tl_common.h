@@ -187,6 +187,22 @@ __device__ __forceinline__ uint32_t codes4_rne(float4 v, float inv) {
 }
 
 // ---------------------------------------------------------------------------
+// argmax keys: the float's bits made monotonic in the high word, the index
+// complemented in the low word, so the largest key is the largest value and,
+// among equal values, the lowest index (torch.argmax's first-max rule)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t argmax_key(float v, int n) {
+  const uint32_t b = __float_as_uint(v);
+  const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((uint64_t)o << 32) | (uint64_t)(0xffffffffu - (uint32_t)n);
+}
+__device__ __forceinline__ int argmax_key_index(uint64_t k) { return (int)(0xffffffffu - (uint32_t)k); }
+__device__ __forceinline__ float argmax_key_value(uint64_t k) {
+  const uint32_t o = (uint32_t)(k >> 32);
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+
+// ---------------------------------------------------------------------------
 // int8 dot products
 // ---------------------------------------------------------------------------
 __device__ inline int dot16(uint4 w, uint4 x, int acc) {

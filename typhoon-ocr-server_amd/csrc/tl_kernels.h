@@ -10,7 +10,9 @@ namespace tl {
 __host__ __device__ inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 
 // GEMV epilogues (gemv.hip)
-enum { EPI_W8A32 = 0, EPI_W8A8 = 1, EPI_ACC = 2 };
+// EPI_ARGMAX: W8A32 outputs (optionally stored), reduced per work-group to
+// the key of its largest output (argmax_key) written to keys[blockIdx.x]
+enum { EPI_W8A32 = 0, EPI_W8A8 = 1, EPI_ACC = 2, EPI_ARGMAX = 3 };
 // GEMM A-operand modes and output types (gemm.hip)
 enum { A_I8 = 0, A_BF16 = 1, A_F16 = 2, A_F32X3 = 3 };
 enum { OUT_F32 = 0, OUT_BF16 = 1, OUT_F16 = 2, OUT_I32 = 3 };
@@ -23,6 +25,10 @@ hipError_t launch_quantize_rows(const float* src, int8_t* dst, float* scales, in
 hipError_t launch_quantize_rows_tiled(const float* src, int rows, int cols, uint8_t* tiles,
                                       float* scales, bool clamp127, hipStream_t st);
 hipError_t launch_pack_tiles(const int8_t* w, int rows, int cols, uint8_t* tiles, hipStream_t st);
+// final RMSNorm of one hidden row, numpy's float32 order (K = 128 * 2^j)
+hipError_t launch_rmsnorm_np(const float* h, const float* w, float* out, int K, float eps, hipStream_t st);
+// token = argmax over the per-work-group keys of an EPI_ARGMAX GEMV
+hipError_t launch_argmax_keys(const uint64_t* keys, int n, int32_t* token, float* value, hipStream_t st);
 // 4-byte-word copy by a kernel (bytes % 4 == 0), e.g. from mapped pinned host memory
 hipError_t launch_copy_words(const void* src, void* dst, size_t bytes, hipStream_t st);
 
@@ -41,10 +47,15 @@ struct GemvLaunch {
   float* y = nullptr;
   int32_t* acc_out = nullptr;
   float* xs_out = nullptr;
+  uint64_t* keys = nullptr;       // EPI_ARGMAX: one key per work-group (gemv_plan().blocks)
+  bool norm = false;              // final RMSNorm of x first (gemv_fused_norm_ok)
+  const float* norm_w = nullptr;  //   its weights (null: none)
+  float norm_eps = 1e-6f;
   int N = 0, K = 0, epi = EPI_W8A32;
 };
 GemvPlan gemv_plan(int N, int K);
 int gemv_fused_xv(int K);
+bool gemv_fused_norm_ok(int K, const float* x, const float* norm_w);
 hipError_t launch_gemv_i8(const GemvLaunch& L, hipStream_t st);
 // process-wide override of the GEMV plan for tuning: rows per work-group
 // (16 or 8) and load instructions per batch (0 = planner's choice)

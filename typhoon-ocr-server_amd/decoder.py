@@ -179,6 +179,16 @@ class Decoder:
         _lin.check(self._lib, "w8a32_linear")
         return self._logits_buf
 
+    def next_token(self, h_np: np.ndarray) -> int:
+        """Greedy next token, get_logits + sample in one library call
+        (tl_lm_head_argmax): the same final RMSNorm in numpy's float32 order,
+        the same lm_head GEMV, the first index of the largest logit; only the
+        4-byte token id comes back instead of the vocab-sized logits."""
+        if self._lm_head_w is None:
+            raise RuntimeError("Decoder has no lm_head")
+        h = np.ascontiguousarray(np.atleast_2d(h_np)[-1], dtype=np.float32)
+        return _lin.lm_head_argmax(h, self._final_norm_w, self._lm_head_w, self._lm_head_s)
+
     @staticmethod
     def sample(logits_1d: np.ndarray) -> int:
         """Greedy branch of _sample (reference :463-464): first index of the max."""

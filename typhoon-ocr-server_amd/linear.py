@@ -57,6 +57,9 @@ SIGNATURES = {
     "tl_w8a16_linear_dev": (_int, [_vp, _int, _vp, _vp, _vp, _int, _int, _vp]),
     "tl_w8a32_gemv_acc_dev": (_int, [_vp, _vp, _vp, _vp, _vp]),
     "tl_w8a8_gemm_acc_dev": (_int, [_vp, _vp, _vp, _int, _vp]),
+    "tl_lm_head_argmax_dev": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "tl_lm_head_argmax": (_int, [_f32p, _f32p, _i8p, _f32p, _int, _int, _f32p, ctypes.POINTER(ctypes.c_int32)]),
+    "tl_rmsnorm_np_dev": (_int, [_vp, _vp, _vp, _int, _vp]),
 }
 
 _LIB: Optional[ctypes.CDLL] = None
@@ -274,3 +277,32 @@ def gemm_acc_dev(x_q, W: DeviceWeights, acc, stream=None):
     lib = load_library()
     _rc(lib, lib.tl_w8a8_gemm_acc_dev(x_q.data_ptr(), W.handle, acc.data_ptr(), x_q.shape[0],
                                       _stream(stream)), "tl_w8a8_gemm_acc_dev")
+
+
+def lm_head_argmax_dev(h, norm_w, W: DeviceWeights, token, logits=None, max_logit=None, stream=None):
+    """Greedy token from the last hidden row h [K] (device tensors): final
+    RMSNorm (numpy's float32 order), lm_head GEMV, argmax, into token (int32[1])."""
+    lib = load_library()
+    _rc(lib, lib.tl_lm_head_argmax_dev(h.data_ptr(), _ptr(norm_w), W.handle, _ptr(logits), token.data_ptr(),
+                                       _ptr(max_logit), _stream(stream)), "tl_lm_head_argmax_dev")
+
+
+def lm_head_argmax(h: np.ndarray, norm_w: Optional[np.ndarray], w: np.ndarray, scales: np.ndarray,
+                   logits: Optional[np.ndarray] = None) -> int:
+    """Host-pointer variant: returns the greedy token id."""
+    lib = load_library()
+    h = np.ascontiguousarray(h, dtype=np.float32).reshape(-1)
+    nw = None if norm_w is None else np.ascontiguousarray(norm_w, dtype=np.float32)
+    tok = ctypes.c_int32(-1)
+    rc = lib.tl_lm_head_argmax(_p(h, ctypes.c_float), _p(nw, ctypes.c_float), _p(w, ctypes.c_int8),
+                               _p(scales, ctypes.c_float), w.shape[0], w.shape[1], _p(logits, ctypes.c_float),
+                               ctypes.byref(tok))
+    if rc != 0:
+        check(lib, "tl_lm_head_argmax")
+    return int(tok.value)
+
+
+def rmsnorm_np_dev(h, norm_w, out, stream=None):
+    lib = load_library()
+    _rc(lib, lib.tl_rmsnorm_np_dev(h.data_ptr(), _ptr(norm_w), out.data_ptr(), h.numel(), _stream(stream)),
+        "tl_rmsnorm_np_dev")
