@@ -260,11 +260,13 @@ def test_w8a32_batch_fp32(lin, orc, M, N, K):
     assert rel_l2(lin.w8a32_linear(x, w, s, bias=b), orc.w8a32_linear(x, w, s, bias=b)) <= 1e-5
 
 
-@pytest.mark.parametrize("M,N,K", [(3, 32776, 200), (8, 40000, 2048), (16, 33000, 130)])
+@pytest.mark.parametrize("M,N,K", [(3, 32776, 200), (8, 40000, 2048), (16, 33000, 130), (48, 33000, 130),
+                                   (30, 32800, 256), (64, 4100, 512), (20, 700, 2048)])
 def test_small_m_wide_n(lin, orc, M, N, K):
-    """M <= 16 token rows over N >= 32768 outputs (the lm_head's regime, where
-    a work-group covers several 16-row groups): W8A32 fp32 within 1e-5,
-    W8A16 fp32 out within 1e-5, W8A8 exact accumulator epilogue."""
+    """M <= 64 token rows (one to four 16-row token groups per weight tile),
+    also over N >= 32768 outputs (the lm_head's regime, where a work-group
+    covers several 16-row weight groups): W8A32 fp32 within 1e-5, W8A16 fp32
+    out within 1e-5, W8A8 within 1e-5."""
     say(f"small-M wide-N M={M} N={N} K={K}")
     rng = np.random.default_rng(M * 7 + N + K)
     x, w, s = make(rng, M, N, K)

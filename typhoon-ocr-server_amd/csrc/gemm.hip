@@ -412,7 +412,12 @@ hipError_t launch_gemm(const GemmLaunch& L, hipStream_t st) {
   a.cnt = L.cnt;
   if (p.split > 1 && (!L.part || !L.cnt)) return hipErrorInvalidValue;
   if (L.amode == A_I8 && L.out != OUT_I32 && !L.xs) return hipErrorInvalidValue;
-  if (L.M <= 16 && gemm_small_supported(L)) return launch_gemm_small(L, st);
+  // up to 16 token rows always stream the weights once; up to 64 rows too
+  // while N is small (N <= 4096: the tiled kernels would leave CUs idle), but
+  // for wide N the activation fragments every work-group re-reads cost more
+  // than the tiled kernels' reuse
+  if (gemm_small_supported(L) && (L.M <= 16 || (L.M <= 64 && cdiv(L.N, 16) <= 256)))
+    return launch_gemm_small(L, st);
   if (L.amode == A_I8 && L.M > 16) return launch_gemm_i8(L, st);
   if (L.amode != A_I8 && L.M > 16 && gemm_b16_supported(L)) return launch_gemm_b16(L, st);
   switch (L.amode) {

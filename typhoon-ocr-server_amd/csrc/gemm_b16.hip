@@ -276,10 +276,17 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
 // ---------------------------------------------------------------------------
 // 16-bit X:  cfg 0  128 x 192 tiles, 4-deep ring (112 KiB)
 //            cfg 1   64 x 128 tiles, 8-deep ring (128 KiB)
+//            cfg 2   32 x  64 tiles, 8-deep ring (64 KiB)
 // fp32 X:    cfg 0   64 x 128 tiles, 4-deep ring (96 KiB)
 //            cfg 1   64 x  64 tiles, 6-deep ring (96 KiB)
+//            cfg 2   32 x  64 tiles, 6-deep ring (72 KiB)
+// The smaller tiles exist for mid-size M (64 < M <= 512) with small N, where
+// the larger ones leave most CUs idle.
 static void b16_cfg(int amode, int cfg, int& mt, int& nt) {
-  if (amode == A_F32X3) {
+  if (cfg == 2) {
+    mt = 2;
+    nt = 4;
+  } else if (amode == A_F32X3) {
     mt = 4;
     nt = (cfg == 0) ? 8 : 4;
   } else {
@@ -318,7 +325,7 @@ hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st) {
   // the configuration whose tile count best fills 256 CUs
   int best = 0;
   double best_eff = -1.0;
-  for (int cfg : {0, 1}) {
+  for (int cfg : {0, 1, 2}) {
     int mt, nt;
     b16_cfg(L.amode, cfg, mt, nt);
     const int tiles = cdiv(a.MG, mt) * cdiv(a.NG, nt);
@@ -336,15 +343,18 @@ hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st) {
   switch (L.amode) {
     case A_BF16:
       if (best == 0) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_BF16, 8, 12, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
-      else hipLaunchKernelGGL((gemm_b16_lds_kernel<A_BF16, 4, 8, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
+      else if (best == 1) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_BF16, 4, 8, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
+      else hipLaunchKernelGGL((gemm_b16_lds_kernel<A_BF16, 2, 4, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
       break;
     case A_F16:
       if (best == 0) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F16, 8, 12, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
-      else hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F16, 4, 8, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
+      else if (best == 1) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F16, 4, 8, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
+      else hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F16, 2, 4, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
       break;
     default:
       if (best == 0) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F32X3, 4, 8, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
-      else hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F32X3, 4, 4, 6, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
+      else if (best == 1) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F32X3, 4, 4, 6, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
+      else hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F32X3, 2, 4, 6, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
       break;
   }
   return hipGetLastError();

@@ -1,5 +1,5 @@
-// gemm_small.hip -- M <= 16 token rows over int8 weight tiles (decode rows
-// M = 2..8 of w8a32_linear, W8A16 at M = 1..16, W8A8 batches of 2..16).
+// gemm_small.hip -- M <= 64 token rows over int8 weight tiles (decode rows
+// M = 2..8 of w8a32_linear, W8A16 at M = 1..64, W8A8 batches of 2..64).
 //
 // HBM-bound like the M = 1 GEMV, and organised the same way: a work-group
 // owns one 16-row weight group, its 4 waves split K, each wave streams its
@@ -33,6 +33,7 @@ struct GemmSmallArgs {
   void* Y;
   int ldy;
   int M, N, K, KB, NG;
+  int MG;               // 16-row token groups: ceil(M / 16) (A_I8 tile rows)
   int ep, out;
 };
 
@@ -42,16 +43,17 @@ struct AFrag {
   uint4 v[AMODE == A_I8 ? 1 : (AMODE == A_F32X3 ? 4 : 2)];
 };
 
+// activation fragment of k-block kb for token group tg (rows 16 tg ..)
 template <int AMODE>
-__device__ inline AFrag<AMODE> load_a(const GemmSmallArgs& a, int kb, int lane) {
+__device__ inline AFrag<AMODE> load_a(const GemmSmallArgs& a, int kb, int tg, int lane) {
   AFrag<AMODE> f;
   if constexpr (AMODE == A_I8) {
-    f.v[0] = reinterpret_cast<const uint4*>(a.A)[(size_t)kb * 64 + lane];
+    f.v[0] = reinterpret_cast<const uint4*>(a.A)[((size_t)kb * a.MG + min(tg, a.MG - 1)) * 64 + lane];
   } else {
     constexpr int ESZ = (AMODE == A_F32X3) ? 4 : 2;
     constexpr int NV = (AMODE == A_F32X3) ? 4 : 2;
     constexpr int EPV = 16 / ESZ;                     // elements per uint4
-    const int row = min(lane & 15, a.M - 1);
+    const int row = min(tg * 16 + (lane & 15), a.M - 1);
     const int k0 = kb * 64 + 16 * (lane >> 4);
     const char* base = static_cast<const char*>(a.A) + (size_t)row * a.lda * ESZ;
 #pragma unroll
@@ -119,31 +121,41 @@ __device__ inline XOps<AMODE> prepare_x(const AFrag<AMODE>& x) {
   return o;
 }
 
-// the weights of one row group against a prepared activation fragment
+// MFMA operands of one weight tile: int8 as loaded, or widened to two
+// 16-bit K halves (exact), once per tile for all token groups
 template <int AMODE>
-__device__ inline acc_small_t<AMODE> mma_x(uint4 w, const XOps<AMODE>& x, acc_small_t<AMODE> c) {
+struct WOps {
+  uint4 v[AMODE == A_I8 ? 1 : 2];
+};
+
+template <int AMODE>
+__device__ inline WOps<AMODE> prepare_w(uint4 w) {
+  WOps<AMODE> o;
+  if constexpr (AMODE == A_I8) o.v[0] = w;
+  else if constexpr (AMODE == A_F16) widen_f16(w, o.v[0], o.v[1]);
+  else widen_bf16(w, o.v[0], o.v[1]);
+  return o;
+}
+
+// one prepared weight tile against one prepared activation fragment
+template <int AMODE>
+__device__ inline acc_small_t<AMODE> mma_x(const WOps<AMODE>& w, const XOps<AMODE>& x, acc_small_t<AMODE> c) {
   if constexpr (AMODE == A_I8) {
-    return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, w), __builtin_bit_cast(v4i, x.v[0]), c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, w.v[0]), __builtin_bit_cast(v4i, x.v[0]), c, 0, 0, 0);
   } else if constexpr (AMODE == A_BF16) {
-    uint4 h0, h1;
-    widen_bf16(w, h0, h1);
-    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h0), __builtin_bit_cast(v8bf, x.v[0]), c, 0, 0, 0);
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h1), __builtin_bit_cast(v8bf, x.v[1]), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, w.v[0]), __builtin_bit_cast(v8bf, x.v[0]), c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, w.v[1]), __builtin_bit_cast(v8bf, x.v[1]), c, 0, 0, 0);
   } else if constexpr (AMODE == A_F16) {
-    uint4 h0, h1;
-    widen_f16(w, h0, h1);
-    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h_s, h0), __builtin_bit_cast(v8h_s, x.v[0]), c, 0, 0, 0);
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h_s, h1), __builtin_bit_cast(v8h_s, x.v[1]), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h_s, w.v[0]), __builtin_bit_cast(v8h_s, x.v[0]), c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h_s, w.v[1]), __builtin_bit_cast(v8h_s, x.v[1]), c, 0, 0, 0);
   } else {
-    uint4 h[2];
-    widen_bf16(w, h[0], h[1]);
     // smallest term first: the three products of a K half are added to the
     // fp32 accumulator in increasing magnitude
 #pragma unroll
     for (int hh = 0; hh < 2; hh++) {
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h[hh]), __builtin_bit_cast(v8bf, x.v[3 * hh + 2]), c, 0, 0, 0);
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h[hh]), __builtin_bit_cast(v8bf, x.v[3 * hh + 1]), c, 0, 0, 0);
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, h[hh]), __builtin_bit_cast(v8bf, x.v[3 * hh]), c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, w.v[hh]), __builtin_bit_cast(v8bf, x.v[3 * hh + 2]), c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, w.v[hh]), __builtin_bit_cast(v8bf, x.v[3 * hh + 1]), c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, w.v[hh]), __builtin_bit_cast(v8bf, x.v[3 * hh]), c, 0, 0, 0);
     }
     return c;
   }
@@ -151,11 +163,13 @@ __device__ inline acc_small_t<AMODE> mma_x(uint4 w, const XOps<AMODE>& x, acc_sm
 
 // R row groups per work-group share every activation fragment (loaded and,
 // for fp32 activations, split into bf16 terms once per k-block), so the
-// activation work per weight byte falls by R for large N.
-template <int AMODE, int U, int R>
+// activation work per weight byte falls by R for large N.  TG token groups of
+// 16 rows (M <= 16 TG) ride along on every weight tile: the weights are
+// streamed once for all of them.
+template <int AMODE, int U, int R, int TG>
 __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
   using acc_t = acc_small_t<AMODE>;
-  __shared__ acc_t s_part[R][4][64];
+  __shared__ acc_t s_part[R][TG][4][64];
 
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -169,34 +183,43 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
 #pragma unroll
   for (int r = 0; r < R; r++) goff[r] = min(g0 + r, a.NG - 1) * 64;
 
-  acc_t acc[R];
+  acc_t acc[R][TG];
 #pragma unroll
-  for (int r = 0; r < R; r++) acc[r] = acc_t{0, 0, 0, 0};
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int g = 0; g < TG; g++) acc[r][g] = acc_t{0, 0, 0, 0};
   uint4 b0[U][R], b1[U][R];
-  AFrag<AMODE> x0[U], x1[U];
-  auto load = [&](uint4 (&b)[U][R], AFrag<AMODE> (&x)[U], int t0) {
+  AFrag<AMODE> x0[U][TG], x1[U][TG];
+  auto load = [&](uint4 (&b)[U][R], AFrag<AMODE> (&x)[U][TG], int t0) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int t = min(t0 + u, last);
 #pragma unroll
       for (int r = 0; r < R; r++) b[u][r] = wbase[(size_t)t * tstride + goff[r]];
-      x[u] = load_a<AMODE>(a, min(kb0 + t, a.KB - 1), lane);
+#pragma unroll
+      for (int g = 0; g < TG; g++) x[u][g] = load_a<AMODE>(a, min(kb0 + t, a.KB - 1), g, lane);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  auto consume = [&](const uint4 (&b)[U][R], const AFrag<AMODE> (&x)[U], int t0) {
+  auto consume = [&](const uint4 (&b)[U][R], const AFrag<AMODE> (&x)[U][TG], int t0) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      // clamped repeats add exactly 0: their activations are zeroed (the
-      // weights are finite int8, so 0 * w == 0 even when X holds Inf/NaN)
-      AFrag<AMODE> xv = x[u];
-      if (!(t0 + u < n_t)) {
+      WOps<AMODE> wo[R];
 #pragma unroll
-        for (int q = 0; q < (int)(sizeof(xv.v) / sizeof(uint4)); q++) xv.v[q] = make_uint4(0, 0, 0, 0);
+      for (int r = 0; r < R; r++) wo[r] = prepare_w<AMODE>(b[u][r]);
+#pragma unroll
+      for (int g = 0; g < TG; g++) {
+        // clamped repeats add exactly 0: their activations are zeroed (the
+        // weights are finite int8, so 0 * w == 0 even when X holds Inf/NaN)
+        AFrag<AMODE> xv = x[u][g];
+        if (!(t0 + u < n_t)) {
+#pragma unroll
+          for (int q = 0; q < (int)(sizeof(xv.v) / sizeof(uint4)); q++) xv.v[q] = make_uint4(0, 0, 0, 0);
+        }
+        const XOps<AMODE> xo = prepare_x<AMODE>(xv);
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r][g] = mma_x<AMODE>(wo[r], xo, acc[r][g]);
       }
-      const XOps<AMODE> xo = prepare_x<AMODE>(xv);
-#pragma unroll
-      for (int r = 0; r < R; r++) acc[r] = mma_x<AMODE>(b[u][r], xo, acc[r]);
     }
   };
 
@@ -213,18 +236,22 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
   consume(b1, x1, t + U);
 
 #pragma unroll
-  for (int r = 0; r < R; r++) s_part[r][wv][lane] = acc[r];
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int g = 0; g < TG; g++) s_part[r][g][wv][lane] = acc[r][g];
   __syncthreads();
   if (wv != 0) return;
-  // lane holds D[n .. n+3][m]: m = lane & 15, n = 16 g + 4 (lane >> 4)
-  const int m = lane & 15;
-  if (m >= a.M) return;
+  // lane holds D[n .. n+3][m]: m = 16 tg + (lane & 15), n = 16 g + 4 (lane >> 4)
+#pragma unroll
+  for (int tg = 0; tg < TG; tg++)
 #pragma unroll
   for (int rg = 0; rg < R; rg++) {
-    acc_t tot = s_part[rg][0][lane];
+    const int m = tg * 16 + (lane & 15);
+    if (m >= a.M) continue;
+    acc_t tot = s_part[rg][tg][0][lane];
 #pragma unroll
     for (int w = 1; w < 4; w++) {
-      const acc_t p = s_part[rg][w][lane];
+      const acc_t p = s_part[rg][tg][w][lane];
 #pragma unroll
       for (int q = 0; q < 4; q++) tot[q] += p[q];
     }
@@ -262,24 +289,31 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
 }
 
 bool gemm_small_supported(const GemmLaunch& L) {
-  if (L.M < 1 || L.M > 16) return false;
+  if (L.M < 1 || L.M > 64) return false;
   if (L.amode == A_I8) return true;                    // code tiles, any K
   const int epv = (L.amode == A_F32X3) ? 4 : 8;        // elements per 16 bytes
   if (L.K % epv != 0 || L.lda % epv != 0) return false;
   return (((uintptr_t)L.A) & 15) == 0;
 }
 
-template <int AMODE, int R>
-static void launch_small_r(const GemmSmallArgs& a, int u, hipStream_t st) {
+template <int AMODE, int R, int TG>
+static void launch_small_rt(const GemmSmallArgs& a, int u, hipStream_t st) {
   const dim3 grid(cdiv(a.NG, R)), block(256);
-  if (u == 4) hipLaunchKernelGGL((gemm_small_kernel<AMODE, 4, R>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((gemm_small_kernel<AMODE, 2, R>), grid, block, 0, st, a);
+  if (u == 4) hipLaunchKernelGGL((gemm_small_kernel<AMODE, 4, R, TG>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((gemm_small_kernel<AMODE, 2, R, TG>), grid, block, 0, st, a);
+}
+
+template <int AMODE, int R>
+static void launch_small_r(const GemmSmallArgs& a, int u, int tg, hipStream_t st) {
+  if (tg == 1) launch_small_rt<AMODE, R, 1>(a, u, st);
+  else if (tg == 2) launch_small_rt<AMODE, R, 2>(a, u, st);
+  else launch_small_rt<AMODE, R, 4>(a, u, st);
 }
 
 template <int AMODE>
-static void launch_small_mode(const GemmSmallArgs& a, int u, int r, hipStream_t st) {
-  if (r == 4) launch_small_r<AMODE, 4>(a, u, st);
-  else launch_small_r<AMODE, 1>(a, u, st);
+static void launch_small_mode(const GemmSmallArgs& a, int u, int r, int tg, hipStream_t st) {
+  if (r == 4) launch_small_r<AMODE, 4>(a, u, tg, st);
+  else launch_small_r<AMODE, 1>(a, u, tg, st);
 }
 
 hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st) {
@@ -298,6 +332,7 @@ hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st) {
   a.K = L.K;
   a.KB = cdiv(L.K, 64);
   a.NG = cdiv(L.N, 16);
+  a.MG = cdiv(L.M, 16);
   a.ep = L.ep;
   a.out = L.out;
   if (L.amode == A_I8 && L.out != OUT_I32 && !L.xs) return hipErrorInvalidValue;
@@ -305,12 +340,15 @@ hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st) {
   // four row groups per work-group once there are work-groups to spare
   // (>= 2048 row groups: the lm_head), else one
   const int r = a.NG >= 2048 ? 4 : 1;
-  const int u = (r == 1 && n_t >= 8) ? 4 : 2;
+  const int tg = a.MG <= 1 ? 1 : (a.MG <= 2 ? 2 : 4);
+  // batches of 4 tiles only with one token group: more activation fragments
+  // in flight push the waves past 256 VGPRs (one wave per SIMD)
+  const int u = (r == 1 && n_t >= 8 && tg == 1) ? 4 : 2;
   switch (L.amode) {
-    case A_I8: launch_small_mode<A_I8>(a, u, r, st); break;
-    case A_BF16: launch_small_mode<A_BF16>(a, u, r, st); break;
-    case A_F16: launch_small_mode<A_F16>(a, u, r, st); break;
-    default: launch_small_mode<A_F32X3>(a, u, r, st); break;
+    case A_I8: launch_small_mode<A_I8>(a, u, r, tg, st); break;
+    case A_BF16: launch_small_mode<A_BF16>(a, u, r, tg, st); break;
+    case A_F16: launch_small_mode<A_F16>(a, u, r, tg, st); break;
+    default: launch_small_mode<A_F32X3>(a, u, r, tg, st); break;
   }
   return hipGetLastError();
 }
