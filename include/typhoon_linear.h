@@ -103,6 +103,13 @@ int tl_registry_entries(void);
  * with 8 rows).  Zeros restore the built-in planner. */
 int tl_gemv_set_plan(int rows, int u);
 
+/* Tuning override of the int8 MFMA GEMM (W8A8, M > 16) for every later call
+ * in the process: -1 restores the planner; 0..2 stage both operands through
+ * LDS (tiles 128x192, 64x128, 128x128); 3..7 load weight tiles straight into
+ * registers (128x192 with prefetch 3, 5, 7 stages; 64x128 and 128x128 with
+ * prefetch 7). */
+int tl_gemm_i8_set_cfg(int cfg);
+
 /* ---- device-resident weights ------------------------------------------- */
 typedef struct tl_weights tl_weights;
 

@@ -331,6 +331,37 @@ def test_w8a8_gemm(lin, orc, dev, M, N, K):
     W.close()
 
 
+@pytest.mark.parametrize("M,N,K", [(80, 130, 300), (100, 2048, 6144), (300, 1000, 1000), (1024, 6144, 2048)])
+def test_w8a8_gemm_configs_bit_exact(lin, orc, dev, M, N, K):
+    """Every int8 MFMA GEMM configuration (both LDS-staged layouts and the
+    register-loaded weight variants with each prefetch depth) gives the exact
+    int32 accumulators and the exact fp32 epilogue, on ragged shapes (M, N, K
+    off the tile sizes, K shorter than the prefetch distance) and full size."""
+    import torch
+    rng = np.random.default_rng(M + N + K)
+    x, w, s = make(rng, M, N, K)
+    xq, xs = orc.quantize_rows(x)
+    want = orc.int_acc(xq, w)
+    want_y = exact_epilogue(want, s, xs)
+    W = lin.DeviceWeights.from_codes(w, s)
+    xqd, xd = torch.from_numpy(xq).to(dev), torch.from_numpy(x).to(dev)
+    lib = lin.load_library()
+    try:
+        for cfg in range(8):
+            say(f"w8a8 gemm cfg={cfg} M={M} N={N} K={K}")
+            assert lib.tl_gemm_i8_set_cfg(cfg) == 0
+            acc = torch.full((M, N), -7, dtype=torch.int32, device=dev)
+            lin.gemm_acc_dev(xqd, W, acc)
+            y = torch.empty((M, N), dtype=torch.float32, device=dev)
+            lin.w8a8_linear_f32_dev(xd, W, y)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(acc.cpu().numpy(), want)
+            np.testing.assert_array_equal(y.cpu().numpy(), want_y)
+    finally:
+        lib.tl_gemm_i8_set_cfg(-1)
+    W.close()
+
+
 def test_w8a8_prefill_full_size(lin, orc, dev):
     """Config shape M=1024, N=6144, K=2048: codes on a row subset bit-exact,
     full accumulators bit-exact, fp32 outputs of sampled rows within 1e-5."""

@@ -680,6 +680,13 @@ int tl_gemv_set_plan(int rows, int u) {
   });
 }
 
+int tl_gemm_i8_set_cfg(int cfg) {
+  return guarded("tl_gemm_i8_set_cfg", [&] {
+    REQUIRE(cfg >= -1 && cfg <= 7, "cfg must be -1 (planner) or 0..7");
+    gemm_i8_set_cfg(cfg);
+  });
+}
+
 int tl_register_weights(const int8_t* w_int8, const float* scales, int rows, int cols) {
   return guarded("tl_register_weights", [&] {
     std::lock_guard<std::mutex> lk(g_host_mu);

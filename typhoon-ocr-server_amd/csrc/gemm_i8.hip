@@ -259,17 +259,209 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds_kernel(GemmI8Args a)
 }
 
 // ---------------------------------------------------------------------------
+// Column-split variant: the 4 waves of a work-group split the tile's N columns
+// (wave w owns weight row groups ng0 + FN w .. ng0 + FN w + FN - 1) and all
+// share its MT activation row groups.  Weight tiles are private to one wave,
+// so they go from global memory straight into that wave's registers (one
+// 16-byte load per lane per tile, already in MFMA operand order); only the
+// shared activation tiles pass through an LDS ring.  Per 64-wide K stage and
+// work-group: MT KiB copied into LDS, 4 MT KiB of LDS fragment reads, 4 FN KiB
+// of register loads and 4 MT FN MFMAs (against 3 (MT + NT) KiB of LDS traffic
+// in gemm_i8_lds_kernel with its 2 x 2 wave grid).
+//
+// Pipeline: stage s's copies and loads are issued D steps ahead (its weight
+// registers are set s % (D + 1), its LDS buffer s % D).  Step s waits for
+// stage s + 1, then one barrier makes its activation tiles visible and frees
+// buffer s % D, whose copy for stage s + D follows; the MFMAs of stage s run
+// interleaved with the fragment reads of stage s + 1 and the issue of stage
+// s + D.  The loop is unrolled D + 1 times so every register set index is a
+// compile-time constant.  Copies and loads are branch-free (the compiler's
+// own vmcnt waits stay exact only over straight-line code): stages past the
+// last one re-read the last k-block, and nothing reads what they bring in.
+template <int MT, int FN, int D>
+__global__ __launch_bounds__(256) void gemm_i8_wcol_kernel(GemmI8Args a) {
+  constexpr int NW = 4, NT = NW * FN, PA = MT / NW;
+  constexpr int NB = D + 1;          // weight register sets
+  constexpr int PS = PA + FN;        // vector memory operations per wave per stage
+  static_assert(MT % NW == 0, "activation copies must divide over the waves");
+  static_assert(NB % 2 == 0, "fragment double buffer needs an even unroll");
+  static_assert(PS * (D - 1) < 64, "vmcnt range");
+  __shared__ uint4 sA[D * MT * 64];
+
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+  const int ntiles = a.ntm * a.ntn;
+  int t = blockIdx.x;
+  if (ntiles % 8 == 0) t = (blockIdx.x % 8) * (ntiles / 8) + blockIdx.x / 8;
+  const int tn = t / a.ntm, tm = t - (t / a.ntm) * a.ntm;
+  const int mg0 = tm * MT, ng0 = tn * NT + wv * FN;
+
+  const uint4* A4 = reinterpret_cast<const uint4*>(a.At) + lane;
+  const uint4* B4 = reinterpret_cast<const uint4*>(a.Bt) + lane;
+  const int KB = a.KB;
+  const size_t astride = (size_t)a.MG * 64, bstride = (size_t)a.NG * 64;
+  // rows / columns past the matrix edge re-read a valid tile (their
+  // accumulators are never stored)
+  const uint4* asrc[PA];
+#pragma unroll
+  for (int p = 0; p < PA; p++) asrc[p] = A4 + (size_t)min(mg0 + wv + NW * p, a.MG - 1) * 64;
+  const uint4* bsrc[FN];
+#pragma unroll
+  for (int j = 0; j < FN; j++) bsrc[j] = B4 + (size_t)min(ng0 + j, a.NG - 1) * 64;
+  const uint32_t sbase = lds_addr(sA);
+  constexpr uint32_t SBYTES = MT * 1024;
+
+  uint4 wb[NB][FN];
+  auto copy_a = [&](int st, int p) {
+    const uint4* g = asrc[p] + (size_t)min(st, KB - 1) * astride;
+    dma_tile(g, sbase + (uint32_t)(st % D) * SBYTES + (uint32_t)(wv + NW * p) * 1024u);
+  };
+  auto load_b = [&](int st, int c, int j) { wb[c][j] = bsrc[j][(size_t)min(st, KB - 1) * bstride]; };
+
+  // epilogue operands first (older than every copy, so the first wait covers them)
+  const int mrow = lane & 15;
+  const int ncol = (lane >> 4) * 4;
+  float4 e_ws[FN], e_b[FN];
+  float e_xs[MT];
+#pragma unroll
+  for (int j = 0; j < FN; j++) {
+    const int n = (ng0 + j) * 16 + ncol;
+    float w4[4], b4[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int nn = min(n + r, a.N - 1);
+      w4[r] = a.ws[nn];
+      b4[r] = a.bias ? a.bias[nn] : 0.0f;
+    }
+    e_ws[j] = make_float4(w4[0], w4[1], w4[2], w4[3]);
+    e_b[j] = make_float4(b4[0], b4[1], b4[2], b4[3]);
+  }
+#pragma unroll
+  for (int i = 0; i < MT; i++) {
+    const int m = min((mg0 + i) * 16 + mrow, a.M - 1);
+    e_xs[i] = (a.out == OUT_I32) ? 0.0f : a.xs[m];
+  }
+
+  v4i acc[MT][FN];
+#pragma unroll
+  for (int i = 0; i < MT; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++) acc[i][j] = v4i{0, 0, 0, 0};
+
+  uint4 fa[2][MT];
+  auto read_frags = [&](int st, int c) {
+    const uint4* buf = sA + (size_t)(st % D) * (MT * 64);
+#pragma unroll
+    for (int i = 0; i < MT; i++) fa[c][i] = buf[i * 64 + lane];
+  };
+
+  // prologue: stages 0 .. D-1 in flight, stage 0 visible and its fragments read
+#pragma unroll
+  for (int b = 0; b < D; b++) {
+#pragma unroll
+    for (int p = 0; p < PA; p++) copy_a(b, p);
+#pragma unroll
+    for (int j = 0; j < FN; j++) load_b(b, b, j);
+  }
+  wait_vm<PS * (D - 1)>();
+  stage_barrier();
+  read_frags(0, 0);
+
+  // step s (set b = s % NB, fragment set f = s & 1)
+  auto step = [&](int st, int b, int f) {
+    wait_vm<PS * (D - 2)>();   // stage s + 1 landed (this wave's part)
+    wait_lgkm0();              // this wave's reads of stage s are done
+    stage_barrier();           // stage s + 1 visible; buffer s % D free
+    constexpr int NMEM = MT + PS;
+    const int nb = (b + D) % NB;
+    auto mem_op = [&](int q) {
+      if (q < PA) copy_a(st + D, q);
+      else if (q < PS) load_b(st + D, nb, q - PA);
+      else {
+        const uint4* buf = sA + (size_t)((st + 1) % D) * (MT * 64);
+        fa[f ^ 1][q - PS] = buf[(q - PS) * 64 + lane];
+      }
+    };
+#pragma unroll
+    for (int m = 0; m < MT * FN; m++) {
+      const int i = m / FN, j = m % FN;
+      acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, wb[b][j]),
+                                                        __builtin_bit_cast(v4i, fa[f][i]), acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (m < NMEM) mem_op(m);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int q = MT * FN; q < NMEM; q++) mem_op(q);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  const int kfull = KB - KB % NB;
+  for (int st = 0; st < kfull; st += NB) {
+#pragma unroll
+    for (int b = 0; b < NB; b++) step(st + b, b, b & 1);
+  }
+#pragma unroll
+  for (int b = 0; b < NB - 1; b++)
+    if (kfull + b < KB) step(kfull + b, b, b & 1);
+
+  wait_vm<0>();   // no copy may still be landing in LDS when the work-group exits
+
+  const bool vec_ok = ((a.ldy & 3) == 0) && ((((uintptr_t)a.Y) & 15) == 0);
+#pragma unroll
+  for (int i = 0; i < MT; i++) {
+    const int m = (mg0 + i) * 16 + mrow;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+      const int n = (ng0 + j) * 16 + ncol;
+      if (n >= a.N) continue;
+      const v4i c = acc[i][j];
+      if (a.out == OUT_I32) {
+        int32_t* yp = reinterpret_cast<int32_t*>(a.Y) + (size_t)m * a.ldy + n;
+        if (vec_ok && n + 4 <= a.N) {
+          *reinterpret_cast<int4*>(yp) = make_int4(c[0], c[1], c[2], c[3]);
+        } else {
+          for (int r = 0; r < 4 && n + r < a.N; r++) yp[r] = c[r];
+        }
+        continue;
+      }
+      const float ws4[4] = {e_ws[j].x, e_ws[j].y, e_ws[j].z, e_ws[j].w};
+      const float b4[4] = {e_b[j].x, e_b[j].y, e_b[j].z, e_b[j].w};
+      float y[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        y[r] = __fmul_rn(__fmul_rn((float)c[r], ws4[r]), e_xs[i]);
+        if (a.bias) y[r] = __fadd_rn(y[r], b4[r]);
+      }
+      float* yp = reinterpret_cast<float*>(a.Y) + (size_t)m * a.ldy + n;
+      if (vec_ok && n + 4 <= a.N) {
+        *reinterpret_cast<float4*>(yp) = make_float4(y[0], y[1], y[2], y[3]);
+      } else {
+        for (int r = 0; r < 4 && n + r < a.N; r++) yp[r] = y[r];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // planning and launch
 // ---------------------------------------------------------------------------
 // Measured on MI355X at M = 1024 (ring depth and stage width swept):
 // cfg 0: 128 x 192 tiles (8 x 12 fragments), K stage 64, 4 buffers (80 KiB)
-//        best for N = 6144, K = 2048 (256 work-groups)
+//        (N = 6144, K = 2048: 22.0 us; cfg 4 below takes its place)
 // cfg 1:  64 x 128 tiles (4 x 8),  K stage 64, 8 buffers (96 KiB)
 //        best for N = 2048, K = 6144 (256 work-groups)
 // cfg 2: 128 x 128 tiles (8 x 8),  K stage 64, 8 buffers (128 KiB)
+// cfg 3..7: column-split kernel (weights straight to registers)
+//   3: 128 x 192, prefetch 3   4: 128 x 192, prefetch 5   5: 128 x 192, prefetch 7
+//   6:  64 x 128, prefetch 7   7: 128 x 128, prefetch 7
 static void i8_cfg(int cfg, int& mt, int& nt) {
   if (cfg == 0) { mt = 8; nt = 12; }
   else if (cfg == 1) { mt = 4; nt = 8; }
+  else if (cfg == 2) { mt = 8; nt = 8; }
+  else if (cfg <= 5) { mt = 8; nt = 12; }
+  else if (cfg == 6) { mt = 4; nt = 8; }
   else { mt = 8; nt = 8; }
 }
 
@@ -281,10 +473,13 @@ int gemm_i8_pick_cfg(int M, int N, int K) {
   (void)K;
   const int MG = cdiv(M, 16), NG = cdiv(N, 16);
   // the configuration whose tile count best fills 256 CUs (at least one
-  // full wave of work-groups, then the fewest idle CUs in the last wave)
+  // full wave of work-groups, then the fewest idle CUs in the last wave).
+  // 128 x 192 tiles run on the register-loaded weight kernel (cfg 4: 20.7 us
+  // against 22.0 us for cfg 0 at M = 1024, N = 6144, K = 2048); at 64 x 128
+  // the two kernels measured the same (23.7 / 24.0 us, N = 2048, K = 6144).
   int best = 2;
   double best_eff = -1.0;
-  for (int cfg : {0, 1, 2}) {
+  for (int cfg : {4, 1, 2}) {
     int mt, nt;
     i8_cfg(cfg, mt, nt);
     const int tiles = cdiv(MG, mt) * cdiv(NG, nt);
@@ -323,12 +518,16 @@ hipError_t launch_gemm_i8(const GemmLaunch& L, hipStream_t st) {
   a.ntm = cdiv(a.MG, mt);
   a.ntn = cdiv(a.NG, nt);
   const int blocks = a.ntm * a.ntn;
-  if (cfg == 0)
-    hipLaunchKernelGGL((gemm_i8_lds_kernel<8, 12, 1, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
-  else if (cfg == 1)
-    hipLaunchKernelGGL((gemm_i8_lds_kernel<4, 8, 1, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((gemm_i8_lds_kernel<8, 8, 1, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
+  switch (cfg) {
+    case 0: hipLaunchKernelGGL((gemm_i8_lds_kernel<8, 12, 1, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((gemm_i8_lds_kernel<4, 8, 1, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((gemm_i8_lds_kernel<8, 8, 1, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((gemm_i8_wcol_kernel<8, 3, 3>), dim3(blocks), dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((gemm_i8_wcol_kernel<8, 3, 5>), dim3(blocks), dim3(256), 0, st, a); break;
+    case 5: hipLaunchKernelGGL((gemm_i8_wcol_kernel<8, 3, 7>), dim3(blocks), dim3(256), 0, st, a); break;
+    case 6: hipLaunchKernelGGL((gemm_i8_wcol_kernel<4, 2, 7>), dim3(blocks), dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL((gemm_i8_wcol_kernel<8, 2, 7>), dim3(blocks), dim3(256), 0, st, a); break;
+  }
   return hipGetLastError();
 }
 

@@ -39,6 +39,7 @@ SIGNATURES = {
     "tl_version": (ctypes.c_char_p, []),
     "tl_device_count": (_int, []),
     "tl_gemv_set_plan": (_int, [_int, _int]),
+    "tl_gemm_i8_set_cfg": (_int, [_int]),
     "tl_register_weights": (_int, [_i8p, _f32p, _int, _int]),
     "tl_evict_weights": (_int, [_i8p]),
     "tl_registry_clear": (None, []),
