@@ -123,6 +123,32 @@ tl_weights *tl_weights_create(const int8_t *w_int8, const float *scales, int row
 tl_weights *tl_weights_quantize_dev(const float *w_fp32, int rows, int cols, int8_t *codes_out,
                                     float *scales_out, void *stream);
 void tl_weights_destroy(tl_weights *w);
+
+/* Packed-weight cache file (no counterpart in the reference, which
+ * re-quantizes every fp32 matrix at load: decoder.py:248-260 through
+ * w8a32_quantize, kernel/w8a32_kernel.c:63-108).  A file is a sequence of
+ * named records, each holding one matrix's HBM tiles and scales exactly as
+ * resident, with a checksum; loading is a copy into HBM with no kernel.
+ *   tl_weights_save   writes W as record `name` (append != 0 adds it at the
+ *                     end of an existing file, else the file is replaced)
+ *   tl_weights_load   reads the first record called `name` into HBM on the
+ *                     current device; NULL on error (missing record, bad
+ *                     magic/version/sizes, checksum mismatch)
+ *   tl_weights_cache_list  number of records (-1 on error); their names,
+ *                     one per line, into names when it is non-NULL */
+int tl_weights_save(const tl_weights *W, const char *path, const char *name, int append);
+tl_weights *tl_weights_load(const char *path, const char *name);
+int tl_weights_cache_list(const char *path, char *names, size_t names_len);
+
+/* Copies W's codes out as row-major int8 [rows x cols] and its fp32 scales
+ * [rows] (either may be NULL), into host or device memory. */
+int tl_weights_export(const tl_weights *W, int8_t *codes, float *scales, int dst_on_device);
+
+/* Makes W the device copy the host-pointer entry points use for the host
+ * arrays (w_int8 [rows x cols], scales [rows]), which must hold W's codes
+ * and scales (e.g. from tl_weights_export): later calls on those arrays
+ * upload nothing.  On success the registry owns W (do not destroy it). */
+int tl_registry_adopt(const int8_t *w_int8, const float *scales, tl_weights *W);
 int tl_weights_rows(const tl_weights *w);
 int tl_weights_cols(const tl_weights *w);
 size_t tl_weights_bytes(const tl_weights *w);

@@ -330,6 +330,23 @@ const tl_weights* registry_get(const int8_t* w, const float* s, int rows, int co
   return W;
 }
 
+// makes W (owned by the registry from here on) the entry of host arrays
+// (w, s) that hold its codes and scales; replaces an existing entry
+void registry_put(const int8_t* w, const float* s, tl_weights* W) {
+  const uint64_t fp = fingerprint(w, s, W->rows, W->cols);
+  std::lock_guard<std::mutex> lk(g_reg_mu);
+  RegKey key{w, s, W->rows, W->cols, W->dev};
+  auto it = g_reg.find(key);
+  if (it != g_reg.end()) {
+    g_reg_bytes -= it->second.W->bytes;
+    if (it->second.W != W) weights_free(it->second.W);
+    g_reg.erase(it);
+  }
+  registry_evict_lru_locked(W->bytes);
+  g_reg[key] = RegEntry{W, fp, ++g_tick};
+  g_reg_bytes += W->bytes;
+}
+
 // --------------------------------------------------------------------------
 // host-call context (Part 1): one per device, calls serialized
 // --------------------------------------------------------------------------
@@ -527,25 +544,161 @@ void op_w8a16(const void* X, int x_type, const tl_weights* W, const float* bias,
   run_gemm(ws, L, st);
 }
 
+// Quantizes rows of host fp32 on the GPU and returns codes and scales to the
+// host.  With `pack` (the weight quantizers) the same device codes are also
+// packed into HBM tiles as they are produced, and the packed matrix becomes
+// the registry entry of the returned host arrays: the load step quantizes and
+// packs in one pass, and the first linear call on those arrays uploads
+// nothing (the reference quantizes on the CPU at load, decoder.py:248-260,
+// then hands the arrays to the C decoder, decoder.c:393-423).
 void host_quantize(const char* fn, const float* src, int8_t* dst, float* scales, int rows,
-                   int cols, bool clamp127) {
+                   int cols, bool clamp127, bool pack) {
   (void)fn;
   REQUIRE(src && dst && scales, "NULL pointer");
   REQUIRE(rows >= 1 && cols >= 1, "rows and cols must be >= 1");
   std::lock_guard<std::mutex> lk(g_host_mu);
   HostCtx& c = host_ctx(current_device());
-  // chunks of at most 64 MiB of fp32 input
+  // chunks of at most 64 MiB of fp32 input, whole 16-row groups when packing
   int chunk = (int)std::max<size_t>(1, ((size_t)64 << 20) / ((size_t)cols * 4));
+  if (pack) chunk = std::max(16, chunk & ~15);
   if (chunk > rows) chunk = rows;
-  c.y.ensure((size_t)chunk * cols, c.st);
-  c.xs.ensure((size_t)chunk * sizeof(float), c.st);
-  for (int r0 = 0; r0 < rows; r0 += chunk) {
-    const int nr = std::min(chunk, rows - r0);
-    h2d(c, c.x, src + (size_t)r0 * cols, (size_t)nr * cols * sizeof(float));
-    HIP_OK(launch_quantize_rows(static_cast<const float*>(c.x.p), static_cast<int8_t*>(c.y.p),
-                                static_cast<float*>(c.xs.p), nr, cols, clamp127, c.st));
-    d2h(c, dst + (size_t)r0 * cols, c.y.p, (size_t)nr * cols);
-    d2h(c, scales + r0, c.xs.p, (size_t)nr * sizeof(float));
+  tl_weights* W = nullptr;
+  if (pack) {
+    W = weights_alloc(rows, cols);
+  }
+  try {
+    if (W) HIP_OK(hipMemsetAsync(W->scales, 0, (size_t)W->NG * 16 * sizeof(float), c.st));
+    c.y.ensure((size_t)chunk * cols, c.st);
+    c.xs.ensure((size_t)chunk * sizeof(float), c.st);
+    for (int r0 = 0; r0 < rows; r0 += chunk) {
+      const int nr = std::min(chunk, rows - r0);
+      h2d(c, c.x, src + (size_t)r0 * cols, (size_t)nr * cols * sizeof(float));
+      HIP_OK(launch_quantize_rows(static_cast<const float*>(c.x.p), static_cast<int8_t*>(c.y.p),
+                                  static_cast<float*>(c.xs.p), nr, cols, clamp127, c.st));
+      if (W) {
+        HIP_OK(launch_pack_tiles_rows(static_cast<const int8_t*>(c.y.p), nr, cols, W->NG, r0 / 16, W->tiles,
+                                      c.st));
+        HIP_OK(hipMemcpyAsync(W->scales + r0, c.xs.p, (size_t)nr * sizeof(float), hipMemcpyDeviceToDevice,
+                              c.st));
+      }
+      d2h(c, dst + (size_t)r0 * cols, c.y.p, (size_t)nr * cols);
+      d2h(c, scales + r0, c.xs.p, (size_t)nr * sizeof(float));
+    }
+  } catch (...) {
+    if (W) {
+      (void)hipStreamSynchronize(c.st);
+      weights_free(W);
+    }
+    throw;
+  }
+  if (W) registry_put(dst, scales, W);
+}
+
+// --------------------------------------------------------------------------
+// packed-weight cache file
+// --------------------------------------------------------------------------
+// A file is a sequence of self-describing records, one per matrix:
+//   RecHeader (64 bytes, little-endian)
+//   name      (name_len bytes, zero padded to a multiple of 64)
+//   tiles     (NG * KB * 1024 bytes: the HBM tile array as resident)
+//   scales    (NG * 16 * 4 bytes: fp32, zero padded)
+// The payload is copied between the file and HBM as it is, with no kernel.
+// `checksum` covers tiles then scales (cache_hash below); readers check the
+// magic, the version, that the sizes follow from rows and cols, and the sum.
+constexpr char kRecMagic[8] = {'T', 'L', 'W', 'C', 'R', 'E', 'C', '1'};
+constexpr uint32_t kRecVersion = 1;
+struct RecHeader {
+  char magic[8];
+  uint32_t version;
+  uint32_t name_len;
+  int32_t rows, cols, NG, KB;
+  uint64_t tile_bytes, scale_bytes, checksum;
+  uint64_t reserved;
+};
+static_assert(sizeof(RecHeader) == 64, "record header is 64 bytes");
+
+size_t pad64(size_t n) { return (n + 63) & ~(size_t)63; }
+
+// 64-bit streaming hash over 32-byte blocks (four independent multiply-xor
+// lanes, so it runs at memory speed); every chunk but the last is a multiple
+// of 32 bytes
+struct CacheHash {
+  uint64_t h[4] = {0x243f6a8885a308d3ull, 0x13198a2e03707344ull, 0xa4093822299f31d0ull,
+                   0x082efa98ec4e6c89ull};
+  uint64_t n = 0;
+  static uint64_t step(uint64_t h, uint64_t v) {
+    h ^= v;
+    h *= 0x9e3779b97f4a7c15ull;
+    return h ^ (h >> 32);
+  }
+  void add(const void* p, size_t bytes) {
+    const uint8_t* b = static_cast<const uint8_t*>(p);
+    size_t i = 0;
+    for (; i + 32 <= bytes; i += 32) {
+      uint64_t v[4];
+      std::memcpy(v, b + i, 32);
+      h[0] = step(h[0], v[0]);
+      h[1] = step(h[1], v[1]);
+      h[2] = step(h[2], v[2]);
+      h[3] = step(h[3], v[3]);
+    }
+    for (; i < bytes; i++) h[i & 3] = step(h[i & 3], (uint64_t)b[i] | 0x100);
+    n += bytes;
+  }
+  uint64_t value() const { return mix64(mix64(mix64(mix64(n, h[0]), h[1]), h[2]), h[3]); }
+};
+
+struct File {
+  std::FILE* f = nullptr;
+  ~File() {
+    if (f) std::fclose(f);
+  }
+};
+
+constexpr size_t kCacheChunk = (size_t)64 << 20;
+
+// reads the next record header (and name) at the current position; false at
+// a clean end of file
+bool read_rec_header(std::FILE* f, RecHeader& h, std::string& name) {
+  const size_t got = std::fread(&h, 1, sizeof h, f);
+  if (got == 0 && std::feof(f)) return false;
+  REQUIRE(got == sizeof h, "truncated record header");
+  REQUIRE(std::memcmp(h.magic, kRecMagic, 8) == 0, "not a weight cache record (bad magic)");
+  REQUIRE(h.version == kRecVersion, "unsupported weight cache version");
+  REQUIRE(h.rows > 0 && h.cols > 0 && h.NG == cdiv(h.rows, 16) && h.KB == cdiv(h.cols, 64),
+          "inconsistent record shape");
+  REQUIRE(h.tile_bytes == (uint64_t)h.NG * h.KB * 1024 && h.scale_bytes == (uint64_t)h.NG * 16 * 4,
+          "inconsistent record sizes");
+  REQUIRE(h.name_len < 4096, "record name too long");
+  std::vector<char> nb(pad64(h.name_len));
+  REQUIRE(std::fread(nb.data(), 1, nb.size(), f) == nb.size(), "truncated record name");
+  name.assign(nb.data(), h.name_len);
+  return true;
+}
+
+// streams `bytes` from the file into device memory through pinned staging
+void file_to_device(std::FILE* f, void* dst, size_t bytes, PinnedBuf& stage, CacheHash& hash,
+                    hipStream_t st) {
+  stage.ensure(std::min(bytes, kCacheChunk));
+  for (size_t off = 0; off < bytes; off += kCacheChunk) {
+    const size_t n = std::min(kCacheChunk, bytes - off);
+    HIP_OK(hipStreamSynchronize(st));  // staging idle
+    REQUIRE(std::fread(stage.p, 1, n, f) == n, "truncated record payload");
+    hash.add(stage.p, n);
+    HIP_OK(hipMemcpyAsync(static_cast<char*>(dst) + off, stage.p, n, hipMemcpyHostToDevice, st));
+  }
+  HIP_OK(hipStreamSynchronize(st));
+}
+
+void device_to_file(std::FILE* f, const void* src, size_t bytes, PinnedBuf& stage, CacheHash* hash,
+                    hipStream_t st) {
+  stage.ensure(std::min(bytes, kCacheChunk));
+  for (size_t off = 0; off < bytes; off += kCacheChunk) {
+    const size_t n = std::min(kCacheChunk, bytes - off);
+    HIP_OK(hipMemcpyAsync(stage.p, static_cast<const char*>(src) + off, n, hipMemcpyDeviceToHost, st));
+    HIP_OK(hipStreamSynchronize(st));
+    if (hash) hash->add(stage.p, n);
+    if (f) REQUIRE(std::fwrite(stage.p, 1, n, f) == n, "write failed");
   }
 }
 
@@ -557,22 +710,22 @@ void host_quantize(const char* fn, const float* src, int8_t* dst, float* scales,
 extern "C" {
 
 void w8a32_quantize(const float* w_fp32, int8_t* w_int8, float* scales, int rows, int cols) {
-  guarded("w8a32_quantize", [&] { host_quantize("w8a32_quantize", w_fp32, w_int8, scales, rows, cols, true); });
+  guarded("w8a32_quantize", [&] { host_quantize("w8a32_quantize", w_fp32, w_int8, scales, rows, cols, true, true); });
 }
 
 void w8a8_quantize_weights(const float* w_fp32, int8_t* w_int8, float* w_scales, int rows, int cols) {
   guarded("w8a8_quantize_weights",
-          [&] { host_quantize("w8a8_quantize_weights", w_fp32, w_int8, w_scales, rows, cols, true); });
+          [&] { host_quantize("w8a8_quantize_weights", w_fp32, w_int8, w_scales, rows, cols, true, true); });
 }
 
 void w8a8_quantize_activations(const float* x_fp32, int8_t* x_int8, float* x_scales, int batch, int K) {
   guarded("w8a8_quantize_activations",
-          [&] { host_quantize("w8a8_quantize_activations", x_fp32, x_int8, x_scales, batch, K, true); });
+          [&] { host_quantize("w8a8_quantize_activations", x_fp32, x_int8, x_scales, batch, K, true, false); });
 }
 
 void w8a16_quantize_weights(const float* w_fp32, int8_t* w_int8, float* scales, int rows, int cols) {
   guarded("w8a16_quantize_weights",
-          [&] { host_quantize("w8a16_quantize_weights", w_fp32, w_int8, scales, rows, cols, true); });
+          [&] { host_quantize("w8a16_quantize_weights", w_fp32, w_int8, scales, rows, cols, true, true); });
 }
 
 void w8a32_linear(const float* X, const int8_t* w_int8, const float* scales, const float* bias,
@@ -971,6 +1124,153 @@ int tl_w8a8_gemm_acc_dev(const int8_t* x_int8, const tl_weights* W, int32_t* acc
     check_weights(W);
     REQUIRE(batch >= 1 && x_int8 && acc, "bad arguments");
     op_w8a8_codes(x_int8, nullptr, W, nullptr, acc, OUT_I32, batch, static_cast<hipStream_t>(stream));
+  });
+}
+
+// --------------------------------------------------------------------------
+// packed-weight cache file, registry adoption, code export
+// --------------------------------------------------------------------------
+int tl_weights_save(const tl_weights* W, const char* path, const char* name, int append) {
+  return guarded("tl_weights_save", [&] {
+    check_weights(W);
+    REQUIRE(path && name, "NULL path or name");
+    const size_t nl = std::strlen(name);
+    REQUIRE(nl < 4096, "record name too long");
+    hipStream_t st = nullptr;
+    PinnedBuf stage;
+    struct Free {
+      PinnedBuf& b;
+      ~Free() {
+        if (b.p) (void)hipHostFree(b.p);
+      }
+    } free_stage{stage};
+    File file;
+    if (append) file.f = std::fopen(path, "r+b");
+    if (!file.f) file.f = std::fopen(path, "wb");
+    REQUIRE(file.f, std::string("cannot open ") + path + " for writing");
+    REQUIRE(std::fseek(file.f, 0, SEEK_END) == 0, "seek failed");
+    const long pos = std::ftell(file.f);
+    REQUIRE(pos >= 0, "ftell failed");
+    // header with the checksum filled in after the payload went out
+    RecHeader h{};
+    std::memcpy(h.magic, kRecMagic, 8);
+    h.version = kRecVersion;
+    h.name_len = (uint32_t)nl;
+    h.rows = W->rows;
+    h.cols = W->cols;
+    h.NG = W->NG;
+    h.KB = W->KB;
+    h.tile_bytes = (uint64_t)W->NG * W->KB * 1024;
+    h.scale_bytes = (uint64_t)W->NG * 16 * 4;
+    REQUIRE(std::fwrite(&h, 1, sizeof h, file.f) == sizeof h, "write failed");
+    std::vector<char> nb(pad64(nl), 0);
+    std::memcpy(nb.data(), name, nl);
+    REQUIRE(std::fwrite(nb.data(), 1, nb.size(), file.f) == nb.size(), "write failed");
+    CacheHash hash;
+    device_to_file(file.f, W->tiles, h.tile_bytes, stage, &hash, st);
+    device_to_file(file.f, W->scales, h.scale_bytes, stage, &hash, st);
+    h.checksum = hash.value();
+    REQUIRE(std::fseek(file.f, pos, SEEK_SET) == 0, "seek failed");
+    REQUIRE(std::fwrite(&h, 1, sizeof h, file.f) == sizeof h, "write failed");
+    REQUIRE(std::fflush(file.f) == 0, "write failed");
+  });
+}
+
+tl_weights* tl_weights_load(const char* path, const char* name) {
+  tl_weights* out = nullptr;
+  guarded("tl_weights_load", [&] {
+    REQUIRE(path && name, "NULL path or name");
+    File file;
+    file.f = std::fopen(path, "rb");
+    REQUIRE(file.f, std::string("cannot open ") + path);
+    RecHeader h;
+    std::string rn;
+    for (;;) {
+      REQUIRE(read_rec_header(file.f, h, rn), std::string("no record named ") + name + " in " + path);
+      if (rn == name) break;
+      REQUIRE(std::fseek(file.f, (long)(h.tile_bytes + h.scale_bytes), SEEK_CUR) == 0, "seek failed");
+    }
+    tl_weights* W = weights_alloc(h.rows, h.cols);
+    PinnedBuf stage;
+    try {
+      hipStream_t st = nullptr;
+      CacheHash hash;
+      file_to_device(file.f, W->tiles, h.tile_bytes, stage, hash, st);
+      file_to_device(file.f, W->scales, h.scale_bytes, stage, hash, st);
+      REQUIRE(hash.value() == h.checksum, std::string("checksum mismatch in record ") + name);
+    } catch (...) {
+      if (stage.p) (void)hipHostFree(stage.p);
+      weights_free(W);
+      throw;
+    }
+    if (stage.p) (void)hipHostFree(stage.p);
+    out = W;
+  });
+  return out;
+}
+
+int tl_weights_cache_list(const char* path, char* names, size_t names_len) {
+  int count = -1;
+  guarded("tl_weights_cache_list", [&] {
+    REQUIRE(path, "NULL path");
+    File file;
+    file.f = std::fopen(path, "rb");
+    REQUIRE(file.f, std::string("cannot open ") + path);
+    RecHeader h;
+    std::string rn, all;
+    int n = 0;
+    while (read_rec_header(file.f, h, rn)) {
+      all += rn;
+      all += '\n';
+      n++;
+      REQUIRE(std::fseek(file.f, (long)(h.tile_bytes + h.scale_bytes), SEEK_CUR) == 0, "seek failed");
+    }
+    if (names && names_len) {
+      REQUIRE(all.size() < names_len, "names buffer too small");
+      std::memcpy(names, all.c_str(), all.size() + 1);
+    }
+    count = n;
+  });
+  return count;
+}
+
+int tl_weights_export(const tl_weights* W, int8_t* codes, float* scales, int dst_on_device) {
+  return guarded("tl_weights_export", [&] {
+    check_weights(W);
+    REQUIRE(codes || scales, "nothing to export");
+    hipStream_t st = nullptr;
+    const size_t cb = (size_t)W->rows * W->cols, sb = (size_t)W->rows * sizeof(float);
+    if (dst_on_device) {
+      if (codes) HIP_OK(launch_unpack_tiles(W->tiles, W->rows, W->cols, codes, st));
+      if (scales) HIP_OK(hipMemcpyAsync(scales, W->scales, sb, hipMemcpyDeviceToDevice, st));
+      HIP_OK(hipStreamSynchronize(st));
+      return;
+    }
+    if (codes) {
+      DevBuf tmp;
+      struct Free {
+        DevBuf& b;
+        ~Free() {
+          if (b.p) (void)hipFree(b.p);
+        }
+      } free_tmp{tmp};
+      tmp.ensure(cb, st);
+      HIP_OK(launch_unpack_tiles(W->tiles, W->rows, W->cols, static_cast<int8_t*>(tmp.p), st));
+      HIP_OK(hipMemcpyAsync(codes, tmp.p, cb, hipMemcpyDeviceToHost, st));
+      HIP_OK(hipStreamSynchronize(st));
+    }
+    if (scales) {
+      HIP_OK(hipMemcpyAsync(scales, W->scales, sb, hipMemcpyDeviceToHost, st));
+      HIP_OK(hipStreamSynchronize(st));
+    }
+  });
+}
+
+int tl_registry_adopt(const int8_t* w_int8, const float* scales, tl_weights* W) {
+  return guarded("tl_registry_adopt", [&] {
+    check_weights(W);
+    REQUIRE(w_int8 && scales, "NULL pointer");
+    registry_put(w_int8, scales, W);
   });
 }
 

@@ -209,9 +209,12 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_vec_kernel(const floa
 }
 
 // one thread per (tile, lane): 16 bytes of W[16g + (l&15)][64kb + 16(l>>4) ..]
+// for the row groups of rows [0, rows) of w, written as row groups g0 .. of a
+// tile array with NGt row groups per k-block (g0 = 0, NGt = NG for a whole
+// matrix; a row chunk starting at row 16 g0 of a larger one otherwise)
 __global__ __launch_bounds__(256) void pack_tiles_kernel(const int8_t* __restrict__ w, int rows,
-                                                         int cols, int KB, long long total,
-                                                         uint8_t* __restrict__ tiles) {
+                                                         int cols, int KB, long long total, int NGt,
+                                                         int g0, uint8_t* __restrict__ tiles) {
   const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
   if (t >= total) return;
   const int lane = (int)(t & 63);
@@ -236,7 +239,31 @@ __global__ __launch_bounds__(256) void pack_tiles_kernel(const int8_t* __restric
       q.w = b[12] | (b[13] << 8) | (b[14] << 16) | ((uint32_t)b[15] << 24);
     }
   }
-  reinterpret_cast<uint4*>(tiles)[t] = q;
+  reinterpret_cast<uint4*>(tiles)[((size_t)kb * NGt + g0 + g) * 64 + lane] = q;
+}
+
+// inverse of pack_tiles_kernel over a whole matrix: tiles -> row-major codes
+__global__ __launch_bounds__(256) void unpack_tiles_kernel(const uint8_t* __restrict__ tiles, int rows,
+                                                           int cols, int KB, long long total,
+                                                           int8_t* __restrict__ w) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= total) return;
+  const int lane = (int)(t & 63);
+  const long long tile = t >> 6;
+  const int NG = (rows + 15) / 16;
+  const int g = (int)(tile % NG);
+  const int kb = (int)(tile / NG);
+  const int r = g * 16 + (lane & 15);
+  const int k0 = kb * 64 + (lane >> 4) * 16;
+  if (r >= rows || k0 >= cols) return;
+  const uint4 q = reinterpret_cast<const uint4*>(tiles)[t];
+  int8_t* p = w + (size_t)r * cols + k0;
+  if (k0 + 16 <= cols && ((((uintptr_t)p) & 15) == 0)) {
+    *reinterpret_cast<uint4*>(p) = q;
+  } else {
+    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+    for (int j = 0; j < 16 && k0 + j < cols; j++) p[j] = (int8_t)((d[j >> 2] >> (8 * (j & 3))) & 0xff);
+  }
 }
 
 // Word copy, used to bring a small host-resident (pinned, device-mapped)
@@ -299,13 +326,29 @@ hipError_t launch_quantize_rows_tiled(const float* src, int rows, int cols, uint
   return hipGetLastError();
 }
 
-hipError_t launch_pack_tiles(const int8_t* w, int rows, int cols, uint8_t* tiles, hipStream_t st) {
+hipError_t launch_pack_tiles_rows(const int8_t* w, int rows, int cols, int NGt, int g0, uint8_t* tiles,
+                                  hipStream_t st) {
   if (rows <= 0 || cols <= 0) return hipSuccess;
+  if (g0 < 0 || g0 + cdiv(rows, 16) > NGt) return hipErrorInvalidValue;
   const int KB = cdiv(cols, 64);
   const long long total = (long long)cdiv(rows, 16) * KB * 64;
   const long long blocks = (total + 255) / 256;
   hipLaunchKernelGGL(pack_tiles_kernel, dim3((unsigned)blocks), dim3(256), 0, st, w, rows, cols, KB,
-                     total, tiles);
+                     total, NGt, g0, tiles);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_tiles(const int8_t* w, int rows, int cols, uint8_t* tiles, hipStream_t st) {
+  return launch_pack_tiles_rows(w, rows, cols, cdiv(rows, 16), 0, tiles, st);
+}
+
+hipError_t launch_unpack_tiles(const uint8_t* tiles, int rows, int cols, int8_t* w, hipStream_t st) {
+  if (rows <= 0 || cols <= 0) return hipSuccess;
+  const int KB = cdiv(cols, 64);
+  const long long total = (long long)cdiv(rows, 16) * KB * 64;
+  const long long blocks = (total + 255) / 256;
+  hipLaunchKernelGGL(unpack_tiles_kernel, dim3((unsigned)blocks), dim3(256), 0, st, tiles, rows, cols, KB,
+                     total, w);
   return hipGetLastError();
 }
 

@@ -25,6 +25,11 @@ hipError_t launch_quantize_rows(const float* src, int8_t* dst, float* scales, in
 hipError_t launch_quantize_rows_tiled(const float* src, int rows, int cols, uint8_t* tiles,
                                       float* scales, bool clamp127, hipStream_t st);
 hipError_t launch_pack_tiles(const int8_t* w, int rows, int cols, uint8_t* tiles, hipStream_t st);
+// rows [0, rows) of w into row groups g0.. of a tile array with NGt row groups
+hipError_t launch_pack_tiles_rows(const int8_t* w, int rows, int cols, int NGt, int g0, uint8_t* tiles,
+                                  hipStream_t st);
+// whole-matrix tiles -> row-major int8 codes
+hipError_t launch_unpack_tiles(const uint8_t* tiles, int rows, int cols, int8_t* w, hipStream_t st);
 // final RMSNorm of one hidden row, numpy's float32 order (K = 128 * 2^j)
 hipError_t launch_rmsnorm_np(const float* h, const float* w, float* out, int K, float eps, hipStream_t st);
 // token = argmax over the per-work-group keys of an EPI_ARGMAX GEMV

@@ -11,10 +11,13 @@ This module keeps those steps with the same names, argument meaning and
 error behaviour, on the MI355X library:
   * load_decoder_lib() binds w8a32_quantize / w8a32_linear with the
     reference's argtypes (decoder.py:145-157) plus tl_last_error;
-  * Decoder quantizes on the GPU, packs the fused matrices, and registers
-    every quantized matrix with tl_register_weights, which uploads it once
-    into HBM tiles (the step the reference's decoder_set_layer_weights_v32
-    performs by pointer);
+  * Decoder quantizes on the GPU (w8a32_quantize packs the HBM tiles in the
+    same pass and keeps them for the returned host arrays), packs the fused
+    matrices, and registers every quantized matrix with tl_register_weights
+    (the step the reference's decoder_set_layer_weights_v32 performs by
+    pointer; only the fused copies upload anything there);
+  * save_cache() / from_cache() write and read a packed-weight cache file,
+    so a later load copies the HBM tiles back with no quantization;
   * project() runs one projection through w8a32_linear with the reference's
     batch-dependent numerics; get_logits() / sample() are _get_logits and the
     greedy branch of _sample.
@@ -117,6 +120,69 @@ class Decoder:
             self._weight_store.append(self._lm_head_scratch)
             self._register(q, s)
             self._logits_buf = np.empty(self._lm_head_M, dtype=np.float32)
+
+    # -- packed-weight cache file ---------------------------------------------
+    def _matrices(self):
+        for l_idx, entry in enumerate(self.layers):
+            for name, (w, s) in entry.items():
+                yield f"layers.{l_idx}.{name}", w, s
+        if self._lm_head_w is not None:
+            yield "lm_head", self._lm_head_w, self._lm_head_s
+
+    def save_cache(self, path: str) -> None:
+        """Write every quantized matrix (the seven projections and the fused
+        Q||K||V and gate||up of each layer, then the lm_head) as the records
+        of one packed-weight cache file, named layers.<l>.<projection> and
+        lm_head.  The file replaces any existing one."""
+        first = True
+        for name, w, s in self._matrices():
+            W = _lin.DeviceWeights.from_codes(w, s)
+            try:
+                W.save(path, name, append=not first)
+            finally:
+                W.close()
+            first = False
+
+    @classmethod
+    def from_cache(cls, path: str, lib: Optional[ctypes.CDLL] = None,
+                   final_norm: Optional[np.ndarray] = None) -> "Decoder":
+        """A Decoder whose quantized matrices come from a packed-weight cache
+        file (save_cache) instead of fp32 weights: each record is copied into
+        HBM as it is, its codes and scales are exported to host arrays (the
+        arrays the reference keeps in _weight_store), and the device copy is
+        handed to the host-pointer registry for those arrays, so no matrix is
+        quantized, packed or uploaded a second time."""
+        self = cls.__new__(cls)
+        self._lib = lib or load_decoder_lib()
+        self._weight_store = []
+        self.layers = []
+        names = _lin.cache_list(path)
+        n_layers = 1 + max((int(n.split(".")[1]) for n in names if n.startswith("layers.")), default=-1)
+        for l_idx in range(n_layers):
+            entry = {}
+            for name in PROJECTIONS + ("qkv_proj", "gate_up_proj"):
+                entry[name] = self._load_record(path, f"layers.{l_idx}.{name}")
+            self.layers.append(entry)
+        self._final_norm_w = None if final_norm is None else np.ascontiguousarray(final_norm, np.float32)
+        self._lm_head_w = None
+        if "lm_head" in names:
+            q, s = self._load_record(path, "lm_head")
+            self._lm_head_w, self._lm_head_s = q, s
+            self._lm_head_M, self._lm_head_K = q.shape
+            self._lm_head_scratch = np.empty((TILE_M, self._lm_head_K), dtype=np.float32)
+            self._weight_store.append(self._lm_head_scratch)
+            self._logits_buf = np.empty(self._lm_head_M, dtype=np.float32)
+        return self
+
+    def _load_record(self, path: str, name: str):
+        W = _lin.DeviceWeights.load(path, name)
+        try:
+            codes, scales = W.export()
+            W.adopt_into_registry(codes, scales)
+        finally:
+            W.close()
+        self._weight_store.extend([codes, scales])
+        return codes, scales
 
     # -- weight quantization helpers (reference :248-317) -------------------
     def _quantize_and_keep(self, w_fp32: np.ndarray):

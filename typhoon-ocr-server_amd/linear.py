@@ -10,7 +10,8 @@ missing or the GPU call fails, the wrapper raises.
 from __future__ import annotations
 
 import ctypes
-from typing import Optional
+import os
+from typing import List, Optional
 
 import numpy as np
 
@@ -40,6 +41,11 @@ SIGNATURES = {
     "tl_device_count": (_int, []),
     "tl_gemv_set_plan": (_int, [_int, _int]),
     "tl_gemm_i8_set_cfg": (_int, [_int]),
+    "tl_weights_save": (_int, [_vp, ctypes.c_char_p, ctypes.c_char_p, _int]),
+    "tl_weights_load": (_vp, [ctypes.c_char_p, ctypes.c_char_p]),
+    "tl_weights_cache_list": (_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
+    "tl_weights_export": (_int, [_vp, _vp, _vp, _int]),
+    "tl_registry_adopt": (_int, [_i8p, _f32p, _vp]),
     "tl_register_weights": (_int, [_i8p, _f32p, _int, _int]),
     "tl_evict_weights": (_int, [_i8p]),
     "tl_registry_clear": (None, []),
@@ -213,6 +219,40 @@ class DeviceWeights:
             raise RuntimeError("tl_weights_quantize_dev failed")
         return cls(h, rows, cols)
 
+    @classmethod
+    def load(cls, path: str, name: str) -> "DeviceWeights":
+        """Record `name` of a packed-weight cache file, copied into HBM."""
+        lib = load_library()
+        h = lib.tl_weights_load(os.fsencode(path), name.encode())
+        if not h:
+            check(lib, "tl_weights_load")
+            raise RuntimeError("tl_weights_load failed")
+        return cls(h, lib.tl_weights_rows(h), lib.tl_weights_cols(h))
+
+    def save(self, path: str, name: str, append: bool = True) -> None:
+        """Write this matrix as record `name` of a packed-weight cache file."""
+        lib = load_library()
+        _rc(lib, lib.tl_weights_save(self.handle, os.fsencode(path), name.encode(), int(append)),
+            "tl_weights_save")
+
+    def export(self):
+        """(row-major int8 codes [rows, cols], fp32 scales [rows]) as numpy arrays."""
+        lib = load_library()
+        codes = np.empty((self.rows, self.cols), dtype=np.int8)
+        scales = np.empty(self.rows, dtype=np.float32)
+        _rc(lib, lib.tl_weights_export(self.handle, codes.ctypes.data, scales.ctypes.data, 0),
+            "tl_weights_export")
+        return codes, scales
+
+    def adopt_into_registry(self, codes: np.ndarray, scales: np.ndarray) -> None:
+        """Hand this device copy to the host-pointer registry for the host
+        arrays (codes, scales) that hold its contents; this object no longer
+        owns it afterwards."""
+        lib = load_library()
+        _rc(lib, lib.tl_registry_adopt(_p(codes, ctypes.c_int8), _p(scales, ctypes.c_float), self.handle),
+            "tl_registry_adopt")
+        self.handle = None
+
     def bytes(self) -> int:
         return load_library().tl_weights_bytes(self.handle)
 
@@ -226,6 +266,19 @@ class DeviceWeights:
             self.close()
         except Exception:
             pass
+
+
+def cache_list(path: str) -> List[str]:
+    """Record names of a packed-weight cache file, in file order."""
+    lib = load_library()
+    n = lib.tl_weights_cache_list(os.fsencode(path), None, 0)
+    if n < 0:
+        check(lib, "tl_weights_cache_list")
+        raise RuntimeError("tl_weights_cache_list failed")
+    buf = ctypes.create_string_buffer(4097 * (n + 1))   # names are < 4096 bytes each
+    _rc(lib, 0 if lib.tl_weights_cache_list(os.fsencode(path), buf, len(buf)) >= 0 else -1,
+        "tl_weights_cache_list")
+    return buf.value.decode().split("\n")[:n]
 
 
 def _rc(lib, rc, what):
