@@ -53,6 +53,35 @@ void orc_w8a16_linear(const uint16_t *x_bf16, const int8_t *w,
 void orc_w8a32_gemv_timed(const float *x, const int8_t *w, const float *scales,
                           float *y, int N, int K, int threads);
 
+/* ---- decoder layer step (decoder_ref.c) -------------------------------- */
+/* Arm FRECPE / FRSQRTE estimates and their Newton steps (positive normal x). */
+float orc_frecpe(float x);
+float orc_frsqrte(float x);
+float orc_frecps(float a, float b);
+float orc_frsqrts(float a, float b);
+/* rmsnorm_f32 (kernel/ops.c:22-56); out may alias x. */
+void orc_rmsnorm(float *out, const float *x, const float *w, int dim, float eps);
+/* mrope_precompute (kernel/ops.c:150-177), tables [max_seq x head_dim/2]. */
+void orc_mrope_precompute(float *cos_tab, float *sin_tab, int max_seq, int head_dim, float theta);
+/* mrope_apply (kernel/ops.c:233-289), in place. */
+void orc_mrope_apply(float *q, float *k, const float *cos_tab, const float *sin_tab, int num_q_heads,
+                     int num_kv_heads, int head_dim, int pos);
+/* fast_exp_f32 (kernel/ops.c:478-491), silu of the vector loop, and
+ * silu_mul_inplace (kernel/ops.c:493-531). */
+float orc_fast_exp(float x);
+float orc_silu_fast(float g);
+void orc_silu_mul(float *gate, const float *up, int n);
+/* attention_decode_gqa (kernel/attention.c:172-224); cache per kv head
+ * [max_seq x 128], positions 0..S-1. */
+void orc_attention_decode(const float *q, const float *Kc, const float *Vc, float *out, int num_q_heads,
+                          int num_kv_heads, int max_seq, int S, float scale);
+/* decoder_layer_forward in DECODE_MODE (kernel/decoder.c:33-157). */
+void orc_decode_layer(const int8_t *const *w, const float *const *s, const float *input_ln,
+                      const float *post_attn_ln, const float *q_norm, const float *k_norm, float *Kc,
+                      float *Vc, int max_seq, float *hidden, const float *cos_tab, const float *sin_tab,
+                      int cache_len, int rope_pos, int hidden_dim, int ffn_dim, int num_q_heads,
+                      int num_kv_heads, int threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,24 @@ def load(native: bool = False) -> ctypes.CDLL:
     for f in ("orc_quantize_rows", "orc_int_acc", "orc_w8a32_linear", "orc_w8a8_linear",
               "orc_w8a16_linear", "orc_w8a32_gemv_timed"):
         getattr(lib, f).restype = None
+    _f = ctypes.c_float
+    _i = ctypes.c_int
+    for f in ("orc_frecpe", "orc_frsqrte", "orc_fast_exp", "orc_silu_fast"):
+        getattr(lib, f).argtypes = [_f]
+        getattr(lib, f).restype = _f
+    for f in ("orc_frecps", "orc_frsqrts"):
+        getattr(lib, f).argtypes = [_f, _f]
+        getattr(lib, f).restype = _f
+    lib.orc_rmsnorm.argtypes = [_f32p, _f32p, _f32p, _i, _f]
+    lib.orc_mrope_precompute.argtypes = [_f32p, _f32p, _i, _i, _f]
+    lib.orc_mrope_apply.argtypes = [_f32p, _f32p, _f32p, _f32p, _i, _i, _i, _i]
+    lib.orc_silu_mul.argtypes = [_f32p, _f32p, _i]
+    lib.orc_attention_decode.argtypes = [_f32p, _f32p, _f32p, _f32p, _i, _i, _i, _i, _f]
+    lib.orc_decode_layer.argtypes = [ctypes.POINTER(_i8p), ctypes.POINTER(_f32p), _f32p, _f32p, _f32p, _f32p,
+                                     _f32p, _f32p, _i, _f32p, _f32p, _f32p, _i, _i, _i, _i, _i, _i, _i]
+    for f in ("orc_rmsnorm", "orc_mrope_precompute", "orc_mrope_apply", "orc_silu_mul",
+              "orc_attention_decode", "orc_decode_layer"):
+        getattr(lib, f).restype = None
     _LIBS[key] = lib
     return lib
 
@@ -150,3 +168,109 @@ def w8a32_gemv_timed(x: np.ndarray, w: np.ndarray, scales: np.ndarray, y: np.nda
     load(native).orc_w8a32_gemv_timed(_p(x, ctypes.c_float), _p(w, ctypes.c_int8),
                                       _p(scales, ctypes.c_float), _p(y, ctypes.c_float),
                                       n, k, threads)
+
+
+# ---------------------------------------------------------------------------
+# decoder layer step (decoder_ref.c)
+# ---------------------------------------------------------------------------
+HEAD_DIM = 128
+ROPE_THETA = 5000000.0          # MROPE_THETA_BASE, reference decoder.py:41
+
+
+def frecpe(x: float) -> float:
+    return load().orc_frecpe(x)
+
+
+def frsqrte(x: float) -> float:
+    return load().orc_frsqrte(x)
+
+
+def frecps(a: float, b: float) -> float:
+    return load().orc_frecps(a, b)
+
+
+def frsqrts(a: float, b: float) -> float:
+    return load().orc_frsqrts(a, b)
+
+
+def fast_exp(x: float) -> float:
+    return load().orc_fast_exp(x)
+
+
+def silu_fast(g: float) -> float:
+    return load().orc_silu_fast(g)
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    """rmsnorm_f32 over the last axis (rows independent)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.empty_like(x)
+    dim = x.shape[-1]
+    xr, orow = x.reshape(-1, dim), out.reshape(-1, dim)
+    for r in range(xr.shape[0]):
+        load().orc_rmsnorm(_p(orow[r], ctypes.c_float), _p(xr[r], ctypes.c_float), _p(w, ctypes.c_float),
+                           dim, eps)
+    return out
+
+
+def rope_tables(max_seq: int, head_dim: int = HEAD_DIM, theta: float = ROPE_THETA):
+    half = head_dim // 2
+    c = np.empty((max_seq, half), np.float32)
+    s_ = np.empty((max_seq, half), np.float32)
+    load().orc_mrope_precompute(_p(c, ctypes.c_float), _p(s_, ctypes.c_float), max_seq, head_dim, theta)
+    return c, s_
+
+
+def mrope_apply(q: np.ndarray, k: np.ndarray, cos_tab, sin_tab, pos: int):
+    """Returns rotated copies of q [nq*128] and k [nk*128] at position pos."""
+    q = np.array(q, dtype=np.float32, copy=True)
+    k = np.array(k, dtype=np.float32, copy=True)
+    load().orc_mrope_apply(_p(q, ctypes.c_float), _p(k, ctypes.c_float), _p(cos_tab, ctypes.c_float),
+                           _p(sin_tab, ctypes.c_float), q.size // HEAD_DIM, k.size // HEAD_DIM, HEAD_DIM, pos)
+    return q, k
+
+
+def silu_mul(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    g = np.array(gate, dtype=np.float32, copy=True)
+    u = np.ascontiguousarray(up, dtype=np.float32)
+    load().orc_silu_mul(_p(g, ctypes.c_float), _p(u, ctypes.c_float), g.size)
+    return g
+
+
+def attention_decode(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, S: int,
+                     scale: float = 0.08838834764831843) -> np.ndarray:
+    """q [nq*128]; kc/vc [nkv, max_seq, 128]; attends to positions 0..S-1."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    kc = np.ascontiguousarray(kc, dtype=np.float32)
+    vc = np.ascontiguousarray(vc, dtype=np.float32)
+    nkv, max_seq, _ = kc.shape
+    out = np.empty_like(q)
+    load().orc_attention_decode(_p(q, ctypes.c_float), _p(kc, ctypes.c_float), _p(vc, ctypes.c_float),
+                                _p(out, ctypes.c_float), q.size // HEAD_DIM, nkv, max_seq, S, scale)
+    return out
+
+
+LAYER_PROJ = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+
+def decode_layer(layer: dict, kc: np.ndarray, vc: np.ndarray, hidden: np.ndarray, cos_tab, sin_tab,
+                 cache_len: int, rope_pos: int, threads: int | None = None) -> np.ndarray:
+    """One DECODE_MODE layer.  layer: name -> (int8 codes, fp32 scales) for
+    the seven projections, plus input_ln / post_attn_ln / q_norm / k_norm
+    fp32 vectors.  kc/vc: this layer's cache [nkv, max_seq, 128], updated in
+    place at position cache_len.  Returns the new hidden row."""
+    h = np.array(hidden, dtype=np.float32, copy=True).reshape(-1)
+    ws = [np.ascontiguousarray(layer[n][0], dtype=np.int8) for n in LAYER_PROJ]
+    ss = [np.ascontiguousarray(layer[n][1], dtype=np.float32) for n in LAYER_PROJ]
+    norms = [np.ascontiguousarray(layer[n], dtype=np.float32)
+             for n in ("input_ln", "post_attn_ln", "q_norm", "k_norm")]
+    assert kc.flags["C_CONTIGUOUS"] and vc.flags["C_CONTIGUOUS"] and kc.dtype == np.float32
+    nkv, max_seq, _ = kc.shape
+    warr = (_i8p * 7)(*[_p(w, ctypes.c_int8) for w in ws])
+    sarr = (_f32p * 7)(*[_p(s, ctypes.c_float) for s in ss])
+    load().orc_decode_layer(warr, sarr, *[_p(n, ctypes.c_float) for n in norms], _p(kc, ctypes.c_float),
+                            _p(vc, ctypes.c_float), max_seq, _p(h, ctypes.c_float),
+                            _p(cos_tab, ctypes.c_float), _p(sin_tab, ctypes.c_float), cache_len, rope_pos,
+                            h.size, ws[4].shape[0], ws[0].shape[0] // HEAD_DIM, nkv, _threads(threads))
+    return h
