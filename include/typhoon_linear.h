@@ -202,6 +202,86 @@ int tl_w8a32_gemv_acc_dev(const float *x, const tl_weights *W, int32_t *acc, flo
                           void *stream);
 int tl_w8a8_gemm_acc_dev(const int8_t *x_int8, const tl_weights *W, int32_t *acc, int batch,
                          void *stream);
+/* The M=1 GEMV with the decoder's fusions (device pointers): norm 0 none,
+ * 1 numpy final RMSNorm, 2 the decoder's RMSNorm (kernel/ops.c:22-56) of x
+ * with norm_w first; epi 0 W8A32 (+ bias as its own rounding; bias may be y
+ * itself: the residual add of decoder.c:122-123), 4 SwiGLU over gate/up rows
+ * interleaved per 16-row group (y[8b + r] = silu(gate) * up, kernel/ops.c:
+ * 493-531, N/2 outputs). */
+int tl_gemv_fused_dev(const float *x, const tl_weights *W, const float *bias, float *y, int epi, int norm,
+                      const float *norm_w, void *stream);
+
+/* ==========================================================================
+ * Part 3 -- the decoder loop (kernel/decoder.h, kernel/decoder.c:300-526)
+ *
+ * The reference's decoder handles and entry points, same names, signatures
+ * and void returns, with the layer loop resident on the GPU: weights are
+ * packed into HBM at decoder_set_layer_weights*, the KV cache and scratch
+ * live in HBM, and each decode step is one replay of a captured HIP graph.
+ * Dimensions are the reference's (decoder.h, scratch.h): hidden 2048, FFN
+ * 6144, 16 q / 8 kv heads of 128; layers run from 0 to the first layer not
+ * set (the reference always runs its 28).  Host pointers are borrowed for the
+ * call.  Failures set tl_last_error().
+ * ========================================================================== */
+typedef struct ModelWeights ModelWeights;
+typedef struct KVCache KVCache;
+typedef struct DecoderScratch DecoderScratch;
+
+ModelWeights *decoder_model_alloc(void);                      /* decoder.c:322 */
+void decoder_model_free(ModelWeights *m);                     /* decoder.c:327 */
+KVCache *decoder_cache_alloc(int max_seq);                    /* decoder.c:332 */
+void decoder_cache_free(KVCache *c);                          /* decoder.c:337 */
+void decoder_cache_clear(KVCache *c);                         /* decoder.c:342 */
+void decoder_cache_set_rope_offset(KVCache *c, int offset);   /* decoder.c:347 */
+DecoderScratch *decoder_scratch_alloc_fn(int max_seq);        /* decoder.c:352 */
+void decoder_scratch_free_fn(DecoderScratch *s);              /* decoder.c:357 */
+
+/* decoder.c:363-391: int8 codes row-major + fp32 scales per projection, the
+ * two RMSNorm weights [2048] and the q/k head norms [128]; copied into HBM
+ * (Q||K||V fused; gate/up interleaved per 16-row group for the fused SwiGLU). */
+void decoder_set_layer_weights(ModelWeights *model, int layer_idx, const int8_t *q_w, const float *q_s,
+                               const int8_t *k_w, const float *k_s, const int8_t *v_w, const float *v_s,
+                               const int8_t *o_w, const float *o_s, const int8_t *gate_w, const float *gate_s,
+                               const int8_t *up_w, const float *up_s, const int8_t *down_w, const float *down_s,
+                               const float *input_ln, const float *post_attn_ln, const float *q_norm,
+                               const float *k_norm);
+/* decoder.c:393-424: as above, with the fused Q||K||V given directly (the
+ * fused gate||up is accepted and re-laid out from gate and up). */
+void decoder_set_layer_weights_v32(ModelWeights *model, int layer_idx, const int8_t *q_w, const float *q_s,
+                                   const int8_t *k_w, const float *k_s, const int8_t *v_w, const float *v_s,
+                                   const int8_t *o_w, const float *o_s, const int8_t *gate_w,
+                                   const float *gate_s, const int8_t *up_w, const float *up_s,
+                                   const int8_t *down_w, const float *down_s, const float *input_ln,
+                                   const float *post_attn_ln, const float *q_norm, const float *k_norm,
+                                   const int8_t *qkv_w, const float *qkv_s, const int8_t *gate_up_w,
+                                   const float *gate_up_s);
+/* decoder.c:509-516 -> ops.c:150-177: sequential-position rope tables
+ * [max_seq x head_dim/2] on the host. */
+void decoder_precompute_rope(float *cos_tab, float *sin_tab, int max_seq, int head_dim, const int sections[3],
+                             const float theta_bases[3]);
+/* decoder.c:426-435: one decode step of every set layer on hidden [2048]
+ * (host, in/out); the tables are the host arrays decoder_precompute_rope
+ * filled for the cache's max_seq (copied to HBM once, re-checked by a
+ * sampled fingerprint). */
+void decoder_decode_step(const ModelWeights *model, KVCache *cache, float *hidden, DecoderScratch *scratch,
+                         const float *cos_tab, const float *sin_tab);
+
+/* Extensions (no reference counterpart). */
+int tl_decoder_num_layers(const ModelWeights *model);
+int tl_decoder_cache_len(const KVCache *cache);
+/* Copies one layer's K and V cache ([8][max_seq][128] fp32 each; either may
+ * be NULL) to host memory. */
+int tl_decoder_read_cache(const KVCache *cache, int layer, float *k, float *v);
+/* Device-resident greedy generation (the decode loop of decoder.py:494-507
+ * with do_sample=False): from first_token, n_steps steps of
+ *   hidden = embed[token]; every layer; lm_head logits of the numpy final
+ *   RMSNorm (final_norm, host [2048], may be NULL); token = argmax
+ * as graph replays with no host round trip; the n_steps tokens go to tokens
+ * (host).  embed: device [vocab x 2048] fp32.  The cache advances by
+ * n_steps. */
+int tl_decoder_generate(const ModelWeights *model, KVCache *cache, DecoderScratch *scratch,
+                        const tl_weights *lm_head, const float *final_norm, const float *embed, int first_token,
+                        int n_steps, int32_t *tokens, const float *cos_tab, const float *sin_tab);
 
 #ifdef __cplusplus
 }

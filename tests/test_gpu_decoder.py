@@ -1,0 +1,210 @@
+"""GPU parity of the device-resident decoder loop (survey row f-1; reference
+kernel/decoder.c:33-157 decode mode, :300-526 handles and entry points,
+decoder.py:494-507 greedy loop) against the oracle (oracle/decoder_ref.c).
+
+Bars, written in each test:
+  * SwiGLU epilogue: bit-exact (same GEMV codes and scale, the reference's
+    fast-exp silu and FRECPE step restated exactly);
+  * residual epilogue (bias = y in place): bit-exact;
+  * decoder RMSNorm prologue: bit-exact where every partial sum of squares is
+    exact (so the summation order cannot matter); elsewhere the sum is a tree
+    here and four sequential fused chains in the reference: relative L2
+    <= 1e-5;
+  * layer step vs the oracle: hidden rows relative L2 <= 1e-3 per step,
+    K/V cache rows relative L2 <= 1e-4 (tolerance, as for every path whose
+    reference summation order is not reproduced);
+  * greedy tokens: the graph-replayed generate loop equals the host step path
+    exactly, and equals the oracle's greedy tokens.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+F = np.float32
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def test_swiglu_epilogue_bit_exact(lin, orc, dev):
+    import torch
+    say("gemv swiglu epilogue")
+    rng = np.random.default_rng(20)
+    FF, H = 6144, 2048
+    g = orc.quantize_rows((rng.standard_normal((FF, H)) * 0.02).astype(F))
+    u = orc.quantize_rows((rng.standard_normal((FF, H)) * 0.02).astype(F))
+    w = np.empty((2 * FF, H), np.int8)
+    s = np.empty(2 * FF, F)
+    for b in range(FF // 8):
+        w[16 * b:16 * b + 8] = g[0][8 * b:8 * b + 8]
+        w[16 * b + 8:16 * b + 16] = u[0][8 * b:8 * b + 8]
+        s[16 * b:16 * b + 8] = g[1][8 * b:8 * b + 8]
+        s[16 * b + 8:16 * b + 16] = u[1][8 * b:8 * b + 8]
+    W = lin.DeviceWeights.from_codes(w, s)
+    for scale in (0.3, 3.0, 40.0):
+        x = (rng.standard_normal(H) * scale).astype(F)
+        y = torch.empty(FF, dtype=torch.float32, device=dev)
+        lin.gemv_fused_dev(torch.from_numpy(x).to(dev), W, y, epi=4)
+        torch.cuda.synchronize()
+        gate = orc.w8a32_linear(x[None], *g)[0]
+        up = orc.w8a32_linear(x[None], *u)[0]
+        np.testing.assert_array_equal(y.cpu().numpy(), orc.silu_mul(gate, up))
+    W.close()
+
+
+def test_residual_epilogue_in_place(lin, orc, dev):
+    import torch
+    say("gemv residual in place")
+    rng = np.random.default_rng(21)
+    w, s = orc.quantize_rows((rng.standard_normal((2048, 6144)) * 0.02).astype(F))
+    W = lin.DeviceWeights.from_codes(w, s)
+    x = rng.standard_normal(6144).astype(F)
+    h = rng.standard_normal(2048).astype(F)
+    hd = torch.from_numpy(h).to(dev)
+    lin.gemv_fused_dev(torch.from_numpy(x).to(dev), W, hd, epi=0, bias=hd)
+    torch.cuda.synchronize()
+    want = (orc.w8a32_linear(x[None], w, s)[0] + h).astype(F)
+    np.testing.assert_array_equal(hd.cpu().numpy(), want)
+    W.close()
+
+
+def test_decoder_rmsnorm_prologue(lin, orc, dev):
+    """Inputs on a grid of quarters make every partial sum of squares exact,
+    so the tree sum here and the reference's sequential chains agree and the
+    rest of the prologue (rsqrt estimate, Newton steps, x * r * w, codes) must
+    be bit-exact; random inputs are held to relative L2 <= 1e-5."""
+    import torch
+    say("gemv decoder rmsnorm prologue")
+    rng = np.random.default_rng(22)
+    w, s = orc.quantize_rows((rng.standard_normal((4096, 2048)) * 0.02).astype(F))
+    W = lin.DeviceWeights.from_codes(w, s)
+    nw = (1 + 0.1 * rng.standard_normal(2048)).astype(F)
+    nwd = torch.from_numpy(nw).to(dev)
+    cases = [("grid", (rng.integers(-40, 41, 2048) * 0.25).astype(F))]
+    cases += [(f"random x{sc}", (rng.standard_normal(2048) * sc).astype(F)) for sc in (0.05, 1.0, 30.0)]
+    for name, h in cases:
+        y = torch.empty(4096, dtype=torch.float32, device=dev)
+        lin.gemv_fused_dev(torch.from_numpy(h).to(dev), W, y, epi=0, norm=2, norm_w=nwd)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        want = orc.w8a32_linear(orc.rmsnorm(h, nw)[None], w, s)[0]
+        if name == "grid":
+            np.testing.assert_array_equal(got, want)
+        else:
+            assert rel_l2(got, want) <= 1e-5, (name, rel_l2(got, want))
+    W.close()
+
+
+def _model(rng, orc, n_layers, vocab=None):
+    from typhoon_ocr_server_amd import decoder as dec
+    layers = [dec.random_layer_weights(rng, norms=True) for _ in range(n_layers)]
+    lm = None if vocab is None else (rng.standard_normal((vocab, 2048)) * 0.02).astype(F)
+    nw = (1 + 0.1 * rng.standard_normal(2048)).astype(F)
+    return layers, lm, nw
+
+
+def _oracle_layers(d, layers):
+    """The Decoder's quantized matrices + norms, in the oracle's layer form."""
+    out = []
+    for l_idx, layer in enumerate(layers):
+        entry = {n: d.layers[l_idx][n] for n in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj",
+                                                  "up_proj", "down_proj")}
+        for n in ("input_ln", "post_attn_ln", "q_norm", "k_norm"):
+            entry[n] = layer[n]
+        out.append(entry)
+    return out
+
+
+def test_decode_step_matches_oracle(lin, orc, dev):
+    """decoder_decode_step over 2 layers and 6 steps (rope offset set as after
+    a multimodal prefill) against the oracle's decode_layer chain."""
+    from typhoon_ocr_server_amd import decoder as dec
+    say("decoder_decode_step vs oracle, 2 layers x 6 steps")
+    rng = np.random.default_rng(23)
+    layers, _, _ = _model(rng, orc, 2)
+    max_seq = 160
+    d = dec.Decoder(layers, max_seq=max_seq)
+    ol = _oracle_layers(d, layers)
+    c, s = d._cos_tab, d._sin_tab
+    kc = [np.zeros((8, max_seq, 128), F) for _ in ol]
+    vc = [np.zeros((8, max_seq, 128), F) for _ in ol]
+    # start with a cache already holding 70 positions (written by both sides)
+    d.reset()
+    warm = 70
+    for t in range(warm):
+        h = (rng.standard_normal((1, 2048)) * 2).astype(F)
+        hg = d.step(h)
+        ho = h[0]
+        for l, layer in enumerate(ol):
+            ho = orc.decode_layer(layer, kc[l], vc[l], ho, c, s, cache_len=t, rope_pos=t)
+        assert rel_l2(hg[0], ho) <= 1e-3, t
+    # keep both caches identical from here (the GPU's), so each step's error is its own
+    for l in range(len(ol)):
+        kc[l], vc[l] = d.read_cache(l)
+    d.set_rope_offset(100)
+    for t in range(warm, warm + 6):
+        h = (rng.standard_normal((1, 2048)) * 2).astype(F)
+        hg = d.step(h)
+        ho = h[0]
+        for l, layer in enumerate(ol):
+            ho = orc.decode_layer(layer, kc[l], vc[l], ho, c, s, cache_len=t, rope_pos=100 + (t - warm))
+        assert rel_l2(hg[0], ho) <= 1e-3, t
+        for l in range(len(ol)):
+            kg, vg = d.read_cache(l)
+            assert rel_l2(kg[:, t], kc[l][:, t]) <= 1e-4
+            assert rel_l2(vg[:, t], vc[l][:, t]) <= 1e-4
+            np.testing.assert_array_equal(kg[:, :t], kc[l][:, :t])
+            kc[l][:, t], vc[l][:, t] = kg[:, t], vg[:, t]
+    assert d.cache_len == warm + 6
+    d.close()
+
+
+def test_generate_greedy_matches_step_path_and_oracle(lin, orc, dev):
+    """The graph-replayed greedy loop equals the host step path token for
+    token, and the oracle's greedy tokens (2 layers, vocab 32768, 12 steps)."""
+    import torch
+    from typhoon_ocr_server_amd import decoder as dec
+    say("tl_decoder_generate vs step path vs oracle")
+    rng = np.random.default_rng(24)
+    V = 32768
+    layers, lm, nw = _model(rng, orc, 2, vocab=V)
+    embed = (rng.standard_normal((V, 2048)) * 1.5).astype(F)
+    d = dec.Decoder(layers, lm_head=lm, final_norm=nw, max_seq=64)
+    lm_dev = lin.DeviceWeights.from_codes(d._lm_head_w, d._lm_head_s)
+    embed_dev = torch.from_numpy(embed).to(dev)
+    first, n = 1234, 12
+    d.reset()
+    toks = d.generate_greedy(first, n, embed_dev, lm_dev)
+    assert d.cache_len == n
+    # host step path: decoder_decode_step + next_token
+    d.reset()
+    tok, ref = first, []
+    for _ in range(n):
+        hg = d.step(embed[tok][None])
+        tok = d.next_token(hg)
+        ref.append(tok)
+    np.testing.assert_array_equal(toks, np.array(ref, np.int32))
+    # oracle greedy loop
+    ol = _oracle_layers(d, layers)
+    kc = [np.zeros((8, 64, 128), F) for _ in ol]
+    vc = [np.zeros((8, 64, 128), F) for _ in ol]
+    tok, want = first, []
+    for t in range(n):
+        h = embed[tok].copy()
+        for l, layer in enumerate(ol):
+            h = orc.decode_layer(layer, kc[l], vc[l], h, d._cos_tab, d._sin_tab, cache_len=t, rope_pos=t)
+        rms = np.sqrt(np.mean(h * h) + 1e-6)
+        x = ((h / rms) * nw).astype(F)
+        logits = orc.w8a32_linear(x[None], d._lm_head_w, d._lm_head_s)[0]
+        tok = int(np.argmax(logits))
+        want.append(tok)
+    np.testing.assert_array_equal(toks, np.array(want, np.int32))
+    lm_dev.close()
+    d.close()

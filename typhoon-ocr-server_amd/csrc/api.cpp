@@ -14,8 +14,7 @@
 // Part 2 exposes the same kernels on device pointers and caller streams.
 // Split-reduction work-space (partials + arrival counters, counters zero at
 // rest) is owned per (device, stream).
-#include "../../include/typhoon_linear.h"
-#include "tl_kernels.h"
+#include "host.h"
 
 #include <hip/hip_runtime.h>
 
@@ -32,57 +31,16 @@
 
 using namespace tl;
 
-struct tl_weights {
-  int dev = -1;
-  int rows = 0, cols = 0;
-  int KB = 0, NG = 0;
-  uint8_t* tiles = nullptr;   // NG * KB * 1024 bytes
-  float* scales = nullptr;    // NG * 16 floats, zero padded
-  size_t bytes = 0;
-};
 
-namespace {
+namespace tlhost {
 
-// --------------------------------------------------------------------------
-// errors
-// --------------------------------------------------------------------------
 thread_local std::string t_err;
 thread_local bool t_has_err = false;
-
-struct Fail {
-  std::string msg;
-};
 
 void record_error(const char* fn, const std::string& msg) {
   t_err = std::string(fn) + ": " + msg;
   t_has_err = true;
   std::fprintf(stderr, "[typhoon_linear] %s\n", t_err.c_str());
-}
-
-#define HIP_OK(expr)                                                                     \
-  do {                                                                                   \
-    hipError_t _e = (expr);                                                              \
-    if (_e != hipSuccess) throw Fail{std::string(#expr) + " -> " + hipGetErrorString(_e)}; \
-  } while (0)
-#define REQUIRE(cond, msg) \
-  do {                     \
-    if (!(cond)) throw Fail{msg}; \
-  } while (0)
-
-template <class F>
-int guarded(const char* fn, F&& f) {
-  t_has_err = false;
-  try {
-    f();
-    return 0;
-  } catch (const Fail& e) {
-    record_error(fn, e.msg);
-  } catch (const std::exception& e) {
-    record_error(fn, e.what());
-  } catch (...) {
-    record_error(fn, "unknown error");
-  }
-  return -1;
 }
 
 int current_device() {
@@ -91,86 +49,6 @@ int current_device() {
   return d;
 }
 
-// --------------------------------------------------------------------------
-// buffers
-// --------------------------------------------------------------------------
-struct DevBuf {
-  void* p = nullptr;
-  size_t n = 0;
-  // grows to at least `bytes`; `st` is synchronized before an old buffer is freed
-  void ensure(size_t bytes, hipStream_t st) {
-    if (bytes <= n) return;
-    if (p) {
-      HIP_OK(hipStreamSynchronize(st));
-      HIP_OK(hipFree(p));
-      p = nullptr;
-      n = 0;
-    }
-    size_t want = bytes < 256 ? 256 : bytes;
-    HIP_OK(hipMalloc(&p, want));
-    n = want;
-  }
-};
-
-// pinned host staging, mapped into the device address space (dp)
-struct PinnedBuf {
-  void* p = nullptr;
-  void* dp = nullptr;
-  size_t n = 0;
-  void ensure(size_t bytes) {
-    if (bytes <= n) return;
-    if (p) {
-      HIP_OK(hipHostFree(p));
-      p = dp = nullptr;
-      n = 0;
-    }
-    size_t want = bytes < 4096 ? 4096 : bytes;
-    HIP_OK(hipHostMalloc(&p, want, hipHostMallocDefault));
-    n = want;
-    HIP_OK(hipHostGetDevicePointer(&dp, p, 0));
-  }
-};
-
-// --------------------------------------------------------------------------
-// per (device, stream) work-space
-// --------------------------------------------------------------------------
-struct Workspace {
-  DevBuf part;        // split partial sums
-  DevBuf cnt;         // arrival counters (zero at rest)
-  size_t cnt_n = 0;
-  DevBuf act;         // activation codes (tiles or padded rows)
-  DevBuf act_s;       // activation scales
-  DevBuf xn;          // normalised hidden row (lm_head argmax)
-  DevBuf keys;        // per-work-group argmax keys
-};
-
-std::mutex g_ws_mu;
-std::map<std::pair<int, hipStream_t>, Workspace*> g_ws;
-
-Workspace& workspace(int dev, hipStream_t st) {
-  std::lock_guard<std::mutex> lk(g_ws_mu);
-  auto key = std::make_pair(dev, st);
-  auto it = g_ws.find(key);
-  if (it != g_ws.end()) return *it->second;
-  Workspace* w = new Workspace();
-  g_ws[key] = w;
-  return *w;
-}
-
-uint32_t* ensure_counters(Workspace& w, size_t n, hipStream_t st) {
-  if (n > w.cnt_n) {
-    size_t want = n < 65536 ? 65536 : n;
-    w.cnt.ensure(want * sizeof(uint32_t), st);
-    HIP_OK(hipMemsetAsync(w.cnt.p, 0, want * sizeof(uint32_t), st));
-    HIP_OK(hipStreamSynchronize(st));
-    w.cnt_n = want;
-  }
-  return static_cast<uint32_t*>(w.cnt.p);
-}
-
-// --------------------------------------------------------------------------
-// weights
-// --------------------------------------------------------------------------
 tl_weights* weights_alloc(int rows, int cols) {
   REQUIRE(rows > 0 && cols > 0, "rows and cols must be positive");
   tl_weights* W = new tl_weights();
@@ -228,6 +106,54 @@ tl_weights* weights_from_codes(const int8_t* w, const float* s, int rows, int co
     throw;
   }
   return W;
+}
+
+void check_weights(const tl_weights* W) {
+  REQUIRE(W != nullptr, "weights handle is NULL");
+  REQUIRE(W->dev == current_device(), "weights live on another device");
+}
+
+}  // namespace tlhost
+
+using namespace tlhost;
+
+namespace {
+
+// --------------------------------------------------------------------------
+// per (device, stream) work-space
+// --------------------------------------------------------------------------
+struct Workspace {
+  DevBuf part;        // split partial sums
+  DevBuf cnt;         // arrival counters (zero at rest)
+  size_t cnt_n = 0;
+  DevBuf act;         // activation codes (tiles or padded rows)
+  DevBuf act_s;       // activation scales
+  DevBuf xn;          // normalised hidden row (lm_head argmax)
+  DevBuf keys;        // per-work-group argmax keys
+};
+
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, Workspace*> g_ws;
+
+Workspace& workspace(int dev, hipStream_t st) {
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  auto key = std::make_pair(dev, st);
+  auto it = g_ws.find(key);
+  if (it != g_ws.end()) return *it->second;
+  Workspace* w = new Workspace();
+  g_ws[key] = w;
+  return *w;
+}
+
+uint32_t* ensure_counters(Workspace& w, size_t n, hipStream_t st) {
+  if (n > w.cnt_n) {
+    size_t want = n < 65536 ? 65536 : n;
+    w.cnt.ensure(want * sizeof(uint32_t), st);
+    HIP_OK(hipMemsetAsync(w.cnt.p, 0, want * sizeof(uint32_t), st));
+    HIP_OK(hipStreamSynchronize(st));
+    w.cnt_n = want;
+  }
+  return static_cast<uint32_t*>(w.cnt.p);
 }
 
 // --------------------------------------------------------------------------
@@ -391,10 +317,6 @@ void check_shape(int batch, int M, int K) {
 // --------------------------------------------------------------------------
 // device-level operations shared by Part 1 and Part 2
 // --------------------------------------------------------------------------
-void check_weights(const tl_weights* W) {
-  REQUIRE(W != nullptr, "weights handle is NULL");
-  REQUIRE(W->dev == current_device(), "weights live on another device");
-}
 
 // precomputed codes for the GEMV: row-major, zero padded to KB*64
 uint8_t* quantize_padded(Workspace& ws, const float* x, int K, float** xs_dev, hipStream_t st) {
@@ -1054,7 +976,7 @@ void op_lm_head_argmax(const float* h, const float* norm_w, const tl_weights* W,
   if (gemv_fused_norm_ok(K, h, norm_w)) {
     // every GEMV work-group normalises the row itself: one launch fewer
     L.x = h;
-    L.norm = true;
+    L.norm = NORM_NUMPY;
     L.norm_w = norm_w;
   } else {
     ws.xn.ensure((size_t)K * sizeof(float), st);
@@ -1115,6 +1037,30 @@ int tl_lm_head_argmax(const float* h, const float* norm_w, const int8_t* w_int8,
       HIP_OK(hipStreamSynchronize(c.st));
     }
     *token = *static_cast<const int32_t*>(c.htok.p);
+  });
+}
+
+int tl_gemv_fused_dev(const float* x, const tl_weights* W, const float* bias, float* y, int epi, int norm,
+                      const float* norm_w, void* stream) {
+  return guarded("tl_gemv_fused_dev", [&] {
+    check_weights(W);
+    REQUIRE(x && y, "bad arguments");
+    REQUIRE(epi == EPI_W8A32 || epi == EPI_SWIGLU, "epi must be 0 (W8A32) or 4 (SwiGLU)");
+    REQUIRE(norm >= NORM_NONE && norm <= NORM_DECODER, "norm must be 0, 1 or 2");
+    REQUIRE(norm == NORM_NONE || gemv_fused_norm_ok(W->cols, x, norm_w ? norm_w : x),
+            "a fused RMSNorm needs K = 1024 * 2^j <= 16384 and 16-byte aligned vectors");
+    GemvLaunch L;
+    L.x = x;
+    L.wt = W->tiles;
+    L.ws = W->scales;
+    L.bias = bias;
+    L.y = y;
+    L.N = W->rows;
+    L.K = W->cols;
+    L.epi = epi;
+    L.norm = norm;
+    L.norm_w = norm_w;
+    HIP_OK(launch_gemv_i8(L, static_cast<hipStream_t>(stream)));
   });
 }
 

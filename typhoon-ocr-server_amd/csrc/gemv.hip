@@ -48,9 +48,9 @@ struct GemvArgs {
   int32_t* acc_out;    // [N] (EPI_ACC)
   float* xs_out;       // optional activation scale output
   uint64_t* keys;      // EPI_ARGMAX: per-work-group keys
-  const float* norm_w; // final RMSNorm weights (norm)
+  const float* norm_w; // RMSNorm weights (norm)
   float norm_eps;
-  bool norm;
+  int norm;            // NORM_*
   int N, K, KB, NG, epi;
   int x_vec;           // 2: K == 1024*XV and x 16-byte aligned (unguarded loads)
 };
@@ -179,11 +179,51 @@ __device__ void final_rmsnorm(float4 (&xv)[XV], const float4 (&nwv)[XV], bool ha
   }
 }
 
+// The decoder's RMSNorm of the hidden row held in xv (kernel/ops.c:22-56):
+// rms_sq = sum(x^2) / K + eps, r = FRSQRTE(rms_sq) refined by two FRSQRTS
+// Newton steps, x = fl(fl(x * r) * w).  The reference sums the squares with
+// four sequential fused chains; the sum here is a tree (fused squares per
+// thread, DPP and LDS across the work-group), so rms_sq can differ in its
+// last bits: parity with the reference is by tolerance.
+template <int XV>
+__device__ void decoder_rmsnorm(float4 (&xv)[XV], const float4 (&nwv)[XV], bool has_w, int K, float eps) {
+  __shared__ float s_part[4];
+  float sq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < XV; i++) {
+    sq = __fmaf_rn(xv[i].x, xv[i].x, sq);
+    sq = __fmaf_rn(xv[i].y, xv[i].y, sq);
+    sq = __fmaf_rn(xv[i].z, xv[i].z, sq);
+    sq = __fmaf_rn(xv[i].w, xv[i].w, sq);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sq = __fadd_rn(sq, __shfl_xor(sq, o, 64));
+  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = sq;
+  __syncthreads();
+  const float tot = __fadd_rn(__fadd_rn(s_part[0], s_part[1]), __fadd_rn(s_part[2], s_part[3]));
+  const float r = ref_rsqrt(__fadd_rn(__fdiv_rn(tot, (float)K), eps));
+#pragma unroll
+  for (int i = 0; i < XV; i++) {
+    float4 v = xv[i];
+    v.x = __fmul_rn(v.x, r);
+    v.y = __fmul_rn(v.y, r);
+    v.z = __fmul_rn(v.z, r);
+    v.w = __fmul_rn(v.w, r);
+    if (has_w) {
+      v.x = __fmul_rn(v.x, nwv[i].x);
+      v.y = __fmul_rn(v.y, nwv[i].y);
+      v.z = __fmul_rn(v.z, nwv[i].z);
+      v.w = __fmul_rn(v.w, nwv[i].w);
+    }
+    xv[i] = v;
+  }
+}
+
 // Arguments are scalars so that the leading ones (through `flags`) are
 // preloaded into SGPRs at wave launch (kernarg preload, -amdgpu-kernarg-
 // preload-count in the build): the first loads need no kernarg fetch.
-// flags: bits 0-1 x_vec, bits 2-3 epilogue, bit 4 bias present, bit 5 final
-// RMSNorm of x first (K == 1024 XV a power of two, x_vec 2).
+// flags: bits 0-1 x_vec, bits 2-4 epilogue, bit 5 bias present, bits 6-7
+// RMSNorm of x first (NORM_*; K == 1024 XV a power of two, x_vec 2).
 template <int XV, int U, int RH>
 __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint8_t* wt, const float* ws,
                                                       float* y, int N, int K, int NG, int KB, int flags,
@@ -197,19 +237,19 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
   a.xs_in = xs_in;
   a.wt = wt;
   a.ws = ws;
-  a.bias = (flags & 16) ? bias : nullptr;
+  a.bias = (flags & 32) ? bias : nullptr;
   a.y = y;
   a.acc_out = acc_out;
   a.xs_out = xs_out;
   a.keys = keys;
   a.norm_w = norm_w;
   a.norm_eps = norm_eps;
-  a.norm = (flags & 32) != 0;
+  a.norm = (flags >> 6) & 3;
   a.N = N;
   a.K = K;
   a.KB = KB;
   a.NG = NG;
-  a.epi = (flags >> 2) & 3;
+  a.epi = (flags >> 2) & 7;
   a.x_vec = flags & 3;
   __shared__ uint4 s_codes[XV > 0 ? XV * 64 : 1];
   __shared__ uint32_t s_mx[4];
@@ -243,7 +283,7 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
   // never waits for weights
   float4 xv[XV > 0 ? XV : 1];
   float4 nwv[XV > 0 ? XV : 1];
-  const bool norm = (flags & 32) != 0;   // x is a hidden row to normalise first
+  const bool norm = ((flags >> 6) & 3) != NORM_NONE;   // x is a hidden row to normalise first
   if constexpr (XV > 0) {
     if (a.x_vec == 2) {
 #pragma unroll
@@ -276,7 +316,8 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
 
   float xs;
   if constexpr (XV > 0) {
-    if (norm) final_rmsnorm<XV>(xv, nwv, norm_w != nullptr, K, norm_eps);
+    if (a.norm == NORM_NUMPY) final_rmsnorm<XV>(xv, nwv, norm_w != nullptr, K, norm_eps);
+    else if (a.norm == NORM_DECODER) decoder_rmsnorm<XV>(xv, nwv, norm_w != nullptr, K, norm_eps);
     // ---- fused per-token activation quantization --------------------------
     uint32_t* sc = reinterpret_cast<uint32_t*>(s_codes);
     if ((K & 15) == 0) {
@@ -386,7 +427,14 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
       tot += (v.x + v.y) + (v.z + v.w);
     }
     const int n = row0 + lane;
-    if (n < a.N) {
+    if (a.epi == EPI_SWIGLU) {
+      // RH == 16: lanes 0-7 hold gate rows 8b + lane, lanes 8-15 the matching
+      // up rows; rows past N are zero rows (their value is never stored)
+      const float g = __fmul_rn(__fmul_rn((float)tot, wsv), xs);
+      const float u = __shfl(g, lane + 8, 64);
+      const int m = (row0 >> 1) + lane;
+      if (lane < 8 && m < (a.N >> 1)) a.y[m] = __fmul_rn(ref_silu(g), u);
+    } else if (n < a.N) {
       if (a.epi == EPI_ARGMAX) {
         float r = __fmul_rn(__fmul_rn((float)tot, wsv), xs);
         if (a.bias) r = __fadd_rn(r, bv);
@@ -416,8 +464,8 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
 // ---------------------------------------------------------------------------
 template <int XV, int U, int RH>
 static void launch_one(const GemvArgs& a, int blocks, hipStream_t st) {
-  const int flags = (a.x_vec & 3) | ((a.epi & 3) << 2) | (a.bias ? 16 : 0) | (a.norm ? 32 : 0);
-  const size_t dyn = a.norm ? (size_t)a.K * sizeof(float) : 0;
+  const int flags = (a.x_vec & 3) | ((a.epi & 7) << 2) | (a.bias ? 32 : 0) | ((a.norm & 3) << 6);
+  const size_t dyn = a.norm == NORM_NUMPY ? (size_t)a.K * sizeof(float) : 0;
   hipLaunchKernelGGL((gemv_i8_kernel<XV, U, RH>), dim3(blocks), dim3(256), dyn, st, a.x, a.wt, a.ws, a.y,
                      a.N, a.K, a.NG, a.KB, flags, a.xq, a.xs_in, a.bias, a.acc_out, a.xs_out, a.keys,
                      a.norm_w, a.norm_eps);
@@ -523,6 +571,7 @@ hipError_t launch_gemv_i8(const GemvLaunch& L, hipStream_t st) {
   a.norm_eps = L.norm_eps;
   a.norm = L.norm;
   if (L.epi == EPI_ARGMAX && !L.keys) return hipErrorInvalidValue;
+  if (L.epi == EPI_SWIGLU && (L.N % 16 != 0 || L.bias)) return hipErrorInvalidValue;
   a.N = L.N;
   a.K = L.K;
   a.KB = cdiv(L.K, 64);
@@ -530,7 +579,19 @@ hipError_t launch_gemv_i8(const GemvLaunch& L, hipStream_t st) {
   a.epi = L.epi;
   a.x_vec = 0;
   if (L.N <= 0 || L.K <= 0) return hipErrorInvalidValue;
-  const GemvPlan p = gemv_plan(L.N, L.K);
+  GemvPlan p = gemv_plan(L.N, L.K);
+  if (L.epi == EPI_SWIGLU && p.rows != 16) {
+    // gate and up rows meet in one 16-row work-group
+    p.rows = 16;
+    p.blocks = cdiv(L.N, 16);
+    const int n_i = cdiv(cdiv(L.K, 64), 4);
+    p.u = 8;
+    for (int u : {2, 4, 8, 12})
+      if (2 * u >= n_i) {
+        p.u = u;
+        break;
+      }
+  }
   const int xv = L.x ? gemv_fused_xv(L.K) : 0;
   if (L.x && xv == 0) return hipErrorInvalidValue;  // caller must quantize first
   if (L.x && L.K == 1024 * xv && (((uintptr_t)L.x) & 15) == 0) a.x_vec = 2;

@@ -260,6 +260,77 @@ __device__ inline uint2 i8x4_to_bf16x4(uint32_t w) {
 }
 
 // ---------------------------------------------------------------------------
+// The reference decoder's NEON estimate arithmetic (kernel/ops.c:22-56 RMSNorm
+// rsqrt, :478-531 SwiGLU), restated from the Arm architecture pseudocode
+// (FPRecipEstimate / FPRSqrtEstimate: 8-bit estimates, FZ = 0) for positive
+// normal inputs, the only inputs the decoder gives them.
+// ---------------------------------------------------------------------------
+// FRECPE: 1/x to 8 bits
+__device__ __forceinline__ float arm_frecpe(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const int e = (int)((u >> 23) & 0xff);
+  const uint32_t a = 2u * (256u + ((u & 0x7fffffu) >> 15)) + 1u;   // midpoint, units of 1/1024
+  uint32_t b = (uint32_t)(524288.0f / (float)a);                     // floor(2^19 / a), fixed below
+  if (b * a > 524288u) b--;
+  if ((b + 1u) * a <= 524288u) b++;
+  const uint32_t est = ((b + 1u) >> 1) & 0xffu;
+  int re = 253 - e;
+  uint32_t rf;
+  if (re == 0) {
+    rf = (1u << 22) | (est << 14);
+  } else if (re == -1) {
+    rf = (1u << 21) | (est << 13);
+    re = 0;
+  } else {
+    rf = est << 15;
+  }
+  return __uint_as_float((u & 0x80000000u) | ((uint32_t)re << 23) | rf);
+}
+
+// FRSQRTE: 1/sqrt(x) to 8 bits
+__device__ __forceinline__ float arm_frsqrte(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const int e = (int)((u >> 23) & 0xff);
+  const uint32_t f = u & 0x7fffffu;
+  uint32_t a = (e & 1) ? 128u + (f >> 16) : 256u + (f >> 15);      // [0.25, 1) in units of 1/512
+  if (a < 256u) a = a * 2u + 1u;
+  else a = ((a >> 1) << 1) * 2u + 2u;
+  // b = largest integer with a b^2 < 2^28
+  uint32_t b = (uint32_t)sqrtf(268435456.0f / (float)a);
+  while ((uint64_t)a * b * b >= (1ull << 28)) b--;
+  while ((uint64_t)a * (b + 1) * (b + 1) < (1ull << 28)) b++;
+  const uint32_t est = ((b + 1u) >> 1) & 0xffu;
+  const int re = (380 - e) / 2;
+  return __uint_as_float(((uint32_t)re << 23) | (est << 15));
+}
+
+// FRECPS / FRSQRTS: one rounding each
+__device__ __forceinline__ float arm_frecps(float a, float b) { return __fmaf_rn(-a, b, 2.0f); }
+__device__ __forceinline__ float arm_frsqrts(float a, float b) { return __fmul_rn(__fmaf_rn(-a, b, 3.0f), 0.5f); }
+
+// rsqrt as rmsnorm_f32 computes it: estimate and two Newton steps
+__device__ __forceinline__ float ref_rsqrt(float v) {
+  float r = arm_frsqrte(v);
+  r = __fmul_rn(r, arm_frsqrts(__fmul_rn(v, r), r));
+  r = __fmul_rn(r, arm_frsqrts(__fmul_rn(v, r), r));
+  return r;
+}
+
+// fast_exp_f32 (Schraudolph, exponent bits only): 2^(trunc(x log2 e + 126.94) - 127)
+__device__ __forceinline__ float ref_fast_exp(float x) {
+  x = fminf(fmaxf(x, -88.0f), 88.0f);
+  const int i = (int)__fmaf_rn(x, 1.4426950408889634f, 126.94269504f);   // truncates toward zero
+  return __uint_as_float((uint32_t)i << 23);
+}
+
+// silu of silu_mul_inplace's vector loop: (g * r0) * (2 - d r0), d = 1 + e^-g
+__device__ __forceinline__ float ref_silu(float g) {
+  const float d = __fadd_rn(1.0f, ref_fast_exp(-g));
+  const float r0 = arm_frecpe(d);
+  return __fmul_rn(__fmul_rn(g, r0), arm_frecps(d, r0));
+}
+
+// ---------------------------------------------------------------------------
 // global -> LDS tile copies and explicit waits (LDS-staged GEMMs)
 // ---------------------------------------------------------------------------
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0]+[15:14], expcnt[6:4],

@@ -12,7 +12,13 @@ __host__ __device__ inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 // GEMV epilogues (gemv.hip)
 // EPI_ARGMAX: W8A32 outputs (optionally stored), reduced per work-group to
 // the key of its largest output (argmax_key) written to keys[blockIdx.x]
-enum { EPI_W8A32 = 0, EPI_W8A8 = 1, EPI_ACC = 2, EPI_ARGMAX = 3 };
+// EPI_SWIGLU: W8A32 outputs of a gate/up weight interleaved per 16-row group
+// (rows 16b..16b+7 = gate rows 8b.., rows 16b+8.. = up rows 8b..), written as
+// y[8b + r] = fl(silu(gate) * up) with the reference's fast-exp silu
+enum { EPI_W8A32 = 0, EPI_W8A8 = 1, EPI_ACC = 2, EPI_ARGMAX = 3, EPI_SWIGLU = 4 };
+// GEMV x prologues: the numpy final RMSNorm (decoder.py:444-446) or the
+// decoder's RMSNorm (kernel/ops.c:22-56, estimate-based rsqrt)
+enum { NORM_NONE = 0, NORM_NUMPY = 1, NORM_DECODER = 2 };
 // GEMM A-operand modes and output types (gemm.hip)
 enum { A_I8 = 0, A_BF16 = 1, A_F16 = 2, A_F32X3 = 3 };
 enum { OUT_F32 = 0, OUT_BF16 = 1, OUT_F16 = 2, OUT_I32 = 3 };
@@ -37,6 +43,28 @@ hipError_t launch_argmax_keys(const uint64_t* keys, int n, int32_t* token, float
 // 4-byte-word copy by a kernel (bytes % 4 == 0), e.g. from mapped pinned host memory
 hipError_t launch_copy_words(const void* src, void* dst, size_t bytes, hipStream_t st);
 
+// ---- decode-step kernels (decoder.hip) ------------------------------------
+struct AttnDecodeArgs {
+  const float* qkv = nullptr;      // [nq*128 | nkv*128 | nkv*128] of the QKV GEMV
+  const float* q_norm = nullptr;   // [128]
+  const float* k_norm = nullptr;   // [128]
+  const float* cos_tab = nullptr;  // [max_seq x 64]
+  const float* sin_tab = nullptr;
+  float* kc = nullptr;             // this layer's cache [nkv][max_seq][128]
+  float* vc = nullptr;
+  const int* state = nullptr;      // device decode state (position, rotary position, counter)
+  float* pm = nullptr;             // partial maxima [nq][C]
+  float* pl = nullptr;             // partial sums [nq][C]
+  float* po = nullptr;             // partial outputs [nq][C][128]
+  int nq = 16, nkv = 8, max_seq = 0, C = 0;
+  float scale = 0.0f, eps = 1e-6f;
+};
+int attn_chunks(int max_seq);
+hipError_t launch_attn_decode(const AttnDecodeArgs& a, hipStream_t st);
+hipError_t launch_attn_combine(const AttnDecodeArgs& a, float* out, hipStream_t st);
+hipError_t launch_step_end(const uint64_t* keys, int n, const float* embed, int H, float* hidden, int* state,
+                           int32_t* tokens, int max_tokens, hipStream_t st);
+
 // ---- M=1 GEMV (gemv.hip) --------------------------------------------------
 struct GemvPlan {
   int rows = 16;       // rows per work-group (16 or 8)
@@ -53,7 +81,7 @@ struct GemvLaunch {
   int32_t* acc_out = nullptr;
   float* xs_out = nullptr;
   uint64_t* keys = nullptr;       // EPI_ARGMAX: one key per work-group (gemv_plan().blocks)
-  bool norm = false;              // final RMSNorm of x first (gemv_fused_norm_ok)
+  int norm = NORM_NONE;           // RMSNorm of x first (gemv_fused_norm_ok)
   const float* norm_w = nullptr;  //   its weights (null: none)
   float norm_eps = 1e-6f;
   int N = 0, K = 0, epi = EPI_W8A32;

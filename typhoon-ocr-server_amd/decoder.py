@@ -22,8 +22,11 @@ error behaviour, on the MI355X library:
     batch-dependent numerics; get_logits() / sample() are _get_logits and the
     greedy branch of _sample.
 
-The 28-layer loop itself (norms, M-RoPE, attention, KV cache:
-kernel/decoder.c:33-314) is not part of this library.
+With the layer norms given (random_layer_weights(norms=True) or real
+weights), the Decoder also builds the device-resident layer loop through the
+reference's decoder C ABI (decoder_set_layer_weights, decoder_decode_step:
+kernel/decoder.c:300-526): step() is the reference's Decoder.step, and
+generate_greedy() runs the greedy decode loop on the GPU.
 """
 from __future__ import annotations
 
@@ -80,13 +83,24 @@ def qwen3vl_shapes(num_layers: int = NUM_LAYERS, vocab: int = VOCAB) -> Dict[str
     return out
 
 
+NORMS = ("input_ln", "post_attn_ln", "q_norm", "k_norm")
+MROPE_SECTIONS = (24, 20, 20)           # reference decoder.py:40
+MROPE_THETA_BASE = (5000000.0,) * 3     # reference decoder.py:41
+
+
 def random_layer_weights(rng: np.random.Generator, hidden: int = HIDDEN_DIM, kv: int = KV_DIM,
-                         ffn: int = FFN_DIM, std: float = 0.02) -> Dict[str, np.ndarray]:
-    """Random-init fp32 weights of one layer's seven projections."""
+                         ffn: int = FFN_DIM, std: float = 0.02, norms: bool = False) -> Dict[str, np.ndarray]:
+    """Random-init fp32 weights of one layer's seven projections (and, with
+    norms=True, its RMSNorm weights: input_ln / post_attn_ln [hidden],
+    q_norm / k_norm [128], around 1)."""
     shapes = {"q_proj": (hidden, hidden), "k_proj": (kv, hidden), "v_proj": (kv, hidden),
               "o_proj": (hidden, hidden), "gate_proj": (ffn, hidden), "up_proj": (ffn, hidden),
               "down_proj": (hidden, ffn)}
-    return {k: (rng.standard_normal(s, dtype=np.float32) * np.float32(std)) for k, s in shapes.items()}
+    out = {k: (rng.standard_normal(s, dtype=np.float32) * np.float32(std)) for k, s in shapes.items()}
+    if norms:
+        for k, n in (("input_ln", hidden), ("post_attn_ln", hidden), ("q_norm", HEAD_DIM), ("k_norm", HEAD_DIM)):
+            out[k] = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    return out
 
 
 class Decoder:
@@ -100,10 +114,12 @@ class Decoder:
 
     def __init__(self, layers: List[Mapping[str, np.ndarray]], lib: Optional[ctypes.CDLL] = None,
                  lm_head: Optional[np.ndarray] = None, final_norm: Optional[np.ndarray] = None,
-                 verbose: bool = False):
+                 verbose: bool = False, max_seq: int = MAX_SEQ_LEN):
         self._lib = lib or load_decoder_lib()
         self._weight_store: list = []          # keep numpy arrays alive (reference :215)
         self.layers: List[Dict[str, tuple]] = []
+        self._max_seq = max_seq
+        self._c_model = self._c_cache = self._c_scratch = None   # device loop, built with the first norms
         for l_idx, layer in enumerate(layers):
             self._register_layer(l_idx, layer)
             if verbose and ((l_idx + 1) % 7 == 0 or l_idx == len(layers) - 1):
@@ -156,6 +172,8 @@ class Decoder:
         self._lib = lib or load_decoder_lib()
         self._weight_store = []
         self.layers = []
+        self._max_seq = MAX_SEQ_LEN
+        self._c_model = self._c_cache = self._c_scratch = None
         names = _lin.cache_list(path)
         n_layers = 1 + max((int(n.split(".")[1]) for n in names if n.startswith("layers.")), default=-1)
         for l_idx in range(n_layers):
@@ -203,6 +221,10 @@ class Decoder:
 
     def _register_layer(self, l_idx: int, layer: Mapping[str, np.ndarray]) -> None:
         q = {name: self._quantize_and_keep(layer[name]) for name in PROJECTIONS}
+        if all(n in layer for n in NORMS):
+            norms = [np.ascontiguousarray(layer[n], dtype=np.float32) for n in NORMS]
+            self._weight_store.extend(norms)
+            self._set_device_layer(l_idx, q, norms)
         # fused Q||K||V [4096 x 2048] and gate||up [12288 x 2048] (reference :290-302)
         qkv_w = np.ascontiguousarray(np.concatenate([q["q_proj"][0], q["k_proj"][0], q["v_proj"][0]], axis=0))
         qkv_s = np.ascontiguousarray(np.concatenate([q["q_proj"][1], q["k_proj"][1], q["v_proj"][1]]))
@@ -215,6 +237,93 @@ class Decoder:
         for w, s in entry.values():
             self._register(w, s)
         self.layers.append(entry)
+
+    # -- device layer loop (reference decoder.py:197-210, :304-317, :322-370) --
+    def _init_device_loop(self) -> None:
+        if self._c_model:
+            return
+        lib = self._lib
+        max_seq = self._max_seq
+        self._c_model = lib.decoder_model_alloc()
+        self._c_cache = lib.decoder_cache_alloc(max_seq)
+        self._c_scratch = lib.decoder_scratch_alloc_fn(max_seq)
+        if not (self._c_model and self._c_cache and self._c_scratch):
+            _lin.check(lib, "decoder handles")
+            raise RuntimeError("decoder handle allocation failed")
+        half = HEAD_DIM // 2
+        self._cos_tab = np.empty((max_seq, half), dtype=np.float32)
+        self._sin_tab = np.empty((max_seq, half), dtype=np.float32)
+        lib.decoder_precompute_rope(_np_ptr(self._cos_tab), _np_ptr(self._sin_tab), max_seq, HEAD_DIM,
+                                    (ctypes.c_int * 3)(*MROPE_SECTIONS), (ctypes.c_float * 3)(*MROPE_THETA_BASE))
+        _lin.check(lib, "decoder_precompute_rope")
+
+    def _set_device_layer(self, l_idx: int, q: Mapping[str, tuple], norms: List[np.ndarray]) -> None:
+        self._init_device_loop()
+        args = []
+        for name in PROJECTIONS:
+            w, s_ = q[name]
+            args += [_np_ptr(w, ctypes.c_int8), _np_ptr(s_)]
+        args += [_np_ptr(n) for n in norms]
+        self._lib.decoder_set_layer_weights(self._c_model, l_idx, *args)
+        _lin.check(self._lib, "decoder_set_layer_weights")
+
+    def reset(self) -> None:
+        """Clear the KV cache for a new sequence (reference :322-323)."""
+        self._lib.decoder_cache_clear(self._c_cache)
+
+    def set_rope_offset(self, offset: int) -> None:
+        self._lib.decoder_cache_set_rope_offset(self._c_cache, offset)
+
+    @property
+    def cache_len(self) -> int:
+        return self._lib.tl_decoder_cache_len(self._c_cache)
+
+    def step(self, hidden_np: np.ndarray) -> np.ndarray:
+        """One decode step of every layer for hidden [1, HIDDEN_DIM]
+        (reference :360-370, decoder_decode_step)."""
+        assert hidden_np.ndim == 2 and hidden_np.shape == (1, HIDDEN_DIM)
+        hidden_c = np.array(hidden_np, dtype=np.float32, copy=True)
+        self._lib.decoder_decode_step(self._c_model, self._c_cache, _np_ptr(hidden_c), self._c_scratch,
+                                      _np_ptr(self._cos_tab), _np_ptr(self._sin_tab))
+        _lin.check(self._lib, "decoder_decode_step")
+        return hidden_c
+
+    def read_cache(self, layer: int):
+        """(K, V) of one layer, each [8, max_seq, 128] fp32."""
+        k = np.empty((NUM_KV_HEADS, self._max_seq, HEAD_DIM), np.float32)
+        v = np.empty_like(k)
+        if self._lib.tl_decoder_read_cache(self._c_cache, layer, _np_ptr(k), _np_ptr(v)) != 0:
+            _lin.check(self._lib, "tl_decoder_read_cache")
+        return k, v
+
+    def generate_greedy(self, first_token: int, n_steps: int, embed_dev, lm_head_dev: "_lin.DeviceWeights"):
+        """Greedy decode loop on the device (reference :494-507 with
+        do_sample=False): n_steps tokens after first_token; embed_dev is a
+        device tensor [vocab, HIDDEN_DIM] fp32, lm_head_dev the packed lm_head."""
+        tokens = np.empty(n_steps, np.int32)
+        fn = None if self._final_norm_w is None else _np_ptr(self._final_norm_w)
+        rc = self._lib.tl_decoder_generate(self._c_model, self._c_cache, self._c_scratch, lm_head_dev.handle, fn,
+                                           embed_dev.data_ptr(), int(first_token), int(n_steps),
+                                           tokens.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                                           _np_ptr(self._cos_tab), _np_ptr(self._sin_tab))
+        if rc != 0:
+            _lin.check(self._lib, "tl_decoder_generate")
+        return tokens
+
+    def close(self) -> None:
+        lib = self._lib
+        for attr, fn in (("_c_model", lib.decoder_model_free), ("_c_cache", lib.decoder_cache_free),
+                         ("_c_scratch", lib.decoder_scratch_free_fn)):
+            h = getattr(self, attr, None)
+            if h:
+                fn(h)
+                setattr(self, attr, None)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
     # -- core operations ------------------------------------------------------
     def project(self, l_idx: int, name: str, x: np.ndarray, out: Optional[np.ndarray] = None) -> np.ndarray:

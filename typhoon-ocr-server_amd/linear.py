@@ -41,6 +41,25 @@ SIGNATURES = {
     "tl_device_count": (_int, []),
     "tl_gemv_set_plan": (_int, [_int, _int]),
     "tl_gemm_i8_set_cfg": (_int, [_int]),
+    "tl_gemv_fused_dev": (_int, [_vp, _vp, _vp, _vp, _int, _int, _vp, _vp]),
+    # decoder loop (Part 3), reference argtypes (decoder.py:86-143)
+    "decoder_model_alloc": (_vp, []),
+    "decoder_model_free": (None, [_vp]),
+    "decoder_cache_alloc": (_vp, [_int]),
+    "decoder_cache_free": (None, [_vp]),
+    "decoder_cache_clear": (None, [_vp]),
+    "decoder_cache_set_rope_offset": (None, [_vp, _int]),
+    "decoder_scratch_alloc_fn": (_vp, [_int]),
+    "decoder_scratch_free_fn": (None, [_vp]),
+    "decoder_set_layer_weights": (None, [_vp, _int] + [_i8p, _f32p] * 7 + [_f32p] * 4),
+    "decoder_set_layer_weights_v32": (None, [_vp, _int] + [_i8p, _f32p] * 7 + [_f32p] * 4 + [_i8p, _f32p] * 2),
+    "decoder_precompute_rope": (None, [_f32p, _f32p, _int, _int, ctypes.POINTER(ctypes.c_int), _f32p]),
+    "decoder_decode_step": (None, [_vp, _vp, _f32p, _vp, _f32p, _f32p]),
+    "tl_decoder_num_layers": (_int, [_vp]),
+    "tl_decoder_cache_len": (_int, [_vp]),
+    "tl_decoder_read_cache": (_int, [_vp, _int, _f32p, _f32p]),
+    "tl_decoder_generate": (_int, [_vp, _vp, _vp, _vp, _f32p, _vp, _int, _int,
+                                   ctypes.POINTER(ctypes.c_int32), _f32p, _f32p]),
     "tl_weights_save": (_int, [_vp, ctypes.c_char_p, ctypes.c_char_p, _int]),
     "tl_weights_load": (_vp, [ctypes.c_char_p, ctypes.c_char_p]),
     "tl_weights_cache_list": (_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
@@ -331,6 +350,13 @@ def gemm_acc_dev(x_q, W: DeviceWeights, acc, stream=None):
     lib = load_library()
     _rc(lib, lib.tl_w8a8_gemm_acc_dev(x_q.data_ptr(), W.handle, acc.data_ptr(), x_q.shape[0],
                                       _stream(stream)), "tl_w8a8_gemm_acc_dev")
+
+
+def gemv_fused_dev(x, W: DeviceWeights, y, epi=0, norm=0, norm_w=None, bias=None, stream=None):
+    """The M=1 GEMV with the decoder's fusions (tl_gemv_fused_dev)."""
+    lib = load_library()
+    _rc(lib, lib.tl_gemv_fused_dev(x.data_ptr(), W.handle, _ptr(bias), y.data_ptr(), epi, norm, _ptr(norm_w),
+                                   _stream(stream)), "tl_gemv_fused_dev")
 
 
 def lm_head_argmax_dev(h, norm_w, W: DeviceWeights, token, logits=None, max_logit=None, stream=None):
