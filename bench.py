@@ -192,6 +192,81 @@ def bench_w8a8_prefill(lin, torch, dev, reps=20):
     return out
 
 
+def bench_decoder_generate(lin, torch, dev, n_layers=28, vocab=151936, prefix=1200, steps=512):
+    """Device-resident greedy decode of the full 28-layer decoder (the decode
+    phase of the 1200-token-prefill, 512-step workload): random int8 weights
+    per row-scaled projection, a random fp32 embedding table, lm_head over
+    the full vocabulary.  The KV cache is first filled to `prefix` positions
+    by decode steps (untimed); then `steps` greedy steps run as graph replays
+    (28 x 6 layer launches + lm_head + token/embedding step) and are timed."""
+    import ctypes
+    lib = lin.load_library()
+    rng = np.random.default_rng(5)
+    H, KV, FF, HD = 2048, 1024, 6144, 128
+    max_seq = 2048
+    model = lib.decoder_model_alloc()
+    cache = lib.decoder_cache_alloc(max_seq)
+    scratch = lib.decoder_scratch_alloc_fn(max_seq)
+    f32p = ctypes.POINTER(ctypes.c_float)
+    i8p = ctypes.POINTER(ctypes.c_int8)
+
+    def mat(n, k):
+        w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+        s = rng.uniform(1e-4, 5e-4, n).astype(np.float32)   # keeps activations O(1)
+        return w, s
+
+    def vec(n):
+        return (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    for l in range(n_layers):
+        mats = [mat(H, H), mat(KV, H), mat(KV, H), mat(H, H), mat(FF, H), mat(FF, H), mat(H, FF)]
+        norms = [vec(H), vec(H), vec(HD), vec(HD)]
+        args = []
+        for w, s in mats:
+            args += [w.ctypes.data_as(i8p), s.ctypes.data_as(f32p)]
+        args += [n.ctypes.data_as(f32p) for n in norms]
+        lib.decoder_set_layer_weights(model, l, *args)
+        lin.check(lib, "decoder_set_layer_weights")
+    lm_w = torch.randint(-127, 128, (vocab, H), dtype=torch.int8, device=dev)
+    lm_s = torch.rand(vocab, device=dev) * 4e-4 + 1e-4
+    lm = lin.DeviceWeights.from_codes(lm_w, lm_s)
+    del lm_w
+    embed = torch.randn((vocab, H), device=dev)
+    fnorm = vec(H)
+    half = HD // 2
+    cos = np.empty((max_seq, half), np.float32)
+    sin = np.empty((max_seq, half), np.float32)
+    lib.decoder_precompute_rope(cos.ctypes.data_as(f32p), sin.ctypes.data_as(f32p), max_seq, HD,
+                                (ctypes.c_int * 3)(24, 20, 20), (ctypes.c_float * 3)(5e6, 5e6, 5e6))
+
+    def generate(first, n):
+        toks = np.empty(n, np.int32)
+        rc = lib.tl_decoder_generate(model, cache, scratch, lm.handle, fnorm.ctypes.data_as(f32p),
+                                     embed.data_ptr(), int(first), int(n),
+                                     toks.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                                     cos.ctypes.data_as(f32p), sin.ctypes.data_as(f32p))
+        if rc != 0:
+            lin.check(lib, "tl_decoder_generate")
+        return toks
+
+    lib.decoder_cache_clear(cache)
+    t0 = time.perf_counter()
+    toks = generate(1, prefix)                     # fills the cache (and captures the graph)
+    t_fill = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    toks2 = generate(int(toks[-1]), steps)
+    t = time.perf_counter() - t0
+    out = {"tok_s": round(steps / t, 1), "ms_per_token": round(t / steps * 1e3, 4),
+           "layers": n_layers, "vocab": vocab, "cache_len_start": prefix, "steps": steps,
+           "launches_per_token": n_layers * 6 + 2, "fill_tok_s": round(prefix / t_fill, 1),
+           "distinct_tokens": int(len(set(toks2.tolist()))),
+           "timing": "host wall clock around graph replays + the tokens' device-to-host copy"}
+    lm.close()
+    lib.decoder_model_free(model)
+    lib.decoder_cache_free(cache)
+    lib.decoder_scratch_free_fn(scratch)
+    return out
+
+
 def cpu_baseline(seconds=10.0):
     """The oracle's M=1 GEMV (same formula as the reference's w8a32_gemv,
     OpenMP over row chunks like its GCD fan-out) on the host cores, over the
@@ -373,6 +448,8 @@ def main():
                     help="decode set only (no prefill, sweeps or CPU baseline)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the W8A8 prefill timing (for counter runs)")
+    ap.add_argument("--decoder-only", action="store_true",
+                    help="only the device-resident 28-layer greedy decoder timing")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run a 512 MiB device copy (counter calibration) and one eager decode "
                          "step, then exit; used under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
@@ -394,6 +471,9 @@ def main():
 
     if args.prefill_only:
         print(json.dumps({"w8a8_prefill": bench_w8a8_prefill(lin, torch, dev)}), flush=True)
+        return
+    if args.decoder_only:
+        print(json.dumps({"decoder_greedy": bench_decoder_generate(lin, torch, dev)}), flush=True)
         return
     log("building the decode set (1.72 GB of int8 weights)")
     items = build_decode_set(lin, torch, dev)
@@ -480,6 +560,11 @@ def main():
         log("W8A32 prefill (fp32 semantics)")
         pre32 = bench_w8a32_prefill(lin, torch, dev)
 
+    dec = None
+    if not args.quick:
+        log("device-resident greedy decoder (28 layers)")
+        dec = bench_decoder_generate(lin, torch, dev)
+
     cpu = None
     if not args.no_cpu and not args.quick and rank == 0:
         log("CPU baseline")
@@ -506,6 +591,7 @@ def main():
         "wall_s": round(wall, 3),
         "roofline": roofline,
         "lm_head_greedy": greedy,
+        "decoder_greedy": dec,
         "w8a8_prefill": prefill,
         "w8a32_decode_rows": rows,
         "w8a16_sweep": sweep,

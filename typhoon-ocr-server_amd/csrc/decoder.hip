@@ -47,17 +47,14 @@ __device__ __forceinline__ float head_rmsnorm(float v, float w, float* s_two, fl
   return __fmul_rn(__fmul_rn(v, r), w);
 }
 
-// rotate_half at one position: element d of a head held in s_head[0..127]
-__device__ __forceinline__ float rope_at(const float* s_head, int d, const float* co, const float* si) {
-  const int j = d & 63;
-  const float lo = s_head[j], hi = s_head[j + 64];
-  const float c = co[j], s = si[j];
-  return d < 64 ? __fsub_rn(__fmul_rn(lo, c), __fmul_rn(hi, s)) : __fadd_rn(__fmul_rn(hi, c), __fmul_rn(lo, s));
-}
 
 // Work-group (c, h): kv head h, positions [64 c, 64 c + 64) of the S = len + 1
-// that the new token attends to; two q heads (GQA group 2).  256 threads:
-// thread t holds element t & 127 of q head 2h + (t >> 7).
+// that the new token attends to; two q heads (GQA group 2).  256 threads.
+// Every load of the chunk (its K and V rows, the q/k/v rows of the QKV
+// output, norm weights, rope row) is issued first, so the norm/rotation
+// prologue runs while they are in flight.  Positions past the chunk end read
+// a clamped valid row and are masked; position p (the new token, whose cache
+// row this work-group writes) is taken from LDS instead of memory.
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   const int c = blockIdx.x, h = blockIdx.y;
   const int p = a.state[0];                 // position of the new token
@@ -66,67 +63,86 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   if (t0 >= S) return;                      // uniform: the whole work-group leaves
   const int t1 = min(t0 + ATT_T, S);
   const int rp = a.state[1];
-  const float* co = a.cos_tab + (size_t)rp * 64;
-  const float* si = a.sin_tab + (size_t)rp * 64;
 
   __shared__ float s_x[2][HD];              // normalised heads before the rotation
   __shared__ float s_q[2][HD];              // rotated q heads
   __shared__ float s_k[HD], s_v[HD];        // the new token's k (rotated) and v
   __shared__ float s_red[4];
   __shared__ float s_p[2][ATT_T];           // scores, then probabilities
+  __shared__ float4 s_o[8][2][HD / 4];      // V partial sums of the 8 position groups
 
   const int tid = threadIdx.x, g = tid >> 7, d = tid & 127;
   const int lane = tid & 63, wv = tid >> 6;
   const bool has_new = p < t1;              // this chunk holds position p
 
-  // q: RMSNorm with q_norm, then the rotation
-  const float qn = head_rmsnorm(a.qkv[(2 * h + g) * HD + d], a.q_norm[d], s_red, a.eps);
-  s_x[g][d] = qn;
-  __syncthreads();
-  s_q[g][d] = rope_at(s_x[g], d, co, si);
-  __syncthreads();
+  // ---- loads ---------------------------------------------------------------
+  // scores: 16 lanes per position (8 elements each), wave w takes positions
+  // t0 + 16 w + 4 it + (lane >> 4), it = 0..3
+  const int seg = lane & 15;
+  const float* kbase = a.kc + (size_t)h * a.max_seq * HD;
+  float4 kr[4][2];
+#pragma unroll
+  for (int it = 0; it < 4; it++) {
+    const int t = min(t0 + wv * 16 + it * 4 + (lane >> 4), t1 - 1);
+    const float4* kp = reinterpret_cast<const float4*>(kbase + (size_t)t * HD + seg * 8);
+    kr[it][0] = kp[0];
+    kr[it][1] = kp[1];
+  }
+  // V: thread (pg = tid >> 5, d4 = tid & 31) reads float4 d4 of positions
+  // t0 + pg + 8 i, i = 0..7
+  const int pg = tid >> 5, d4 = tid & 31;
+  const float4* vbase = reinterpret_cast<const float4*>(a.vc + (size_t)h * a.max_seq * HD) + d4;
+  float4 vr[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) vr[i] = vbase[(size_t)min(t0 + pg + 8 * i, t1 - 1) * (HD / 4)];
+  const float qraw = a.qkv[(2 * h + g) * HD + d];
+  const float qw = a.q_norm[d];
+  const float* kv_src = a.qkv + a.nq * HD + (g == 0 ? h * HD : a.nkv * HD + h * HD);
+  const float kvraw = has_new ? kv_src[d] : 0.0f;
+  const float kw = a.k_norm[d];
+  const int j = d & 63;
+  const float co = a.cos_tab[(size_t)rp * 64 + j], si = a.sin_tab[(size_t)rp * 64 + j];
 
+  // ---- q: RMSNorm with q_norm, then the rotation -----------------------------
+  s_x[g][d] = head_rmsnorm(qraw, qw, s_red, a.eps);
+  __syncthreads();
+  {
+    const float lo = s_x[g][j], hi = s_x[g][j + 64];
+    s_q[g][d] = d < 64 ? __fsub_rn(__fmul_rn(lo, co), __fmul_rn(hi, si)) : __fadd_rn(__fmul_rn(hi, co), __fmul_rn(lo, si));
+  }
   if (has_new) {
     // threads 0-127: k of kv head h (k_norm, rotation); 128-255: v
-    const float* kv_src = a.qkv + a.nq * HD + (g == 0 ? h * HD : a.nkv * HD + h * HD);
-    const float raw = kv_src[d];
-    const float kn = head_rmsnorm(raw, a.k_norm[d], s_red, a.eps);   // all threads; g == 1 unused
+    const float kn = head_rmsnorm(kvraw, kw, s_red, a.eps);   // every thread; g == 1 unused
     if (g == 0) s_x[0][d] = kn;
     __syncthreads();
     const size_t off = ((size_t)h * a.max_seq + p) * HD + d;
     if (g == 0) {
-      const float kr = rope_at(s_x[0], d, co, si);
-      s_k[d] = kr;
-      a.kc[off] = kr;
+      const float lo = s_x[0][j], hi = s_x[0][j + 64];
+      const float kr_ = d < 64 ? __fsub_rn(__fmul_rn(lo, co), __fmul_rn(hi, si)) : __fadd_rn(__fmul_rn(hi, co), __fmul_rn(lo, si));
+      s_k[d] = kr_;
+      a.kc[off] = kr_;
     } else {
-      s_v[d] = raw;
-      a.vc[off] = raw;
+      s_v[d] = kvraw;
+      a.vc[off] = kvraw;
     }
-    __syncthreads();
   }
+  __syncthreads();
 
-  // scores: 16 lanes per position (8 elements each), 4 positions per wave
-  // instruction, wave w takes positions t0 + 16 w .. t0 + 16 w + 15
-  const int seg = lane & 15;
+  // ---- scores ----------------------------------------------------------------
   float q0[8], q1[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) {
     q0[i] = s_q[0][seg * 8 + i];
     q1[i] = s_q[1][seg * 8 + i];
   }
-  const float* kbase = a.kc + (size_t)h * a.max_seq * HD;
 #pragma unroll
   for (int it = 0; it < 4; it++) {
     const int t = t0 + wv * 16 + it * 4 + (lane >> 4);
-    float kv8[8];
-    if (t < t1 && t != p) {
-      const float4* kp = reinterpret_cast<const float4*>(kbase + (size_t)t * HD + seg * 8);
-      const float4 k0 = kp[0], k1 = kp[1];
-      kv8[0] = k0.x; kv8[1] = k0.y; kv8[2] = k0.z; kv8[3] = k0.w;
-      kv8[4] = k1.x; kv8[5] = k1.y; kv8[6] = k1.z; kv8[7] = k1.w;
-    } else {
+    float kv8[8] = {kr[it][0].x, kr[it][0].y, kr[it][0].z, kr[it][0].w,
+                    kr[it][1].x, kr[it][1].y, kr[it][1].z, kr[it][1].w};
+    if (t == p) {
 #pragma unroll
-      for (int i = 0; i < 8; i++) kv8[i] = (t == p) ? s_k[seg * 8 + i] : 0.0f;
+      for (int i = 0; i < 8; i++) kv8[i] = s_k[seg * 8 + i];
     }
     float d0 = 0.0f, d1 = 0.0f;
 #pragma unroll
@@ -146,7 +162,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   }
   __syncthreads();
 
-  // chunk softmax statistics: wave g for q head 2h + g
+  // ---- chunk softmax statistics: wave g for q head 2h + g ---------------------
   const int n = t1 - t0;
   if (wv < 2) {
     const float sc = lane < n ? s_p[wv][lane] : -3.0e38f;
@@ -157,7 +173,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
     float l = e;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) l = __fadd_rn(l, __shfl_xor(l, o, 64));
-    if (lane < n) s_p[wv][lane] = e;
+    s_p[wv][lane] = e;                      // zero past the chunk end
     if (lane == 0) {
       const int qh = 2 * h + wv;
       a.pm[qh * a.C + c] = m;
@@ -166,37 +182,67 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   }
   __syncthreads();
 
-  // unnormalised output of the chunk: thread (g, d) over the chunk's positions
-  const float* vbase = a.vc + (size_t)h * a.max_seq * HD + d;
+  // ---- unnormalised output of the chunk ------------------------------------------
+  float4 o0 = make_float4(0.f, 0.f, 0.f, 0.f), o1 = o0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int t = t0 + pg + 8 * i;
+    float4 v = vr[i];
+    if (t == p) v = reinterpret_cast<const float4*>(s_v)[d4];
+    if (t >= t1) v = make_float4(0.f, 0.f, 0.f, 0.f);
+    const float w0 = s_p[0][pg + 8 * i], w1 = s_p[1][pg + 8 * i];
+    o0.x = __fmaf_rn(w0, v.x, o0.x); o0.y = __fmaf_rn(w0, v.y, o0.y);
+    o0.z = __fmaf_rn(w0, v.z, o0.z); o0.w = __fmaf_rn(w0, v.w, o0.w);
+    o1.x = __fmaf_rn(w1, v.x, o1.x); o1.y = __fmaf_rn(w1, v.y, o1.y);
+    o1.z = __fmaf_rn(w1, v.z, o1.z); o1.w = __fmaf_rn(w1, v.w, o1.w);
+  }
+  s_o[pg][0][d4] = o0;
+  s_o[pg][1][d4] = o1;
+  __syncthreads();
+  const float* so = reinterpret_cast<const float*>(&s_o[0][0][0]);
   float o = 0.0f;
-  int t = t0;
-  for (; t + 4 <= t1; t += 4) {
-    float v4[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) v4[i] = (t + i == p) ? s_v[d] : vbase[(size_t)(t + i) * HD];
-#pragma unroll
-    for (int i = 0; i < 4; i++) o = __fmaf_rn(s_p[g][t + i - t0], v4[i], o);
-  }
-  for (; t < t1; t++) {
-    const float v = (t == p) ? s_v[d] : vbase[(size_t)t * HD];
-    o = __fmaf_rn(s_p[g][t - t0], v, o);
-  }
+  for (int q = 0; q < 8; q++) o = __fadd_rn(o, so[(q * 2 + g) * HD + d]);
   a.po[((size_t)(2 * h + g) * a.C + c) * HD + d] = o;
 }
 
-// one work-group per q head: out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c
+// One work-group per q head: out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
+// The chunk statistics go through LDS; each thread's partial outputs are
+// loaded 32 chunks at a time, all in flight together.
 __global__ __launch_bounds__(128) void attn_combine_kernel(const float* __restrict__ pm, const float* __restrict__ pl,
                                                            const float* __restrict__ po, const int* __restrict__ state,
                                                            int C, float* __restrict__ out) {
   const int qh = blockIdx.x, d = threadIdx.x;
   const int nc = cdiv(state[0] + 1, ATT_T);
-  float M = -3.0e38f;
-  for (int c = 0; c < nc; c++) M = fmaxf(M, pm[qh * C + c]);
+  __shared__ float s_m[128], s_l[128];
+  __shared__ float s_M;
+  for (int c = d; c < nc; c += 128) {
+    s_m[c] = pm[qh * C + c];
+    s_l[c] = pl[qh * C + c];
+  }
+  __syncthreads();
+  if (d < 64) {
+    float m = -3.0e38f;
+    for (int c = d; c < nc; c += 64) m = fmaxf(m, s_m[c]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if (d == 0) s_M = m;
+  }
+  __syncthreads();
+  const float M = s_M;
   float L = 0.0f, o = 0.0f;
-  for (int c = 0; c < nc; c++) {
-    const float w = expf(__fsub_rn(pm[qh * C + c], M));
-    L = __fmaf_rn(w, pl[qh * C + c], L);
-    o = __fmaf_rn(w, po[((size_t)qh * C + c) * HD + d], o);
+  for (int c0 = 0; c0 < nc; c0 += 32) {
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) v[i] = (c0 + i < nc) ? po[((size_t)qh * C + c0 + i) * HD + d] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+      if (c0 + i < nc) {
+        const float w = expf(__fsub_rn(s_m[c0 + i], M));
+        L = __fmaf_rn(w, s_l[c0 + i], L);
+        o = __fmaf_rn(w, v[i], o);
+      }
+    }
   }
   out[qh * HD + d] = __fmul_rn(o, __fdiv_rn(1.0f, L));
 }
@@ -237,7 +283,8 @@ __global__ __launch_bounds__(1024) void step_end_kernel(const uint64_t* __restri
 }
 
 hipError_t launch_attn_decode(const AttnDecodeArgs& a, hipStream_t st) {
-  if (a.nq != 2 * a.nkv || a.C * ATT_T < a.max_seq) return hipErrorInvalidValue;
+  // the combine kernel keeps up to 128 chunk statistics in LDS
+  if (a.nq != 2 * a.nkv || a.C * ATT_T < a.max_seq || a.C > 128) return hipErrorInvalidValue;
   hipLaunchKernelGGL(attn_decode_kernel, dim3(a.C, a.nkv), dim3(256), 0, st, a);
   return hipGetLastError();
 }
