@@ -482,6 +482,7 @@ void decoder_decode_step(const ModelWeights* model, KVCache* cache, float* hidde
 // ==========================================================================
 int tl_decoder_num_layers(const ModelWeights* model) { return model ? model->num_layers() : -1; }
 
+
 int tl_decoder_read_cache(const KVCache* cache, int layer, float* k, float* v) {
   return guarded("tl_decoder_read_cache", [&] {
     REQUIRE(cache && layer >= 0 && layer < NL, "bad arguments");

@@ -29,23 +29,6 @@ namespace tl {
 constexpr int HD = 128;          // head dim
 constexpr int ATT_T = 64;        // positions per attention work-group
 
-// RMSNorm of one 128-wide head held one element per thread by the 128
-// threads [g*128, g*128 + 128) (two waves): sum of squares through DPP and
-// LDS, rsqrt as the reference computes it (FRSQRTE + two Newton steps),
-// x * r * w.  s_two: 2 floats of LDS per head slot.  Called by all threads of
-// the work-group (it has a barrier).
-__device__ __forceinline__ float head_rmsnorm(float v, float w, float* s_two, float eps) {
-  float sq = __fmul_rn(v, v);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) sq = __fadd_rn(sq, __shfl_xor(sq, o, 64));
-  const int wv = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) s_two[wv] = sq;
-  __syncthreads();
-  const int w0 = wv & ~1;
-  const float tot = __fadd_rn(s_two[w0], s_two[w0 + 1]);
-  const float r = ref_rsqrt(__fadd_rn(__fdiv_rn(tot, (float)HD), eps));
-  return __fmul_rn(__fmul_rn(v, r), w);
-}
 
 
 // Work-group (c, h): kv head h, positions [64 c, 64 c + 64) of the S = len + 1
@@ -64,10 +47,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   const int t1 = min(t0 + ATT_T, S);
   const int rp = a.state[1];
 
-  __shared__ float s_x[2][HD];              // normalised heads before the rotation
+  __shared__ float s_x[2][HD];              // normalised q heads before the rotation
+  __shared__ float s_xk[HD];                // normalised new k before the rotation
   __shared__ float s_q[2][HD];              // rotated q heads
   __shared__ float s_k[HD], s_v[HD];        // the new token's k (rotated) and v
-  __shared__ float s_red[4];
+  __shared__ float s_red[8];
   __shared__ float s_p[2][ATT_T];           // scores, then probabilities
   __shared__ float4 s_o[8][2][HD / 4];      // V partial sums of the 8 position groups
 
@@ -103,30 +87,45 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   const int j = d & 63;
   const float co = a.cos_tab[(size_t)rp * 64 + j], si = a.sin_tab[(size_t)rp * 64 + j];
 
-  // ---- q: RMSNorm with q_norm, then the rotation -----------------------------
-  s_x[g][d] = head_rmsnorm(qraw, qw, s_red, a.eps);
-  __syncthreads();
+  // ---- q and the new k: RMSNorm (q_norm / k_norm) in one reduction pass, then
+  //      the rotation; threads 0-127 also hold element d of k, 128-255 of v
   {
+    float sq = __fmul_rn(qraw, qraw), sk = __fmul_rn(kvraw, kvraw);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      sq = __fadd_rn(sq, __shfl_xor(sq, o, 64));
+      sk = __fadd_rn(sk, __shfl_xor(sk, o, 64));
+    }
+    if (lane == 0) {
+      s_red[wv] = sq;
+      s_red[4 + wv] = sk;
+    }
+    __syncthreads();
+    const int w0 = wv & ~1;
+    const float rq = ref_rsqrt(__fadd_rn(__fdiv_rn(__fadd_rn(s_red[w0], s_red[w0 + 1]), (float)HD), a.eps));
+    s_x[g][d] = __fmul_rn(__fmul_rn(qraw, rq), qw);
+    if (has_new && g == 0) {
+      const float rk = ref_rsqrt(__fadd_rn(__fdiv_rn(__fadd_rn(s_red[4], s_red[5]), (float)HD), a.eps));
+      s_xk[d] = __fmul_rn(__fmul_rn(kvraw, rk), kw);
+    }
+    __syncthreads();
     const float lo = s_x[g][j], hi = s_x[g][j + 64];
     s_q[g][d] = d < 64 ? __fsub_rn(__fmul_rn(lo, co), __fmul_rn(hi, si)) : __fadd_rn(__fmul_rn(hi, co), __fmul_rn(lo, si));
-  }
-  if (has_new) {
-    // threads 0-127: k of kv head h (k_norm, rotation); 128-255: v
-    const float kn = head_rmsnorm(kvraw, kw, s_red, a.eps);   // every thread; g == 1 unused
-    if (g == 0) s_x[0][d] = kn;
-    __syncthreads();
-    const size_t off = ((size_t)h * a.max_seq + p) * HD + d;
-    if (g == 0) {
-      const float lo = s_x[0][j], hi = s_x[0][j + 64];
-      const float kr_ = d < 64 ? __fsub_rn(__fmul_rn(lo, co), __fmul_rn(hi, si)) : __fadd_rn(__fmul_rn(hi, co), __fmul_rn(lo, si));
-      s_k[d] = kr_;
-      a.kc[off] = kr_;
-    } else {
-      s_v[d] = kvraw;
-      a.vc[off] = kvraw;
+    if (has_new) {
+      const size_t off = ((size_t)h * a.max_seq + p) * HD + d;
+      if (g == 0) {
+        const float klo = s_xk[j], khi = s_xk[j + 64];
+        const float kr_ = d < 64 ? __fsub_rn(__fmul_rn(klo, co), __fmul_rn(khi, si))
+                                 : __fadd_rn(__fmul_rn(khi, co), __fmul_rn(klo, si));
+        s_k[d] = kr_;
+        a.kc[off] = kr_;
+      } else {
+        s_v[d] = kvraw;
+        a.vc[off] = kvraw;
+      }
     }
+    __syncthreads();
   }
-  __syncthreads();
 
   // ---- scores ----------------------------------------------------------------
   float q0[8], q1[8];
@@ -207,44 +206,43 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
 }
 
 // One work-group per q head: out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
-// The chunk statistics go through LDS; each thread's partial outputs are
-// loaded 32 chunks at a time, all in flight together.
+// Two dependent memory round trips: the decode state, then every chunk's
+// statistics and this thread's partial outputs together (up to 32 chunks per
+// batch in flight).
 __global__ __launch_bounds__(128) void attn_combine_kernel(const float* __restrict__ pm, const float* __restrict__ pl,
                                                            const float* __restrict__ po, const int* __restrict__ state,
                                                            int C, float* __restrict__ out) {
   const int qh = blockIdx.x, d = threadIdx.x;
   const int nc = cdiv(state[0] + 1, ATT_T);
-  __shared__ float s_m[128], s_l[128];
-  __shared__ float s_M;
-  for (int c = d; c < nc; c += 128) {
-    s_m[c] = pm[qh * C + c];
-    s_l[c] = pl[qh * C + c];
-  }
-  __syncthreads();
-  if (d < 64) {
-    float m = -3.0e38f;
-    for (int c = d; c < nc; c += 64) m = fmaxf(m, s_m[c]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    if (d == 0) s_M = m;
-  }
-  __syncthreads();
-  const float M = s_M;
-  float L = 0.0f, o = 0.0f;
+  float L = 0.0f, acc = 0.0f, M = -3.0e38f;
   for (int c0 = 0; c0 < nc; c0 += 32) {
-    float v[32];
+    float v[32], m[32], l[32];
 #pragma unroll
-    for (int i = 0; i < 32; i++) v[i] = (c0 + i < nc) ? po[((size_t)qh * C + c0 + i) * HD + d] : 0.0f;
+    for (int i = 0; i < 32; i++) {
+      const bool ok = c0 + i < nc;
+      const int cc = min(c0 + i, nc - 1);
+      v[i] = po[((size_t)qh * C + cc) * HD + d];
+      m[i] = ok ? pm[qh * C + cc] : -3.0e38f;
+      l[i] = pl[qh * C + cc];
+    }
+    float Mb = M;
+#pragma unroll
+    for (int i = 0; i < 32; i++) Mb = fmaxf(Mb, m[i]);
+    // rescale what earlier batches accumulated (one batch for S <= 2048)
+    const float r = expf(__fsub_rn(M, Mb));
+    L = __fmul_rn(L, r);
+    acc = __fmul_rn(acc, r);
 #pragma unroll
     for (int i = 0; i < 32; i++) {
       if (c0 + i < nc) {
-        const float w = expf(__fsub_rn(s_m[c0 + i], M));
-        L = __fmaf_rn(w, s_l[c0 + i], L);
-        o = __fmaf_rn(w, v[i], o);
+        const float w = expf(__fsub_rn(m[i], Mb));
+        L = __fmaf_rn(w, l[i], L);
+        acc = __fmaf_rn(w, v[i], acc);
       }
     }
+    M = Mb;
   }
-  out[qh * HD + d] = __fmul_rn(o, __fdiv_rn(1.0f, L));
+  out[qh * HD + d] = __fmul_rn(acc, __fdiv_rn(1.0f, L));
 }
 
 // greedy token (largest argmax key: largest logit, lowest index on ties),
@@ -283,8 +281,7 @@ __global__ __launch_bounds__(1024) void step_end_kernel(const uint64_t* __restri
 }
 
 hipError_t launch_attn_decode(const AttnDecodeArgs& a, hipStream_t st) {
-  // the combine kernel keeps up to 128 chunk statistics in LDS
-  if (a.nq != 2 * a.nkv || a.C * ATT_T < a.max_seq || a.C > 128) return hipErrorInvalidValue;
+  if (a.nq != 2 * a.nkv || a.C * ATT_T < a.max_seq) return hipErrorInvalidValue;
   hipLaunchKernelGGL(attn_decode_kernel, dim3(a.C, a.nkv), dim3(256), 0, st, a);
   return hipGetLastError();
 }
