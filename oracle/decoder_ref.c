@@ -302,3 +302,182 @@ void orc_decode_layer(const int8_t *const *w, const float *const *s, const float
 
     free(residual); free(xn); free(q); free(k); free(v); free(attn); free(gate); free(up); free(y);
 }
+
+/* ---------------------------------------------------------------------- */
+/* prefill (decoder.c:33-157 in PREFILL_MODE / PREFILL_3D_MODE)            */
+/* ---------------------------------------------------------------------- */
+
+/* mrope_build_cos_sin_3d (ops.c:188-223) with the section map of
+ * _init_section_map (ops.c:128-146): dims j < 3 * min(s1, s2) cycle T, H, W;
+ * the rest are T.  pos_ids [3 x seq_len]. */
+void orc_mrope_build_3d(float *cos_out, float *sin_out, const int *pos_ids, int seq_len, int head_dim,
+                        const int sections[3], float theta)
+{
+    const int half = head_dim / 2;
+    int min_s = sections[1] < sections[2] ? sections[1] : sections[2];
+    for (int t = 0; t < seq_len; t++)
+        for (int j = 0; j < half; j++) {
+            const int sect = j < 3 * min_s ? j % 3 : 0;
+            const int pos = pos_ids[sect * seq_len + t];
+            const float inv_freq = 1.0f / powf(theta, (float)(2 * j) / (float)head_dim);
+            const float angle = (float)pos * inv_freq;
+            cos_out[(size_t)t * half + j] = cosf(angle);
+            sin_out[(size_t)t * half + j] = sinf(angle);
+        }
+}
+
+/* exp_f32_poly4 (attention.c:57-91): Cody-Waite reduction, degree-5 Horner,
+ * 2^n through the exponent field */
+static float exp_poly4(float x)
+{
+    x = fmaxf(x, -88.0f);
+    x = fminf(x, 88.0f);
+    const float n = roundf(x * 1.4426950408889634f);            /* vrndaq: ties away */
+    float r = fmaf(-n, 6.93147182464599609375e-1f, x);
+    r = fmaf(-n, -1.90465429995776716e-9f, r);
+    float p = 1.0f / 120.0f;
+    p = fmaf(r, p, 1.0f / 24.0f);
+    p = fmaf(r, p, 1.0f / 6.0f);
+    p = fmaf(r, p, 1.0f / 2.0f);
+    p = fmaf(r, p, 1.0f);
+    p = fmaf(r, p, 1.0f);
+    const int32_t ni = (int32_t)n;
+    return p * u2f((uint32_t)(ni + 127) << 23);
+}
+
+#define TQ 32
+#define TKV 256
+
+/* _flash_worker (attention.c:252-344), token-major q [Sq x nq x 128],
+ * k/v [Sk x nkv x 128], causal within the chunk (key j <= query i) */
+void orc_attention_prefill(const float *q, const float *k, const float *v, float *out, int Sq, int nq, int nkv,
+                           float scale)
+{
+    const int group = nq / nkv;
+    const int qs = nq * HD, ks = nkv * HD;
+    float *s_tile = (float *)malloc((size_t)TQ * TKV * sizeof(float));
+    float *o_tile = (float *)malloc((size_t)TQ * HD * sizeof(float));
+    if (!s_tile || !o_tile) abort();
+    float m_tile[TQ], l_tile[TQ];
+    const int ntq = (Sq + TQ - 1) / TQ;
+    for (int kvh = 0; kvh < nkv; kvh++)
+        for (int qt = 0; qt < ntq; qt++) {
+            const int t_q0 = qt * TQ;
+            const int t_q1 = t_q0 + TQ < Sq ? t_q0 + TQ : Sq;
+            const int tq = t_q1 - t_q0;
+            for (int g = 0; g < group; g++) {
+                const int qh = kvh * group + g;
+                for (int qi = 0; qi < tq; qi++) { m_tile[qi] = -1e38f; l_tile[qi] = 0.f; }
+                memset(o_tile, 0, (size_t)tq * HD * sizeof(float));
+                for (int kv0 = 0; kv0 < t_q1; kv0 += TKV) {
+                    const int kv1 = kv0 + TKV < Sq ? kv0 + TKV : Sq;
+                    const int tkv = kv1 - kv0;
+                    for (int qi = 0; qi < tq; qi++) {
+                        const int qpos = t_q0 + qi;
+                        const float *qv = q + (size_t)qpos * qs + (size_t)qh * HD;
+                        float *sp = s_tile + qi * TKV;
+                        for (int ki = 0; ki < tkv; ki++) {
+                            const int kpos = kv0 + ki;
+                            if (kpos > qpos) { sp[ki] = -1e38f; continue; }
+                            sp[ki] = dot128(qv, k + (size_t)kpos * ks + (size_t)kvh * HD) * scale;
+                        }
+                    }
+                    for (int qi = 0; qi < tq; qi++) {
+                        float *sp = s_tile + qi * TKV;
+                        const float m_old = m_tile[qi];
+                        float m_new = m_old;
+                        for (int ki = 0; ki < tkv; ki++)
+                            if (sp[ki] > m_new) m_new = sp[ki];
+                        const float rescale = expf(m_old - m_new);
+                        float l_new = l_tile[qi] * rescale;
+                        float *oi = o_tile + (size_t)qi * HD;
+                        for (int d = 0; d < HD; d++) oi[d] = oi[d] * rescale;
+                        int ki = 0;
+                        for (; ki + 3 < tkv; ki += 4) {
+                            float e[4];
+                            for (int jj = 0; jj < 4; jj++) {
+                                e[jj] = exp_poly4(sp[ki + jj] - m_new);
+                                sp[ki + jj] = e[jj];
+                            }
+                            l_new += (e[0] + e[1]) + (e[2] + e[3]);
+                        }
+                        for (; ki < tkv; ki++) {
+                            sp[ki] = expf(sp[ki] - m_new);
+                            l_new += sp[ki];
+                        }
+                        for (ki = 0; ki < tkv; ki++) {
+                            const float *vt = v + (size_t)(kv0 + ki) * ks + (size_t)kvh * HD;
+                            for (int d = 0; d < HD; d++) oi[d] = fmaf(sp[ki], vt[d], oi[d]);
+                        }
+                        m_tile[qi] = m_new;
+                        l_tile[qi] = l_new;
+                    }
+                }
+                for (int qi = 0; qi < tq; qi++) {
+                    const float inv_l = l_tile[qi] > 0.f ? 1.f / l_tile[qi] : 0.f;
+                    float *o = out + (size_t)(t_q0 + qi) * qs + (size_t)qh * HD;
+                    for (int d = 0; d < HD; d++) o[d] = o_tile[(size_t)qi * HD + d] * inv_l;
+                }
+            }
+        }
+    free(s_tile);
+    free(o_tile);
+}
+
+/* decoder_layer_forward with seq_len = S > 1 (decoder.c:33-157):
+ * PREFILL_MODE when token_cos is NULL (token t rotated at position
+ * cache_len + t of cos_tab/sin_tab), PREFILL_3D_MODE otherwise (row t of
+ * token_cos/token_sin).  Fused Q||K||V and gate||up GEMMs are row
+ * concatenations of the separate weights; orc_w8a32_linear at batch S is the
+ * float64 dequant-then-dot restatement.  hidden [S x H] in/out; the cache rows
+ * cache_len .. cache_len + S - 1 of Kc/Vc receive k and v. */
+void orc_prefill_layer(const int8_t *const *w, const float *const *s, const float *input_ln,
+                       const float *post_attn_ln, const float *q_norm, const float *k_norm, float *Kc, float *Vc,
+                       int max_seq, float *hidden, int S, const float *cos_tab, const float *sin_tab,
+                       const float *token_cos, const float *token_sin, int cache_len, int hidden_dim, int ffn_dim,
+                       int num_q_heads, int num_kv_heads, int threads)
+{
+    const int H = hidden_dim, KV = num_kv_heads * HD, F = ffn_dim;
+    const size_t SH = (size_t)S * H;
+    float *residual = (float *)malloc(SH * 4), *xn = (float *)malloc(SH * 4);
+    float *q = (float *)malloc(SH * 4), *k = (float *)malloc((size_t)S * KV * 4);
+    float *v = (float *)malloc((size_t)S * KV * 4), *attn = (float *)malloc(SH * 4);
+    float *gate = (float *)malloc((size_t)S * F * 4), *up = (float *)malloc((size_t)S * F * 4);
+    float *y = (float *)malloc(SH * 4);
+    if (!residual || !xn || !q || !k || !v || !attn || !gate || !up || !y) abort();
+
+    memcpy(residual, hidden, SH * 4);
+    for (int t = 0; t < S; t++) orc_rmsnorm(xn + (size_t)t * H, hidden + (size_t)t * H, input_ln, H, 1e-6f);
+    orc_w8a32_linear(xn, w[0], s[0], NULL, q, S, H, H, threads, NULL, NULL, NULL);
+    orc_w8a32_linear(xn, w[1], s[1], NULL, k, S, KV, H, threads, NULL, NULL, NULL);
+    orc_w8a32_linear(xn, w[2], s[2], NULL, v, S, KV, H, threads, NULL, NULL, NULL);
+    for (int r = 0; r < S * num_q_heads; r++) orc_rmsnorm(q + (size_t)r * HD, q + (size_t)r * HD, q_norm, HD, 1e-6f);
+    for (int r = 0; r < S * num_kv_heads; r++) orc_rmsnorm(k + (size_t)r * HD, k + (size_t)r * HD, k_norm, HD, 1e-6f);
+    for (int t = 0; t < S; t++) {
+        float *qt = q + (size_t)t * H, *kt = k + (size_t)t * KV;
+        if (token_cos) {
+            rope_heads(qt, token_cos + (size_t)t * (HD / 2), token_sin + (size_t)t * (HD / 2), num_q_heads, HD);
+            rope_heads(kt, token_cos + (size_t)t * (HD / 2), token_sin + (size_t)t * (HD / 2), num_kv_heads, HD);
+        } else {
+            orc_mrope_apply(qt, kt, cos_tab, sin_tab, num_q_heads, num_kv_heads, HD, cache_len + t);
+        }
+    }
+    for (int t = 0; t < S; t++)
+        for (int h = 0; h < num_kv_heads; h++) {
+            memcpy(Kc + ((size_t)h * max_seq + cache_len + t) * HD, k + (size_t)t * KV + h * HD, HD * 4);
+            memcpy(Vc + ((size_t)h * max_seq + cache_len + t) * HD, v + (size_t)t * KV + h * HD, HD * 4);
+        }
+    orc_attention_prefill(q, k, v, attn, S, num_q_heads, num_kv_heads, 0.08838834764831843f);
+    orc_w8a32_linear(attn, w[3], s[3], NULL, y, S, H, H, threads, NULL, NULL, NULL);
+    for (size_t i = 0; i < SH; i++) hidden[i] = y[i] + residual[i];
+
+    memcpy(residual, hidden, SH * 4);
+    for (int t = 0; t < S; t++) orc_rmsnorm(xn + (size_t)t * H, hidden + (size_t)t * H, post_attn_ln, H, 1e-6f);
+    orc_w8a32_linear(xn, w[4], s[4], NULL, gate, S, F, H, threads, NULL, NULL, NULL);
+    orc_w8a32_linear(xn, w[5], s[5], NULL, up, S, F, H, threads, NULL, NULL, NULL);
+    orc_silu_mul(gate, up, S * F);
+    orc_w8a32_linear(gate, w[6], s[6], NULL, y, S, H, F, threads, NULL, NULL, NULL);
+    for (size_t i = 0; i < SH; i++) hidden[i] = y[i] + residual[i];
+
+    free(residual); free(xn); free(q); free(k); free(v); free(attn); free(gate); free(up); free(y);
+}

@@ -82,6 +82,20 @@ void orc_decode_layer(const int8_t *const *w, const float *const *s, const float
                       int cache_len, int rope_pos, int hidden_dim, int ffn_dim, int num_q_heads,
                       int num_kv_heads, int threads);
 
+/* ---- prefill (decoder_ref.c) ------------------------------------------ */
+/* mrope_build_cos_sin_3d (kernel/ops.c:188-223), pos_ids [3 x seq_len]. */
+void orc_mrope_build_3d(float *cos_out, float *sin_out, const int *pos_ids, int seq_len, int head_dim,
+                        const int sections[3], float theta);
+/* attention_prefill_gqa / _flash_worker (kernel/attention.c:252-344). */
+void orc_attention_prefill(const float *q, const float *k, const float *v, float *out, int Sq, int nq, int nkv,
+                           float scale);
+/* decoder_layer_forward in PREFILL_MODE / PREFILL_3D_MODE (kernel/decoder.c:33-157). */
+void orc_prefill_layer(const int8_t *const *w, const float *const *s, const float *input_ln,
+                       const float *post_attn_ln, const float *q_norm, const float *k_norm, float *Kc, float *Vc,
+                       int max_seq, float *hidden, int S, const float *cos_tab, const float *sin_tab,
+                       const float *token_cos, const float *token_sin, int cache_len, int hidden_dim, int ffn_dim,
+                       int num_q_heads, int num_kv_heads, int threads);
+
 #ifdef __cplusplus
 }
 #endif

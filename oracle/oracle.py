@@ -66,8 +66,14 @@ def load(native: bool = False) -> ctypes.CDLL:
     lib.orc_attention_decode.argtypes = [_f32p, _f32p, _f32p, _f32p, _i, _i, _i, _i, _f]
     lib.orc_decode_layer.argtypes = [ctypes.POINTER(_i8p), ctypes.POINTER(_f32p), _f32p, _f32p, _f32p, _f32p,
                                      _f32p, _f32p, _i, _f32p, _f32p, _f32p, _i, _i, _i, _i, _i, _i, _i]
+    lib.orc_mrope_build_3d.argtypes = [_f32p, _f32p, _i32p, _i, _i, _i32p, _f]
+    lib.orc_attention_prefill.argtypes = [_f32p, _f32p, _f32p, _f32p, _i, _i, _i, _f]
+    lib.orc_prefill_layer.argtypes = [ctypes.POINTER(_i8p), ctypes.POINTER(_f32p), _f32p, _f32p, _f32p, _f32p,
+                                      _f32p, _f32p, _i, _f32p, _i, _f32p, _f32p, _f32p, _f32p, _i, _i, _i, _i,
+                                      _i, _i]
     for f in ("orc_rmsnorm", "orc_mrope_precompute", "orc_mrope_apply", "orc_silu_mul",
-              "orc_attention_decode", "orc_decode_layer"):
+              "orc_attention_decode", "orc_decode_layer", "orc_mrope_build_3d", "orc_attention_prefill",
+              "orc_prefill_layer"):
         getattr(lib, f).restype = None
     _LIBS[key] = lib
     return lib
@@ -273,4 +279,50 @@ def decode_layer(layer: dict, kc: np.ndarray, vc: np.ndarray, hidden: np.ndarray
                             _p(vc, ctypes.c_float), max_seq, _p(h, ctypes.c_float),
                             _p(cos_tab, ctypes.c_float), _p(sin_tab, ctypes.c_float), cache_len, rope_pos,
                             h.size, ws[4].shape[0], ws[0].shape[0] // HEAD_DIM, nkv, _threads(threads))
+    return h
+
+
+def rope_tables_3d(pos_ids: np.ndarray, head_dim: int = HEAD_DIM, sections=(24, 20, 20),
+                   theta: float = ROPE_THETA):
+    """Per-token tables [S, head_dim/2] from pos_ids [3, S] (mrope_build_cos_sin_3d)."""
+    pos = np.ascontiguousarray(pos_ids, dtype=np.int32)
+    S = pos.shape[1]
+    c = np.empty((S, head_dim // 2), np.float32)
+    s_ = np.empty((S, head_dim // 2), np.float32)
+    sec = (ctypes.c_int32 * 3)(*sections)
+    load().orc_mrope_build_3d(_p(c, ctypes.c_float), _p(s_, ctypes.c_float), _p(pos, ctypes.c_int32), S, head_dim,
+                              sec, theta)
+    return c, s_
+
+
+def attention_prefill(q: np.ndarray, k: np.ndarray, v: np.ndarray, nq: int = 16, nkv: int = 8,
+                      scale: float = 0.08838834764831843) -> np.ndarray:
+    """q [S, nq*128], k/v [S, nkv*128] token-major; causal within the chunk."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    out = np.empty_like(q)
+    load().orc_attention_prefill(_p(q, ctypes.c_float), _p(k, ctypes.c_float), _p(v, ctypes.c_float),
+                                 _p(out, ctypes.c_float), q.shape[0], nq, nkv, scale)
+    return out
+
+
+def prefill_layer(layer: dict, kc: np.ndarray, vc: np.ndarray, hidden: np.ndarray, cos_tab=None, sin_tab=None,
+                  token_cos=None, token_sin=None, cache_len: int = 0, threads: int | None = None) -> np.ndarray:
+    """One PREFILL_MODE (cos_tab/sin_tab rows cache_len + t) or PREFILL_3D_MODE
+    (token_cos/token_sin rows t) layer over hidden [S, H]; kc/vc updated in place."""
+    h = np.array(hidden, dtype=np.float32, copy=True)
+    S, H = h.shape
+    ws = [np.ascontiguousarray(layer[n][0], dtype=np.int8) for n in LAYER_PROJ]
+    ss = [np.ascontiguousarray(layer[n][1], dtype=np.float32) for n in LAYER_PROJ]
+    norms = [np.ascontiguousarray(layer[n], dtype=np.float32)
+             for n in ("input_ln", "post_attn_ln", "q_norm", "k_norm")]
+    nkv, max_seq, _ = kc.shape
+    warr = (_i8p * 7)(*[_p(w, ctypes.c_int8) for w in ws])
+    sarr = (_f32p * 7)(*[_p(s, ctypes.c_float) for s in ss])
+    f = lambda a: None if a is None else _p(np.ascontiguousarray(a, dtype=np.float32), ctypes.c_float)
+    load().orc_prefill_layer(warr, sarr, *[_p(n, ctypes.c_float) for n in norms], _p(kc, ctypes.c_float),
+                             _p(vc, ctypes.c_float), max_seq, _p(h, ctypes.c_float), S, f(cos_tab), f(sin_tab),
+                             f(token_cos), f(token_sin), cache_len, H, ws[4].shape[0], ws[0].shape[0] // HEAD_DIM,
+                             nkv, _threads(threads))
     return h

@@ -173,3 +173,95 @@ def test_decode_layer_is_the_reference_composition(o):
         np.testing.assert_array_equal(h, h2)
         np.testing.assert_array_equal(kc, kc2)
         np.testing.assert_array_equal(vc, vc2)
+
+
+def test_attention_prefill_against_float64(o):
+    """Causal flash attention (attention.c:252-344, 32-query x 256-key tiles,
+    online softmax, polynomial exp) against a float64 softmax, across
+    several key tiles and a ragged last query tile."""
+    rng = np.random.default_rng(5)
+    S = 300
+    q = rng.standard_normal((S, 16 * 128)).astype(F)
+    k = rng.standard_normal((S, 8 * 128)).astype(F)
+    v = rng.standard_normal((S, 8 * 128)).astype(F)
+    got = o.attention_prefill(q, k, v)
+    want = np.empty((S, 16 * 128))
+    for qh in range(16):
+        kv = qh // 2
+        Q = q[:, qh * 128:(qh + 1) * 128].astype(np.float64)
+        K = k[:, kv * 128:(kv + 1) * 128].astype(np.float64)
+        V = v[:, kv * 128:(kv + 1) * 128].astype(np.float64)
+        sc = Q @ K.T * 0.08838834764831843
+        sc[np.triu_indices(S, 1)] = -np.inf
+        p = np.exp(sc - sc.max(axis=1, keepdims=True))
+        want[:, qh * 128:(qh + 1) * 128] = (p / p.sum(axis=1, keepdims=True)) @ V
+    assert np.max(np.abs(got - want)) < 5e-6
+    # the first query attends only to itself: its output is v of position 0
+    np.testing.assert_allclose(got[0].reshape(16, 128), v[0].reshape(8, 128).repeat(2, axis=0), rtol=0, atol=0)
+
+
+def test_rope_tables_3d(o):
+    """Per-token M-RoPE tables: dims j < 60 take the T/H/W position j % 3,
+    the rest T (ops.c:128-146); sequential positions reproduce the 1-D table."""
+    rng = np.random.default_rng(6)
+    S = 40
+    pos = np.stack([rng.integers(0, 30, S), rng.integers(0, 30, S), rng.integers(0, 30, S)]).astype(np.int32)
+    c3, s3 = o.rope_tables_3d(pos)
+    c1, s1 = o.rope_tables(64)
+    for t in range(S):
+        for j in range(64):
+            sect = j % 3 if j < 60 else 0
+            p = pos[sect, t]
+            assert c3[t, j] == c1[p, j] and s3[t, j] == s1[p, j]
+    seq = np.tile(np.arange(S, dtype=np.int32), (3, 1))
+    c3, s3 = o.rope_tables_3d(seq)
+    np.testing.assert_array_equal(c3, c1[:S])
+    np.testing.assert_array_equal(s3, s1[:S])
+
+
+def test_prefill_layer_is_the_reference_composition(o):
+    """The C prefill layer equals the operators composed in the order of
+    kernel/decoder.c:33-157 (PREFILL and PREFILL_3D modes), bit for bit."""
+    rng = np.random.default_rng(7)
+    H, FF, nkv, max_seq, S = 256, 384, 1, 48, 37
+    KV = nkv * 128
+
+    def quant(n, k):
+        return o.quantize_rows((rng.standard_normal((n, k)) * 0.05).astype(F))
+    layer = {"q_proj": quant(H, H), "k_proj": quant(KV, H), "v_proj": quant(KV, H), "o_proj": quant(H, H),
+             "gate_proj": quant(FF, H), "up_proj": quant(FF, H), "down_proj": quant(H, FF),
+             "input_ln": (1 + 0.1 * rng.standard_normal(H)).astype(F),
+             "post_attn_ln": (1 + 0.1 * rng.standard_normal(H)).astype(F),
+             "q_norm": (1 + 0.1 * rng.standard_normal(128)).astype(F),
+             "k_norm": (1 + 0.1 * rng.standard_normal(128)).astype(F)}
+    c, s = o.rope_tables(max_seq)
+    pos = np.stack([np.arange(S), np.arange(S) // 4, np.arange(S) % 4]).astype(np.int32)
+    tc, ts = o.rope_tables_3d(pos)
+    h0 = rng.standard_normal((S, H)).astype(F)
+    for mode in ("1d", "3d"):
+        kc = np.zeros((nkv, max_seq, 128), F)
+        vc = np.zeros_like(kc)
+        if mode == "1d":
+            got = o.prefill_layer(layer, kc, vc, h0, cos_tab=c, sin_tab=s, cache_len=5)
+        else:
+            got = o.prefill_layer(layer, kc, vc, h0, token_cos=tc, token_sin=ts, cache_len=5)
+        lin = lambda x, name: o.w8a32_linear(x, *layer[name])
+        res = h0.copy()
+        xn = o.rmsnorm(h0, layer["input_ln"])
+        q = o.rmsnorm(lin(xn, "q_proj").reshape(-1, 128), layer["q_norm"]).reshape(S, -1)
+        k = o.rmsnorm(lin(xn, "k_proj").reshape(-1, 128), layer["k_norm"]).reshape(S, -1)
+        v = lin(xn, "v_proj")
+        for t in range(S):
+            if mode == "1d":
+                q[t], k[t] = o.mrope_apply(q[t], k[t], c, s, 5 + t)
+            else:
+                q[t], k[t] = o.mrope_apply(q[t], k[t], tc[t:t + 1], ts[t:t + 1], 0)
+        np.testing.assert_array_equal(kc[:, 5:5 + S], k.reshape(S, nkv, 128).transpose(1, 0, 2))
+        np.testing.assert_array_equal(vc[:, 5:5 + S], v.reshape(S, nkv, 128).transpose(1, 0, 2))
+        attn = o.attention_prefill(q, k, v, nq=H // 128, nkv=nkv)
+        h = (lin(attn, "o_proj") + res).astype(F)
+        res = h.copy()
+        xn = o.rmsnorm(h, layer["post_attn_ln"])
+        mlp = o.silu_mul(lin(xn, "gate_proj").reshape(-1), lin(xn, "up_proj").reshape(-1)).reshape(S, FF)
+        h = (lin(mlp, "down_proj") + res).astype(F)
+        np.testing.assert_array_equal(got, h)
