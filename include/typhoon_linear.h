@@ -266,6 +266,30 @@ void decoder_precompute_rope(float *cos_tab, float *sin_tab, int max_seq, int he
 void decoder_decode_step(const ModelWeights *model, KVCache *cache, float *hidden, DecoderScratch *scratch,
                          const float *cos_tab, const float *sin_tab);
 
+/* decoder.c:437-447: prefill of seq_len tokens (hidden [seq_len x 2048],
+ * host, in/out) through every layer: token t rotated at position
+ * seq_len_of_cache + t, K/V appended, causal attention within the new tokens
+ * (PREFILL_MODE); the cache advances by seq_len. */
+void decoder_prefill_step(const ModelWeights *model, KVCache *cache, float *hidden, DecoderScratch *scratch,
+                          const float *cos_tab, const float *sin_tab, int seq_len);
+/* decoder.c:449-474: the same in chunks of chunk_size tokens, each attending
+ * to every cached position (CHUNKED_PREFILL_MODE). */
+void decoder_chunked_prefill_step(const ModelWeights *model, KVCache *cache, float *hidden, DecoderScratch *scratch,
+                                  const float *cos_tab, const float *sin_tab, int total_seq_len, int chunk_size);
+/* decoder.c:476-493: equal to decoder_prefill_step (the reference chunks only
+ * its GEMMs; chunk_size is accepted and unused). */
+void decoder_hybrid_chunked_prefill_step(const ModelWeights *model, KVCache *cache, float *hidden,
+                                         DecoderScratch *scratch, const float *cos_tab, const float *sin_tab,
+                                         int seq_len, int chunk_size);
+/* decoder.c:495-507: prefill with per-token rope tables [seq_len x 64] (host),
+ * built by decoder_build_rope_3d from 3-D position ids (PREFILL_3D_MODE). */
+void decoder_prefill_step_3d(const ModelWeights *model, KVCache *cache, float *hidden, DecoderScratch *scratch,
+                             const float *token_cos, const float *token_sin, int seq_len);
+/* decoder.c:518-526 -> ops.c:188-223: per-token tables from pos_ids [3 x
+ * seq_len] (temporal, height, width), on the host. */
+void decoder_build_rope_3d(float *cos_out, float *sin_out, const int *pos_ids, int seq_len, int head_dim,
+                           const int sections[3], const float theta_bases[3]);
+
 /* Extensions (no reference counterpart). */
 int tl_decoder_num_layers(const ModelWeights *model);
 int tl_decoder_cache_len(const KVCache *cache);

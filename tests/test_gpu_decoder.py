@@ -208,3 +208,127 @@ def test_generate_greedy_matches_step_path_and_oracle(lin, orc, dev):
     np.testing.assert_array_equal(toks, np.array(want, np.int32))
     lm_dev.close()
     d.close()
+
+
+# ---------------------------------------------------------------------------
+# prefill (survey row f-4): decoder.c:33-157 with seq_len > 1, decoder.c:437-507
+# ---------------------------------------------------------------------------
+def test_prefill_matches_oracle(lin, orc, dev):
+    """decoder_prefill_step (sequential positions) and decoder_prefill_step_3d
+    (3-D M-RoPE tables) over 2 layers and 130 tokens (three 64-query tiles,
+    the last ragged) against the oracle's prefill layer chain: hidden rows
+    relative L2 <= 1e-3, K/V cache rows <= 1e-4.  The linear layers are the
+    fp32-accurate GEMM and the attention fp32, so both sides differ only in
+    summation order; what widens the gap is the reference's fast-exp SiLU,
+    which is discontinuous (the exp term doubles when a gate value crosses a
+    truncation step), so a last-bit difference can move a few mlp elements."""
+    from typhoon_ocr_server_amd import decoder as dec
+    say("prefill vs oracle, 2 layers x 130 tokens")
+    rng = np.random.default_rng(25)
+    layers, _, _ = _model(rng, orc, 2)
+    S, max_seq = 130, 192
+    d = dec.Decoder(layers, max_seq=max_seq)
+    ol = _oracle_layers(d, layers)
+    h0 = (rng.standard_normal((S, 2048)) * 2).astype(F)
+    pos = np.stack([np.arange(S), 3 + np.arange(S) // 10, np.arange(S) % 10]).astype(np.int32)
+    tc, ts = orc.rope_tables_3d(pos)
+    for mode in ("1d", "3d"):
+        d.reset()
+        hg = d.prefill(h0) if mode == "1d" else d.prefill_3d(h0, pos)
+        assert d.cache_len == S
+        kc = [np.zeros((8, max_seq, 128), F) for _ in ol]
+        vc = [np.zeros((8, max_seq, 128), F) for _ in ol]
+        ho = h0.copy()
+        for l, layer in enumerate(ol):
+            if mode == "1d":
+                ho = orc.prefill_layer(layer, kc[l], vc[l], ho, cos_tab=d._cos_tab, sin_tab=d._sin_tab)
+            else:
+                ho = orc.prefill_layer(layer, kc[l], vc[l], ho, token_cos=tc, token_sin=ts)
+        assert rel_l2(hg, ho) <= 1e-3, (mode, rel_l2(hg, ho))
+        for l in range(len(ol)):
+            kg, vg = d.read_cache(l)
+            assert rel_l2(kg[:, :S], kc[l][:, :S]) <= 1e-4, (mode, l)
+            assert rel_l2(vg[:, :S], vc[l][:, :S]) <= 1e-4, (mode, l)
+    d.close()
+
+
+def test_chunked_prefill_equals_full_prefill(lin, orc, dev):
+    """Chunks that attend to the whole cache (decoder_chunked_prefill_step)
+    give the full causal prefill (relative L2 <= 1e-3: the chunks' GEMMs run
+    at another batch size, hence other tile plans and summation orders, and
+    the fast-exp SiLU magnifies last-bit differences), and the hybrid variant
+    equals the plain one bit for bit."""
+    from typhoon_ocr_server_amd import decoder as dec
+    say("chunked / hybrid prefill vs full prefill")
+    rng = np.random.default_rng(26)
+    layers, _, _ = _model(rng, orc, 1)
+    S = 150
+    d = dec.Decoder(layers, max_seq=256)
+    h0 = rng.standard_normal((S, 2048)).astype(F)
+    d.reset()
+    full = d.prefill(h0)
+    kf, vf = d.read_cache(0)
+    d.reset()
+    ch = d.prefill(h0, chunk=48)
+    kc, vc = d.read_cache(0)
+    assert d.cache_len == S
+    assert rel_l2(ch, full) <= 1e-3
+    assert rel_l2(kc[:, :S], kf[:, :S]) <= 1e-4 and rel_l2(vc[:, :S], vf[:, :S]) <= 1e-4
+    d.reset()
+    hh = np.array(h0, copy=True)
+    d._lib.decoder_hybrid_chunked_prefill_step(d._c_model, d._c_cache, hh.ctypes.data_as(
+        __import__("ctypes").POINTER(__import__("ctypes").c_float)), d._c_scratch,
+        d._cos_tab.ctypes.data_as(__import__("ctypes").POINTER(__import__("ctypes").c_float)),
+        d._sin_tab.ctypes.data_as(__import__("ctypes").POINTER(__import__("ctypes").c_float)), S, 32)
+    np.testing.assert_array_equal(hh, full)
+    d.close()
+
+
+def test_prefill_then_greedy_decode_matches_oracle(lin, orc, dev):
+    """3-D prefill of 100 tokens, rope offset as the reference sets it after a
+    multimodal prefill, then 8 greedy steps on the device: the tokens equal the
+    oracle's (decoder.py:390-507 with do_sample=False)."""
+    import torch
+    from typhoon_ocr_server_amd import decoder as dec
+    say("prefill + greedy decode vs oracle")
+    rng = np.random.default_rng(27)
+    V = 32768
+    layers, lm, nw = _model(rng, orc, 2, vocab=V)
+    embed = (rng.standard_normal((V, 2048)) * 1.5).astype(F)
+    S, n, max_seq = 100, 8, 160
+    d = dec.Decoder(layers, lm_head=lm, final_norm=nw, max_seq=max_seq)
+    lm_dev = lin.DeviceWeights.from_codes(d._lm_head_w, d._lm_head_s)
+    embed_dev = torch.from_numpy(embed).to(dev)
+    ids = rng.integers(0, V, S)
+    h0 = embed[ids]
+    pos = np.stack([np.arange(S), np.arange(S) // 7, np.arange(S) % 7]).astype(np.int32)
+    d.reset()
+    hg = d.prefill_3d(h0, pos)
+    first = d.next_token(hg)
+    d.set_rope_offset(int(pos.max()) + 1)
+    toks = d.generate_greedy(first, n, embed_dev, lm_dev)
+    # oracle
+    ol = _oracle_layers(d, layers)
+    tc, ts = orc.rope_tables_3d(pos)
+    kc = [np.zeros((8, max_seq, 128), F) for _ in ol]
+    vc = [np.zeros((8, max_seq, 128), F) for _ in ol]
+    ho = h0.astype(F)
+    for l, layer in enumerate(ol):
+        ho = orc.prefill_layer(layer, kc[l], vc[l], ho, token_cos=tc, token_sin=ts)
+
+    def greedy(h):
+        rms = np.sqrt(np.mean(h * h) + 1e-6)
+        return int(np.argmax(orc.w8a32_linear(((h / rms) * nw).astype(F)[None], d._lm_head_w, d._lm_head_s)[0]))
+    tok = greedy(ho[-1])
+    assert tok == first
+    rope0 = int(pos.max()) + 1
+    want = []
+    for t in range(n):
+        h = embed[tok].copy()
+        for l, layer in enumerate(ol):
+            h = orc.decode_layer(layer, kc[l], vc[l], h, d._cos_tab, d._sin_tab, cache_len=S + t, rope_pos=rope0 + t)
+        tok = greedy(h)
+        want.append(tok)
+    np.testing.assert_array_equal(toks, np.array(want, np.int32))
+    lm_dev.close()
+    d.close()

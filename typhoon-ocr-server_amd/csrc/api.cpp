@@ -626,6 +626,12 @@ void device_to_file(std::FILE* f, const void* src, size_t bytes, PinnedBuf& stag
 
 }  // namespace
 
+namespace tlhost {
+void linear_w8a32(const float* X, const tl_weights* W, const float* bias, float* Y, int batch, hipStream_t st) {
+  op_w8a32(X, W, bias, Y, batch, st);
+}
+}  // namespace tlhost
+
 // ==========================================================================
 // Part 1 -- reference entry points
 // ==========================================================================

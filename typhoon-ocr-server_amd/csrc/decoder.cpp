@@ -28,6 +28,7 @@
 // Calls on one scratch must not overlap (the reference's are synchronous too).
 #include "host.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -118,6 +119,8 @@ struct DecoderScratch {
   int C = 0;
   DevBuf keys, tokens, fnorm;
   PinnedBuf pin;
+  // prefill activations (token-major, grown to the longest prefill)
+  DevBuf p_h, p_xn, p_qkv, p_att, p_gu, p_mlp, p_y, p_cos, p_sin;
   // captured graphs and what they were captured for
   hipGraphExec_t layers_exec = nullptr;
   const void* layers_key[4] = {nullptr, nullptr, nullptr, nullptr};
@@ -205,6 +208,88 @@ void enqueue_layers(const ModelWeights* m, const KVCache* c, DecoderScratch* s, 
     gemv(L.o, s->attn, s->hidden, s->hidden, EPI_W8A32, NORM_NONE, nullptr, st);
     gemv(L.gu, s->hidden, s->mlp, nullptr, EPI_SWIGLU, NORM_DECODER, L.norms + H, st);
     gemv(L.down, s->mlp, s->hidden, s->hidden, EPI_W8A32, NORM_NONE, nullptr, st);
+  }
+}
+
+void advance(KVCache* c, int n);
+
+// Prefill of S tokens through every layer (decoder.c:33-157 with seq_len > 1):
+// token t is rotated with rows t of cos_rows / sin_rows, its K/V go to cache
+// row row0 + t, and it attends cache rows key0 .. key0 + qoff + t.
+void enqueue_prefill(const ModelWeights* m, KVCache* c, DecoderScratch* s, int S, const float* cos_rows,
+                     const float* sin_rows, int row0, int key0, int qoff, hipStream_t st) {
+  float* Hd = static_cast<float*>(s->p_h.p);
+  float* Xn = static_cast<float*>(s->p_xn.p);
+  float* QKV = static_cast<float*>(s->p_qkv.p);
+  float* ATT = static_cast<float*>(s->p_att.p);
+  float* GU = static_cast<float*>(s->p_gu.p);
+  float* MLP = static_cast<float*>(s->p_mlp.p);
+  float* Y = static_cast<float*>(s->p_y.p);
+  const long long n = (long long)S * H;
+  for (int l = 0; l < m->num_layers(); l++) {
+    const LayerDev& L = m->layers[l];
+    float* kc = c->k + (size_t)l * c->layer_floats();
+    float* vc = c->v + (size_t)l * c->layer_floats();
+    HIP_OK(launch_rmsnorm_rows(Hd, L.norms, Xn, S, H, EPS, st));
+    linear_w8a32(Xn, L.qkv, nullptr, QKV, S, st);
+    HIP_OK(launch_prefill_qk(QKV, L.norms + 2 * H, L.norms + 2 * H + HDIM, cos_rows, sin_rows, kc, vc, c->max_seq,
+                             row0, S, NKV, EPS, st));
+    HIP_OK(launch_flash_prefill(QKV, kc, vc, ATT, S, NQ, c->max_seq, key0, qoff, SCALE, st));
+    linear_w8a32(ATT, L.o, nullptr, Y, S, st);
+    HIP_OK(launch_residual_add(Y, Hd, n, st));
+    HIP_OK(launch_rmsnorm_rows(Hd, L.norms + H, Xn, S, H, EPS, st));
+    linear_w8a32(Xn, L.gu, nullptr, GU, S, st);
+    HIP_OK(launch_swiglu_rows(GU, MLP, S, FF, st));
+    linear_w8a32(MLP, L.down, nullptr, Y, S, st);
+    HIP_OK(launch_residual_add(Y, Hd, n, st));
+  }
+}
+
+void ensure_prefill_buffers(DecoderScratch* s, int S) {
+  s->p_h.ensure((size_t)S * H * 4, s->st);
+  s->p_xn.ensure((size_t)S * H * 4, s->st);
+  s->p_qkv.ensure((size_t)S * QKVD * 4, s->st);
+  s->p_att.ensure((size_t)S * H * 4, s->st);
+  s->p_gu.ensure((size_t)S * 2 * FF * 4, s->st);
+  s->p_mlp.ensure((size_t)S * FF * 4, s->st);
+  s->p_y.ensure((size_t)S * H * 4, s->st);
+}
+
+// one prefill call on host hidden rows: chunks of at most `chunk` tokens
+// (chunked mode: each attends to the whole cache), then the cache advances
+void prefill_host(const ModelWeights* m, KVCache* c, float* hidden, DecoderScratch* s, int S, const float* cos_tab,
+                  const float* sin_tab, const float* token_cos, const float* token_sin, int chunk, bool chunked) {
+  check_handles(m, c, s);
+  REQUIRE(hidden && S >= 1, "bad arguments");
+  REQUIRE(c->seq_len + S <= c->max_seq, "KV cache too small for the prefill");
+  const float* cos_dev = nullptr;
+  const float* sin_dev = nullptr;
+  if (token_cos) {
+    REQUIRE(token_sin, "NULL token_sin");
+    s->p_cos.ensure((size_t)S * 64 * 4, s->st);
+    s->p_sin.ensure((size_t)S * 64 * 4, s->st);
+    HIP_OK(hipMemcpyAsync(s->p_cos.p, token_cos, (size_t)S * 64 * 4, hipMemcpyHostToDevice, s->st));
+    HIP_OK(hipMemcpyAsync(s->p_sin.p, token_sin, (size_t)S * 64 * 4, hipMemcpyHostToDevice, s->st));
+    cos_dev = static_cast<const float*>(s->p_cos.p);
+    sin_dev = static_cast<const float*>(s->p_sin.p);
+  } else {
+    const RopeDev& r = rope_device(c, cos_tab, sin_tab);
+    cos_dev = r.cos;
+    sin_dev = r.sin;
+  }
+  const int step = chunked ? std::max(1, chunk) : S;
+  ensure_prefill_buffers(s, std::min(step, S));
+  for (int t0 = 0; t0 < S; t0 += step) {
+    const int n = std::min(step, S - t0);
+    const int base = c->seq_len;
+    HIP_OK(hipMemcpyAsync(s->p_h.p, hidden + (size_t)t0 * H, (size_t)n * H * 4, hipMemcpyHostToDevice, s->st));
+    // sequential positions: rows base + t of the tables; 3-D: rows t0 + t of the token tables
+    const size_t rrow = token_cos ? (size_t)t0 : (size_t)base;
+    enqueue_prefill(m, c, s, n, cos_dev + rrow * 64, sin_dev + rrow * 64, base, chunked ? 0 : base,
+                    chunked ? base : 0, s->st);
+    HIP_OK(hipMemcpyAsync(hidden + (size_t)t0 * H, s->p_h.p, (size_t)n * H * 4, hipMemcpyDeviceToHost, s->st));
+    HIP_OK(hipStreamSynchronize(s->st));
+    advance(c, n);
   }
 }
 
@@ -394,6 +479,8 @@ void decoder_scratch_free_fn(DecoderScratch* s) {
   drop_graph(s->gen_exec);
   for (float* p : {s->hidden, s->qkv, s->attn, s->mlp, s->pm, s->pl, s->po})
     if (p) (void)hipFree(p);
+  for (DevBuf* b : {&s->p_h, &s->p_xn, &s->p_qkv, &s->p_att, &s->p_gu, &s->p_mlp, &s->p_y, &s->p_cos, &s->p_sin})
+    if (b->p) (void)hipFree(b->p);
   if (s->keys.p) (void)hipFree(s->keys.p);
   if (s->tokens.p) (void)hipFree(s->tokens.p);
   if (s->fnorm.p) (void)hipFree(s->fnorm.p);
@@ -474,6 +561,66 @@ void decoder_decode_step(const ModelWeights* model, KVCache* cache, float* hidde
     HIP_OK(hipStreamSynchronize(s->st));
     std::memcpy(hidden, stage, (size_t)H * 4);
     advance(cache, 1);
+  });
+}
+
+// ---- prefill (decoder.c:437-507) --------------------------------------------
+void decoder_prefill_step(const ModelWeights* model, KVCache* cache, float* hidden, DecoderScratch* scratch,
+                          const float* cos_tab, const float* sin_tab, int seq_len) {
+  guarded("decoder_prefill_step", [&] {
+    REQUIRE(cache, "NULL cache");
+    REQUIRE(cache->seq_len + seq_len <= cache->max_seq, "rotary positions past the rope tables");
+    prefill_host(model, cache, hidden, scratch, seq_len, cos_tab, sin_tab, nullptr, nullptr, 0, false);
+  });
+}
+
+void decoder_chunked_prefill_step(const ModelWeights* model, KVCache* cache, float* hidden, DecoderScratch* scratch,
+                                  const float* cos_tab, const float* sin_tab, int total_seq_len, int chunk_size) {
+  guarded("decoder_chunked_prefill_step", [&] {
+    REQUIRE(cache, "NULL cache");
+    REQUIRE(chunk_size >= 1, "chunk_size must be >= 1");
+    REQUIRE(cache->seq_len + total_seq_len <= cache->max_seq, "rotary positions past the rope tables");
+    prefill_host(model, cache, hidden, scratch, total_seq_len, cos_tab, sin_tab, nullptr, nullptr, chunk_size, true);
+  });
+}
+
+void decoder_hybrid_chunked_prefill_step(const ModelWeights* model, KVCache* cache, float* hidden,
+                                         DecoderScratch* scratch, const float* cos_tab, const float* sin_tab,
+                                         int seq_len, int chunk_size) {
+  (void)chunk_size;   // the reference chunks only its GEMMs; the results are those of one pass
+  guarded("decoder_hybrid_chunked_prefill_step", [&] {
+    REQUIRE(cache, "NULL cache");
+    REQUIRE(cache->seq_len + seq_len <= cache->max_seq, "rotary positions past the rope tables");
+    prefill_host(model, cache, hidden, scratch, seq_len, cos_tab, sin_tab, nullptr, nullptr, 0, false);
+  });
+}
+
+void decoder_prefill_step_3d(const ModelWeights* model, KVCache* cache, float* hidden, DecoderScratch* scratch,
+                             const float* token_cos, const float* token_sin, int seq_len) {
+  guarded("decoder_prefill_step_3d", [&] {
+    REQUIRE(token_cos && token_sin, "NULL token tables");
+    prefill_host(model, cache, hidden, scratch, seq_len, nullptr, nullptr, token_cos, token_sin, 0, false);
+  });
+}
+
+// mrope_build_cos_sin_3d (ops.c:188-223): dims j < 3 min(sections[1],
+// sections[2]) take the T / H / W position j % 3, the rest T
+void decoder_build_rope_3d(float* cos_out, float* sin_out, const int* pos_ids, int seq_len, int head_dim,
+                           const int sections[3], const float theta_bases[3]) {
+  guarded("decoder_build_rope_3d", [&] {
+    REQUIRE(cos_out && sin_out && pos_ids && sections && theta_bases && seq_len >= 1 && head_dim >= 2,
+            "bad arguments");
+    const int half = head_dim / 2;
+    const int min_s = std::min(sections[1], sections[2]);
+    for (int t = 0; t < seq_len; t++)
+      for (int j = 0; j < half; j++) {
+        const int sect = j < 3 * min_s ? j % 3 : 0;
+        const int pos = pos_ids[sect * seq_len + t];
+        const float inv_freq = 1.0f / powf(theta_bases[0], (float)(2 * j) / (float)head_dim);
+        const float angle = (float)pos * inv_freq;
+        cos_out[(size_t)t * half + j] = cosf(angle);
+        sin_out[(size_t)t * half + j] = sinf(angle);
+      }
   });
 }
 

@@ -111,5 +111,8 @@ void weights_free(tl_weights* W);
 tl_weights* weights_from_codes(const int8_t* w, const float* s, int rows, int cols, bool on_device,
                                hipStream_t st);
 void check_weights(const tl_weights* W);
+// w8a32_linear semantics on device pointers (batch 1: GEMV; batch > 1: the
+// fp32-accurate GEMM), stream-ordered
+void linear_w8a32(const float* X, const tl_weights* W, const float* bias, float* Y, int batch, hipStream_t st);
 
 }  // namespace tlhost

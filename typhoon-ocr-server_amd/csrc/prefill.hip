@@ -1,0 +1,326 @@
+// prefill.hip -- the prefill-step kernels around the batch > 1 linear layers.
+//
+// Reference: kernel/decoder.c:33-157 with seq_len = S > 1 (PREFILL_MODE and
+// PREFILL_3D_MODE): rmsnorm_seq_f32 (kernel/ops.c:75-105), per-head QK
+// RMSNorm, mrope_apply_seq / mrope_apply_seq_3d (:347-458), the KV cache
+// prefill append (kernel/kv_cache.c:70-104), attention_prefill_gqa
+// (kernel/attention.c:252-360), silu_mul_inplace (ops.c:493-531) and
+// vec_add_f32 (:537-549).  The linear layers are the fp32-accurate batch > 1
+// GEMM (gemm_b16.hip, A_F32X3).
+//
+// Layouts: activations token-major, as the reference's scratch: hidden
+// [S][2048], qkv [S][4096] (q | k | v), attention output [S][2048], gate/up
+// [S][12288] in the decoder's per-16-row interleave, mlp [S][6144].  The KV
+// cache is [kv head][max_seq][128] per layer.
+#include "tl_common.h"
+#include "tl_kernels.h"
+
+namespace tl {
+
+constexpr int PHD = 128;
+
+// out[t] = x[t] * r_t * w, the decoder's RMSNorm (estimate-based rsqrt) of
+// each 2048-wide row: one work-group per row, 8 elements per thread
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                           float* __restrict__ out, int K, float eps) {
+  __shared__ float s_part[4];
+  const size_t row = blockIdx.x;
+  const float4* xr = reinterpret_cast<const float4*>(x + row * K);
+  const float4* wr = reinterpret_cast<const float4*>(w);
+  const int n4 = K >> 2;
+  float4 v[2], wv[2];
+  float sq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int f = threadIdx.x + 256 * i;
+    v[i] = f < n4 ? xr[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+    wv[i] = f < n4 ? wr[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+    sq = __fmaf_rn(v[i].x, v[i].x, sq);
+    sq = __fmaf_rn(v[i].y, v[i].y, sq);
+    sq = __fmaf_rn(v[i].z, v[i].z, sq);
+    sq = __fmaf_rn(v[i].w, v[i].w, sq);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sq = __fadd_rn(sq, __shfl_xor(sq, o, 64));
+  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = sq;
+  __syncthreads();
+  const float tot = __fadd_rn(__fadd_rn(s_part[0], s_part[1]), __fadd_rn(s_part[2], s_part[3]));
+  const float r = ref_rsqrt(__fadd_rn(__fdiv_rn(tot, (float)K), eps));
+  float4* orow = reinterpret_cast<float4*>(out + row * K);
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int f = threadIdx.x + 256 * i;
+    if (f < n4)
+      orow[f] = make_float4(__fmul_rn(__fmul_rn(v[i].x, r), wv[i].x), __fmul_rn(__fmul_rn(v[i].y, r), wv[i].y),
+                            __fmul_rn(__fmul_rn(v[i].z, r), wv[i].z), __fmul_rn(__fmul_rn(v[i].w, r), wv[i].w));
+  }
+}
+
+// Work-group (t, h): token t, kv head h.  q heads 2h, 2h+1 (RMSNorm with
+// q_norm, rotation, written back in place in qkv), k head h (k_norm,
+// rotation) and v head h to cache row `row0 + t`.  The rotation uses row t of
+// cos / sin (the caller points them at the token's first row).
+__global__ __launch_bounds__(256) void prefill_qk_kernel(float* __restrict__ qkv, const float* __restrict__ q_norm,
+                                                         const float* __restrict__ k_norm, const float* __restrict__ cos_t,
+                                                         const float* __restrict__ sin_t, float* __restrict__ kc,
+                                                         float* __restrict__ vc, int max_seq, int row0, float eps) {
+  const int t = blockIdx.x, h = blockIdx.y;
+  const int tid = threadIdx.x, g = tid >> 7, d = tid & 127, lane = tid & 63, wv = tid >> 6;
+  __shared__ float s_x[2][PHD], s_xk[PHD], s_red[8];
+  float* row = qkv + (size_t)t * 4096;
+  const float qraw = row[(2 * h + g) * PHD + d];
+  const float kvraw = row[2048 + (g == 0 ? h * PHD : 1024 + h * PHD) + d];
+  const float qw = q_norm[d], kw = k_norm[d];
+  const int j = d & 63;
+  const float co = cos_t[(size_t)t * 64 + j], si = sin_t[(size_t)t * 64 + j];
+  float sq = __fmul_rn(qraw, qraw), sk = __fmul_rn(kvraw, kvraw);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    sq = __fadd_rn(sq, __shfl_xor(sq, o, 64));
+    sk = __fadd_rn(sk, __shfl_xor(sk, o, 64));
+  }
+  if (lane == 0) {
+    s_red[wv] = sq;
+    s_red[4 + wv] = sk;
+  }
+  __syncthreads();
+  const int w0 = wv & ~1;
+  const float rq = ref_rsqrt(__fadd_rn(__fdiv_rn(__fadd_rn(s_red[w0], s_red[w0 + 1]), (float)PHD), eps));
+  s_x[g][d] = __fmul_rn(__fmul_rn(qraw, rq), qw);
+  if (g == 0) {
+    const float rk = ref_rsqrt(__fadd_rn(__fdiv_rn(__fadd_rn(s_red[4], s_red[5]), (float)PHD), eps));
+    s_xk[d] = __fmul_rn(__fmul_rn(kvraw, rk), kw);
+  }
+  __syncthreads();
+  const float lo = s_x[g][j], hi = s_x[g][j + 64];
+  row[(2 * h + g) * PHD + d] =
+      d < 64 ? __fsub_rn(__fmul_rn(lo, co), __fmul_rn(hi, si)) : __fadd_rn(__fmul_rn(hi, co), __fmul_rn(lo, si));
+  const size_t off = ((size_t)h * max_seq + row0 + t) * PHD + d;
+  if (g == 0) {
+    const float klo = s_xk[j], khi = s_xk[j + 64];
+    kc[off] = d < 64 ? __fsub_rn(__fmul_rn(klo, co), __fmul_rn(khi, si)) : __fadd_rn(__fmul_rn(khi, co), __fmul_rn(klo, si));
+  } else {
+    vc[off] = kvraw;
+  }
+}
+
+// Causal flash attention over one q head: work-group (qt, qh) takes queries
+// [64 qt, 64 qt + 64) of the S-token chunk (q rows of qkv, already rotated);
+// query i attends keys j <= qoff + i, read from cache rows key0 + j of kv head
+// qh / 2 (qoff = 0, key0 = chunk start: attention within the chunk, as
+// PREFILL_MODE; key0 = 0, qoff = chunk start: the whole cache, as
+// CHUNKED_PREFILL_MODE), in 64-key tiles staged in LDS with an online softmax.  Thread (ti, tj) =
+// (tid / 16, tid % 16) owns query rows ti + 16 i and key columns tj + 16 c
+// of a score tile (interleaved so that the LDS reads of a wave hit distinct
+// banks), and output columns 8 tj .. 8 tj + 7 of its query rows.  The row
+// statistics live in the 16 lanes of a row group.  fp32 throughout.
+constexpr int FT = 64;          // queries / keys per tile
+constexpr int FQS = PHD + 4;    // padded row stride of the Q and K tiles
+
+__global__ __launch_bounds__(256) void flash_prefill_kernel(const float* __restrict__ qkv, const float* __restrict__ kc,
+                                                            const float* __restrict__ vc, float* __restrict__ out,
+                                                            int S, int max_seq, int key0, int qoff, float scale) {
+  const int ntq = gridDim.x;
+  const int qt = ntq - 1 - blockIdx.x;      // longest (most keys) first
+  const int qh = blockIdx.y, h = qh >> 1;
+  const int q0 = qt * FT;
+  const int nq = min(FT, S - q0);
+  const int tid = threadIdx.x, ti = tid >> 4, tj = tid & 15;
+
+  // float4 storage keeps every 16-byte LDS access aligned
+  __shared__ float4 sQ4[FT * FQS / 4];
+  __shared__ float4 sK4[FT * FQS / 4];
+  __shared__ float4 sV4[FT * PHD / 4];
+  __shared__ float4 sP4[FT * (FT + 4) / 4];
+  float* const sQ = reinterpret_cast<float*>(sQ4);
+  float* const sK = reinterpret_cast<float*>(sK4);
+  float* const sV = reinterpret_cast<float*>(sV4);
+  float* const sP = reinterpret_cast<float*>(sP4);
+
+  // Q tile (rows past S are zero)
+  for (int i = tid; i < FT * (PHD / 4); i += 256) {
+    const int r = i >> 5, c4 = i & 31;
+    const float4 v = r < nq ? reinterpret_cast<const float4*>(qkv + (size_t)(q0 + r) * 4096 + qh * PHD)[c4]
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+    *reinterpret_cast<float4*>(&sQ[r * FQS + 4 * c4]) = v;
+  }
+  const float* kbase = kc + ((size_t)h * max_seq + key0) * PHD;
+  const float* vbase = vc + ((size_t)h * max_seq + key0) * PHD;
+
+  float m[4], l[4], o[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    m[i] = -3.0e38f;
+    l[i] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; c++) o[i][c] = 0.0f;
+  }
+  const int Sk = qoff + S;                  // keys of the last query
+  const int nkt = (qoff + q0 + nq - 1) / FT + 1;   // key tiles up to the last query's
+  // K/V rows of the next tile, prefetched into registers
+  float4 kreg[8], vreg[8];
+  auto load_tile = [&](int kt) {
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int i = tid + 256 * u;
+      const int r = i >> 5, c4 = i & 31;
+      const int key = min(kt * FT + r, Sk - 1);
+      kreg[u] = reinterpret_cast<const float4*>(kbase + (size_t)key * PHD)[c4];
+      vreg[u] = reinterpret_cast<const float4*>(vbase + (size_t)key * PHD)[c4];
+    }
+  };
+  load_tile(0);
+  for (int kt = 0; kt < nkt; kt++) {
+    __syncthreads();                        // previous tile's LDS reads are done
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int i = tid + 256 * u;
+      const int r = i >> 5, c4 = i & 31;
+      *reinterpret_cast<float4*>(&sK[r * FQS + 4 * c4]) = kreg[u];
+      *reinterpret_cast<float4*>(&sV[r * PHD + 4 * c4]) = vreg[u];
+    }
+    __syncthreads();
+    if (kt + 1 < nkt) load_tile(kt + 1);
+
+    // scores s[i][c] = q[ti + 16 i] . k[tj + 16 c]
+    float s[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int c = 0; c < 4; c++) s[i][c] = 0.0f;
+#pragma unroll 4
+    for (int d = 0; d < PHD; d += 4) {
+      float4 qv[4], kv[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) qv[i] = *reinterpret_cast<const float4*>(&sQ[(ti + 16 * i) * FQS + d]);
+#pragma unroll
+      for (int c = 0; c < 4; c++) kv[c] = *reinterpret_cast<const float4*>(&sK[(tj + 16 * c) * FQS + d]);
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          s[i][c] = __fmaf_rn(qv[i].x, kv[c].x, s[i][c]);
+          s[i][c] = __fmaf_rn(qv[i].y, kv[c].y, s[i][c]);
+          s[i][c] = __fmaf_rn(qv[i].z, kv[c].z, s[i][c]);
+          s[i][c] = __fmaf_rn(qv[i].w, kv[c].w, s[i][c]);
+        }
+    }
+    // causal mask, online softmax per query row
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int qi = qoff + q0 + ti + 16 * i;
+      float mx = -3.0e38f;
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const int kj = kt * FT + tj + 16 * c;
+        s[i][c] = (kj <= qi && kj < Sk) ? __fmul_rn(s[i][c], scale) : -3.0e38f;
+        mx = fmaxf(mx, s[i][c]);
+      }
+#pragma unroll
+      for (int w = 1; w < 16; w <<= 1) mx = fmaxf(mx, __shfl_xor(mx, w, 64));
+      const float m_new = fmaxf(m[i], mx);
+      const float resc = expf(__fsub_rn(m[i], m_new));
+      float ps = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const float p = s[i][c] > -1.0e38f ? expf(__fsub_rn(s[i][c], m_new)) : 0.0f;
+        sP[(ti + 16 * i) * (FT + 4) + tj + 16 * c] = p;
+        ps = __fadd_rn(ps, p);
+      }
+#pragma unroll
+      for (int w = 1; w < 16; w <<= 1) ps = __fadd_rn(ps, __shfl_xor(ps, w, 64));
+      l[i] = __fmaf_rn(l[i], resc, ps);
+      m[i] = m_new;
+#pragma unroll
+      for (int c = 0; c < 8; c++) o[i][c] = __fmul_rn(o[i][c], resc);
+    }
+    __syncthreads();                        // sP complete
+    // o[i][c] += sum_k P[row][k] V[k][8 tj + c]
+    const int kmax = min(FT, Sk - kt * FT);
+    for (int k = 0; k < kmax; k++) {
+      const float4 v0 = *reinterpret_cast<const float4*>(&sV[k * PHD + 8 * tj]);
+      const float4 v1 = *reinterpret_cast<const float4*>(&sV[k * PHD + 8 * tj + 4]);
+      const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float p = sP[(ti + 16 * i) * (FT + 4) + k];
+#pragma unroll
+        for (int c = 0; c < 8; c++) o[i][c] = __fmaf_rn(p, vv[c], o[i][c]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int r = ti + 16 * i;
+    if (r < nq) {
+      const float inv = __fdiv_rn(1.0f, l[i]);
+      float4* op = reinterpret_cast<float4*>(out + (size_t)(q0 + r) * 2048 + qh * PHD + 8 * tj);
+      op[0] = make_float4(__fmul_rn(o[i][0], inv), __fmul_rn(o[i][1], inv), __fmul_rn(o[i][2], inv),
+                          __fmul_rn(o[i][3], inv));
+      op[1] = make_float4(__fmul_rn(o[i][4], inv), __fmul_rn(o[i][5], inv), __fmul_rn(o[i][6], inv),
+                          __fmul_rn(o[i][7], inv));
+    }
+  }
+}
+
+// mlp[t][8b + r] = silu(gu[t][16b + r]) * gu[t][16b + 8 + r] (the decoder's
+// per-16-row gate/up interleave; silu as silu_mul_inplace's vector loop)
+__global__ __launch_bounds__(256) void swiglu_rows_kernel(const float* __restrict__ gu, float* __restrict__ mlp,
+                                                          long long n_out, int ffn) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n_out) return;
+  const long long t = i / ffn;
+  const int c = (int)(i - t * ffn);
+  const int b = c >> 3, r = c & 7;
+  const float* row = gu + t * 2 * ffn;
+  mlp[i] = __fmul_rn(ref_silu(row[16 * b + r]), row[16 * b + 8 + r]);
+}
+
+// h = y + h (vec_add_f32 of the residual), float4 per thread
+__global__ __launch_bounds__(256) void residual_add_kernel(const float4* __restrict__ y, float4* __restrict__ h,
+                                                           long long n4) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  const float4 a = y[i], b = h[i];
+  h[i] = make_float4(__fadd_rn(a.x, b.x), __fadd_rn(a.y, b.y), __fadd_rn(a.z, b.z), __fadd_rn(a.w, b.w));
+}
+
+hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int rows, int K, float eps,
+                               hipStream_t st) {
+  if (K % 4 != 0 || K > 2048 || rows < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(256), 0, st, x, w, out, K, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill_qk(float* qkv, const float* q_norm, const float* k_norm, const float* cos_t,
+                             const float* sin_t, float* kc, float* vc, int max_seq, int row0, int S, int nkv,
+                             float eps, hipStream_t st) {
+  if (S < 1 || row0 < 0 || row0 + S > max_seq) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(prefill_qk_kernel, dim3(S, nkv), dim3(256), 0, st, qkv, q_norm, k_norm, cos_t, sin_t, kc, vc,
+                     max_seq, row0, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_flash_prefill(const float* qkv, const float* kc, const float* vc, float* out, int S, int nq,
+                                int max_seq, int key0, int qoff, float scale, hipStream_t st) {
+  if (S < 1 || key0 < 0 || qoff < 0 || key0 + qoff + S > max_seq) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(flash_prefill_kernel, dim3(cdiv(S, FT), nq), dim3(256), 0, st, qkv, kc, vc, out, S, max_seq,
+                     key0, qoff, scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu_rows(const float* gu, float* mlp, int S, int ffn, hipStream_t st) {
+  const long long n = (long long)S * ffn;
+  hipLaunchKernelGGL(swiglu_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gu, mlp, n, ffn);
+  return hipGetLastError();
+}
+
+hipError_t launch_residual_add(const float* y, float* h, long long n, hipStream_t st) {
+  if (n % 4 != 0) return hipErrorInvalidValue;
+  const long long n4 = n / 4;
+  hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st,
+                     reinterpret_cast<const float4*>(y), reinterpret_cast<float4*>(h), n4);
+  return hipGetLastError();
+}
+
+}  // namespace tl

@@ -65,6 +65,17 @@ hipError_t launch_attn_combine(const AttnDecodeArgs& a, float* out, hipStream_t 
 hipError_t launch_step_end(const uint64_t* keys, int n, const float* embed, int H, float* hidden, int* state,
                            int32_t* tokens, int max_tokens, hipStream_t st);
 
+// ---- prefill-step kernels (prefill.hip) -----------------------------------
+hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int rows, int K, float eps,
+                               hipStream_t st);
+hipError_t launch_prefill_qk(float* qkv, const float* q_norm, const float* k_norm, const float* cos_t,
+                             const float* sin_t, float* kc, float* vc, int max_seq, int row0, int S, int nkv,
+                             float eps, hipStream_t st);
+hipError_t launch_flash_prefill(const float* qkv, const float* kc, const float* vc, float* out, int S, int nq,
+                                int max_seq, int key0, int qoff, float scale, hipStream_t st);
+hipError_t launch_swiglu_rows(const float* gu, float* mlp, int S, int ffn, hipStream_t st);
+hipError_t launch_residual_add(const float* y, float* h, long long n, hipStream_t st);
+
 // ---- M=1 GEMV (gemv.hip) --------------------------------------------------
 struct GemvPlan {
   int rows = 16;       // rows per work-group (16 or 8)

@@ -278,6 +278,40 @@ class Decoder:
     def cache_len(self) -> int:
         return self._lib.tl_decoder_cache_len(self._c_cache)
 
+    def prefill(self, hidden_np: np.ndarray, chunk: int = 0) -> np.ndarray:
+        """Prefill hidden [seq_len, HIDDEN_DIM] at sequential positions
+        (decoder_prefill_step; with chunk > 0 decoder_chunked_prefill_step,
+        whose chunks attend to the whole cache)."""
+        assert hidden_np.ndim == 2 and hidden_np.shape[1] == HIDDEN_DIM
+        h = np.array(hidden_np, dtype=np.float32, copy=True)
+        if chunk > 0:
+            self._lib.decoder_chunked_prefill_step(self._c_model, self._c_cache, _np_ptr(h), self._c_scratch,
+                                                   _np_ptr(self._cos_tab), _np_ptr(self._sin_tab), h.shape[0], chunk)
+        else:
+            self._lib.decoder_prefill_step(self._c_model, self._c_cache, _np_ptr(h), self._c_scratch,
+                                           _np_ptr(self._cos_tab), _np_ptr(self._sin_tab), h.shape[0])
+        _lin.check(self._lib, "decoder_prefill_step")
+        return h
+
+    def prefill_3d(self, hidden_np: np.ndarray, position_ids_3d: np.ndarray) -> np.ndarray:
+        """Prefill with 3-D M-RoPE position ids [3, seq_len] (reference
+        :325-358: decoder_build_rope_3d, then decoder_prefill_step_3d)."""
+        assert hidden_np.ndim == 2 and hidden_np.shape[1] == HIDDEN_DIM
+        h = np.ascontiguousarray(hidden_np, dtype=np.float32).copy()
+        S = h.shape[0]
+        pos = np.ascontiguousarray(position_ids_3d, dtype=np.int32)
+        assert pos.shape == (3, S), f"position_ids_3d shape {pos.shape} != (3, {S})"
+        half = HEAD_DIM // 2
+        tc = np.empty((S, half), np.float32)
+        ts = np.empty((S, half), np.float32)
+        self._lib.decoder_build_rope_3d(_np_ptr(tc), _np_ptr(ts), pos.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), S,
+                                        HEAD_DIM, (ctypes.c_int * 3)(*MROPE_SECTIONS),
+                                        (ctypes.c_float * 3)(*MROPE_THETA_BASE))
+        self._lib.decoder_prefill_step_3d(self._c_model, self._c_cache, _np_ptr(h), self._c_scratch, _np_ptr(tc),
+                                          _np_ptr(ts), S)
+        _lin.check(self._lib, "decoder_prefill_step_3d")
+        return h
+
     def step(self, hidden_np: np.ndarray) -> np.ndarray:
         """One decode step of every layer for hidden [1, HIDDEN_DIM]
         (reference :360-370, decoder_decode_step)."""

@@ -55,6 +55,12 @@ SIGNATURES = {
     "decoder_set_layer_weights_v32": (None, [_vp, _int] + [_i8p, _f32p] * 7 + [_f32p] * 4 + [_i8p, _f32p] * 2),
     "decoder_precompute_rope": (None, [_f32p, _f32p, _int, _int, ctypes.POINTER(ctypes.c_int), _f32p]),
     "decoder_decode_step": (None, [_vp, _vp, _f32p, _vp, _f32p, _f32p]),
+    "decoder_prefill_step": (None, [_vp, _vp, _f32p, _vp, _f32p, _f32p, _int]),
+    "decoder_chunked_prefill_step": (None, [_vp, _vp, _f32p, _vp, _f32p, _f32p, _int, _int]),
+    "decoder_hybrid_chunked_prefill_step": (None, [_vp, _vp, _f32p, _vp, _f32p, _f32p, _int, _int]),
+    "decoder_prefill_step_3d": (None, [_vp, _vp, _f32p, _vp, _f32p, _f32p, _int]),
+    "decoder_build_rope_3d": (None, [_f32p, _f32p, ctypes.POINTER(ctypes.c_int), _int, _int,
+                                     ctypes.POINTER(ctypes.c_int), _f32p]),
     "tl_decoder_num_layers": (_int, [_vp]),
     "tl_decoder_cache_len": (_int, [_vp]),
     "tl_decoder_read_cache": (_int, [_vp, _int, _f32p, _f32p]),
