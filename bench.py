@@ -194,7 +194,8 @@ def bench_w8a8_prefill(lin, torch, dev, reps=20):
 
 def bench_decoder_generate(lin, torch, dev, n_layers=28, vocab=151936, prefix=1200, steps=512):
     """The full-decoder workload: 28 layers, a `prefix`-token prefill
-    (decoder_prefill_step) then `steps` greedy decode steps on the device
+    (decoder_prefill_step, timed with W8A8 and with fp32-activation linears)
+    then `steps` greedy decode steps on the device
     (graph replays of 28 x 6 layer launches + lm_head + token/embedding
     step).  Random int8 weights per row-scaled projection, a random fp32
     embedding table, lm_head over the full vocabulary; the prompt is the
@@ -253,19 +254,28 @@ def bench_decoder_generate(lin, torch, dev, n_layers=28, vocab=151936, prefix=12
     hidden0 = embed[torch.from_numpy(ids).to(dev)].cpu().numpy()
     lib.decoder_cache_clear(cache)
     hw = np.ascontiguousarray(hidden0[:64])
-    lib.decoder_prefill_step(model, cache, hw.ctypes.data_as(f32p), scratch, cos.ctypes.data_as(f32p),
-                             sin.ctypes.data_as(f32p), 64)
-    lin.check(lib, "decoder_prefill_step")
+    for w8 in (1, 0):
+        lib.tl_decoder_set_prefill_w8a8(model, w8)
+        lib.decoder_cache_clear(cache)
+        lib.decoder_prefill_step(model, cache, hw.ctypes.data_as(f32p), scratch, cos.ctypes.data_as(f32p),
+                                 sin.ctypes.data_as(f32p), 64)
+        lin.check(lib, "decoder_prefill_step")
     generate(1, 4)
-    # the workload: prefill `prefix` tokens, greedy token from the last row, `steps` decode steps
-    lib.decoder_cache_clear(cache)
-    h = np.array(hidden0, copy=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    lib.decoder_prefill_step(model, cache, h.ctypes.data_as(f32p), scratch, cos.ctypes.data_as(f32p),
-                             sin.ctypes.data_as(f32p), prefix)
-    lin.check(lib, "decoder_prefill_step")
-    t_pre = time.perf_counter() - t0
+    # the workload: prefill `prefix` tokens, greedy token from the last row, `steps` decode steps.
+    # The prefill runs twice: W8A8 linears (the workload's prefill), then the
+    # reference decoder's fp32-activation linears, whose cache the decode uses.
+    def prefill(w8a8):
+        lib.tl_decoder_set_prefill_w8a8(model, w8a8)
+        lib.decoder_cache_clear(cache)
+        hh = np.array(hidden0, copy=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        lib.decoder_prefill_step(model, cache, hh.ctypes.data_as(f32p), scratch, cos.ctypes.data_as(f32p),
+                                 sin.ctypes.data_as(f32p), prefix)
+        lin.check(lib, "decoder_prefill_step")
+        return hh, time.perf_counter() - t0
+    _, t_pre8 = prefill(1)
+    h, t_pre = prefill(0)
     lm_logits_tok = torch.empty(1, dtype=torch.int32, device=dev)
     lin.lm_head_argmax_dev(torch.from_numpy(h[-1].copy()).to(dev), torch.from_numpy(fnorm).to(dev), lm,
                            lm_logits_tok)
@@ -276,9 +286,10 @@ def bench_decoder_generate(lin, torch, dev, n_layers=28, vocab=151936, prefix=12
     out = {"tok_s": round(steps / t, 1), "ms_per_token": round(t / steps * 1e3, 4),
            "layers": n_layers, "vocab": vocab, "cache_len_start": prefix, "steps": steps,
            "launches_per_token": n_layers * 6 + 2,
-           "prefill_tokens": prefix, "prefill_ms": round(t_pre * 1e3, 3),
-           "prefill_tok_s": round(prefix / t_pre, 1),
-           "end_to_end_s": round(t_pre + t, 4),
+           "prefill_tokens": prefix,
+           "prefill_w8a8_ms": round(t_pre8 * 1e3, 3), "prefill_w8a8_tok_s": round(prefix / t_pre8, 1),
+           "prefill_w8a32_ms": round(t_pre * 1e3, 3), "prefill_w8a32_tok_s": round(prefix / t_pre, 1),
+           "end_to_end_s": round(t_pre8 + t, 4),
            "distinct_tokens": int(len(set(toks2.tolist()))),
            "timing": "host wall clock: the prefill call (hidden rows in and out over PCIe included), "
                      "then the graph-replayed decode steps + the tokens' device-to-host copy"}

@@ -293,6 +293,11 @@ void decoder_build_rope_3d(float *cos_out, float *sin_out, const int *pos_ids, i
 /* Extensions (no reference counterpart). */
 int tl_decoder_num_layers(const ModelWeights *model);
 int tl_decoder_cache_len(const KVCache *cache);
+/* Prefill linear layers: 0 (default) w8a32_linear at batch seq_len, the
+ * reference decoder's fp32 activations (decoder.c:56-155); 1 W8A8, per-token
+ * int8 activations (w8a8_quantize_activations, kernel/w8a8_kernel.c:109-114)
+ * and the exact int8 GEMM. */
+int tl_decoder_set_prefill_w8a8(ModelWeights *model, int on);
 /* Copies one layer's K and V cache ([8][max_seq][128] fp32 each; either may
  * be NULL) to host memory. */
 int tl_decoder_read_cache(const KVCache *cache, int layer, float *k, float *v);

@@ -431,11 +431,30 @@ void orc_attention_prefill(const float *q, const float *k, const float *v, float
  * concatenations of the separate weights; orc_w8a32_linear at batch S is the
  * float64 dequant-then-dot restatement.  hidden [S x H] in/out; the cache rows
  * cache_len .. cache_len + S - 1 of Kc/Vc receive k and v. */
+/* batch-S linear of the prefill: w8a32_linear (fp32 activations), or with
+ * w8a8 set per-token activation codes (w8a8_quantize_activations,
+ * w8a8_kernel.c:109-114) and w8a8_linear (:259-268) */
+static void prefill_linear(const float *x, const int8_t *w, const float *s, float *y, int S, int N, int K, int w8a8,
+                           int threads)
+{
+    if (!w8a8) {
+        orc_w8a32_linear(x, w, s, NULL, y, S, N, K, threads, NULL, NULL, NULL);
+        return;
+    }
+    int8_t *q = (int8_t *)malloc((size_t)S * K);
+    float *xs = (float *)malloc((size_t)S * sizeof(float));
+    if (!q || !xs) abort();
+    orc_quantize_rows(x, q, xs, S, K, 1);
+    orc_w8a8_linear(q, xs, w, s, NULL, y, S, N, K, threads);
+    free(q);
+    free(xs);
+}
+
 void orc_prefill_layer(const int8_t *const *w, const float *const *s, const float *input_ln,
                        const float *post_attn_ln, const float *q_norm, const float *k_norm, float *Kc, float *Vc,
                        int max_seq, float *hidden, int S, const float *cos_tab, const float *sin_tab,
                        const float *token_cos, const float *token_sin, int cache_len, int hidden_dim, int ffn_dim,
-                       int num_q_heads, int num_kv_heads, int threads)
+                       int num_q_heads, int num_kv_heads, int threads, int w8a8)
 {
     const int H = hidden_dim, KV = num_kv_heads * HD, F = ffn_dim;
     const size_t SH = (size_t)S * H;
@@ -448,9 +467,9 @@ void orc_prefill_layer(const int8_t *const *w, const float *const *s, const floa
 
     memcpy(residual, hidden, SH * 4);
     for (int t = 0; t < S; t++) orc_rmsnorm(xn + (size_t)t * H, hidden + (size_t)t * H, input_ln, H, 1e-6f);
-    orc_w8a32_linear(xn, w[0], s[0], NULL, q, S, H, H, threads, NULL, NULL, NULL);
-    orc_w8a32_linear(xn, w[1], s[1], NULL, k, S, KV, H, threads, NULL, NULL, NULL);
-    orc_w8a32_linear(xn, w[2], s[2], NULL, v, S, KV, H, threads, NULL, NULL, NULL);
+    prefill_linear(xn, w[0], s[0], q, S, H, H, w8a8, threads);
+    prefill_linear(xn, w[1], s[1], k, S, KV, H, w8a8, threads);
+    prefill_linear(xn, w[2], s[2], v, S, KV, H, w8a8, threads);
     for (int r = 0; r < S * num_q_heads; r++) orc_rmsnorm(q + (size_t)r * HD, q + (size_t)r * HD, q_norm, HD, 1e-6f);
     for (int r = 0; r < S * num_kv_heads; r++) orc_rmsnorm(k + (size_t)r * HD, k + (size_t)r * HD, k_norm, HD, 1e-6f);
     for (int t = 0; t < S; t++) {
@@ -468,15 +487,15 @@ void orc_prefill_layer(const int8_t *const *w, const float *const *s, const floa
             memcpy(Vc + ((size_t)h * max_seq + cache_len + t) * HD, v + (size_t)t * KV + h * HD, HD * 4);
         }
     orc_attention_prefill(q, k, v, attn, S, num_q_heads, num_kv_heads, 0.08838834764831843f);
-    orc_w8a32_linear(attn, w[3], s[3], NULL, y, S, H, H, threads, NULL, NULL, NULL);
+    prefill_linear(attn, w[3], s[3], y, S, H, H, w8a8, threads);
     for (size_t i = 0; i < SH; i++) hidden[i] = y[i] + residual[i];
 
     memcpy(residual, hidden, SH * 4);
     for (int t = 0; t < S; t++) orc_rmsnorm(xn + (size_t)t * H, hidden + (size_t)t * H, post_attn_ln, H, 1e-6f);
-    orc_w8a32_linear(xn, w[4], s[4], NULL, gate, S, F, H, threads, NULL, NULL, NULL);
-    orc_w8a32_linear(xn, w[5], s[5], NULL, up, S, F, H, threads, NULL, NULL, NULL);
+    prefill_linear(xn, w[4], s[4], gate, S, F, H, w8a8, threads);
+    prefill_linear(xn, w[5], s[5], up, S, F, H, w8a8, threads);
     orc_silu_mul(gate, up, S * F);
-    orc_w8a32_linear(gate, w[6], s[6], NULL, y, S, H, F, threads, NULL, NULL, NULL);
+    prefill_linear(gate, w[6], s[6], y, S, H, F, w8a8, threads);
     for (size_t i = 0; i < SH; i++) hidden[i] = y[i] + residual[i];
 
     free(residual); free(xn); free(q); free(k); free(v); free(attn); free(gate); free(up); free(y);

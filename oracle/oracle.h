@@ -94,7 +94,7 @@ void orc_prefill_layer(const int8_t *const *w, const float *const *s, const floa
                        const float *post_attn_ln, const float *q_norm, const float *k_norm, float *Kc, float *Vc,
                        int max_seq, float *hidden, int S, const float *cos_tab, const float *sin_tab,
                        const float *token_cos, const float *token_sin, int cache_len, int hidden_dim, int ffn_dim,
-                       int num_q_heads, int num_kv_heads, int threads);
+                       int num_q_heads, int num_kv_heads, int threads, int w8a8);
 
 #ifdef __cplusplus
 }

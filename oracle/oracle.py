@@ -70,7 +70,7 @@ def load(native: bool = False) -> ctypes.CDLL:
     lib.orc_attention_prefill.argtypes = [_f32p, _f32p, _f32p, _f32p, _i, _i, _i, _f]
     lib.orc_prefill_layer.argtypes = [ctypes.POINTER(_i8p), ctypes.POINTER(_f32p), _f32p, _f32p, _f32p, _f32p,
                                       _f32p, _f32p, _i, _f32p, _i, _f32p, _f32p, _f32p, _f32p, _i, _i, _i, _i,
-                                      _i, _i]
+                                      _i, _i, _i]
     for f in ("orc_rmsnorm", "orc_mrope_precompute", "orc_mrope_apply", "orc_silu_mul",
               "orc_attention_decode", "orc_decode_layer", "orc_mrope_build_3d", "orc_attention_prefill",
               "orc_prefill_layer"):
@@ -308,9 +308,11 @@ def attention_prefill(q: np.ndarray, k: np.ndarray, v: np.ndarray, nq: int = 16,
 
 
 def prefill_layer(layer: dict, kc: np.ndarray, vc: np.ndarray, hidden: np.ndarray, cos_tab=None, sin_tab=None,
-                  token_cos=None, token_sin=None, cache_len: int = 0, threads: int | None = None) -> np.ndarray:
+                  token_cos=None, token_sin=None, cache_len: int = 0, threads: int | None = None,
+                  w8a8: bool = False) -> np.ndarray:
     """One PREFILL_MODE (cos_tab/sin_tab rows cache_len + t) or PREFILL_3D_MODE
-    (token_cos/token_sin rows t) layer over hidden [S, H]; kc/vc updated in place."""
+    (token_cos/token_sin rows t) layer over hidden [S, H]; kc/vc updated in
+    place.  w8a8: the linears on per-token int8 activations."""
     h = np.array(hidden, dtype=np.float32, copy=True)
     S, H = h.shape
     ws = [np.ascontiguousarray(layer[n][0], dtype=np.int8) for n in LAYER_PROJ]
@@ -324,5 +326,5 @@ def prefill_layer(layer: dict, kc: np.ndarray, vc: np.ndarray, hidden: np.ndarra
     load().orc_prefill_layer(warr, sarr, *[_p(n, ctypes.c_float) for n in norms], _p(kc, ctypes.c_float),
                              _p(vc, ctypes.c_float), max_seq, _p(h, ctypes.c_float), S, f(cos_tab), f(sin_tab),
                              f(token_cos), f(token_sin), cache_len, H, ws[4].shape[0], ws[0].shape[0] // HEAD_DIM,
-                             nkv, _threads(threads))
+                             nkv, _threads(threads), 1 if w8a8 else 0)
     return h

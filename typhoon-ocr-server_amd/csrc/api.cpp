@@ -630,6 +630,9 @@ namespace tlhost {
 void linear_w8a32(const float* X, const tl_weights* W, const float* bias, float* Y, int batch, hipStream_t st) {
   op_w8a32(X, W, bias, Y, batch, st);
 }
+void linear_w8a8(const float* X, const tl_weights* W, const float* bias, float* Y, int batch, hipStream_t st) {
+  if (tl_w8a8_linear_f32_dev(X, W, bias, Y, batch, st) != 0) throw Fail{t_err};
+}
 }  // namespace tlhost
 
 // ==========================================================================

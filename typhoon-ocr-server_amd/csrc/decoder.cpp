@@ -92,6 +92,7 @@ struct ModelWeights {
   int dev = -1;
   LayerDev layers[NL];
   uint64_t version = 0;
+  bool prefill_w8a8 = false;    // prefill linears on per-token int8 activations
   int num_layers() const {
     int n = 0;
     while (n < NL && layers[n].qkv) n++;
@@ -226,21 +227,23 @@ void enqueue_prefill(const ModelWeights* m, KVCache* c, DecoderScratch* s, int S
   float* MLP = static_cast<float*>(s->p_mlp.p);
   float* Y = static_cast<float*>(s->p_y.p);
   const long long n = (long long)S * H;
+  // w8a32_linear at batch S (decoder.c), or W8A8 with per-token activation codes
+  auto linear = m->prefill_w8a8 ? linear_w8a8 : linear_w8a32;
   for (int l = 0; l < m->num_layers(); l++) {
     const LayerDev& L = m->layers[l];
     float* kc = c->k + (size_t)l * c->layer_floats();
     float* vc = c->v + (size_t)l * c->layer_floats();
     HIP_OK(launch_rmsnorm_rows(Hd, L.norms, Xn, S, H, EPS, st));
-    linear_w8a32(Xn, L.qkv, nullptr, QKV, S, st);
+    linear(Xn, L.qkv, nullptr, QKV, S, st);
     HIP_OK(launch_prefill_qk(QKV, L.norms + 2 * H, L.norms + 2 * H + HDIM, cos_rows, sin_rows, kc, vc, c->max_seq,
                              row0, S, NKV, EPS, st));
     HIP_OK(launch_flash_prefill(QKV, kc, vc, ATT, S, NQ, c->max_seq, key0, qoff, SCALE, st));
-    linear_w8a32(ATT, L.o, nullptr, Y, S, st);
+    linear(ATT, L.o, nullptr, Y, S, st);
     HIP_OK(launch_residual_add(Y, Hd, n, st));
     HIP_OK(launch_rmsnorm_rows(Hd, L.norms + H, Xn, S, H, EPS, st));
-    linear_w8a32(Xn, L.gu, nullptr, GU, S, st);
+    linear(Xn, L.gu, nullptr, GU, S, st);
     HIP_OK(launch_swiglu_rows(GU, MLP, S, FF, st));
-    linear_w8a32(MLP, L.down, nullptr, Y, S, st);
+    linear(MLP, L.down, nullptr, Y, S, st);
     HIP_OK(launch_residual_add(Y, Hd, n, st));
   }
 }
@@ -641,6 +644,13 @@ int tl_decoder_read_cache(const KVCache* cache, int layer, float* k, float* v) {
 }
 
 int tl_decoder_cache_len(const KVCache* cache) { return cache ? cache->seq_len : -1; }
+
+int tl_decoder_set_prefill_w8a8(ModelWeights* model, int on) {
+  return guarded("tl_decoder_set_prefill_w8a8", [&] {
+    REQUIRE(model, "NULL model");
+    model->prefill_w8a8 = on != 0;
+  });
+}
 
 int tl_decoder_generate(const ModelWeights* model, KVCache* cache, DecoderScratch* scratch,
                         const tl_weights* lm_head, const float* final_norm, const float* embed, int first_token,

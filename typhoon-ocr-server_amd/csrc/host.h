@@ -114,5 +114,7 @@ void check_weights(const tl_weights* W);
 // w8a32_linear semantics on device pointers (batch 1: GEMV; batch > 1: the
 // fp32-accurate GEMM), stream-ordered
 void linear_w8a32(const float* X, const tl_weights* W, const float* bias, float* Y, int batch, hipStream_t st);
+// per-token int8 activations of fp32 X, int8 GEMM, fp32 out (tl_w8a8_linear_f32_dev)
+void linear_w8a8(const float* X, const tl_weights* W, const float* bias, float* Y, int batch, hipStream_t st);
 
 }  // namespace tlhost

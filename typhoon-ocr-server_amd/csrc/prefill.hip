@@ -104,60 +104,70 @@ __global__ __launch_bounds__(256) void prefill_qk_kernel(float* __restrict__ qkv
   }
 }
 
-// Causal flash attention over one q head: work-group (qt, qh) takes queries
-// [64 qt, 64 qt + 64) of the S-token chunk (q rows of qkv, already rotated);
-// query i attends keys j <= qoff + i, read from cache rows key0 + j of kv head
-// qh / 2 (qoff = 0, key0 = chunk start: attention within the chunk, as
-// PREFILL_MODE; key0 = 0, qoff = chunk start: the whole cache, as
-// CHUNKED_PREFILL_MODE), in 64-key tiles staged in LDS with an online softmax.  Thread (ti, tj) =
-// (tid / 16, tid % 16) owns query rows ti + 16 i and key columns tj + 16 c
-// of a score tile (interleaved so that the LDS reads of a wave hit distinct
-// banks), and output columns 8 tj .. 8 tj + 7 of its query rows.  The row
-// statistics live in the 16 lanes of a row group.  fp32 throughout.
+// Causal flash attention over one q head on fp32 MFMA
+// (v_mfma_f32_16x16x4f32: exact fp32 products, fp32 accumulation).
+// Work-group (qt, qh) takes queries [64 qt, 64 qt + 64) of the S-token chunk
+// (q rows of qkv, already rotated); query i attends keys j <= qoff + i, read
+// from cache rows key0 + j of kv head qh / 2 (qoff = 0, key0 = chunk start:
+// attention within the chunk, as PREFILL_MODE; key0 = 0, qoff = chunk start:
+// the whole cache, as CHUNKED_PREFILL_MODE), in 64-key tiles staged in LDS
+// with an online softmax.
 constexpr int FT = 64;          // queries / keys per tile
-constexpr int FQS = PHD + 4;    // padded row stride of the Q and K tiles
+constexpr int FQS = PHD + 4;    // padded row stride of the K tile
 
-__global__ __launch_bounds__(256) void flash_prefill_kernel(const float* __restrict__ qkv, const float* __restrict__ kc,
-                                                            const float* __restrict__ vc, float* __restrict__ out,
-                                                            int S, int max_seq, int key0, int qoff, float scale) {
+// Wave w holds the 16 queries q0 + 16 w + c in lanes (g, c) = (lane >> 4,
+// lane & 15).
+//   scores   D[key][query] += K[key][d] Q[query][d]: K is the first operand,
+//            Q (kept in registers) the second; MFMA t = 4u + e of a 16-key
+//            block reads, in lane group g, dimension d = 16u + 4g + e (any
+//            bijection of d works, this one makes every operand read a
+//            float4).  The block's keys are permuted so that output row
+//            4g + r is key 16b + 4r + g: lane (g, c) then holds the scores of
+//            query c for keys 16b + 4r + g, r = 0..3 ...
+//   P.V      ... which is exactly the second operand of the four P.V MFMAs
+//            of that block (MFMA m needs key 16b + 4m + g in lane group g):
+//            no transpose.  V^T is the first operand, read from LDS, and the
+//            output lane (g, c) holds O[query c][16 j + 4g + r], j = 0..7.
+// The online softmax of query c runs in lanes c, c+16, c+32, c+48.
+constexpr int KVS = PHD + 16;   // row stride of the V tile (conflict-free V^T reads)
+
+__global__ __launch_bounds__(256) void flash_prefill_mfma_kernel(const float* __restrict__ qkv,
+                                                                 const float* __restrict__ kc,
+                                                                 const float* __restrict__ vc, float* __restrict__ out,
+                                                                 int S, int max_seq, int key0, int qoff, float scale) {
   const int ntq = gridDim.x;
   const int qt = ntq - 1 - blockIdx.x;      // longest (most keys) first
   const int qh = blockIdx.y, h = qh >> 1;
   const int q0 = qt * FT;
   const int nq = min(FT, S - q0);
-  const int tid = threadIdx.x, ti = tid >> 4, tj = tid & 15;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
 
-  // float4 storage keeps every 16-byte LDS access aligned
-  __shared__ float4 sQ4[FT * FQS / 4];
   __shared__ float4 sK4[FT * FQS / 4];
-  __shared__ float4 sV4[FT * PHD / 4];
-  __shared__ float4 sP4[FT * (FT + 4) / 4];
-  float* const sQ = reinterpret_cast<float*>(sQ4);
+  __shared__ float4 sV4[FT * KVS / 4];
   float* const sK = reinterpret_cast<float*>(sK4);
   float* const sV = reinterpret_cast<float*>(sV4);
-  float* const sP = reinterpret_cast<float*>(sP4);
 
-  // Q tile (rows past S are zero)
-  for (int i = tid; i < FT * (PHD / 4); i += 256) {
-    const int r = i >> 5, c4 = i & 31;
-    const float4 v = r < nq ? reinterpret_cast<const float4*>(qkv + (size_t)(q0 + r) * 4096 + qh * PHD)[c4]
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
-    *reinterpret_cast<float4*>(&sQ[r * FQS + 4 * c4]) = v;
+  // this lane's query and its Q operand (dimensions 16u + 4g .. 16u + 4g + 3)
+  const int qloc = 16 * wv + c;                           // 0..63 within the tile
+  const int qrow = min(q0 + qloc, S - 1);
+  float4 qr[8];
+  {
+    const float4* qp = reinterpret_cast<const float4*>(qkv + (size_t)qrow * 4096 + qh * PHD);
+#pragma unroll
+    for (int u = 0; u < 8; u++) qr[u] = qp[4 * u + g];
   }
+  const int qpos = qoff + q0 + qloc;                      // key index bound of this query
+  const int Sk = qoff + S;
   const float* kbase = kc + ((size_t)h * max_seq + key0) * PHD;
   const float* vbase = vc + ((size_t)h * max_seq + key0) * PHD;
 
-  float m[4], l[4], o[4][8];
+  v4f o[8];
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    m[i] = -3.0e38f;
-    l[i] = 0.0f;
-#pragma unroll
-    for (int c = 0; c < 8; c++) o[i][c] = 0.0f;
-  }
-  const int Sk = qoff + S;                  // keys of the last query
-  const int nkt = (qoff + q0 + nq - 1) / FT + 1;   // key tiles up to the last query's
-  // K/V rows of the next tile, prefetched into registers
+  for (int j = 0; j < 8; j++) o[j] = v4f{0.f, 0.f, 0.f, 0.f};
+  float m = -3.0e38f, l = 0.0f;
+
+  const int nkt = (qoff + q0 + nq - 1) / FT + 1;
   float4 kreg[8], vreg[8];
   auto load_tile = [&](int kt) {
 #pragma unroll
@@ -177,89 +187,75 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const float* __restr
       const int i = tid + 256 * u;
       const int r = i >> 5, c4 = i & 31;
       *reinterpret_cast<float4*>(&sK[r * FQS + 4 * c4]) = kreg[u];
-      *reinterpret_cast<float4*>(&sV[r * PHD + 4 * c4]) = vreg[u];
+      *reinterpret_cast<float4*>(&sV[r * KVS + 4 * c4]) = vreg[u];
     }
     __syncthreads();
     if (kt + 1 < nkt) load_tile(kt + 1);
 
-    // scores s[i][c] = q[ti + 16 i] . k[tj + 16 c]
-    float s[4][4];
+    // scores of the tile's four 16-key blocks
+    v4f sc[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int b = 0; b < 4; b++) {
+      sc[b] = v4f{0.f, 0.f, 0.f, 0.f};
+      const int krow = 16 * b + 4 * (c & 3) + (c >> 2);   // permuted key of operand row c
+      const float* kp = sK + krow * FQS + 4 * g;
 #pragma unroll
-      for (int c = 0; c < 4; c++) s[i][c] = 0.0f;
-#pragma unroll 4
-    for (int d = 0; d < PHD; d += 4) {
-      float4 qv[4], kv[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) qv[i] = *reinterpret_cast<const float4*>(&sQ[(ti + 16 * i) * FQS + d]);
-#pragma unroll
-      for (int c = 0; c < 4; c++) kv[c] = *reinterpret_cast<const float4*>(&sK[(tj + 16 * c) * FQS + d]);
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-          s[i][c] = __fmaf_rn(qv[i].x, kv[c].x, s[i][c]);
-          s[i][c] = __fmaf_rn(qv[i].y, kv[c].y, s[i][c]);
-          s[i][c] = __fmaf_rn(qv[i].z, kv[c].z, s[i][c]);
-          s[i][c] = __fmaf_rn(qv[i].w, kv[c].w, s[i][c]);
-        }
-    }
-    // causal mask, online softmax per query row
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int qi = qoff + q0 + ti + 16 * i;
-      float mx = -3.0e38f;
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        const int kj = kt * FT + tj + 16 * c;
-        s[i][c] = (kj <= qi && kj < Sk) ? __fmul_rn(s[i][c], scale) : -3.0e38f;
-        mx = fmaxf(mx, s[i][c]);
-      }
-#pragma unroll
-      for (int w = 1; w < 16; w <<= 1) mx = fmaxf(mx, __shfl_xor(mx, w, 64));
-      const float m_new = fmaxf(m[i], mx);
-      const float resc = expf(__fsub_rn(m[i], m_new));
-      float ps = 0.0f;
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        const float p = s[i][c] > -1.0e38f ? expf(__fsub_rn(s[i][c], m_new)) : 0.0f;
-        sP[(ti + 16 * i) * (FT + 4) + tj + 16 * c] = p;
-        ps = __fadd_rn(ps, p);
-      }
-#pragma unroll
-      for (int w = 1; w < 16; w <<= 1) ps = __fadd_rn(ps, __shfl_xor(ps, w, 64));
-      l[i] = __fmaf_rn(l[i], resc, ps);
-      m[i] = m_new;
-#pragma unroll
-      for (int c = 0; c < 8; c++) o[i][c] = __fmul_rn(o[i][c], resc);
-    }
-    __syncthreads();                        // sP complete
-    // o[i][c] += sum_k P[row][k] V[k][8 tj + c]
-    const int kmax = min(FT, Sk - kt * FT);
-    for (int k = 0; k < kmax; k++) {
-      const float4 v0 = *reinterpret_cast<const float4*>(&sV[k * PHD + 8 * tj]);
-      const float4 v1 = *reinterpret_cast<const float4*>(&sV[k * PHD + 8 * tj + 4]);
-      const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float p = sP[(ti + 16 * i) * (FT + 4) + k];
-#pragma unroll
-        for (int c = 0; c < 8; c++) o[i][c] = __fmaf_rn(p, vv[c], o[i][c]);
+      for (int u = 0; u < 8; u++) {
+        const float4 kv = *reinterpret_cast<const float4*>(kp + 16 * u);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qr[u].x, sc[b], 0, 0, 0);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qr[u].y, sc[b], 0, 0, 0);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qr[u].z, sc[b], 0, 0, 0);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qr[u].w, sc[b], 0, 0, 0);
       }
     }
+    // mask, online softmax (query c: lanes c, c+16, c+32, c+48)
+    float mx = -3.0e38f;
+#pragma unroll
+    for (int b = 0; b < 4; b++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int key = kt * FT + 16 * b + 4 * r + g;
+        sc[b][r] = (key <= qpos && key < Sk) ? __fmul_rn(sc[b][r], scale) : -3.0e38f;
+        mx = fmaxf(mx, sc[b][r]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);
+    const float resc = expf(__fsub_rn(m, m_new));
+    float ps = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 4; b++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float pv = sc[b][r] > -1.0e38f ? expf(__fsub_rn(sc[b][r], m_new)) : 0.0f;
+        sc[b][r] = pv;
+        ps = __fadd_rn(ps, pv);
+      }
+    ps = __fadd_rn(ps, __shfl_xor(ps, 16, 64));
+    ps = __fadd_rn(ps, __shfl_xor(ps, 32, 64));
+    l = __fmaf_rn(l, resc, ps);
+    m = m_new;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) o[j][r] = __fmul_rn(o[j][r], resc);
+    // O^T[d][query] += V^T[d][key] P^T[key][query]
+#pragma unroll
+    for (int b = 0; b < 4; b++)
+#pragma unroll
+      for (int mm = 0; mm < 4; mm++) {
+        const float* vp = sV + (16 * b + 4 * mm + g) * KVS + c;
+#pragma unroll
+        for (int j = 0; j < 8; j++) o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vp[16 * j], sc[b][mm], o[j], 0, 0, 0);
+      }
   }
+  if (qloc < nq) {
+    const float inv = __fdiv_rn(1.0f, l);
+    float* op = out + (size_t)(q0 + qloc) * 2048 + qh * PHD + 4 * g;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int r = ti + 16 * i;
-    if (r < nq) {
-      const float inv = __fdiv_rn(1.0f, l[i]);
-      float4* op = reinterpret_cast<float4*>(out + (size_t)(q0 + r) * 2048 + qh * PHD + 8 * tj);
-      op[0] = make_float4(__fmul_rn(o[i][0], inv), __fmul_rn(o[i][1], inv), __fmul_rn(o[i][2], inv),
-                          __fmul_rn(o[i][3], inv));
-      op[1] = make_float4(__fmul_rn(o[i][4], inv), __fmul_rn(o[i][5], inv), __fmul_rn(o[i][6], inv),
-                          __fmul_rn(o[i][7], inv));
-    }
+    for (int j = 0; j < 8; j++)
+      *reinterpret_cast<float4*>(op + 16 * j) = make_float4(__fmul_rn(o[j][0], inv), __fmul_rn(o[j][1], inv),
+                                                            __fmul_rn(o[j][2], inv), __fmul_rn(o[j][3], inv));
   }
 }
 
@@ -304,8 +300,8 @@ hipError_t launch_prefill_qk(float* qkv, const float* q_norm, const float* k_nor
 hipError_t launch_flash_prefill(const float* qkv, const float* kc, const float* vc, float* out, int S, int nq,
                                 int max_seq, int key0, int qoff, float scale, hipStream_t st) {
   if (S < 1 || key0 < 0 || qoff < 0 || key0 + qoff + S > max_seq) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(flash_prefill_kernel, dim3(cdiv(S, FT), nq), dim3(256), 0, st, qkv, kc, vc, out, S, max_seq,
-                     key0, qoff, scale);
+  hipLaunchKernelGGL(flash_prefill_mfma_kernel, dim3(cdiv(S, FT), nq), dim3(256), 0, st, qkv, kc, vc, out, S,
+                     max_seq, key0, qoff, scale);
   return hipGetLastError();
 }
 

@@ -278,6 +278,13 @@ class Decoder:
     def cache_len(self) -> int:
         return self._lib.tl_decoder_cache_len(self._c_cache)
 
+    def set_prefill_w8a8(self, on: bool) -> None:
+        """Prefill linears on per-token int8 activations (W8A8) instead of the
+        reference decoder's fp32 activations."""
+        self._init_device_loop()
+        if self._lib.tl_decoder_set_prefill_w8a8(self._c_model, 1 if on else 0) != 0:
+            _lin.check(self._lib, "tl_decoder_set_prefill_w8a8")
+
     def prefill(self, hidden_np: np.ndarray, chunk: int = 0) -> np.ndarray:
         """Prefill hidden [seq_len, HIDDEN_DIM] at sequential positions
         (decoder_prefill_step; with chunk > 0 decoder_chunked_prefill_step,

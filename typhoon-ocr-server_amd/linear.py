@@ -63,6 +63,7 @@ SIGNATURES = {
                                      ctypes.POINTER(ctypes.c_int), _f32p]),
     "tl_decoder_num_layers": (_int, [_vp]),
     "tl_decoder_cache_len": (_int, [_vp]),
+    "tl_decoder_set_prefill_w8a8": (_int, [_vp, _int]),
     "tl_decoder_read_cache": (_int, [_vp, _int, _f32p, _f32p]),
     "tl_decoder_generate": (_int, [_vp, _vp, _vp, _vp, _f32p, _vp, _int, _int,
                                    ctypes.POINTER(ctypes.c_int32), _f32p, _f32p]),
