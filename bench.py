@@ -456,16 +456,21 @@ def bench_host_abi(lin, reps=200):
         if lib.tl_register_weights(lin._p(w, lin.ctypes.c_int8), lin._p(s, lin.ctypes.c_float), N, K) != 0:
             lin.check(lib, "tl_register_weights")
         n = reps if N < 100000 else max(20, reps // 10)
-        for _ in range(5):
+        for _ in range(20):
             lin.w8a32_linear(x, w, s, out=y)
-        t0 = time.perf_counter()
+        # median per-call wall time (robust against the driver's deferred work
+        # after the decode set's 1.72 GB are freed just before)
+        ts = []
         for _ in range(n):
+            t0 = time.perf_counter()
             lin.w8a32_linear(x, w, s, out=y)
-        t = (time.perf_counter() - t0) / n
+            ts.append(time.perf_counter() - t0)
+        t = float(np.median(ts))
         b = gemv_bytes(N, K)
         out[f"{name}_{N}x{K}"] = {"us": round(t * 1e6, 2), "GBps": round(b / t / 1e9, 1)}
         lib.tl_evict_weights(lin._p(w, lin.ctypes.c_int8))
-    out["includes"] = "host x -> HBM, GEMV, HBM -> host y, stream sync; weights already resident"
+    out["includes"] = ("median per call: host x -> HBM, GEMV, HBM -> host y, stream sync; "
+                       "weights already resident")
     return out
 
 
