@@ -285,7 +285,7 @@ def bench_decoder_generate(lin, torch, dev, n_layers=28, vocab=151936, prefix=12
     t = time.perf_counter() - t0
     out = {"tok_s": round(steps / t, 1), "ms_per_token": round(t / steps * 1e3, 4),
            "layers": n_layers, "vocab": vocab, "cache_len_start": prefix, "steps": steps,
-           "launches_per_token": n_layers * 6 + 2,
+           "launches_per_token": n_layers * 5 + 2,
            "prefill_tokens": prefix,
            "prefill_w8a8_ms": round(t_pre8 * 1e3, 3), "prefill_w8a8_tok_s": round(prefix / t_pre8, 1),
            "prefill_w8a32_ms": round(t_pre * 1e3, 3), "prefill_w8a32_tok_s": round(prefix / t_pre, 1),

@@ -12,13 +12,13 @@
 //   DecoderScratch  activation buffers, attention partials, a stream and the
 //                   captured step graphs
 //
-// One layer of a decode step is six launches (decoder.c:33-157):
+// One layer of a decode step is five launches (decoder.c:33-157):
 //   1. QKV GEMV, input RMSNorm in its prologue                  -> qkv
-//   2. attention partials: QK RMSNorm, M-RoPE, KV append, scores -> partials
-//   3. attention combine                                         -> attn
-//   4. O GEMV + residual (the residual is the GEMV bias, in place) -> hidden
-//   5. gate/up GEMV, post-attention RMSNorm prologue, SwiGLU epilogue -> mlp
-//   6. down GEMV + residual                                     -> hidden
+//   2. attention: QK RMSNorm, M-RoPE, KV append, chunk partials, and the
+//      merge in the last work-group of each kv head             -> attn
+//   3. O GEMV + residual (the residual is the GEMV bias, in place) -> hidden
+//   4. gate/up GEMV, post-attention RMSNorm prologue, SwiGLU epilogue -> mlp
+//   5. down GEMV + residual                                     -> hidden
 // The layer loop is captured once into a HIP graph per (model, cache, rope
 // tables) and replayed; the decode state is written before each replay.
 // tl_decoder_generate adds the lm_head (numpy final RMSNorm + argmax keys)
@@ -117,6 +117,7 @@ struct DecoderScratch {
   hipStream_t st = nullptr;
   float *hidden = nullptr, *qkv = nullptr, *attn = nullptr, *mlp = nullptr;
   float *pm = nullptr, *pl = nullptr, *po = nullptr;
+  int* count = nullptr;                 // attention arrival counters [NKV], zero between launches
   int C = 0;
   DevBuf keys, tokens, fnorm;
   PinnedBuf pin;
@@ -198,6 +199,8 @@ void enqueue_layers(const ModelWeights* m, const KVCache* c, DecoderScratch* s, 
     a.pm = s->pm;
     a.pl = s->pl;
     a.po = s->po;
+    a.count = s->count;
+    a.out = s->attn;
     a.nq = NQ;
     a.nkv = NKV;
     a.max_seq = c->max_seq;
@@ -205,7 +208,6 @@ void enqueue_layers(const ModelWeights* m, const KVCache* c, DecoderScratch* s, 
     a.scale = SCALE;
     a.eps = EPS;
     HIP_OK(launch_attn_decode(a, st));
-    HIP_OK(launch_attn_combine(a, s->attn, st));
     gemv(L.o, s->attn, s->hidden, s->hidden, EPI_W8A32, NORM_NONE, nullptr, st);
     gemv(L.gu, s->hidden, s->mlp, nullptr, EPI_SWIGLU, NORM_DECODER, L.norms + H, st);
     gemv(L.down, s->mlp, s->hidden, s->hidden, EPI_W8A32, NORM_NONE, nullptr, st);
@@ -469,6 +471,8 @@ DecoderScratch* decoder_scratch_alloc_fn(int max_seq) {
     HIP_OK(hipMalloc(&p->pm, (size_t)NQ * p->C * 4));
     HIP_OK(hipMalloc(&p->pl, (size_t)NQ * p->C * 4));
     HIP_OK(hipMalloc(&p->po, (size_t)NQ * p->C * HDIM * 4));
+    HIP_OK(hipMalloc(&p->count, (size_t)NKV * sizeof(int)));
+    HIP_OK(hipMemset(p->count, 0, (size_t)NKV * sizeof(int)));
     p->pin.ensure(kStageHidden + (size_t)H * 4);
     s = p.release();
   });
@@ -482,6 +486,7 @@ void decoder_scratch_free_fn(DecoderScratch* s) {
   drop_graph(s->gen_exec);
   for (float* p : {s->hidden, s->qkv, s->attn, s->mlp, s->pm, s->pl, s->po})
     if (p) (void)hipFree(p);
+  if (s->count) (void)hipFree(s->count);
   for (DevBuf* b : {&s->p_h, &s->p_xn, &s->p_qkv, &s->p_att, &s->p_gu, &s->p_mlp, &s->p_y, &s->p_cos, &s->p_sin})
     if (b->p) (void)hipFree(b->p);
   if (s->keys.p) (void)hipFree(s->keys.p);

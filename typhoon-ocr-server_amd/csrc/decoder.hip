@@ -6,10 +6,11 @@
 // as an epilogue); what remains for this file is
 //   attn_decode_kernel   per-head QK RMSNorm (q_norm / k_norm), M-RoPE at the
 //                        decode position, the KV cache append of the new
-//                        token, and split-sequence GQA attention partials
+//                        token, split-sequence GQA attention partials and,
+//                        in the last work-group of each kv head to finish,
+//                        the softmax-weighted merge of the partials
 //                        (kernel/ops.c:233-289, kernel/kv_cache.c:53-64,
 //                        kernel/attention.c:172-224);
-//   attn_combine_kernel  the softmax-weighted merge of the partials;
 //   step_end_kernel      greedy token from the lm_head argmax keys, the next
 //                        step's embedding row, the position advance
 //                        (decoder.py:463-464 and :501-504, kv_cache.c:108-112).
@@ -31,6 +32,52 @@ constexpr int ATT_T = 64;        // positions per attention work-group
 
 
 
+// Loads of the partials.  The merge runs in the same launch that wrote them,
+// possibly on another XCD, so it reads them with agent-scope atomic loads
+// (coherent across the XCDs' L2 caches) and they were stored with
+// agent-scope atomic stores.
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c over the nc live chunks
+// of q head qh, element d; chunks in batches of 32 (all loads of a batch in
+// flight together), each batch rescaling what the earlier ones accumulated.
+__device__ __forceinline__ float merge_chunks(const float* pm, const float* pl, const float* po, int C, int nc,
+                                              int qh, int d) {
+  float L = 0.0f, acc = 0.0f, M = -3.0e38f;
+  for (int c0 = 0; c0 < nc; c0 += 32) {
+    float v[32], m[32], l[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+      const bool ok = c0 + i < nc;
+      const int cc = min(c0 + i, nc - 1);
+      v[i] = ld_agent(po + ((size_t)qh * C + cc) * HD + d);
+      m[i] = ok ? ld_agent(pm + qh * C + cc) : -3.0e38f;
+      l[i] = ld_agent(pl + qh * C + cc);
+    }
+    float Mb = M;
+#pragma unroll
+    for (int i = 0; i < 32; i++) Mb = fmaxf(Mb, m[i]);
+    const float r = expf(__fsub_rn(M, Mb));
+    L = __fmul_rn(L, r);
+    acc = __fmul_rn(acc, r);
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+      if (c0 + i < nc) {
+        const float w = expf(__fsub_rn(m[i], Mb));
+        L = __fmaf_rn(w, l[i], L);
+        acc = __fmaf_rn(w, v[i], acc);
+      }
+    }
+    M = Mb;
+  }
+  return __fmul_rn(acc, __fdiv_rn(1.0f, L));
+}
+
 // Work-group (c, h): kv head h, positions [64 c, 64 c + 64) of the S = len + 1
 // that the new token attends to; two q heads (GQA group 2).  256 threads.
 // Every load of the chunk (its K and V rows, the q/k/v rows of the QKV
@@ -38,6 +85,14 @@ constexpr int ATT_T = 64;        // positions per attention work-group
 // prologue runs while they are in flight.  Positions past the chunk end read
 // a clamped valid row and are masked; position p (the new token, whose cache
 // row this work-group writes) is taken from LDS instead of memory.
+//
+// Merge without a second launch: every work-group stores its partials with
+// agent-scope atomic stores, waits until they are acknowledged (vmcnt 0: the
+// stores bypass the non-coherent L2 path, so no L2 write-back is needed, which
+// a device-scope fence would do), then bumps the kv head's arrival counter.
+// The work-group that brings the counter to the number of live chunks merges
+// the two q heads and resets the counter for the next launch.  Nothing waits
+// on another work-group.
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   const int c = blockIdx.x, h = blockIdx.y;
   const int p = a.state[0];                 // position of the new token
@@ -175,8 +230,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
     s_p[wv][lane] = e;                      // zero past the chunk end
     if (lane == 0) {
       const int qh = 2 * h + wv;
-      a.pm[qh * a.C + c] = m;
-      a.pl[qh * a.C + c] = l;
+      st_agent(a.pm + qh * a.C + c, m);
+      st_agent(a.pl + qh * a.C + c, l);
     }
   }
   __syncthreads();
@@ -202,47 +257,20 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   float o = 0.0f;
 #pragma unroll
   for (int q = 0; q < 8; q++) o = __fadd_rn(o, so[(q * 2 + g) * HD + d]);
-  a.po[((size_t)(2 * h + g) * a.C + c) * HD + d] = o;
-}
+  st_agent(a.po + ((size_t)(2 * h + g) * a.C + c) * HD + d, o);
 
-// One work-group per q head: out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
-// Two dependent memory round trips: the decode state, then every chunk's
-// statistics and this thread's partial outputs together (up to 32 chunks per
-// batch in flight).
-__global__ __launch_bounds__(128) void attn_combine_kernel(const float* __restrict__ pm, const float* __restrict__ pl,
-                                                           const float* __restrict__ po, const int* __restrict__ state,
-                                                           int C, float* __restrict__ out) {
-  const int qh = blockIdx.x, d = threadIdx.x;
-  const int nc = cdiv(state[0] + 1, ATT_T);
-  float L = 0.0f, acc = 0.0f, M = -3.0e38f;
-  for (int c0 = 0; c0 < nc; c0 += 32) {
-    float v[32], m[32], l[32];
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
-      const bool ok = c0 + i < nc;
-      const int cc = min(c0 + i, nc - 1);
-      v[i] = po[((size_t)qh * C + cc) * HD + d];
-      m[i] = ok ? pm[qh * C + cc] : -3.0e38f;
-      l[i] = pl[qh * C + cc];
-    }
-    float Mb = M;
-#pragma unroll
-    for (int i = 0; i < 32; i++) Mb = fmaxf(Mb, m[i]);
-    // rescale what earlier batches accumulated (one batch for S <= 2048)
-    const float r = expf(__fsub_rn(M, Mb));
-    L = __fmul_rn(L, r);
-    acc = __fmul_rn(acc, r);
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
-      if (c0 + i < nc) {
-        const float w = expf(__fsub_rn(m[i], Mb));
-        L = __fmaf_rn(w, l[i], L);
-        acc = __fmaf_rn(w, v[i], acc);
-      }
-    }
-    M = Mb;
-  }
-  out[qh * HD + d] = __fmul_rn(acc, __fdiv_rn(1.0f, L));
+  // ---- arrival; the last work-group of kv head h merges ----------------------
+  __shared__ int s_last;
+  asm volatile("" ::: "memory");
+  wait_vm<0>();                             // this thread's partial stores are acknowledged
+  asm volatile("" ::: "memory");
+  __syncthreads();
+  const int nc = cdiv(S, ATT_T);
+  if (tid == 0) s_last = __hip_atomic_fetch_add(a.count + h, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nc - 1;
+  __syncthreads();
+  if (!s_last) return;
+  if (tid == 0) __hip_atomic_store(a.count + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  a.out[(2 * h + g) * HD + d] = merge_chunks(a.pm, a.pl, a.po, a.C, nc, 2 * h + g, d);
 }
 
 // greedy token (largest argmax key: largest logit, lowest index on ties),
@@ -281,13 +309,8 @@ __global__ __launch_bounds__(1024) void step_end_kernel(const uint64_t* __restri
 }
 
 hipError_t launch_attn_decode(const AttnDecodeArgs& a, hipStream_t st) {
-  if (a.nq != 2 * a.nkv || a.C * ATT_T < a.max_seq) return hipErrorInvalidValue;
+  if (a.nq != 2 * a.nkv || a.C * ATT_T < a.max_seq || !a.count || !a.out) return hipErrorInvalidValue;
   hipLaunchKernelGGL(attn_decode_kernel, dim3(a.C, a.nkv), dim3(256), 0, st, a);
-  return hipGetLastError();
-}
-
-hipError_t launch_attn_combine(const AttnDecodeArgs& a, float* out, hipStream_t st) {
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nq), dim3(HD), 0, st, a.pm, a.pl, a.po, a.state, a.C, out);
   return hipGetLastError();
 }
 

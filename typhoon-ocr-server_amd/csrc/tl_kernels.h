@@ -56,12 +56,13 @@ struct AttnDecodeArgs {
   float* pm = nullptr;             // partial maxima [nq][C]
   float* pl = nullptr;             // partial sums [nq][C]
   float* po = nullptr;             // partial outputs [nq][C][128]
+  int* count = nullptr;            // arrival counters [nkv], zero between launches
+  float* out = nullptr;            // merged attention output [nq*128]
   int nq = 16, nkv = 8, max_seq = 0, C = 0;
   float scale = 0.0f, eps = 1e-6f;
 };
 int attn_chunks(int max_seq);
 hipError_t launch_attn_decode(const AttnDecodeArgs& a, hipStream_t st);
-hipError_t launch_attn_combine(const AttnDecodeArgs& a, float* out, hipStream_t st);
 hipError_t launch_step_end(const uint64_t* keys, int n, const float* embed, int H, float* hidden, int* state,
                            int32_t* tokens, int max_tokens, hipStream_t st);
 
