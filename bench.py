@@ -20,6 +20,7 @@ GEMV, OpenMP on the host cores) on a bounded sample.
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import sys
@@ -227,11 +228,13 @@ def bench_decoder_generate(lin, torch, dev, n_layers=28, vocab=151936, prefix=12
         args += [n.ctypes.data_as(f32p) for n in norms]
         lib.decoder_set_layer_weights(model, l, *args)
         lin.check(lib, "decoder_set_layer_weights")
-    lm_w = torch.randint(-127, 128, (vocab, H), dtype=torch.int8, device=dev)
-    lm_s = torch.rand(vocab, device=dev) * 4e-4 + 1e-4
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    lm_w = torch.randint(-127, 128, (vocab, H), dtype=torch.int8, device=dev, generator=gen)
+    lm_s = torch.rand(vocab, device=dev, generator=gen) * 4e-4 + 1e-4
     lm = lin.DeviceWeights.from_codes(lm_w, lm_s)
     del lm_w
-    embed = torch.randn((vocab, H), device=dev)
+    embed = torch.randn((vocab, H), device=dev, generator=gen)
     fnorm = vec(H)
     half = HD // 2
     cos = np.empty((max_seq, half), np.float32)
@@ -291,6 +294,7 @@ def bench_decoder_generate(lin, torch, dev, n_layers=28, vocab=151936, prefix=12
            "prefill_w8a32_ms": round(t_pre * 1e3, 3), "prefill_w8a32_tok_s": round(prefix / t_pre, 1),
            "end_to_end_s": round(t_pre8 + t, 4),
            "distinct_tokens": int(len(set(toks2.tolist()))),
+           "tokens_sha1": hashlib.sha1(toks2.tobytes()).hexdigest()[:16],
            "timing": "host wall clock: the prefill call (hidden rows in and out over PCIe included), "
                      "then the graph-replayed decode steps + the tokens' device-to-host copy"}
     lm.close()

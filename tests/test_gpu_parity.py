@@ -289,6 +289,43 @@ def test_w8a32_prefill_rows_consistent(lin, orc):
     assert rel_l2(full[sub], want) <= 1e-5
 
 
+@pytest.mark.parametrize("mode", ["w8a32", "w8a16_f32"])
+@pytest.mark.parametrize("M,N,K", [(1200, 4096, 2048), (1024, 2048, 6144), (300, 1000, 1000)])
+def test_prefill_gemm_tail_stages_and_determinism(lin, orc, dev, mode, M, N, K):
+    """The last K blocks of the LDS-staged 16-bit GEMM are the ones a
+    miscounted copy wait computes from a stage buffer before its copy lands
+    (the buffer then still holds a K block NST stages earlier).  X is zero
+    except in its last 256 columns, so such a read contributes zeros and
+    misses the bar by orders of magnitude; eight repeated calls on the same
+    device buffers must also agree bit for bit."""
+    import torch
+    say(f"prefill gemm tail stages {mode} M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + N + K)
+    x, w, s = make(rng, M, N, K)
+    x[:, : K - 256] = 0.0
+    if mode == "w8a16_f32":
+        x = bf16_to_f32(bf16_bits(x))           # exact in bf16, so the same oracle applies
+    W = lin.DeviceWeights.from_codes(w, s)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    if mode == "w8a32":
+        xd = torch.from_numpy(x).to(dev)
+        run = lambda: lin.w8a32_linear_dev(xd, W, y)
+    else:
+        xd = torch.from_numpy(x).to(dev).to(torch.bfloat16)
+        run = lambda: lin.w8a16_linear_dev(xd, W, y)
+    run()
+    torch.cuda.synchronize()
+    first = y.cpu().numpy().copy()
+    rows = np.r_[0:4, M // 2: M // 2 + 4, M - 4:M]
+    want = (x[rows].astype(np.float64) @ w.astype(np.float64).T) * s.astype(np.float64)
+    assert rel_l2(first[rows], want) <= 1e-5
+    for _ in range(7):
+        run()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(y.cpu().numpy(), first)
+    W.close()
+
+
 # ---------------------------------------------------------------------------
 # W8A8
 # ---------------------------------------------------------------------------

@@ -140,17 +140,21 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
     }
   }
   const size_t bstride = (size_t)a.NG * 1024;   // bytes between K blocks of the weights
+  // Every call issues exactly PW copies, so the explicit vmcnt waits in `step`
+  // count exactly: stages past the end of K re-read the last K block into a
+  // buffer that no step reads again.  (Skipping those copies would let the
+  // last NST-2 steps' waits return before their own stage had landed.)
   auto issue = [&](int st, uint4* buf) {
-    if (st >= nst) return;
+    const int sc = min(st, nst - 1);
     const uint32_t base = lds_addr(buf);
 #pragma unroll
     for (int p = 0; p < PW; p++) {
       const uint4* g;
       if (qkoff[p] >= 0) {
-        const int k = st * 64 + qkoff[p];
-        g = (qrow_ok[p] && k < a.K) ? reinterpret_cast<const uint4*>(qsrc[p] + (size_t)st * 64 * ESZ) : Z4;
+        const int k = sc * 64 + qkoff[p];
+        g = (qrow_ok[p] && k < a.K) ? reinterpret_cast<const uint4*>(qsrc[p] + (size_t)sc * 64 * ESZ) : Z4;
       } else {
-        g = reinterpret_cast<const uint4*>(qsrc[p] + (size_t)st * bstride);
+        g = reinterpret_cast<const uint4*>(qsrc[p] + (size_t)sc * bstride);
       }
       dma_tile(g, base + qlds[p]);
     }
