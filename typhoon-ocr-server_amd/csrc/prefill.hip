@@ -106,14 +106,13 @@ __global__ __launch_bounds__(256) void prefill_qk_kernel(float* __restrict__ qkv
 
 // Causal flash attention over one q head on fp32 MFMA
 // (v_mfma_f32_16x16x4f32: exact fp32 products, fp32 accumulation).
-// Work-group (qt, qh) takes queries [64 qt, 64 qt + 64) of the S-token chunk
-// (q rows of qkv, already rotated); query i attends keys j <= qoff + i, read
-// from cache rows key0 + j of kv head qh / 2 (qoff = 0, key0 = chunk start:
-// attention within the chunk, as PREFILL_MODE; key0 = 0, qoff = chunk start:
-// the whole cache, as CHUNKED_PREFILL_MODE), in 64-key tiles staged in LDS
-// with an online softmax.
+// Work-group L takes queries [64 qt, 64 qt + 64) of q head qh (longest tiles
+// first over all heads) of the S-token chunk (q rows of qkv, already
+// rotated); query i attends keys j <= qoff + i, read from cache rows key0 + j
+// of kv head qh / 2 (qoff = 0, key0 = chunk start: attention within the
+// chunk, as PREFILL_MODE; key0 = 0, qoff = chunk start: the whole cache, as
+// CHUNKED_PREFILL_MODE), in 64-key tiles with an online softmax.
 constexpr int FT = 64;          // queries / keys per tile
-constexpr int FQS = PHD + 4;    // padded row stride of the K tile
 
 // Wave w holds the 16 queries q0 + 16 w + c in lanes (g, c) = (lane >> 4,
 // lane & 15).
@@ -126,27 +125,45 @@ constexpr int FQS = PHD + 4;    // padded row stride of the K tile
 //            query c for keys 16b + 4r + g, r = 0..3 ...
 //   P.V      ... which is exactly the second operand of the four P.V MFMAs
 //            of that block (MFMA m needs key 16b + 4m + g in lane group g):
-//            no transpose.  V^T is the first operand, read from LDS, and the
-//            output lane (g, c) holds O[query c][16 j + 4g + r], j = 0..7.
+//            no transpose.  V^T is the first operand: accumulator j, operand
+//            row c is dimension 64 (j >> 2) + 4c + (j & 3), so a lane's eight
+//            operands for one key are two float4 of its V row, and the
+//            output lane (g, c) holds O[query c][64 (j >> 2) + 16g + 4r + (j & 3)].
 // The online softmax of query c runs in lanes c, c+16, c+32, c+48.
-constexpr int KVS = PHD + 16;   // row stride of the V tile (conflict-free V^T reads)
+//
+// K and V tiles go global -> LDS directly (global_load_lds_dwordx4: 64 lanes
+// x 16 bytes land contiguously, two 512-byte rows per copy; each lane picks
+// its own source, so layouts are set by source addressing), double-buffered:
+// the copies of tile kt + 1 fly while tile kt is computed, one wait and one
+// barrier per tile.
+//   K tile  row R = 16b + c holds key 16b + 4 (c & 3) + (c >> 2) (the score
+//           permutation), and its float4 slot p holds dimensions
+//           4 (p ^ (R & 15)) .. + 3: the 16 lanes that read one dimension
+//           group from 16 consecutive rows hit 16 different bank groups.
+//   V tile  row = key, plain: the P.V reads take 16 consecutive float4 of
+//           each of 4 rows.
+// (On gfx950, 16 rows read at one column with a 512-byte stride run at 1/4 of
+// the LDS rate; the swizzle and the 4-row pattern run at full rate.)
+// Each 16-key block's K operands, and each 4-key group's V operands, are read
+// into registers one block ahead of their MFMAs.
 
 __global__ __launch_bounds__(256) void flash_prefill_mfma_kernel(const float* __restrict__ qkv,
                                                                  const float* __restrict__ kc,
                                                                  const float* __restrict__ vc, float* __restrict__ out,
-                                                                 int S, int max_seq, int key0, int qoff, float scale) {
-  const int ntq = gridDim.x;
-  const int qt = ntq - 1 - blockIdx.x;      // longest (most keys) first
-  const int qh = blockIdx.y, h = qh >> 1;
+                                                                 int S, int max_seq, int key0, int qoff, float scale,
+                                                                 int nheads) {
+  // longest first over all heads: work-group L takes query tile ntq-1-L/nheads
+  const int ntq = cdiv(S, FT);
+  const int qt = ntq - 1 - (int)blockIdx.x / nheads;
+  const int qh = (int)blockIdx.x % nheads, h = qh >> 1;
   const int q0 = qt * FT;
   const int nq = min(FT, S - q0);
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c = lane & 15;
 
-  __shared__ float4 sK4[FT * FQS / 4];
-  __shared__ float4 sV4[FT * KVS / 4];
-  float* const sK = reinterpret_cast<float*>(sK4);
-  float* const sV = reinterpret_cast<float*>(sV4);
+  // [buffer][K | V][64 rows x 128 floats]
+  __shared__ float4 sKV[2][2][FT * PHD / 4];
 
   // this lane's query and its Q operand (dimensions 16u + 4g .. 16u + 4g + 3)
   const int qloc = 16 * wv + c;                           // 0..63 within the tile
@@ -159,8 +176,8 @@ __global__ __launch_bounds__(256) void flash_prefill_mfma_kernel(const float* __
   }
   const int qpos = qoff + q0 + qloc;                      // key index bound of this query
   const int Sk = qoff + S;
-  const float* kbase = kc + ((size_t)h * max_seq + key0) * PHD;
-  const float* vbase = vc + ((size_t)h * max_seq + key0) * PHD;
+  const float4* kbase = reinterpret_cast<const float4*>(kc + ((size_t)h * max_seq + key0) * PHD);
+  const float4* vbase = reinterpret_cast<const float4*>(vc + ((size_t)h * max_seq + key0) * PHD);
 
   v4f o[8];
 #pragma unroll
@@ -168,46 +185,64 @@ __global__ __launch_bounds__(256) void flash_prefill_mfma_kernel(const float* __
   float m = -3.0e38f, l = 0.0f;
 
   const int nkt = (qoff + q0 + nq - 1) / FT + 1;
-  float4 kreg[8], vreg[8];
-  auto load_tile = [&](int kt) {
+  // copy q (0..7) of this wave: tile rows R = 16 wv + 2q + (lane >> 5), slot
+  // p = lane & 31 (every lane reads a valid row: keys past the end clamp)
+  const int rsub = lane >> 5, p = lane & 31;
+  auto issue_tile = [&](int kt, int buf) {
+    const uint32_t kb = lds_addr(&sKV[buf][0][0]), vb = lds_addr(&sKV[buf][1][0]);
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
-      const int i = tid + 256 * u;
-      const int r = i >> 5, c4 = i & 31;
-      const int key = min(kt * FT + r, Sk - 1);
-      kreg[u] = reinterpret_cast<const float4*>(kbase + (size_t)key * PHD)[c4];
-      vreg[u] = reinterpret_cast<const float4*>(vbase + (size_t)key * PHD)[c4];
+    for (int q = 0; q < 8; q++) {
+      const int R = 16 * wv + 2 * q + rsub;
+      const int kkey = min(kt * FT + (R & ~15) + 4 * (R & 3) + ((R >> 2) & 3), Sk - 1);
+      const int vkey = min(kt * FT + R, Sk - 1);
+      const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(16 * wv + 2 * q) * (PHD * 4));
+      dma_tile(reinterpret_cast<const uint4*>(kbase + (size_t)kkey * (PHD / 4) + (p ^ (R & 15))), kb + dst);
+      dma_tile(reinterpret_cast<const uint4*>(vbase + (size_t)vkey * (PHD / 4) + p), vb + dst);
     }
   };
-  load_tile(0);
+  issue_tile(0, 0);
   for (int kt = 0; kt < nkt; kt++) {
-    __syncthreads();                        // previous tile's LDS reads are done
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-      const int i = tid + 256 * u;
-      const int r = i >> 5, c4 = i & 31;
-      *reinterpret_cast<float4*>(&sK[r * FQS + 4 * c4]) = kreg[u];
-      *reinterpret_cast<float4*>(&sV[r * KVS + 4 * c4]) = vreg[u];
-    }
-    __syncthreads();
-    if (kt + 1 < nkt) load_tile(kt + 1);
+    const int cb = kt & 1;
+    wait_vm<0>();                           // this wave's copies of tile kt landed
+    wait_lgkm0();                           // and its reads of tile kt - 1 are done
+    stage_barrier();                        // every wave's: tile kt visible, buffer of kt - 1 free
+    if (kt + 1 < nkt) issue_tile(kt + 1, cb ^ 1);
+    const float* sK = reinterpret_cast<const float*>(&sKV[cb][0][0]);
+    const float* sV = reinterpret_cast<const float*>(&sKV[cb][1][0]);
 
-    // scores of the tile's four 16-key blocks
+    // scores of the tile's four 16-key blocks (operand row c of block b is
+    // tile row 16b + c; dimension group g + 4u sits in slot (g + 4u) ^ c)
     v4f sc[4];
+    float4 kf[2][8];
+    auto kread = [&](int b, float4 (&dst)[8]) {
+      const float* kp = sK + (16 * b + c) * PHD;
+#pragma unroll
+      for (int u = 0; u < 8; u++) dst[u] = *reinterpret_cast<const float4*>(kp + 4 * ((g + 4 * u) ^ c));
+    };
+    kread(0, kf[0]);
 #pragma unroll
     for (int b = 0; b < 4; b++) {
+      if (b < 3) kread(b + 1, kf[(b + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);   // the next block's reads stay ahead of these MFMAs
       sc[b] = v4f{0.f, 0.f, 0.f, 0.f};
-      const int krow = 16 * b + 4 * (c & 3) + (c >> 2);   // permuted key of operand row c
-      const float* kp = sK + krow * FQS + 4 * g;
 #pragma unroll
       for (int u = 0; u < 8; u++) {
-        const float4 kv = *reinterpret_cast<const float4*>(kp + 16 * u);
+        const float4 kv = kf[b & 1][u];
         sc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qr[u].x, sc[b], 0, 0, 0);
         sc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qr[u].y, sc[b], 0, 0, 0);
         sc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qr[u].z, sc[b], 0, 0, 0);
         sc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qr[u].w, sc[b], 0, 0, 0);
       }
     }
+    // the first V operands are read while the softmax runs
+    float4 vf[2][2];
+    auto vread = [&](int km, float4 (&dst)[2]) {   // keys 4 km + g
+      const float* vp = sV + (4 * km + g) * PHD + 4 * c;
+      dst[0] = *reinterpret_cast<const float4*>(vp);
+      dst[1] = *reinterpret_cast<const float4*>(vp + 64);
+    };
+    vread(0, vf[0]);
+    __builtin_amdgcn_sched_barrier(0);
     // mask, online softmax (query c: lanes c, c+16, c+32, c+48)
     float mx = -3.0e38f;
 #pragma unroll
@@ -239,23 +274,33 @@ __global__ __launch_bounds__(256) void flash_prefill_mfma_kernel(const float* __
     for (int j = 0; j < 8; j++)
 #pragma unroll
       for (int r = 0; r < 4; r++) o[j][r] = __fmul_rn(o[j][r], resc);
-    // O^T[d][query] += V^T[d][key] P^T[key][query]
+    // O^T[d][query] += V^T[d][key] P^T[key][query], keys 4 km + g, km = 4b + mm
 #pragma unroll
-    for (int b = 0; b < 4; b++)
-#pragma unroll
-      for (int mm = 0; mm < 4; mm++) {
-        const float* vp = sV + (16 * b + 4 * mm + g) * KVS + c;
-#pragma unroll
-        for (int j = 0; j < 8; j++) o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vp[16 * j], sc[b][mm], o[j], 0, 0, 0);
-      }
+    for (int km = 0; km < 16; km++) {
+      if (km < 15) vread(km + 1, vf[(km + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      const float pk = sc[km >> 2][km & 3];
+      const float4 v0 = vf[km & 1][0], v1 = vf[km & 1][1];
+      o[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0.x, pk, o[0], 0, 0, 0);
+      o[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0.y, pk, o[1], 0, 0, 0);
+      o[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0.z, pk, o[2], 0, 0, 0);
+      o[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0.w, pk, o[3], 0, 0, 0);
+      o[4] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1.x, pk, o[4], 0, 0, 0);
+      o[5] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1.y, pk, o[5], 0, 0, 0);
+      o[6] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1.z, pk, o[6], 0, 0, 0);
+      o[7] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1.w, pk, o[7], 0, 0, 0);
+    }
   }
   if (qloc < nq) {
     const float inv = __fdiv_rn(1.0f, l);
-    float* op = out + (size_t)(q0 + qloc) * 2048 + qh * PHD + 4 * g;
+    float* op = out + (size_t)(q0 + qloc) * 2048 + qh * PHD + 16 * g;
 #pragma unroll
-    for (int j = 0; j < 8; j++)
-      *reinterpret_cast<float4*>(op + 16 * j) = make_float4(__fmul_rn(o[j][0], inv), __fmul_rn(o[j][1], inv),
-                                                            __fmul_rn(o[j][2], inv), __fmul_rn(o[j][3], inv));
+    for (int jh = 0; jh < 2; jh++)
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        *reinterpret_cast<float4*>(op + 64 * jh + 4 * r) =
+            make_float4(__fmul_rn(o[4 * jh][r], inv), __fmul_rn(o[4 * jh + 1][r], inv),
+                        __fmul_rn(o[4 * jh + 2][r], inv), __fmul_rn(o[4 * jh + 3][r], inv));
   }
 }
 
@@ -300,8 +345,8 @@ hipError_t launch_prefill_qk(float* qkv, const float* q_norm, const float* k_nor
 hipError_t launch_flash_prefill(const float* qkv, const float* kc, const float* vc, float* out, int S, int nq,
                                 int max_seq, int key0, int qoff, float scale, hipStream_t st) {
   if (S < 1 || key0 < 0 || qoff < 0 || key0 + qoff + S > max_seq) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(flash_prefill_mfma_kernel, dim3(cdiv(S, FT), nq), dim3(256), 0, st, qkv, kc, vc, out, S,
-                     max_seq, key0, qoff, scale);
+  hipLaunchKernelGGL(flash_prefill_mfma_kernel, dim3(cdiv(S, FT) * nq), dim3(256), 0, st, qkv, kc, vc, out, S,
+                     max_seq, key0, qoff, scale, nq);
   return hipGetLastError();
 }
 
