@@ -130,6 +130,7 @@ struct Workspace {
   DevBuf act_s;       // activation scales
   DevBuf xn;          // normalised hidden row (lm_head argmax)
   DevBuf keys;        // per-work-group argmax keys
+  DevBuf planes;      // fp32 activations split into three bf16 planes
 };
 
 std::mutex g_ws_mu;
@@ -395,6 +396,18 @@ void op_w8a32(const float* X, const tl_weights* W, const float* bias, float* Y, 
     L.K = W->cols;
     L.ep = EP_SCALE;
     L.out = OUT_F32;
+    const int K = W->cols;
+    if (batch > 64 && K % 8 == 0) {
+      // batches for the LDS-tiled kernel: split X into its three bf16 terms
+      // once (bit-identical products and order to the in-kernel split)
+      const size_t plane = (size_t)batch * K;
+      ws.planes.ensure(3 * plane * sizeof(uint16_t), st);
+      uint16_t* pl = static_cast<uint16_t*>(ws.planes.p);
+      HIP_OK(launch_split_bf16x3(X, K, batch, K, K, pl, st));
+      L.amode = A_BF16X3;
+      L.A = pl;
+      L.a_plane = (long long)plane;
+    }
     run_gemm(ws, L, st);
   }
 }

@@ -7,6 +7,12 @@
 //           exactly into three bf16 terms (x0 = bf16(x), x1 = bf16(x - x0),
 //           x2 = bf16(x - x0 - x1)); three bf16 MFMAs per fragment give the
 //           fp32 product sum with exact products.
+//   A_BF16X3 the same product with the split done once beforehand
+//           (split_bf16x3_kernel writes the three terms as bf16 planes): the
+//           GEMM copies the planes and runs the same three MFMAs in the same
+//           order, so its output is bit-identical to A_F32X3, without the
+//           per-wave split (the split made A_F32X3 VALU-bound: ~15 VALU
+//           instructions per MFMA).
 //
 // Same skeleton as gemm_i8.hip: a ring of NST LDS stage buffers filled by
 // direct global -> LDS copies (one 16-byte piece per lane per copy), one
@@ -19,9 +25,12 @@
 // k = 16 (l >> 4) + 8 h + 0..7.  Each A copy therefore reads, for lane l,
 //   16-bit X: 8 elements X[row][64 kb + 16 (l >> 4) + 8 h ..]      (2 copies)
 //   fp32  X : 4 elements X[row][64 kb + 16 (l >> 4) + 4 j ..]      (4 copies)
+//   planes  : 8 elements of plane t, t = 0..2, as 16-bit X           (6 copies)
 // and a wave reads its operand with one ds_read_b128 per copy.  Weight tiles
 // stay int8 in LDS and are widened to bf16/fp16 in registers after the read.
 // Lanes whose row is past M or whose k is past K copy 16 bytes of zeros.
+#include <algorithm>
+
 #include "tl_common.h"
 #include "tl_kernels.h"
 
@@ -32,6 +41,7 @@ namespace tl {
 struct GemmB16Args {
   const void* X;         // row-major [M][lda], element type per AMODE
   int lda;
+  long long a_plane;     // A_BF16X3: elements between the three planes
   const uint8_t* Bt;     // weight tiles [KB][NG]
   const float* ws;       // [N]
   const float* bias;     // [N] or null
@@ -79,7 +89,7 @@ __device__ inline v4f mfma16(uint4 w, uint4 x, v4f c) {
 template <int AMODE, int MT, int NT, int NST, int WM, int WN>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args a) {
   constexpr int NW = WM * WN;
-  constexpr int AP = (AMODE == A_F32X3) ? 4 : 2;       // A copies per (row group, K block)
+  constexpr int AP = (AMODE == A_F32X3) ? 4 : (AMODE == A_BF16X3 ? 6 : 2);   // A copies per (row group, K block)
   constexpr int ESZ = (AMODE == A_F32X3) ? 4 : 2;      // bytes per X element
   constexpr int EPC = 16 / ESZ;                        // X elements per copy per lane
   constexpr int TA = MT * AP, TB = NT, TS = TA + TB;
@@ -128,10 +138,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
     if (q < TA) {
       const int i = q / AP, j = q % AP;
       const int row = (mg0 + i) * 16 + (lane & 15);
-      const int koff = 16 * (lane >> 4) + EPC * j;
+      // planes: copy j = 2 t + h is half h of plane t
+      const int koff = 16 * (lane >> 4) + EPC * (AMODE == A_BF16X3 ? (j & 1) : j);
+      const size_t plane = (AMODE == A_BF16X3) ? (size_t)(j >> 1) * a.a_plane : 0;
       qrow_ok[p] = row < a.M;
       qkoff[p] = koff;
-      qsrc[p] = Xb + ((size_t)min(row, a.M - 1) * a.lda + koff) * ESZ;
+      qsrc[p] = Xb + (plane + (size_t)min(row, a.M - 1) * a.lda + koff) * ESZ;
     } else {
       const int ng = min(ng0 + (q - TA), a.NG - 1);
       qrow_ok[p] = true;
@@ -195,6 +207,19 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
                               __uint_as_float(u1.x), __uint_as_float(u1.y), __uint_as_float(u1.z), __uint_as_float(u1.w)};
           uint4 t0, t1, t2;
           split3x8(x, t0, t1, t2);
+#pragma unroll
+          for (int j = 0; j < FN; j++) {
+            acc[i][j] = mfma16<A_BF16>(wb[j][h], t2, acc[i][j]);
+            acc[i][j] = mfma16<A_BF16>(wb[j][h], t1, acc[i][j]);
+            acc[i][j] = mfma16<A_BF16>(wb[j][h], t0, acc[i][j]);
+          }
+        }
+      } else if constexpr (AMODE == A_BF16X3) {
+        // same MFMAs in the same order as A_F32X3 (t2, t1, t0 per half)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const uint4 t0 = buf[(ab + h) * 64 + lane], t1 = buf[(ab + 2 + h) * 64 + lane],
+                      t2 = buf[(ab + 4 + h) * 64 + lane];
 #pragma unroll
           for (int j = 0; j < FN; j++) {
             acc[i][j] = mfma16<A_BF16>(wb[j][h], t2, acc[i][j]);
@@ -276,6 +301,45 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
 }
 
 // ---------------------------------------------------------------------------
+// one pass over fp32 X: thread t splits 8 consecutive elements of a row into
+// the three bf16 terms (split3x8, the split A_F32X3 does per wave) and writes
+// 16 bytes to each plane; elements past K are zero
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void split_bf16x3_kernel(const float* __restrict__ X, int ldx, int M, int K,
+                                                          int kp, uint4* __restrict__ planes) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  const int k8n = kp / 8;
+  const long long total = (long long)M * k8n;
+  if (t >= total) return;
+  const int row = (int)(t / k8n), k0 = (int)(t - (long long)row * k8n) * 8;
+  const float* src = X + (size_t)row * ldx + k0;
+  float x[8];
+  if (k0 + 8 <= K && ((((uintptr_t)src) & 15) == 0)) {
+    const float4 a = reinterpret_cast<const float4*>(src)[0], b = reinterpret_cast<const float4*>(src)[1];
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; e++) x[e] = (k0 + e < K) ? src[e] : 0.0f;
+  }
+  uint4 t0, t1, t2;
+  split3x8(x, t0, t1, t2);
+  const long long plane = total;             // uint4 per plane
+  planes[t] = t0;
+  planes[plane + t] = t1;
+  planes[2 * plane + t] = t2;
+}
+
+hipError_t launch_split_bf16x3(const float* X, int ldx, int M, int K, int kp, uint16_t* planes,
+                               hipStream_t st) {
+  if (M < 1 || K < 1 || kp < K || kp % 8 != 0 || ldx < K || (((uintptr_t)planes) & 15) != 0)
+    return hipErrorInvalidValue;
+  const long long total = (long long)M * (kp / 8);
+  hipLaunchKernelGGL(split_bf16x3_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, X, ldx, M, K,
+                     kp, reinterpret_cast<uint4*>(planes));
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // planning and launch
 // ---------------------------------------------------------------------------
 // 16-bit X:  cfg 0  128 x 192 tiles, 4-deep ring (112 KiB)
@@ -290,7 +354,7 @@ static void b16_cfg(int amode, int cfg, int& mt, int& nt) {
   if (cfg == 2) {
     mt = 2;
     nt = 4;
-  } else if (amode == A_F32X3) {
+  } else if (amode == A_F32X3 || amode == A_BF16X3) {
     mt = 4;
     nt = (cfg == 0) ? 8 : 4;
   } else {
@@ -299,8 +363,57 @@ static void b16_cfg(int amode, int cfg, int& mt, int& nt) {
   }
 }
 
+// 16-bit X: the configuration whose tile count best fills 256 CUs (measured
+// best over the W8A16 sweep).  Three-term X (six MFMAs per fragment pair):
+// the configuration with the least modelled time, rounds of 256 work-groups
+// x K steps x the slowest per-step resource of a work-group's four waves,
+//   MFMA  16 cycles per 16x16x32 MFMA (per wave, one wave per SIMD),
+//   VALU  4 cycles per wave64 instruction: ~40 to widen an int8 weight
+//         fragment, ~160 to split an fp32 row group into three bf16 terms,
+//   LDS   ~107 bytes per cycle per CU of fragment reads (1 KiB per copy),
+// (rates measured on the MI355X): there the large tiles win unless they
+// would leave most CUs idle (W8A32 1200-token prefill: 30.5 -> 26.2 ms).
+static int b16_pick_cfg(int amode, int MG, int NG) {
+  const bool x3 = (amode == A_F32X3 || amode == A_BF16X3);
+  if (!x3) {
+    int best = 0;
+    double best_eff = -1.0;
+    for (int cfg : {0, 1, 2}) {
+      int mt, nt;
+      b16_cfg(amode, cfg, mt, nt);
+      const int tiles = cdiv(MG, mt) * cdiv(NG, nt);
+      const double eff = (double)tiles / (cdiv(tiles, 256) * 256);
+      if (eff > best_eff + 1e-9) {
+        best_eff = eff;
+        best = cfg;
+      }
+    }
+    return best;
+  }
+  const int ap = (amode == A_F32X3) ? 4 : (amode == A_BF16X3 ? 6 : 2);
+  int best = 0;
+  double best_t = 1e300;
+  for (int cfg : {0, 1, 2}) {
+    int mt, nt;
+    b16_cfg(amode, cfg, mt, nt);
+    const int fm = mt / 2, fn = nt / 2;   // 2 x 2 waves
+    const double mfma = fm * fn * (x3 ? 6 : 2) * 16.0;
+    const double valu = (fn * 40.0 + (amode == A_F32X3 ? fm * 160.0 : 0.0)) * 4.0;
+    const double lds = 4.0 * (fm * ap + fn) * 1024.0 / 107.0;
+    const double step = std::max(mfma, std::max(valu, lds));
+    const long long tiles = (long long)cdiv(MG, mt) * cdiv(NG, nt);
+    const double t = (double)((tiles + 255) / 256) * step;
+    if (t < best_t * (1.0 - 1e-9)) {
+      best_t = t;
+      best = cfg;
+    }
+  }
+  return best;
+}
+
 bool gemm_b16_supported(const GemmLaunch& L) {
-  if (L.amode != A_BF16 && L.amode != A_F16 && L.amode != A_F32X3) return false;
+  if (L.amode != A_BF16 && L.amode != A_F16 && L.amode != A_F32X3 && L.amode != A_BF16X3) return false;
+  if (L.amode == A_BF16X3 && L.a_plane < (long long)L.M * L.lda) return false;
   const int align = (L.amode == A_F32X3) ? 4 : 8;   // elements per 16-byte copy
   if (L.K % align != 0 || L.lda % align != 0) return false;
   if ((((uintptr_t)L.A) & 15) != 0) return false;
@@ -312,6 +425,7 @@ hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st) {
   GemmB16Args a;
   a.X = L.A;
   a.lda = L.lda;
+  a.a_plane = L.a_plane;
   a.Bt = L.Bt;
   a.ws = L.ws;
   a.bias = L.bias;
@@ -326,19 +440,7 @@ hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st) {
   a.ep = L.ep;
   a.out = L.out;
   a.zero_tile = L.zero_tile;
-  // the configuration whose tile count best fills 256 CUs
-  int best = 0;
-  double best_eff = -1.0;
-  for (int cfg : {0, 1, 2}) {
-    int mt, nt;
-    b16_cfg(L.amode, cfg, mt, nt);
-    const int tiles = cdiv(a.MG, mt) * cdiv(a.NG, nt);
-    const double eff = (double)tiles / (cdiv(tiles, 256) * 256);
-    if (eff > best_eff + 1e-9) {
-      best_eff = eff;
-      best = cfg;
-    }
-  }
+  const int best = b16_pick_cfg(L.amode, a.MG, a.NG);
   int mt, nt;
   b16_cfg(L.amode, best, mt, nt);
   a.ntm = cdiv(a.MG, mt);
@@ -354,6 +456,11 @@ hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st) {
       if (best == 0) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F16, 8, 12, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
       else if (best == 1) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F16, 4, 8, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
       else hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F16, 2, 4, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
+      break;
+    case A_BF16X3:
+      if (best == 0) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_BF16X3, 4, 8, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
+      else if (best == 1) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_BF16X3, 4, 4, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
+      else hipLaunchKernelGGL((gemm_b16_lds_kernel<A_BF16X3, 2, 4, 6, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
       break;
     default:
       if (best == 0) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F32X3, 4, 8, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a);

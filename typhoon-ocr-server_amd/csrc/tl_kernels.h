@@ -20,7 +20,8 @@ enum { EPI_W8A32 = 0, EPI_W8A8 = 1, EPI_ACC = 2, EPI_ARGMAX = 3, EPI_SWIGLU = 4 
 // decoder's RMSNorm (kernel/ops.c:22-56, estimate-based rsqrt)
 enum { NORM_NONE = 0, NORM_NUMPY = 1, NORM_DECODER = 2 };
 // GEMM A-operand modes and output types (gemm.hip)
-enum { A_I8 = 0, A_BF16 = 1, A_F16 = 2, A_F32X3 = 3 };
+enum { A_I8 = 0, A_BF16 = 1, A_F16 = 2, A_F32X3 = 3,
+       A_BF16X3 = 4 };   // fp32 X already split into three bf16 planes (split_bf16x3)
 enum { OUT_F32 = 0, OUT_BF16 = 1, OUT_F16 = 2, OUT_I32 = 3 };
 // GEMM float epilogues: fl(acc*ws) then + bias, or fma(acc, ws, bias|0)
 enum { EP_SCALE = 0, EP_SCALE_FMA = 1 };
@@ -126,6 +127,7 @@ struct GemmLaunch {
   uint32_t* cnt = nullptr;        // gemm_counter_count zeroed counters
   int force_split = 0;
   const uint8_t* zero_tile = nullptr;   // 1 KiB of device zeros (LDS-staged int8 GEMM)
+  long long a_plane = 0;          // A_BF16X3: elements between the three planes of A
 };
 GemmPlan gemm_plan(int amode, int M, int N, int K);
 size_t gemm_workspace_bytes(int amode, int M, int N, int K);
@@ -140,6 +142,10 @@ void gemm_i8_set_cfg(int cfg);   // tuning override (-1 = planner)
 // ---- LDS-staged 16-bit MFMA GEMM (gemm_b16.hip): A_BF16 / A_F16 / A_F32X3,
 //      used for M > 16 when X rows are 16-byte aligned pieces --------------
 bool gemm_b16_supported(const GemmLaunch& L);
+// fp32 X [M][ldx] -> three bf16 planes [3][M][kp] (row stride kp, a multiple of
+// 8 >= K, zero past K): t0 = bf16(x), t1 = bf16(x - t0), t2 = bf16(x - t0 - t1)
+hipError_t launch_split_bf16x3(const float* X, int ldx, int M, int K, int kp, uint16_t* planes,
+                               hipStream_t st);
 // ---- M <= 16 rows (gemm_small.hip): GEMV-shaped MFMA kernel ---------------
 bool gemm_small_supported(const GemmLaunch& L);
 hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st);
