@@ -70,9 +70,10 @@ __device__ inline void widen(uint4 w, uint4& h0, uint4& h1) {
       o[2 * q] = (uint32_t)__builtin_bit_cast(uint16_t, h0f) | ((uint32_t)__builtin_bit_cast(uint16_t, h1f) << 16);
       o[2 * q + 1] = (uint32_t)__builtin_bit_cast(uint16_t, h2f) | ((uint32_t)__builtin_bit_cast(uint16_t, h3f) << 16);
     } else {
-      // |w| <= 127 is exact in bf16: the high halves of the floats
-      o[2 * q] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
-      o[2 * q + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
+      // |w| <= 127 is exact in bf16: the high halves of the floats, paired by
+      // one byte permute (bytes 2, 3 of f0 then bytes 2, 3 of f1)
+      o[2 * q] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+      o[2 * q + 1] = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
     }
   }
   h0 = make_uint4(o[0], o[1], o[2], o[3]);
@@ -97,8 +98,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
   constexpr int PW = TS / NW;
   constexpr int FM = MT / WM, FN = NT / WN;
   static_assert(MT % WM == 0 && NT % WN == 0, "wave grid must divide the tile");
-  static_assert(NST >= 2 && NST <= 8, "2..8 stage buffers");
-  static_assert(PW * (NST - 2) < 64, "vmcnt range");
+  static_assert(NST >= 2 && NST <= 8 && NST % 2 == 0, "2, 4, 6 or 8 stage buffers");
+  static_assert(PW * (NST - 1) < 64, "vmcnt range");
 
   __shared__ uint4 s0[TS * 64];
   __shared__ uint4 s1[TS * 64];
@@ -156,9 +157,24 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
   // count exactly: stages past the end of K re-read the last K block into a
   // buffer that no step reads again.  (Skipping those copies would let the
   // last NST-2 steps' waits return before their own stage had landed.)
+  // K a multiple of 64 (no piece past K): each copy is a per-lane byte offset
+  // from a uniform per-stage base (rows past M read row M - 1; their outputs
+  // are never stored)
+  const bool kfull = (a.K % 64) == 0;
+  uint32_t qvo[PW];
+#pragma unroll
+  for (int p = 0; p < PW; p++)
+    qvo[p] = (uint32_t)(qsrc[p] - (qkoff[p] >= 0 ? Xb : reinterpret_cast<const char*>(a.Bt)));
   auto issue = [&](int st, uint4* buf) {
     const int sc = min(st, nst - 1);
     const uint32_t base = lds_addr(buf);
+    if (kfull) {
+      const char* sa = Xb + (size_t)sc * 64 * ESZ;
+      const char* sb = reinterpret_cast<const char*>(a.Bt) + (size_t)sc * bstride;
+#pragma unroll
+      for (int p = 0; p < PW; p++) dma_tile_s(qvo[p], (wv + NW * p < TA) ? sa : sb, base + qlds[p]);
+      return;
+    }
 #pragma unroll
     for (int p = 0; p < PW; p++) {
       const uint4* g;
@@ -192,17 +208,31 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
 #pragma unroll
     for (int j = 0; j < FN; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](const uint4* buf) {
+  // A stage's fragments are read from LDS into a register set one step ahead
+  // of their MFMAs (two sets, so the read latency hides behind the previous
+  // stage's MFMAs): set c holds the stage's A copies of this wave's row
+  // groups and its raw int8 weight tiles.
+  uint4 fa[2][FM * AP], fb[2][FN];
+  auto read_frags = [&](const uint4* buf, int c) {
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < AP; j++) fa[c][i * AP + j] = buf[((wm * FM + i) * AP + j) * 64 + lane];
+#pragma unroll
+    for (int j = 0; j < FN; j++) fb[c][j] = buf[(TA + wn * FN + j) * 64 + lane];
+  };
+
+  auto compute = [&](int c) {
     uint4 wb[FN][2];
 #pragma unroll
-    for (int j = 0; j < FN; j++) widen<AMODE>(buf[(TA + wn * FN + j) * 64 + lane], wb[j][0], wb[j][1]);
+    for (int j = 0; j < FN; j++) widen<AMODE>(fb[c][j], wb[j][0], wb[j][1]);
 #pragma unroll
     for (int i = 0; i < FM; i++) {
-      const int ab = (wm * FM + i) * AP;
+      const uint4* f = &fa[c][i * AP];
       if constexpr (AMODE == A_F32X3) {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-          const uint4 u0 = buf[(ab + 2 * h) * 64 + lane], u1 = buf[(ab + 2 * h + 1) * 64 + lane];
+          const uint4 u0 = f[2 * h], u1 = f[2 * h + 1];
           const float x[8] = {__uint_as_float(u0.x), __uint_as_float(u0.y), __uint_as_float(u0.z), __uint_as_float(u0.w),
                               __uint_as_float(u1.x), __uint_as_float(u1.y), __uint_as_float(u1.z), __uint_as_float(u1.w)};
           uint4 t0, t1, t2;
@@ -218,8 +248,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
         // same MFMAs in the same order as A_F32X3 (t2, t1, t0 per half)
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-          const uint4 t0 = buf[(ab + h) * 64 + lane], t1 = buf[(ab + 2 + h) * 64 + lane],
-                      t2 = buf[(ab + 4 + h) * 64 + lane];
+          const uint4 t0 = f[h], t1 = f[2 + h], t2 = f[4 + h];
 #pragma unroll
           for (int j = 0; j < FN; j++) {
             acc[i][j] = mfma16<A_BF16>(wb[j][h], t2, acc[i][j]);
@@ -228,29 +257,44 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
           }
         }
       } else {
-        const uint4 x0 = buf[ab * 64 + lane], x1 = buf[(ab + 1) * 64 + lane];
 #pragma unroll
         for (int j = 0; j < FN; j++) {
-          acc[i][j] = mfma16<AMODE>(wb[j][0], x0, acc[i][j]);
-          acc[i][j] = mfma16<AMODE>(wb[j][1], x1, acc[i][j]);
+          acc[i][j] = mfma16<AMODE>(wb[j][0], f[0], acc[i][j]);
+          acc[i][j] = mfma16<AMODE>(wb[j][1], f[1], acc[i][j]);
         }
       }
     }
   };
 
-  auto step = [&](int st, const uint4* cur, uint4* nxt) {
+  // Step s (register set c = s & 1 holds stage s):
+  //   wait until this wave's copies of stage s+1 landed (later stages may
+  //   still fly) and its reads of stage s completed; barrier: stage s+1 is
+  //   visible and every wave is done reading stage s's buffer;
+  //   read stage s+1's fragments, refill stage s's buffer with stage s+NST,
+  //   then widen and multiply stage s from registers (steps past the last
+  //   stage only keep the copy count exact).
+  auto step = [&](int st, uint4* cur, const uint4* nxt, int c) {
     wait_vm<PW * (NST - 2)>();
     wait_lgkm0();
     stage_barrier();
-    issue(st + NST - 1, nxt);
-    if (st < nst) compute(cur);
+    read_frags(nxt, c ^ 1);
+    issue(st + NST, cur);
+    __builtin_amdgcn_sched_barrier(0);
+    if (st < nst) compute(c);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
+  // prologue: stages 0 .. NST-1 in flight, stage 0's fragments read
 #pragma unroll
-  for (int b = 0; b < NST - 1; b++) issue(b, ring[b]);
+  for (int b = 0; b < NST; b++) issue(b, ring[b]);
+  wait_vm<PW * (NST - 1)>();
+  stage_barrier();
+  read_frags(ring[0], 0);
+  // ring unrolled NST times (NST even: every step's register set is a
+  // compile-time constant)
   for (int st = 0; st < nst; st += NST) {
 #pragma unroll
-    for (int b = 0; b < NST; b++) step(st + b, ring[b], ring[(b + NST - 1) % NST]);
+    for (int b = 0; b < NST; b++) step(st + b, ring[b], ring[(b + 1) % NST], b & 1);
   }
   wait_vm<0>();   // no copy may still be landing in LDS when the work-group exits
 

@@ -352,6 +352,15 @@ __device__ __forceinline__ void dma_tile(const uint4* gsrc, uint32_t lds_base) {
                : "s"(lds_base), "v"(gsrc)
                : "memory");
 }
+// the same copy with the source split into a uniform 64-bit base (SGPRs) and a
+// per-lane 32-bit byte offset, so a stage's source needs no per-lane address
+// arithmetic
+__device__ __forceinline__ void dma_tile_s(uint32_t voff, const void* sbase, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds_base), "v"(voff), "s"(sbase)
+               : "memory");
+}
 __device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
