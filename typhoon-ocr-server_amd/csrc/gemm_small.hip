@@ -53,15 +53,22 @@ __device__ inline AFrag<AMODE> load_a(const GemmSmallArgs& a, int kb, int tg, in
     constexpr int ESZ = (AMODE == A_F32X3) ? 4 : 2;
     constexpr int NV = (AMODE == A_F32X3) ? 4 : 2;
     constexpr int EPV = 16 / ESZ;                     // elements per uint4
-    const int row = min(tg * 16 + (lane & 15), a.M - 1);
+    // only lanes of real rows load (the rest hold zeros, whose output rows are
+    // never stored): at M = 2 this cuts the activation requests, which share
+    // the CU's load path with the weight stream, eightfold
+    const int row = tg * 16 + (lane & 15);
     const int k0 = kb * 64 + 16 * (lane >> 4);
-    const char* base = static_cast<const char*>(a.A) + (size_t)row * a.lda * ESZ;
+    const char* base = static_cast<const char*>(a.A) + (size_t)min(row, a.M - 1) * a.lda * ESZ;
 #pragma unroll
-    for (int v = 0; v < NV; v++) {
-      const int k = k0 + EPV * v;
-      const int kc = min(k, a.K - EPV);               // in-bounds address
-      uint4 u = *reinterpret_cast<const uint4*>(base + (size_t)kc * ESZ);
-      f.v[v] = (k < a.K) ? u : make_uint4(0, 0, 0, 0);
+    for (int v = 0; v < NV; v++) f.v[v] = make_uint4(0, 0, 0, 0);
+    if (row < a.M) {
+#pragma unroll
+      for (int v = 0; v < NV; v++) {
+        const int k = k0 + EPV * v;
+        const int kc = min(k, a.K - EPV);             // in-bounds address
+        const uint4 u = *reinterpret_cast<const uint4*>(base + (size_t)kc * ESZ);
+        if (k < a.K) f.v[v] = u;
+      }
     }
   }
   return f;

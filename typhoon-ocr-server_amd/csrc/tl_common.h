@@ -252,10 +252,11 @@ __device__ inline uint2 i8x4_to_bf16x4(uint32_t w) {
   float f1 = (float)(int8_t)((w >> 8) & 0xff);
   float f2 = (float)(int8_t)((w >> 16) & 0xff);
   float f3 = (float)(int8_t)(w >> 24);
-  // integers |v| <= 128 are exact in bf16: the high halves of the floats
+  // integers |v| <= 128 are exact in bf16: the high halves of the floats,
+  // paired by one byte permute (bytes 2, 3 of the first, then of the second)
   uint2 r;
-  r.x = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
-  r.y = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
+  r.x = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+  r.y = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
   return r;
 }
 
