@@ -490,6 +490,10 @@ def main():
                     help="decode set only (no prefill, sweeps or CPU baseline)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the W8A8 prefill timing (for counter runs)")
+    ap.add_argument("--decoder-layers", type=int, default=28,
+                    help="layers of the full-decoder workload (fewer only to profile it)")
+    ap.add_argument("--decoder-steps", type=int, default=512,
+                    help="greedy steps of the full-decoder workload (fewer only to profile it)")
     ap.add_argument("--decoder-only", action="store_true",
                     help="only the device-resident 28-layer greedy decoder timing")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -515,7 +519,8 @@ def main():
         print(json.dumps({"w8a8_prefill": bench_w8a8_prefill(lin, torch, dev)}), flush=True)
         return
     if args.decoder_only:
-        print(json.dumps({"decoder_greedy": bench_decoder_generate(lin, torch, dev)}), flush=True)
+        print(json.dumps({"decoder_greedy": bench_decoder_generate(lin, torch, dev, n_layers=args.decoder_layers,
+                                                                   steps=args.decoder_steps)}), flush=True)
         return
     log("building the decode set (1.72 GB of int8 weights)")
     items = build_decode_set(lin, torch, dev)
