@@ -252,16 +252,17 @@ def bench_decoder_generate(lin, torch, dev, n_layers=28, vocab=151936, prefix=12
             lin.check(lib, "tl_decoder_generate")
         return toks
 
-    # warm-up: a short prefill and a few steps (graph capture, work-space growth)
+    # warm-up: a full-size prefill in each mode (work-space growth: activation
+    # buffers, pinned row staging) and a few steps (graph capture)
     ids = rng.integers(0, vocab, prefix)
     hidden0 = embed[torch.from_numpy(ids).to(dev)].cpu().numpy()
     lib.decoder_cache_clear(cache)
-    hw = np.ascontiguousarray(hidden0[:64])
     for w8 in (1, 0):
+        hw = np.array(hidden0, copy=True)
         lib.tl_decoder_set_prefill_w8a8(model, w8)
         lib.decoder_cache_clear(cache)
         lib.decoder_prefill_step(model, cache, hw.ctypes.data_as(f32p), scratch, cos.ctypes.data_as(f32p),
-                                 sin.ctypes.data_as(f32p), 64)
+                                 sin.ctypes.data_as(f32p), prefix)
         lin.check(lib, "decoder_prefill_step")
     generate(1, 4)
     # the workload: prefill `prefix` tokens, greedy token from the last row, `steps` decode steps.
