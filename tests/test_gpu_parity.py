@@ -277,6 +277,44 @@ def test_small_m_wide_n(lin, orc, M, N, K):
     assert rel_l2(lin.w8a8_linear(xq, xs, w, s), orc.w8a8_linear(xq, xs, w, s)) <= 1e-5
 
 
+@pytest.mark.parametrize("M,N,K", [(20, 256, 2048), (3, 32800, 2048), (24, 300, 130)])
+def test_w8a32_planes_special_rows(lin, orc, M, N, K):
+    """Batches that run on the int8 MFMA over four int8 planes per fp32 token
+    (more than 16 tokens, or an lm_head-wide N): rows of zeros, of 1e-36 and
+    of 1e35 magnitude (power-of-two plane scales far from 1; the outputs stay
+    normal floats, so the oracle's own rounding is fp32's), a row with one outlier
+    1000x its rms are each within relative L2 1e-5 of the oracle's fp32
+    GEMM (the planes hold x to about 2^-32 of the row's absmax, with an exact
+    power-of-two scale); a row holding NaN gives NaN in every output, a row
+    holding Inf gives no finite output (the reference's sums give NaN or
+    +-Inf there; here every such output is NaN)."""
+    say(f"w8a32 planes special rows M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 3 + N + K)
+    x, w, s = make(rng, M, N, K)
+    x[0] = 0.0
+    x[1] *= F(1e-36)
+    x[2 % M] *= F(1e35)
+    if M > 3:
+        x[3, 17] = F(1000.0) * np.sqrt(np.mean(x[3] ** 2))
+    nan_row, inf_row = M - 1, M - 2
+    x[nan_row, 5] = np.nan
+    x[inf_row, 9] = np.inf
+    b = rng.standard_normal(N).astype(F)
+    got = lin.w8a32_linear(x, w, s, bias=b)
+    want = orc.w8a32_linear(x, w, s, bias=b)
+    for r in range(M):
+        if r == nan_row:
+            assert np.isnan(got[r]).all()
+        elif r == inf_row:
+            assert not np.isfinite(want[r]).any() and np.isnan(got[r]).all()
+        elif r == 0:
+            np.testing.assert_array_equal(got[r], b)
+        else:
+            assert rel_l2(got[r], want[r]) <= 1e-5, (r, rel_l2(got[r], want[r]))
+    # and the same call twice gives the same bits
+    np.testing.assert_array_equal(lin.w8a32_linear(x, w, s, bias=b), got)
+
+
 def test_w8a32_prefill_rows_consistent(lin, orc):
     """1200-token prefill (fused QKV shape): rows are independent, so a
     subset computed alone matches the corresponding rows of the full call."""

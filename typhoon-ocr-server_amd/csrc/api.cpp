@@ -381,7 +381,10 @@ void op_w8a32(const float* X, const tl_weights* W, const float* bias, float* Y, 
       L.xs_in = xs;
     }
     run_gemv(ws, L, st);
-  } else {
+  } else if (batch <= 16 && W->NG < 2048) {
+    // a few token rows over a narrow weight: the small-M kernel splits the
+    // fp32 rows into three bf16 terms as it loads them (one launch; a
+    // separate plane split costs more than it saves at these sizes)
     GemmLaunch L;
     L.amode = A_F32X3;
     L.A = X;
@@ -396,18 +399,33 @@ void op_w8a32(const float* X, const tl_weights* W, const float* bias, float* Y, 
     L.K = W->cols;
     L.ep = EP_SCALE;
     L.out = OUT_F32;
-    const int K = W->cols;
-    if (batch > 64 && K % 8 == 0) {
-      // batches for the LDS-tiled kernel: split X into its three bf16 terms
-      // once (bit-identical products and order to the in-kernel split)
-      const size_t plane = (size_t)batch * K;
-      ws.planes.ensure(3 * plane * sizeof(uint16_t), st);
-      uint16_t* pl = static_cast<uint16_t*>(ws.planes.p);
-      HIP_OK(launch_split_bf16x3(X, K, batch, K, K, pl, st));
-      L.amode = A_BF16X3;
-      L.A = pl;
-      L.a_plane = (long long)plane;
-    }
+    run_gemm(ws, L, st);
+  } else {
+    // fp32 rows as four int8 planes each (x = 2^e (q0 + q1/254 + q2/254^2 +
+    // q3/254^3), about 2^-32 of the row's absmax), then one int8 MFMA GEMM
+    // over the 4 batch code rows whose epilogue folds each token's planes
+    // (no int8 -> 16-bit widening of the weights, the VALU bound of the
+    // three-term bf16 path)
+    const int K = W->cols, M4 = 4 * batch;
+    const size_t tb = (size_t)cdiv(M4, 16) * W->KB * 1024;
+    const size_t xe_off = (tb + 255) & ~(size_t)255;
+    ws.planes.ensure(xe_off + (size_t)batch * sizeof(int), st);
+    uint8_t* tiles = static_cast<uint8_t*>(ws.planes.p);
+    int* xe = reinterpret_cast<int*>(tiles + xe_off);
+    HIP_OK(launch_split_i8x4(X, K, batch, K, tiles, xe, st));
+    GemmLaunch L;
+    L.amode = A_I8;
+    L.A = tiles;
+    L.Bt = W->tiles;
+    L.ws = W->scales;
+    L.xe = xe;
+    L.bias = bias;
+    L.Y = Y;
+    L.ldy = W->rows;
+    L.M = M4;
+    L.N = W->rows;
+    L.K = K;
+    L.out = OUT_F32_X4;
     run_gemm(ws, L, st);
   }
 }

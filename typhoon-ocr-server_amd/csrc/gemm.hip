@@ -411,7 +411,8 @@ hipError_t launch_gemm(const GemmLaunch& L, hipStream_t st) {
   a.part = L.part;
   a.cnt = L.cnt;
   if (p.split > 1 && (!L.part || !L.cnt)) return hipErrorInvalidValue;
-  if (L.amode == A_I8 && L.out != OUT_I32 && !L.xs) return hipErrorInvalidValue;
+  if (L.amode == A_I8 && L.out != OUT_I32 && L.out != OUT_F32_X4 && !L.xs) return hipErrorInvalidValue;
+  if (L.out == OUT_F32_X4 && L.amode != A_I8) return hipErrorInvalidValue;
   // up to 16 token rows always stream the weights once; up to 64 rows too
   // while N is small (N <= 4096: the tiled kernels would leave CUs idle), but
   // for wide N the activation fragments every work-group re-reads cost more

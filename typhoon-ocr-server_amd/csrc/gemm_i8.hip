@@ -31,6 +31,7 @@ struct GemmI8Args {
   const uint8_t* Bt;    // weight tiles [KB][NG]
   const float* ws;      // [N]
   const float* xs;      // [M]
+  const int* xe;        // OUT_F32_X4: per-token exponents [M / 4]
   const float* bias;    // [N] or null
   void* Y;              // fp32 [M][ldy] or int32 (OUT_I32)
   int ldy;
@@ -39,6 +40,32 @@ struct GemmI8Args {
   int out;
   const uint8_t* zero_tile;  // 1 KiB of zeros (source of k-blocks past K)
 };
+
+// OUT_F32_X4 epilogue of one 16x16 accumulator tile (every lane calls it):
+// rows 4t .. 4t+3 are the int8 planes of token t, held by the lane quad
+// 4t .. 4t+3 (mod 16) at the same 4 columns n .. n+3; the quad's first lane
+// combines them and stores row t (16 bytes when aligned and inside N).
+__device__ __forceinline__ void planes_epilogue(const GemmI8Args& a, const v4i c, int m, int n, float4 ws4,
+                                                float4 b4, int e, int lane, bool vec_ok) {
+  float y[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++)
+    y[r] = planes_sum(c[r], __shfl_xor(c[r], 1, 64), __shfl_xor(c[r], 2, 64), __shfl_xor(c[r], 3, 64));
+  if ((lane & 3) != 0 || m >= a.M || n >= a.N) return;
+  const float w[4] = {ws4.x, ws4.y, ws4.z, ws4.w};
+  const float b[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    y[r] = planes_scale(y[r], w[r], e);
+    if (a.bias) y[r] = __fadd_rn(y[r], b[r]);
+  }
+  float* yp = reinterpret_cast<float*>(a.Y) + (size_t)(m >> 2) * a.ldy + n;
+  if (vec_ok && n + 4 <= a.N) {
+    *reinterpret_cast<float4*>(yp) = make_float4(y[0], y[1], y[2], y[3]);
+  } else {
+    for (int r = 0; r < 4 && n + r < a.N; r++) yp[r] = y[r];
+  }
+}
 
 // Stage ring of NST buffers.  Every K stage is NW*PW whole 1 KiB tiles, each
 // copied global -> LDS by one wave with one global_load_lds_dwordx4 (lane l
@@ -144,10 +171,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds_kernel(GemmI8Args a)
     e_ws[j] = make_float4(w4[0], w4[1], w4[2], w4[3]);
     e_b[j] = make_float4(b4[0], b4[1], b4[2], b4[3]);
   }
+  int e_xe[FM];
 #pragma unroll
   for (int i = 0; i < FM; i++) {
     const int m = min((mg0 + wm * FM + i) * 16 + mrow, a.M - 1);
-    e_xs[i] = (a.out == OUT_I32) ? 0.0f : a.xs[m];
+    e_xs[i] = (a.out == OUT_I32 || a.out == OUT_F32_X4) ? 0.0f : a.xs[m];
+    e_xe[i] = (a.out == OUT_F32_X4) ? a.xe[m >> 2] : 0;
   }
 
   v4i acc[FM][FN];
@@ -222,6 +251,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds_kernel(GemmI8Args a)
   // epilogue: y = fl(fl(fl(acc) * ws[n]) * xs[m]) (+ bias[n]); 16-byte stores
   // when the 4 columns are inside N and the row is 16-byte aligned
   const bool vec_ok = ((a.ldy & 3) == 0) && ((((uintptr_t)a.Y) & 15) == 0);
+  if (a.out == OUT_F32_X4) {
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+        planes_epilogue(a, acc[i][j], (mg0 + wm * FM + i) * 16 + mrow, (ng0 + wn * FN + j) * 16 + ncol, e_ws[j],
+                        e_b[j], e_xe[i], lane, vec_ok);
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < FM; i++) {
     const int m = (mg0 + wm * FM + i) * 16 + mrow;
@@ -337,10 +375,12 @@ __global__ __launch_bounds__(256) void gemm_i8_wcol_kernel(GemmI8Args a) {
     e_ws[j] = make_float4(w4[0], w4[1], w4[2], w4[3]);
     e_b[j] = make_float4(b4[0], b4[1], b4[2], b4[3]);
   }
+  int e_xe[MT];
 #pragma unroll
   for (int i = 0; i < MT; i++) {
     const int m = min((mg0 + i) * 16 + mrow, a.M - 1);
-    e_xs[i] = (a.out == OUT_I32) ? 0.0f : a.xs[m];
+    e_xs[i] = (a.out == OUT_I32 || a.out == OUT_F32_X4) ? 0.0f : a.xs[m];
+    e_xe[i] = (a.out == OUT_F32_X4) ? a.xe[m >> 2] : 0;
   }
 
   v4i acc[MT][FN];
@@ -408,6 +448,15 @@ __global__ __launch_bounds__(256) void gemm_i8_wcol_kernel(GemmI8Args a) {
   wait_vm<0>();   // no copy may still be landing in LDS when the work-group exits
 
   const bool vec_ok = ((a.ldy & 3) == 0) && ((((uintptr_t)a.Y) & 15) == 0);
+  if (a.out == OUT_F32_X4) {
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+        planes_epilogue(a, acc[i][j], (mg0 + i) * 16 + mrow, (ng0 + j) * 16 + ncol, e_ws[j], e_b[j], e_xe[i], lane,
+                        vec_ok);
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < MT; i++) {
     const int m = (mg0 + i) * 16 + mrow;
@@ -499,6 +548,7 @@ hipError_t launch_gemm_i8(const GemmLaunch& L, hipStream_t st) {
   a.Bt = L.Bt;
   a.ws = L.ws;
   a.xs = L.xs;
+  a.xe = L.xe;
   a.bias = L.bias;
   a.Y = L.Y;
   a.ldy = L.ldy;
@@ -510,7 +560,8 @@ hipError_t launch_gemm_i8(const GemmLaunch& L, hipStream_t st) {
   a.NG = cdiv(L.N, 16);
   a.out = L.out;
   a.zero_tile = L.zero_tile;
-  if (L.out != OUT_I32 && !L.xs) return hipErrorInvalidValue;
+  if (L.out == OUT_F32_X4 && (!L.xe || L.M % 4 != 0)) return hipErrorInvalidValue;
+  if (L.out != OUT_I32 && L.out != OUT_F32_X4 && !L.xs) return hipErrorInvalidValue;
   if (!L.zero_tile) return hipErrorInvalidValue;
   const int cfg = gemm_i8_pick_cfg(L.M, L.N, L.K);
   int mt, nt;

@@ -29,6 +29,7 @@ struct GemmSmallArgs {
   const uint8_t* Bt;    // weight tiles [KB][NG]
   const float* ws;
   const float* xs;      // per-token scales (A_I8)
+  const int* xe;        // OUT_F32_X4: per-token exponents
   const float* bias;
   void* Y;
   int ldy;
@@ -248,6 +249,43 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
     for (int g = 0; g < TG; g++) s_part[r][g][wv][lane] = acc[r][g];
   __syncthreads();
   if (wv != 0) return;
+  if constexpr (AMODE == A_I8) {
+    if (a.out == OUT_F32_X4) {
+      // rows 4t .. 4t+3 are the planes of token t: the lane quad 4t .. 4t+3
+      // (mod 16) holds them; its first lane combines and stores row t
+#pragma unroll
+      for (int tg = 0; tg < TG; tg++)
+#pragma unroll
+        for (int rg = 0; rg < R; rg++) {
+          acc_t tot = s_part[rg][tg][0][lane];
+#pragma unroll
+          for (int w = 1; w < 4; w++) {
+            const acc_t p = s_part[rg][tg][w][lane];
+#pragma unroll
+            for (int q = 0; q < 4; q++) tot[q] += p[q];
+          }
+          float y[4];
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const int a1 = __shfl_xor(tot[q], 1, 64), a2 = __shfl_xor(tot[q], 2, 64), a3 = __shfl_xor(tot[q], 3, 64);
+            y[q] = planes_sum(tot[q], a1, a2, a3);
+          }
+          const int m = tg * 16 + (lane & 15);
+          if ((lane & 3) != 0 || m >= a.M) continue;
+          const int t = m >> 2;
+          const int e = a.xe[t];
+          const int n0 = (g0 + rg) * 16 + 4 * (lane >> 4);
+          for (int q = 0; q < 4; q++) {
+            const int n = n0 + q;
+            if (n >= a.N) break;
+            float v = planes_scale(y[q], a.ws[n], e);
+            if (a.bias) v = __fadd_rn(v, a.bias[n]);
+            reinterpret_cast<float*>(a.Y)[(size_t)t * a.ldy + n] = v;
+          }
+        }
+      return;
+    }
+  }
   // lane holds D[n .. n+3][m]: m = 16 tg + (lane & 15), n = 16 g + 4 (lane >> 4)
 #pragma unroll
   for (int tg = 0; tg < TG; tg++)
@@ -331,6 +369,7 @@ hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st) {
   a.Bt = L.Bt;
   a.ws = L.ws;
   a.xs = L.xs;
+  a.xe = L.xe;
   a.bias = L.bias;
   a.Y = L.Y;
   a.ldy = L.ldy;
@@ -342,7 +381,8 @@ hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st) {
   a.MG = cdiv(L.M, 16);
   a.ep = L.ep;
   a.out = L.out;
-  if (L.amode == A_I8 && L.out != OUT_I32 && !L.xs) return hipErrorInvalidValue;
+  if (L.out == OUT_F32_X4 && (L.amode != A_I8 || !L.xe || L.M % 4 != 0)) return hipErrorInvalidValue;
+  if (L.amode == A_I8 && L.out != OUT_I32 && L.out != OUT_F32_X4 && !L.xs) return hipErrorInvalidValue;
   const int n_t = cdiv(a.KB, 4);
   // four row groups per work-group once there are work-groups to spare
   // (>= 2048 row groups: the lm_head), else one

@@ -208,6 +208,100 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_vec_kernel(const floa
   }
 }
 
+// fp32 token rows -> four int8 planes each (the A operand of W8A32 batches on
+// the int8 MFMA).  One wave per token t:
+//   e = frexp exponent of the row's absmax - 6, v = x 2^-e (exact), |v| < 64;
+//   q0 = rint(v), r0 = v - q0 (exact), then q_p = rint(254 r_{p-1}) with
+//   r_p = 254 r_{p-1} - q_p for p = 1..3 (|254 r| <= 127: every q fits int8).
+// So x = 2^e (q0 + q1/254 + q2/254^2 + q3/254^3 + d) with |d| below
+// 2^-26 of 64 (the rounding of 254 r and the last residual): about 2^-32 of
+// the row's absmax.  Plane p of token t is code row 4t + p of the 16x64 tile
+// array (each lane writes one dword per plane for its 4 consecutive k; k past
+// K inside the last k-block gets zero codes).  A row holding Inf or NaN gets
+// xe = kXeNonFinite and zero codes.
+__global__ __launch_bounds__(256) void split_i8x4_kernel(const float* __restrict__ X, int ldx, int M, int K,
+                                                         int KB, int MG, uint8_t* __restrict__ tiles,
+                                                         int* __restrict__ xe) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= M) return;
+  const float* row = X + (size_t)t * ldx;
+  const bool vec = ((((uintptr_t)row) & 15) == 0);
+  const int nf = KB * 16;                      // float4 groups in the padded row
+  uint32_t mx = 0;
+  for (int f = lane; f < nf; f += 64) {
+    const int k = 4 * f;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (vec && k + 4 <= K) {
+      v = *reinterpret_cast<const float4*>(row + k);
+    } else {
+      if (k < K) v.x = row[k];
+      if (k + 1 < K) v.y = row[k + 1];
+      if (k + 2 < K) v.z = row[k + 2];
+      if (k + 3 < K) v.w = row[k + 3];
+    }
+    mx = max(mx, max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w))));
+  }
+  mx = wave_umax(mx);
+  const bool finite = mx < 0x7f800000u;
+  int e = 0;
+  if (finite && mx != 0) {
+    int ex;
+    (void)frexpf(__uint_as_float(mx), &ex);
+    e = ex - 6;
+  }
+  if (lane == 0) xe[t] = finite ? e : kXeNonFinite;
+  // tile dword of plane p for float4 group f: row 4t + p of group (4t + p) >> 4
+  uint32_t* t32 = reinterpret_cast<uint32_t*>(tiles);
+  const int r0 = 4 * t;
+  for (int f = lane; f < nf; f += 64) {
+    const int k = 4 * f;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (finite) {
+      if (vec && k + 4 <= K) {
+        const float4 u = *reinterpret_cast<const float4*>(row + k);
+        v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; q++) v[q] = (k + q < K) ? row[k + q] : 0.0f;
+      }
+    }
+    uint32_t code[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      float r = ldexpf(v[q], -e);
+      float c = rintf(r);
+      uint32_t b0 = (uint32_t)((int)c & 0xff);
+      r = __fsub_rn(r, c);
+      uint32_t bp[3];
+#pragma unroll
+      for (int p = 0; p < 3; p++) {
+        const float s = __fmul_rn(r, 254.0f);
+        c = rintf(s);
+        bp[p] = (uint32_t)((int)c & 0xff);
+        r = __fsub_rn(s, c);
+      }
+      code[0] |= b0 << (8 * q);
+      code[1] |= bp[0] << (8 * q);
+      code[2] |= bp[1] << (8 * q);
+      code[3] |= bp[2] << (8 * q);
+    }
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      const int rr = r0 + p;
+      // k-block f >> 4, tile lane (rr & 15) + 16 ((f >> 2) & 3), dword f & 3
+      t32[(((size_t)(f >> 4) * MG + (rr >> 4)) * 64 + (rr & 15) + 16 * ((f >> 2) & 3)) * 4 + (f & 3)] = code[p];
+    }
+  }
+}
+
+hipError_t launch_split_i8x4(const float* X, int ldx, int M, int K, uint8_t* tiles, int* xe, hipStream_t st) {
+  if (M <= 0 || K <= 0 || ldx < K || !X || !tiles || !xe) return hipErrorInvalidValue;
+  const int KB = cdiv(K, 64), MG = cdiv(4 * M, 16);
+  hipLaunchKernelGGL(split_i8x4_kernel, dim3(cdiv(M, 4)), dim3(256), 0, st, X, ldx, M, K, KB, MG, tiles, xe);
+  return hipGetLastError();
+}
+
 // one thread per (tile, lane): 16 bytes of W[16g + (l&15)][64kb + 16(l>>4) ..]
 // for the row groups of rows [0, rows) of w, written as row groups g0 .. of a
 // tile array with NGt row groups per k-block (g0 = 0, NGt = NG for a whole

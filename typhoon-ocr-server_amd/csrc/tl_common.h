@@ -187,6 +187,26 @@ __device__ __forceinline__ uint32_t codes4_rne(float4 v, float inv) {
 }
 
 // ---------------------------------------------------------------------------
+// W8A32 batches on the int8 MFMA: each fp32 token row is four int8 planes
+// (split_i8x4_kernel), x = 2^e (q0 + q1/254 + q2/254^2 + q3/254^3)
+// ---------------------------------------------------------------------------
+constexpr int kXeNonFinite = -100000;   // exponent marking a row with Inf / NaN
+
+// the four plane accumulators of one output: a0 + a1/254 + a2/254^2 +
+// a3/254^3, Horner from the smallest term, each step rounded
+__device__ __forceinline__ float planes_sum(int a0, int a1, int a2, int a3) {
+  const float k = 1.0f / 254.0f;
+  float t = __fadd_rn(__fmul_rn((float)a3, k), (float)a2);
+  t = __fadd_rn(__fmul_rn(t, k), (float)a1);
+  return __fadd_rn(__fmul_rn(t, k), (float)a0);
+}
+// fl(t * ws) scaled by 2^e (exact unless the result leaves the float range);
+// NaN for a row that held Inf or NaN
+__device__ __forceinline__ float planes_scale(float t, float ws, int e) {
+  return e == kXeNonFinite ? __builtin_nanf("") : ldexpf(__fmul_rn(t, ws), e);
+}
+
+// ---------------------------------------------------------------------------
 // argmax keys: the float's bits made monotonic in the high word, the index
 // complemented in the low word, so the largest key is the largest value and,
 // among equal values, the lowest index (torch.argmax's first-max rule)

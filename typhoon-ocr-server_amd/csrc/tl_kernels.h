@@ -22,7 +22,9 @@ enum { NORM_NONE = 0, NORM_NUMPY = 1, NORM_DECODER = 2 };
 // GEMM A-operand modes and output types (gemm.hip)
 enum { A_I8 = 0, A_BF16 = 1, A_F16 = 2, A_F32X3 = 3,
        A_BF16X3 = 4 };   // fp32 X already split into three bf16 planes (split_bf16x3)
-enum { OUT_F32 = 0, OUT_BF16 = 1, OUT_F16 = 2, OUT_I32 = 3 };
+enum { OUT_F32 = 0, OUT_BF16 = 1, OUT_F16 = 2, OUT_I32 = 3,
+       OUT_F32_X4 = 4 };   // A_I8 rows 4t..4t+3 are the int8 planes of fp32 token t (split_i8x4):
+                           // y[t][n] = ldexp((a0 + a1/254 + a2/254^2 + a3/254^3) * ws[n], xe[t]) (+ bias[n])
 // GEMM float epilogues: fl(acc*ws) then + bias, or fma(acc, ws, bias|0)
 enum { EP_SCALE = 0, EP_SCALE_FMA = 1 };
 
@@ -128,6 +130,7 @@ struct GemmLaunch {
   int force_split = 0;
   const uint8_t* zero_tile = nullptr;   // 1 KiB of device zeros (LDS-staged int8 GEMM)
   long long a_plane = 0;          // A_BF16X3: elements between the three planes of A
+  const int* xe = nullptr;        // OUT_F32_X4: per-token power-of-two exponents (split_i8x4)
 };
 GemmPlan gemm_plan(int amode, int M, int N, int K);
 size_t gemm_workspace_bytes(int amode, int M, int N, int K);
@@ -144,6 +147,12 @@ void gemm_i8_set_cfg(int cfg);   // tuning override (-1 = planner)
 bool gemm_b16_supported(const GemmLaunch& L);
 // fp32 X [M][ldx] -> three bf16 planes [3][M][kp] (row stride kp, a multiple of
 // 8 >= K, zero past K): t0 = bf16(x), t1 = bf16(x - t0), t2 = bf16(x - t0 - t1)
+// fp32 rows X [M][ldx] -> int8 code tiles of 4 M rows (tile row groups
+// MG = ceil(4M / 16), k-blocks ceil(K / 64); row 4t + p is plane p of token
+// t) and per-token exponents xe[M]: x = 2^e (q0 + q1/254 + q2/254^2 +
+// q3/254^3) up to 2^-32 of the row's absmax; a row holding Inf or NaN gets
+// xe = kXeNonFinite (tl_common.h; its outputs are NaN)
+hipError_t launch_split_i8x4(const float* X, int ldx, int M, int K, uint8_t* tiles, int* xe, hipStream_t st);
 hipError_t launch_split_bf16x3(const float* X, int ldx, int M, int K, int kp, uint16_t* planes,
                                hipStream_t st);
 // ---- M <= 16 rows (gemm_small.hip): GEMV-shaped MFMA kernel ---------------
