@@ -130,7 +130,7 @@ struct Workspace {
   DevBuf act_s;       // activation scales
   DevBuf xn;          // normalised hidden row (lm_head argmax)
   DevBuf keys;        // per-work-group argmax keys
-  DevBuf planes;      // fp32 activations split into three bf16 planes
+  DevBuf planes;      // W8A32 batches: int8 plane tiles of the fp32 rows and their exponents
 };
 
 std::mutex g_ws_mu;

@@ -421,7 +421,6 @@ hipError_t launch_gemm(const GemmLaunch& L, hipStream_t st) {
     return launch_gemm_small(L, st);
   if (L.amode == A_I8 && L.M > 16) return launch_gemm_i8(L, st);
   if (L.amode != A_I8 && L.M > 16 && gemm_b16_supported(L)) return launch_gemm_b16(L, st);
-  if (L.amode == A_BF16X3) return hipErrorInvalidValue;   // planes run only on the LDS-tiled kernel
   switch (L.amode) {
     case A_I8: return launch_mode<A_I8>(a, p.cfg, p.blocks, st);
     case A_BF16: return launch_mode<A_BF16>(a, p.cfg, p.blocks, st);

@@ -3,16 +3,6 @@
 //           bf16) on v_mfma_f32_16x16x32_bf16, fp32 accumulation, fp32 scale
 //           after the sum, fp32 / bf16 (RNE) / fp16 output.
 //   A_F16   the same with fp16 X on v_mfma_f32_16x16x32_f16.
-//   A_F32X3 W8A32 batch > 1 (kernel/w8a32_kernel.c:297-350): fp32 X split
-//           exactly into three bf16 terms (x0 = bf16(x), x1 = bf16(x - x0),
-//           x2 = bf16(x - x0 - x1)); three bf16 MFMAs per fragment give the
-//           fp32 product sum with exact products.
-//   A_BF16X3 the same product with the split done once beforehand
-//           (split_bf16x3_kernel writes the three terms as bf16 planes): the
-//           GEMM copies the planes and runs the same three MFMAs in the same
-//           order, so its output is bit-identical to A_F32X3, without the
-//           per-wave split (the split made A_F32X3 VALU-bound: ~15 VALU
-//           instructions per MFMA).
 //
 // Same skeleton as gemm_i8.hip: a ring of NST LDS stage buffers filled by
 // direct global -> LDS copies (one 16-byte piece per lane per copy), one
@@ -23,10 +13,8 @@
 // int8 weight tile gives lane l row (l & 15) and k = 16 (l >> 4) + 0..15; the
 // bf16 MFMA consumes 8 k per lane, so the block is two MFMAs, half h taking
 // k = 16 (l >> 4) + 8 h + 0..7.  Each A copy therefore reads, for lane l,
-//   16-bit X: 8 elements X[row][64 kb + 16 (l >> 4) + 8 h ..]      (2 copies)
-//   fp32  X : 4 elements X[row][64 kb + 16 (l >> 4) + 4 j ..]      (4 copies)
-//   planes  : 8 elements of plane t, t = 0..2, as 16-bit X           (6 copies)
-// and a wave reads its operand with one ds_read_b128 per copy.  Weight tiles
+// 8 elements X[row][64 kb + 16 (l >> 4) + 8 h ..] (2 copies per row group and
+// K block), and a wave reads its operand with one ds_read_b128 per copy.  Weight tiles
 // stay int8 in LDS and are widened to bf16/fp16 in registers after the read.
 // Lanes whose row is past M or whose k is past K copy 16 bytes of zeros.
 #include <algorithm>
@@ -41,7 +29,6 @@ namespace tl {
 struct GemmB16Args {
   const void* X;         // row-major [M][lda], element type per AMODE
   int lda;
-  long long a_plane;     // A_BF16X3: elements between the three planes
   const uint8_t* Bt;     // weight tiles [KB][NG]
   const float* ws;       // [N]
   const float* bias;     // [N] or null
@@ -90,8 +77,8 @@ __device__ inline v4f mfma16(uint4 w, uint4 x, v4f c) {
 template <int AMODE, int MT, int NT, int NST, int WM, int WN>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args a) {
   constexpr int NW = WM * WN;
-  constexpr int AP = (AMODE == A_F32X3) ? 4 : (AMODE == A_BF16X3 ? 6 : 2);   // A copies per (row group, K block)
-  constexpr int ESZ = (AMODE == A_F32X3) ? 4 : 2;      // bytes per X element
+  constexpr int AP = 2;                                // A copies per (row group, K block)
+  constexpr int ESZ = 2;                               // bytes per X element
   constexpr int EPC = 16 / ESZ;                        // X elements per copy per lane
   constexpr int TA = MT * AP, TB = NT, TS = TA + TB;
   static_assert(TS % NW == 0, "stage copies must divide evenly over the waves");
@@ -139,12 +126,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
     if (q < TA) {
       const int i = q / AP, j = q % AP;
       const int row = (mg0 + i) * 16 + (lane & 15);
-      // planes: copy j = 2 t + h is half h of plane t
-      const int koff = 16 * (lane >> 4) + EPC * (AMODE == A_BF16X3 ? (j & 1) : j);
-      const size_t plane = (AMODE == A_BF16X3) ? (size_t)(j >> 1) * a.a_plane : 0;
+      const int koff = 16 * (lane >> 4) + EPC * j;
       qrow_ok[p] = row < a.M;
       qkoff[p] = koff;
-      qsrc[p] = Xb + (plane + (size_t)min(row, a.M - 1) * a.lda + koff) * ESZ;
+      qsrc[p] = Xb + ((size_t)min(row, a.M - 1) * a.lda + koff) * ESZ;
     } else {
       const int ng = min(ng0 + (q - TA), a.NG - 1);
       qrow_ok[p] = true;
@@ -229,39 +214,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
 #pragma unroll
     for (int i = 0; i < FM; i++) {
       const uint4* f = &fa[c][i * AP];
-      if constexpr (AMODE == A_F32X3) {
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-          const uint4 u0 = f[2 * h], u1 = f[2 * h + 1];
-          const float x[8] = {__uint_as_float(u0.x), __uint_as_float(u0.y), __uint_as_float(u0.z), __uint_as_float(u0.w),
-                              __uint_as_float(u1.x), __uint_as_float(u1.y), __uint_as_float(u1.z), __uint_as_float(u1.w)};
-          uint4 t0, t1, t2;
-          split3x8(x, t0, t1, t2);
-#pragma unroll
-          for (int j = 0; j < FN; j++) {
-            acc[i][j] = mfma16<A_BF16>(wb[j][h], t2, acc[i][j]);
-            acc[i][j] = mfma16<A_BF16>(wb[j][h], t1, acc[i][j]);
-            acc[i][j] = mfma16<A_BF16>(wb[j][h], t0, acc[i][j]);
-          }
-        }
-      } else if constexpr (AMODE == A_BF16X3) {
-        // same MFMAs in the same order as A_F32X3 (t2, t1, t0 per half)
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-          const uint4 t0 = f[h], t1 = f[2 + h], t2 = f[4 + h];
-#pragma unroll
-          for (int j = 0; j < FN; j++) {
-            acc[i][j] = mfma16<A_BF16>(wb[j][h], t2, acc[i][j]);
-            acc[i][j] = mfma16<A_BF16>(wb[j][h], t1, acc[i][j]);
-            acc[i][j] = mfma16<A_BF16>(wb[j][h], t0, acc[i][j]);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < FN; j++) {
-          acc[i][j] = mfma16<AMODE>(wb[j][0], f[0], acc[i][j]);
-          acc[i][j] = mfma16<AMODE>(wb[j][1], f[1], acc[i][j]);
-        }
+      for (int j = 0; j < FN; j++) {
+        acc[i][j] = mfma16<AMODE>(wb[j][0], f[0], acc[i][j]);
+        acc[i][j] = mfma16<AMODE>(wb[j][1], f[1], acc[i][j]);
       }
     }
   };
@@ -345,110 +301,30 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
 }
 
 // ---------------------------------------------------------------------------
-// one pass over fp32 X: thread t splits 8 consecutive elements of a row into
-// the three bf16 terms (split3x8, the split A_F32X3 does per wave) and writes
-// 16 bytes to each plane; elements past K are zero
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void split_bf16x3_kernel(const float* __restrict__ X, int ldx, int M, int K,
-                                                          int kp, uint4* __restrict__ planes) {
-  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
-  const int k8n = kp / 8;
-  const long long total = (long long)M * k8n;
-  if (t >= total) return;
-  const int row = (int)(t / k8n), k0 = (int)(t - (long long)row * k8n) * 8;
-  const float* src = X + (size_t)row * ldx + k0;
-  float x[8];
-  if (k0 + 8 <= K && ((((uintptr_t)src) & 15) == 0)) {
-    const float4 a = reinterpret_cast<const float4*>(src)[0], b = reinterpret_cast<const float4*>(src)[1];
-    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; e++) x[e] = (k0 + e < K) ? src[e] : 0.0f;
-  }
-  uint4 t0, t1, t2;
-  split3x8(x, t0, t1, t2);
-  const long long plane = total;             // uint4 per plane
-  planes[t] = t0;
-  planes[plane + t] = t1;
-  planes[2 * plane + t] = t2;
-}
-
-hipError_t launch_split_bf16x3(const float* X, int ldx, int M, int K, int kp, uint16_t* planes,
-                               hipStream_t st) {
-  if (M < 1 || K < 1 || kp < K || kp % 8 != 0 || ldx < K || (((uintptr_t)planes) & 15) != 0)
-    return hipErrorInvalidValue;
-  const long long total = (long long)M * (kp / 8);
-  hipLaunchKernelGGL(split_bf16x3_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, X, ldx, M, K,
-                     kp, reinterpret_cast<uint4*>(planes));
-  return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------
 // planning and launch
 // ---------------------------------------------------------------------------
-// 16-bit X:  cfg 0  128 x 192 tiles, 4-deep ring (112 KiB)
-//            cfg 1   64 x 128 tiles, 8-deep ring (128 KiB)
-//            cfg 2   32 x  64 tiles, 8-deep ring (64 KiB)
-// fp32 X:    cfg 0   64 x 128 tiles, 4-deep ring (96 KiB)
-//            cfg 1   64 x  64 tiles, 6-deep ring (96 KiB)
-//            cfg 2   32 x  64 tiles, 6-deep ring (72 KiB)
+// cfg 0  128 x 192 tiles, 4-deep ring (112 KiB)
+// cfg 1   64 x 128 tiles, 8-deep ring (128 KiB)
+// cfg 2   32 x  64 tiles, 8-deep ring (64 KiB)
 // The smaller tiles exist for mid-size M (64 < M <= 512) with small N, where
 // the larger ones leave most CUs idle.
-static void b16_cfg(int amode, int cfg, int& mt, int& nt) {
-  if (cfg == 2) {
-    mt = 2;
-    nt = 4;
-  } else if (amode == A_F32X3 || amode == A_BF16X3) {
-    mt = 4;
-    nt = (cfg == 0) ? 8 : 4;
-  } else {
-    mt = (cfg == 0) ? 8 : 4;
-    nt = (cfg == 0) ? 12 : 8;
-  }
+static void b16_cfg(int cfg, int& mt, int& nt) {
+  mt = (cfg == 0) ? 8 : (cfg == 1 ? 4 : 2);
+  nt = (cfg == 0) ? 12 : (cfg == 1 ? 8 : 4);
 }
 
-// 16-bit X: the configuration whose tile count best fills 256 CUs (measured
-// best over the W8A16 sweep).  Three-term X (six MFMAs per fragment pair):
-// the configuration with the least modelled time, rounds of 256 work-groups
-// x K steps x the slowest per-step resource of a work-group's four waves,
-//   MFMA  16 cycles per 16x16x32 MFMA (per wave, one wave per SIMD),
-//   VALU  4 cycles per wave64 instruction: ~40 to widen an int8 weight
-//         fragment, ~160 to split an fp32 row group into three bf16 terms,
-//   LDS   ~107 bytes per cycle per CU of fragment reads (1 KiB per copy),
-// (rates measured on the MI355X): there the large tiles win unless they
-// would leave most CUs idle (W8A32 1200-token prefill: 30.5 -> 26.2 ms).
-static int b16_pick_cfg(int amode, int MG, int NG) {
-  const bool x3 = (amode == A_F32X3 || amode == A_BF16X3);
-  if (!x3) {
-    int best = 0;
-    double best_eff = -1.0;
-    for (int cfg : {0, 1, 2}) {
-      int mt, nt;
-      b16_cfg(amode, cfg, mt, nt);
-      const int tiles = cdiv(MG, mt) * cdiv(NG, nt);
-      const double eff = (double)tiles / (cdiv(tiles, 256) * 256);
-      if (eff > best_eff + 1e-9) {
-        best_eff = eff;
-        best = cfg;
-      }
-    }
-    return best;
-  }
-  const int ap = (amode == A_F32X3) ? 4 : (amode == A_BF16X3 ? 6 : 2);
+// the configuration whose tile count best fills 256 CUs (measured best over
+// the W8A16 sweep)
+static int b16_pick_cfg(int MG, int NG) {
   int best = 0;
-  double best_t = 1e300;
+  double best_eff = -1.0;
   for (int cfg : {0, 1, 2}) {
     int mt, nt;
-    b16_cfg(amode, cfg, mt, nt);
-    const int fm = mt / 2, fn = nt / 2;   // 2 x 2 waves
-    const double mfma = fm * fn * (x3 ? 6 : 2) * 16.0;
-    const double valu = (fn * 40.0 + (amode == A_F32X3 ? fm * 160.0 : 0.0)) * 4.0;
-    const double lds = 4.0 * (fm * ap + fn) * 1024.0 / 107.0;
-    const double step = std::max(mfma, std::max(valu, lds));
-    const long long tiles = (long long)cdiv(MG, mt) * cdiv(NG, nt);
-    const double t = (double)((tiles + 255) / 256) * step;
-    if (t < best_t * (1.0 - 1e-9)) {
-      best_t = t;
+    b16_cfg(cfg, mt, nt);
+    const int tiles = cdiv(MG, mt) * cdiv(NG, nt);
+    const double eff = (double)tiles / (cdiv(tiles, 256) * 256);
+    if (eff > best_eff + 1e-9) {
+      best_eff = eff;
       best = cfg;
     }
   }
@@ -456,10 +332,8 @@ static int b16_pick_cfg(int amode, int MG, int NG) {
 }
 
 bool gemm_b16_supported(const GemmLaunch& L) {
-  if (L.amode != A_BF16 && L.amode != A_F16 && L.amode != A_F32X3 && L.amode != A_BF16X3) return false;
-  if (L.amode == A_BF16X3 && L.a_plane < (long long)L.M * L.lda) return false;
-  const int align = (L.amode == A_F32X3) ? 4 : 8;   // elements per 16-byte copy
-  if (L.K % align != 0 || L.lda % align != 0) return false;
+  if (L.amode != A_BF16 && L.amode != A_F16) return false;
+  if (L.K % 8 != 0 || L.lda % 8 != 0) return false;   // 8 elements per 16-byte copy
   if ((((uintptr_t)L.A) & 15) != 0) return false;
   return L.zero_tile != nullptr;
 }
@@ -469,7 +343,6 @@ hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st) {
   GemmB16Args a;
   a.X = L.A;
   a.lda = L.lda;
-  a.a_plane = L.a_plane;
   a.Bt = L.Bt;
   a.ws = L.ws;
   a.bias = L.bias;
@@ -484,9 +357,9 @@ hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st) {
   a.ep = L.ep;
   a.out = L.out;
   a.zero_tile = L.zero_tile;
-  const int best = b16_pick_cfg(L.amode, a.MG, a.NG);
+  const int best = b16_pick_cfg(a.MG, a.NG);
   int mt, nt;
-  b16_cfg(L.amode, best, mt, nt);
+  b16_cfg(best, mt, nt);
   a.ntm = cdiv(a.MG, mt);
   a.ntn = cdiv(a.NG, nt);
   const int blocks = a.ntm * a.ntn;
@@ -496,20 +369,10 @@ hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st) {
       else if (best == 1) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_BF16, 4, 8, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
       else hipLaunchKernelGGL((gemm_b16_lds_kernel<A_BF16, 2, 4, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
       break;
-    case A_F16:
+    default:
       if (best == 0) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F16, 8, 12, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
       else if (best == 1) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F16, 4, 8, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
       else hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F16, 2, 4, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
-      break;
-    case A_BF16X3:
-      if (best == 0) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_BF16X3, 4, 8, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
-      else if (best == 1) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_BF16X3, 4, 4, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
-      else hipLaunchKernelGGL((gemm_b16_lds_kernel<A_BF16X3, 2, 4, 6, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
-      break;
-    default:
-      if (best == 0) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F32X3, 4, 8, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
-      else if (best == 1) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F32X3, 4, 4, 6, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
-      else hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F32X3, 2, 4, 6, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
       break;
   }
   return hipGetLastError();

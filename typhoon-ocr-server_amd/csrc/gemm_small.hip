@@ -334,7 +334,7 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
 }
 
 bool gemm_small_supported(const GemmLaunch& L) {
-  if (L.M < 1 || L.M > 64 || L.amode == A_BF16X3) return false;
+  if (L.M < 1 || L.M > 64) return false;
   if (L.amode == A_I8) return true;                    // code tiles, any K
   const int epv = (L.amode == A_F32X3) ? 4 : 8;        // elements per 16 bytes
   if (L.K % epv != 0 || L.lda % epv != 0) return false;

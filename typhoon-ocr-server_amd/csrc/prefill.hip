@@ -6,7 +6,8 @@
 // prefill append (kernel/kv_cache.c:70-104), attention_prefill_gqa
 // (kernel/attention.c:252-360), silu_mul_inplace (ops.c:493-531) and
 // vec_add_f32 (:537-549).  The linear layers are the fp32-accurate batch > 1
-// GEMM (gemm_b16.hip, A_F32X3).
+// GEMM (four int8 planes per token on the int8 MFMA, gemm_i8.hip) or, in
+// W8A8 mode, the int8 GEMM on per-token codes.
 //
 // Layouts: activations token-major, as the reference's scratch: hidden
 // [S][2048], qkv [S][4096] (q | k | v), attention output [S][2048], gate/up

@@ -20,8 +20,7 @@ enum { EPI_W8A32 = 0, EPI_W8A8 = 1, EPI_ACC = 2, EPI_ARGMAX = 3, EPI_SWIGLU = 4 
 // decoder's RMSNorm (kernel/ops.c:22-56, estimate-based rsqrt)
 enum { NORM_NONE = 0, NORM_NUMPY = 1, NORM_DECODER = 2 };
 // GEMM A-operand modes and output types (gemm.hip)
-enum { A_I8 = 0, A_BF16 = 1, A_F16 = 2, A_F32X3 = 3,
-       A_BF16X3 = 4 };   // fp32 X already split into three bf16 planes (split_bf16x3)
+enum { A_I8 = 0, A_BF16 = 1, A_F16 = 2, A_F32X3 = 3 };
 enum { OUT_F32 = 0, OUT_BF16 = 1, OUT_F16 = 2, OUT_I32 = 3,
        OUT_F32_X4 = 4 };   // A_I8 rows 4t..4t+3 are the int8 planes of fp32 token t (split_i8x4):
                            // y[t][n] = ldexp((a0 + a1/254 + a2/254^2 + a3/254^3) * ws[n], xe[t]) (+ bias[n])
@@ -43,6 +42,12 @@ hipError_t launch_unpack_tiles(const uint8_t* tiles, int rows, int cols, int8_t*
 hipError_t launch_rmsnorm_np(const float* h, const float* w, float* out, int K, float eps, hipStream_t st);
 // token = argmax over the per-work-group keys of an EPI_ARGMAX GEMV
 hipError_t launch_argmax_keys(const uint64_t* keys, int n, int32_t* token, float* value, hipStream_t st);
+// fp32 rows X [M][ldx] -> int8 code tiles of 4 M rows (tile row groups
+// MG = ceil(4M / 16), k-blocks ceil(K / 64); row 4t + p is plane p of token
+// t) and per-token exponents xe[M]: x = 2^e (q0 + q1/254 + q2/254^2 +
+// q3/254^3) up to 2^-32 of the row's absmax; a row holding Inf or NaN gets
+// xe = kXeNonFinite (tl_common.h; its outputs are NaN)
+hipError_t launch_split_i8x4(const float* X, int ldx, int M, int K, uint8_t* tiles, int* xe, hipStream_t st);
 // 4-byte-word copy by a kernel (bytes % 4 == 0), e.g. from mapped pinned host memory
 hipError_t launch_copy_words(const void* src, void* dst, size_t bytes, hipStream_t st);
 
@@ -129,7 +134,6 @@ struct GemmLaunch {
   uint32_t* cnt = nullptr;        // gemm_counter_count zeroed counters
   int force_split = 0;
   const uint8_t* zero_tile = nullptr;   // 1 KiB of device zeros (LDS-staged int8 GEMM)
-  long long a_plane = 0;          // A_BF16X3: elements between the three planes of A
   const int* xe = nullptr;        // OUT_F32_X4: per-token power-of-two exponents (split_i8x4)
 };
 GemmPlan gemm_plan(int amode, int M, int N, int K);
@@ -142,19 +146,9 @@ hipError_t launch_gemm_i8(const GemmLaunch& L, hipStream_t st);
 int gemm_i8_pick_cfg(int M, int N, int K);
 void gemm_i8_set_cfg(int cfg);   // tuning override (-1 = planner)
 
-// ---- LDS-staged 16-bit MFMA GEMM (gemm_b16.hip): A_BF16 / A_F16 / A_F32X3,
-//      used for M > 16 when X rows are 16-byte aligned pieces --------------
+// ---- LDS-staged 16-bit MFMA GEMM (gemm_b16.hip): A_BF16 / A_F16, used for
+//      M > 16 when X rows are 16-byte aligned pieces -----------------------
 bool gemm_b16_supported(const GemmLaunch& L);
-// fp32 X [M][ldx] -> three bf16 planes [3][M][kp] (row stride kp, a multiple of
-// 8 >= K, zero past K): t0 = bf16(x), t1 = bf16(x - t0), t2 = bf16(x - t0 - t1)
-// fp32 rows X [M][ldx] -> int8 code tiles of 4 M rows (tile row groups
-// MG = ceil(4M / 16), k-blocks ceil(K / 64); row 4t + p is plane p of token
-// t) and per-token exponents xe[M]: x = 2^e (q0 + q1/254 + q2/254^2 +
-// q3/254^3) up to 2^-32 of the row's absmax; a row holding Inf or NaN gets
-// xe = kXeNonFinite (tl_common.h; its outputs are NaN)
-hipError_t launch_split_i8x4(const float* X, int ldx, int M, int K, uint8_t* tiles, int* xe, hipStream_t st);
-hipError_t launch_split_bf16x3(const float* X, int ldx, int M, int K, int kp, uint16_t* planes,
-                               hipStream_t st);
 // ---- M <= 16 rows (gemm_small.hip): GEMV-shaped MFMA kernel ---------------
 bool gemm_small_supported(const GemmLaunch& L);
 hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st);
