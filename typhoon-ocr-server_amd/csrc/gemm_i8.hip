@@ -41,6 +41,30 @@ struct GemmI8Args {
   const uint8_t* zero_tile;  // 1 KiB of zeros (source of k-blocks past K)
 };
 
+// Work-group -> tile.  Dispatch is round-robin over the 8 XCDs: work-group b
+// runs on XCD b % 8 as that XCD's (b / 8)-th.  When the tile columns divide
+// over the XCDs, XCD x owns a band of ntn / 8 columns and walks it in groups
+// of 4 tile rows x the whole band, so the ~32 work-groups an XCD runs at once
+// share 4 A panels and the band's B panels, which fit its 4 MB L2 (one column
+// at a time keeps ~32 A panels live at once: past the L2 once A exceeds it,
+// e.g. the 4800 plane rows of a 1200-token fp32 batch).  Otherwise each XCD
+// takes a run of consecutive tiles (columns of tm).
+__device__ __forceinline__ void tile_of(int b, int ntm, int ntn, int& tm, int& tn) {
+  if (ntn % 8 == 0) {
+    const int x = b % 8, j = b / 8, bw = ntn / 8;
+    const int grp = j / (4 * bw), r = j - grp * 4 * bw;
+    const int rows = min(4, ntm - 4 * grp);
+    tm = 4 * grp + r % rows;
+    tn = x * bw + r / rows;
+  } else {
+    const int ntiles = ntm * ntn;
+    int t = b;
+    if (ntiles % 8 == 0) t = (b % 8) * (ntiles / 8) + b / 8;
+    tn = t / ntm;
+    tm = t - tn * ntm;
+  }
+}
+
 // OUT_F32_X4 epilogue of one 16x16 accumulator tile (every lane calls it):
 // rows 4t .. 4t+3 are the int8 planes of token t, held by the lane quad
 // 4t .. 4t+3 (mod 16) at the same 4 columns n .. n+3; the quad's first lane
@@ -102,10 +126,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds_kernel(GemmI8Args a)
 
   // XCD-aware tile order: work-group b runs on XCD b % 8; the work-groups of
   // one XCD walk M fastest within a band of N tiles.
-  const int ntiles = a.ntm * a.ntn;
-  int t = blockIdx.x;
-  if (ntiles % 8 == 0) t = (blockIdx.x % 8) * (ntiles / 8) + blockIdx.x / 8;
-  const int tn = t / a.ntm, tm = t - (t / a.ntm) * a.ntm;
+  int tm, tn;
+  tile_of(blockIdx.x, a.ntm, a.ntn, tm, tn);
   const int mg0 = tm * MT, ng0 = tn * NT;
 
   const uint4* A4 = reinterpret_cast<const uint4*>(a.At) + lane;
@@ -329,10 +351,8 @@ __global__ __launch_bounds__(256) void gemm_i8_wcol_kernel(GemmI8Args a) {
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
-  const int ntiles = a.ntm * a.ntn;
-  int t = blockIdx.x;
-  if (ntiles % 8 == 0) t = (blockIdx.x % 8) * (ntiles / 8) + blockIdx.x / 8;
-  const int tn = t / a.ntm, tm = t - (t / a.ntm) * a.ntm;
+  int tm, tn;
+  tile_of(blockIdx.x, a.ntm, a.ntn, tm, tn);
   const int mg0 = tm * MT, ng0 = tn * NT + wv * FN;
 
   const uint4* A4 = reinterpret_cast<const uint4*>(a.At) + lane;
@@ -520,6 +540,12 @@ void gemm_i8_set_cfg(int cfg) { g_i8_force_cfg = cfg; }
 int gemm_i8_pick_cfg(int M, int N, int K) {
   if (g_i8_force_cfg >= 0) return g_i8_force_cfg;
   (void)K;
+  // 2048 rows and more (the 4 x 1200 plane rows of a 1200-token fp32 batch):
+  // many tiles per CU, where the deepest weight prefetch on 64 x 128 tiles
+  // measured best on every decoder shape (per layer 594 -> 442 us at 4800
+  // rows); below, tiles that fill the CUs (at 1024-1200 rows cfg 6 was
+  // faster on some shapes and slower on others)
+  if (M >= 2048) return 6;
   const int MG = cdiv(M, 16), NG = cdiv(N, 16);
   // the configuration whose tile count best fills 256 CUs (at least one
   // full wave of work-groups, then the fewest idle CUs in the last wave).
