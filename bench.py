@@ -1,18 +1,23 @@
 """Benchmark of the INT8 linear path on one MI355X.
 
-Workload (a "step" = one decoded token's linear layers, W8A32 batch==1):
-  28 layers x {QKV 4096x2048, O 2048x2048, gate_up 12288x2048, down 2048x6144}
-  + lm_head 151936x2048, every matrix distinct (1.72 GB of int8 weights, far
-  beyond the 256 MB Infinity Cache), per-row fp32 scales, fp32 activations
-  ~N(0,1) resident in HBM, synthetic data.
-The step is captured once in a HIP graph (113 GEMV launches) and replayed.
+Workload (the metric's configuration; a "step" = W8A32 batch==1 GEMVs):
+  the decode projection set of one Qwen3-VL-2B text layer plus the lm_head,
+  QKV 4096x2048, O 2048x2048, gate_up 12288x2048, down 2048x6144, lm_head
+  151936x2048 (361.5 MB of int8 weights and scales), per-row fp32 scales,
+  fp32 activations ~N(0,1) resident in HBM, synthetic data.  Each step (5
+  GEMV launches) is captured in a HIP graph; step i replays the graph of layer
+  copy i % 28 of 28 distinct ones plus the lm_head, so every step's weights
+  come from HBM (1.72 GB in all, far beyond the 256 MB Infinity Cache; the
+  311 MB lm_head passes through it between steps).
+Also the full decoder's step, 28 layers + lm_head (113 launches, one graph):
+  `decode_step_28_layers`.
 
 value   = algorithmic bytes of one step / step time (GB/s); bytes per GEMV
           launch are N*K + 4N + 4K + 4N (weights, scales, x, y).
-roofline: the GEMV kernel family (every launch of the step is a GEMV),
-          average bytes per launch over its average launch duration (HIP
-          events on the replay stream around the timed replays, divided by
-          the 113 launches each), against the 8 TB/s HBM peak.
+roofline: the GEMV kernel family (every launch is a GEMV), average bytes per
+          launch over its average launch duration (HIP events on the replay
+          stream around the timed steps, divided by the 5 launches of each),
+          against the 8 TB/s HBM peak.
 Also: W8A8 prefill TOPS (M=1024; N=6144,K=2048 and N=2048,K=6144; includes
 the per-token quantization kernel), and the CPU baseline (the oracle's M=1
 GEMV, OpenMP on the host cores) on a bounded sample.
@@ -308,9 +313,10 @@ def bench_decoder_generate(lin, torch, dev, n_layers=28, vocab=151936, prefix=12
 def cpu_baseline(seconds=10.0):
     """The oracle's M=1 GEMV (same formula as the reference's w8a32_gemv,
     OpenMP over row chunks like its GCD fan-out) on the host cores, over the
-    same decode step as the GPU: 28 distinct layer sets + lm_head (1.72 GB of
-    int8 weights, so no cache holds them).  Whole steps are timed until the
-    time budget is spent; the median step time gives GB/s and tok/s."""
+    same steps as the GPU: one layer's projection set (layer copy i % 28 of
+    28 distinct ones) + the lm_head (one of two copies, alternating; 2.0 GB
+    of int8 weights in all, so no cache holds them).  Steps are timed until the time budget is spent; the
+    median step time gives GB/s."""
     from oracle import oracle as orc
     native = True
     try:
@@ -323,23 +329,29 @@ def cpu_baseline(seconds=10.0):
         cores = os.cpu_count() or 1
     cores = max(1, min(cores, 16))
     rng = np.random.default_rng(0)
-    shapes = [(f"l{l}.{n}", N, K) for l in range(LAYERS) for (n, N, K) in LAYER_SHAPES] + [LM_HEAD]
+    # two lm_head copies, alternating: a host last-level cache must not hold
+    # the lm_head from one step to the next
+    shapes = [(f"l{l}.{n}", N, K) for l in range(LAYERS) for (n, N, K) in LAYER_SHAPES] + [LM_HEAD, LM_HEAD]
     mats = []
     for (name, N, K) in shapes:
         w = rng.integers(-127, 128, (N, K), dtype=np.int8)
         s = rng.uniform(0.002, 0.02, N).astype(np.float32)
         x = rng.standard_normal(K, dtype=np.float32)
         mats.append((w, s, x, np.empty(N, np.float32)))
+    nl = len(LAYER_SHAPES)
     for (w, s, x, y) in mats[:4]:
         orc.w8a32_gemv_timed(x, w, s, y, cores, native=native)        # warm-up
     times = []
     t_end = time.perf_counter() + seconds
+    i = 0
     while time.perf_counter() < t_end or len(times) < 2:
+        step = mats[nl * (i % LAYERS):nl * (i % LAYERS) + nl] + [mats[-1 - (i % 2)]]
         t0 = time.perf_counter()
-        for (w, s, x, y) in mats:
+        for (w, s, x, y) in step:
             orc.w8a32_gemv_timed(x, w, s, y, cores, native=native)
         times.append(time.perf_counter() - t0)
-    t_tok = float(np.median(times))
+        i += 1
+    t_step = float(np.median(times))
     model = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -348,13 +360,14 @@ def cpu_baseline(seconds=10.0):
                 break
     except OSError:
         pass
-    step_bytes = sum(gemv_bytes(N, K) for (_, N, K) in shapes)
-    return {"value": round(step_bytes / t_tok / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
-            "tok_s": round(1.0 / t_tok, 2), "steps_timed": len(times),
+    step_bytes = sum(gemv_bytes(N, K) for (_, N, K) in LAYER_SHAPES + [LM_HEAD])
+    return {"value": round(step_bytes / t_step / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
+            "ms_per_step": round(t_step * 1e3, 3), "steps_timed": len(times),
             "host_cpu": model, "nproc": os.cpu_count(),
             "sample": f"oracle M=1 GEMV ({'-march=native' if native else 'x86-64-v3'}, OpenMP, "
-                      f"{cores} threads) over whole decode steps (28 distinct layer sets + lm_head, "
-                      f"1.72 GB int8), median of {len(times)} steps in ~{seconds:.0f} s"}
+                      f"{cores} threads) over the benchmark's steps (one layer's projection set of 28 distinct "
+                      f"copies + one of two lm_head copies, 361.5 MB per step), median of {len(times)} steps "
+                      f"in ~{seconds:.0f} s"}
 
 
 def rotating(lin, torch, dev, N, K, min_bytes=600e6):
@@ -525,6 +538,11 @@ def main():
         return
     log("building the decode set (1.72 GB of int8 weights)")
     items = build_decode_set(lin, torch, dev)
+    # the benchmark's steps: layer copy l's projection set + the lm_head, l = 0..27
+    nl = len(LAYER_SHAPES)
+    seq = []
+    for l in range(LAYERS):
+        seq += items[nl * l:nl * l + nl] + [items[-1]]
     if args.traffic_probe:
         src = torch.empty(COPY_PROBE_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
@@ -532,38 +550,65 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         st = torch.cuda.current_stream()
-        run_step(lin, items, st)
+        run_step(lin, seq, st)
         torch.cuda.synchronize()
         log("traffic probe done")
         return
-    step_bytes = sum(gemv_bytes(N, K) for (_, N, K, *_r) in items)
+    step_bytes = sum(gemv_bytes(N, K) for (_, N, K) in LAYER_SHAPES + [LM_HEAD])
     stream = torch.cuda.Stream()
 
-    log("warm-up (eager) and graph capture")
-    with torch.cuda.stream(stream):
-        for _ in range(max(1, args.warmup)):
-            run_step(lin, items, stream)
-    stream.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        run_step(lin, items, stream)
-    torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
+    def capture(its):
+        with torch.cuda.stream(stream):
+            for _ in range(max(1, args.warmup)):
+                run_step(lin, its, stream)
+        stream.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            run_step(lin, its, stream)
+        torch.cuda.synchronize()
+        for _ in range(args.warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        return g
 
-    log(f"timing {args.steps} graph replays")
+    def time_replays(g, reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / reps, time.perf_counter() - t0
+
+    log("warm-up (eager) and graph capture: one graph per step (layer copy l + lm_head)")
+    graphs = [capture(seq[(nl + 1) * l:(nl + 1) * (l + 1)]) for l in range(LAYERS)]
+    for i in range(args.warmup):
+        graphs[i % LAYERS].replay()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     e0.record()
-    for _ in range(args.steps):
-        graph.replay()
+    for i in range(args.steps):
+        graphs[i % LAYERS].replay()
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     t_step = e0.elapsed_time(e1) * 1e-3 / args.steps
     value = step_bytes / t_step / 1e9
+    del graphs
+
+    log("the full decoder step: 28 layers + lm_head in one graph")
+    graph28 = capture(items)
+    t28, _ = time_replays(graph28, max(5, args.steps // 5))
+    bytes28 = sum(gemv_bytes(N, K) for (_, N, K, *_r) in items)
+    step28 = {"ms": round(t28 * 1e3, 4), "GBps": round(bytes28 / t28 / 1e9, 1),
+              "frac_hbm": round(bytes28 / t28 / 1e9 / HBM_PEAK_GBS, 4), "launches": len(items),
+              "bytes": bytes28, "tok_s_linear_layers": round(1.0 / t28, 1)}
+    del graph28
 
     log("per-shape launch timing (graph replay)")
     per = time_shapes(lin, torch, items, stream, max(5, args.kernel_reps))
@@ -572,15 +617,15 @@ def main():
         b = gemv_bytes(N, K)
         per_shape[key] = {"N": N, "K": K, "us": round(t * 1e6, 2), "GBps": round(b / t / 1e9, 1),
                           "frac_hbm": round(b / t / 1e9 / HBM_PEAK_GBS, 4)}
-    # every launch of the step is the GEMV kernel and graph replay runs them
-    # back to back, so its average launch duration is the step time over the
-    # launch count
-    avg_bytes = step_bytes / len(items)
-    avg_t = t_step / len(items)
+    # every launch is the GEMV kernel and the replays run them back to back,
+    # so its average launch duration is the step time over the launches per step
+    n_per_step = len(LAYER_SHAPES) + 1
+    avg_bytes = step_bytes / n_per_step
+    avg_t = t_step / n_per_step
     achieved = avg_bytes / avg_t / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                "kernel": "gemv_i8_kernel (all 113 launches of a step)",
+                "kernel": f"gemv_i8_kernel (all {n_per_step} launches of a step)",
                 "bytes_per_launch": round(avg_bytes), "avg_launch_us": round(avg_t * 1e6, 3),
                 "per_shape": per_shape}
 
@@ -588,8 +633,6 @@ def main():
     greedy = bench_lm_head_greedy(lin, torch, items[-1][3], items[-1][2], dev, stream)
 
     # the decode set's 1.72 GB is no longer needed
-    n_launch = len(items)
-    del graph
     for it in items:
         it[3].close()
     del items
@@ -631,13 +674,14 @@ def main():
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic",
-        "config": {"workload": "decode projection set of the Qwen3-VL-2B text decoder, W8A32 batch=1: "
-                               "28 x (QKV 4096x2048, O 2048x2048, gate_up 12288x2048, down 2048x6144) "
-                               "+ lm_head 151936x2048, distinct weights, HIP-graph replay",
-                   "step_bytes": step_bytes, "launches_per_step": n_launch},
-        "decode_tok_s": round(1.0 / t_step, 1),
+        "config": {"workload": "batch-1 decode projection set of one Qwen3-VL-2B text layer + lm_head, "
+                               "W8A32: QKV 4096x2048, O 2048x2048, gate_up 12288x2048, down 2048x6144, "
+                               "lm_head 151936x2048; one HIP graph per step, step i on layer copy i % 28 "
+                               "of 28 distinct ones (every step's weights from HBM)",
+                   "step_bytes": step_bytes, "launches_per_step": len(LAYER_SHAPES) + 1},
         "wall_s": round(wall, 3),
         "roofline": roofline,
+        "decode_step_28_layers": step28,
         "lm_head_greedy": greedy,
         "decoder_greedy": dec,
         "w8a8_prefill": prefill,
