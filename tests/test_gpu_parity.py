@@ -277,10 +277,10 @@ def test_small_m_wide_n(lin, orc, M, N, K):
     assert rel_l2(lin.w8a8_linear(xq, xs, w, s), orc.w8a8_linear(xq, xs, w, s)) <= 1e-5
 
 
-@pytest.mark.parametrize("M,N,K", [(20, 256, 2048), (3, 32800, 2048), (24, 300, 130)])
+@pytest.mark.parametrize("M,N,K", [(40, 256, 2048), (3, 32800, 2048), (36, 300, 130)])
 def test_w8a32_planes_special_rows(lin, orc, M, N, K):
     """Batches that run on the int8 MFMA over four int8 planes per fp32 token
-    (more than 16 tokens, or an lm_head-wide N): rows of zeros, of 1e-36 and
+    (more than 32 tokens, or an lm_head-wide N): rows of zeros, of 1e-36 and
     of 1e35 magnitude (power-of-two plane scales far from 1; the outputs stay
     normal floats, so the oracle's own rounding is fp32's), a row with one outlier
     1000x its rms are each within relative L2 1e-5 of the oracle's fp32
@@ -313,6 +313,37 @@ def test_w8a32_planes_special_rows(lin, orc, M, N, K):
             assert rel_l2(got[r], want[r]) <= 1e-5, (r, rel_l2(got[r], want[r]))
     # and the same call twice gives the same bits
     np.testing.assert_array_equal(lin.w8a32_linear(x, w, s, bias=b), got)
+
+
+@pytest.mark.parametrize("M,N,K", [(6, 300, 2048), (20, 2048, 2048)])
+def test_w8a32_small_batch_special_rows(lin, orc, M, N, K):
+    """Small batches on narrow weights (up to 32 tokens, N < 32768) split fp32
+    X into three bf16 terms inside the small-M kernel: rows of zeros, of 1e-36
+    and of 1e30 magnitude and a 1000x outlier row are within relative L2 1e-5
+    of the oracle; a row holding NaN or Inf gives NaN in every output.  (This
+    path sums w * x before the row's weight scale, so activations with an rms
+    above about 1e34 would overflow where the reference, which scales every
+    weight first, stays finite.)"""
+    say(f"w8a32 small-batch special rows M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 5 + N + K)
+    x, w, s = make(rng, M, N, K)
+    x[0] = 0.0
+    x[1] *= F(1e-36)
+    x[2] *= F(1e30)
+    x[3, 17] = F(1000.0) * np.sqrt(np.mean(x[3] ** 2))
+    nan_row, inf_row = M - 1, M - 2
+    x[nan_row, 5] = np.nan
+    x[inf_row, 9] = np.inf
+    b = rng.standard_normal(N).astype(F)
+    got = lin.w8a32_linear(x, w, s, bias=b)
+    want = orc.w8a32_linear(x, w, s, bias=b)
+    for r in range(M):
+        if r in (nan_row, inf_row):
+            assert not np.isfinite(want[r]).any() and np.isnan(got[r]).all(), r
+        elif r == 0:
+            np.testing.assert_allclose(got[r], b, rtol=0, atol=0)
+        else:
+            assert rel_l2(got[r], want[r]) <= 1e-5, (r, rel_l2(got[r], want[r]))
 
 
 def test_w8a32_prefill_rows_consistent(lin, orc):

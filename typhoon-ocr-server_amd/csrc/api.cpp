@@ -381,10 +381,12 @@ void op_w8a32(const float* X, const tl_weights* W, const float* bias, float* Y, 
       L.xs_in = xs;
     }
     run_gemv(ws, L, st);
-  } else if (batch <= 16 && W->NG < 2048) {
+  } else if ((batch <= 16 && W->NG < 2048) || (batch <= 32 && W->NG <= 256)) {
     // a few token rows over a narrow weight: the small-M kernel splits the
     // fp32 rows into three bf16 terms as it loads them (one launch; a
-    // separate plane split costs more than it saves at these sizes)
+    // separate plane split costs more than it saves at these sizes: at
+    // N <= 4096, 24-32 tokens 13.7-15.1 us here against 16.6-17.0 us on the
+    // planes, which win from 48 tokens)
     GemmLaunch L;
     L.amode = A_F32X3;
     L.A = X;
