@@ -389,8 +389,9 @@ hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st) {
   const int r = a.NG >= 2048 ? 4 : 1;
   const int tg = a.MG <= 1 ? 1 : (a.MG <= 2 ? 2 : 4);
   // batches of 4 tiles only with one token group: more activation fragments
-  // in flight push the waves past 256 VGPRs (one wave per SIMD)
-  const int u = (r == 1 && n_t >= 8 && tg == 1) ? 4 : 2;
+  // in flight push the waves past 256 VGPRs (one wave per SIMD); int8 codes
+  // (one 16-byte fragment per tile) also with four row groups
+  const int u = (tg == 1 && n_t >= 8 && (r == 1 || L.amode == A_I8)) ? 4 : 2;
   switch (L.amode) {
     case A_I8: launch_small_mode<A_I8>(a, u, r, tg, st); break;
     case A_BF16: launch_small_mode<A_BF16>(a, u, r, tg, st); break;
