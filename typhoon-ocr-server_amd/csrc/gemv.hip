@@ -37,6 +37,8 @@
 
 namespace tl {
 
+constexpr int kNpNormStride = 136;   // LDS floats per 128-block of the final RMSNorm's squares
+
 struct GemvArgs {
   const float* x;      // fp32 activation [K]                (XV > 0)
   const uint8_t* xq;   // int8 codes zero padded to KB*64    (XV == 0)
@@ -124,7 +126,9 @@ __device__ __forceinline__ void load_batch(uint4 (&b)[U], uint4 (&c)[XV == 0 ? U
 // 128-block b folds x[128b + 8i + j]^2 over i in order, xor butterflies
 // combine the 8 accumulators of a block and the 8 blocks of a wave, every
 // thread finishes the balanced tree over the groups of 8 blocks itself.
-// Then x = fl(fl(x / rms) * w).  Uses the dynamic LDS of the launch (4K bytes).
+// Then x = fl(fl(x / rms) * w).  Uses the dynamic LDS of the launch
+// (kNpNormStride floats per 128-block: the 8-float pad puts the 64 lanes of a
+// fold step, 8 blocks x 8 accumulators, on 64 distinct banks).
 template <int XV>
 __device__ void final_rmsnorm(float4 (&xv)[XV], const float4 (&nwv)[XV], bool has_w, int K, float eps) {
   extern __shared__ float s_sq[];
@@ -132,7 +136,8 @@ __device__ void final_rmsnorm(float4 (&xv)[XV], const float4 (&nwv)[XV], bool ha
 #pragma unroll
   for (int i = 0; i < XV; i++) {
     const float4 v = xv[i];
-    reinterpret_cast<float4*>(s_sq)[threadIdx.x + 256 * i] =
+    const int e = 4 * (threadIdx.x + 256 * i);        // element index, a multiple of 4
+    *reinterpret_cast<float4*>(s_sq + kNpNormStride * (e >> 7) + (e & 127)) =
         make_float4(__fmul_rn(v.x, v.x), __fmul_rn(v.y, v.y), __fmul_rn(v.z, v.z), __fmul_rn(v.w, v.w));
   }
   __syncthreads();
@@ -142,7 +147,7 @@ __device__ void final_rmsnorm(float4 (&xv)[XV], const float4 (&nwv)[XV], bool ha
     const int b = p >> 3, j = p & 7;
     float r = 0.0f;
     if (b < nb) {
-      const float* src = s_sq + 128 * b + j;
+      const float* src = s_sq + kNpNormStride * b + j;
       r = src[0];
 #pragma unroll
       for (int i = 1; i < 16; i++) r = __fadd_rn(r, src[8 * i]);
@@ -465,7 +470,7 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
 template <int XV, int U, int RH>
 static void launch_one(const GemvArgs& a, int blocks, hipStream_t st) {
   const int flags = (a.x_vec & 3) | ((a.epi & 7) << 2) | (a.bias ? 32 : 0) | ((a.norm & 3) << 6);
-  const size_t dyn = a.norm == NORM_NUMPY ? (size_t)a.K * sizeof(float) : 0;
+  const size_t dyn = a.norm == NORM_NUMPY ? (size_t)(a.K / 128) * kNpNormStride * sizeof(float) : 0;
   hipLaunchKernelGGL((gemv_i8_kernel<XV, U, RH>), dim3(blocks), dim3(256), dyn, st, a.x, a.wt, a.ws, a.y,
                      a.N, a.K, a.NG, a.KB, flags, a.xq, a.xs_in, a.bias, a.acc_out, a.xs_out, a.keys,
                      a.norm_w, a.norm_eps);
@@ -508,11 +513,13 @@ int gemv_fused_xv(int K) {
 }
 
 // The in-GEMV final RMSNorm needs all of x in registers (K == 1024 XV, both
-// vectors 16-byte aligned) and a power-of-two K (numpy's pairwise tree is
-// then balanced).
+// vectors 16-byte aligned), a power-of-two K (numpy's pairwise tree is then
+// balanced) and its padded squares within 64 KiB of LDS.
 bool gemv_fused_norm_ok(int K, const float* x, const float* norm_w) {
   const int xv = gemv_fused_xv(K);
   if (xv == 0 || K != 1024 * xv || (K & (K - 1)) != 0) return false;
+  // the padded squares must fit 64 KiB of dynamic LDS (K <= 8192)
+  if ((size_t)(K / 128) * kNpNormStride * sizeof(float) > 65536) return false;
   return ((((uintptr_t)x) | ((uintptr_t)norm_w)) & 15) == 0;
 }
 
