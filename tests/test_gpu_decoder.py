@@ -309,6 +309,42 @@ def test_chunked_prefill_equals_full_prefill(lin, orc, dev):
     d.close()
 
 
+def test_prefill_split_keys_matches_oracle(lin, orc, dev):
+    """Prefill attention's split query tiles: at 330 tokens the last three
+    64-query tiles (6, 5 and 4 key tiles, the last ragged) run as two halves
+    of their key range merged by the second half to arrive; 64-token chunks
+    after the first are single query tiles, also split (the chunk at
+    position 64 into a half whose keys are all past its first queries, which
+    must merge as empty).  Hidden
+    rows against the oracle's prefill layer (relative L2 <= 1e-3, as the
+    unsplit prefill), chunks against the full prefill (<= 1e-3), and a repeat
+    bit for bit (the halves merge in a fixed order whichever finishes
+    first)."""
+    from typhoon_ocr_server_amd import decoder as dec
+    say("split-key prefill vs oracle, 1 layer x 330 tokens; 64-token chunks")
+    rng = np.random.default_rng(27)
+    layers, _, _ = _model(rng, orc, 1)
+    S, max_seq = 330, 384
+    d = dec.Decoder(layers, max_seq=max_seq)
+    ol = _oracle_layers(d, layers)
+    h0 = (rng.standard_normal((S, 2048)) * 2).astype(F)
+    d.reset()
+    hg = d.prefill(h0)
+    kc = np.zeros((8, max_seq, 128), F)
+    vc = np.zeros((8, max_seq, 128), F)
+    ho = orc.prefill_layer(ol[0], kc, vc, h0.copy(), cos_tab=d._cos_tab, sin_tab=d._sin_tab)
+    assert rel_l2(hg, ho) <= 1e-3, rel_l2(hg, ho)
+    for t0 in (0, 63, 64, 250, 329):    # rows of unsplit and split tiles
+        assert rel_l2(hg[t0], ho[t0]) <= 1e-3, t0
+    d.reset()
+    np.testing.assert_array_equal(d.prefill(h0), hg)
+    d.reset()
+    ch = d.prefill(h0, chunk=64)
+    assert d.cache_len == S
+    assert rel_l2(ch, hg) <= 1e-3
+    d.close()
+
+
 def test_prefill_then_greedy_decode_matches_oracle(lin, orc, dev):
     """3-D prefill of 100 tokens, rope offset as the reference sets it after a
     multimodal prefill, then 8 greedy steps on the device: the tokens equal the

@@ -125,6 +125,7 @@ struct DecoderScratch {
   PinnedBuf pin_rows;                   // prefill hidden rows on their way to / from HBM
   // prefill activations (token-major, grown to the longest prefill)
   DevBuf p_h, p_xn, p_qkv, p_att, p_gu, p_mlp, p_y, p_cos, p_sin;
+  DevBuf p_fpart, p_fcnt;               // prefill attention's split-key partials and counters (zero between launches)
   // captured graphs and what they were captured for
   hipGraphExec_t layers_exec = nullptr;
   const void* layers_key[4] = {nullptr, nullptr, nullptr, nullptr};
@@ -241,7 +242,8 @@ void enqueue_prefill(const ModelWeights* m, KVCache* c, DecoderScratch* s, int S
     linear(Xn, L.qkv, nullptr, QKV, S, st);
     HIP_OK(launch_prefill_qk(QKV, L.norms + 2 * H, L.norms + 2 * H + HDIM, cos_rows, sin_rows, kc, vc, c->max_seq,
                              row0, S, NKV, EPS, st));
-    HIP_OK(launch_flash_prefill(QKV, kc, vc, ATT, S, NQ, c->max_seq, key0, qoff, SCALE, st));
+    HIP_OK(launch_flash_prefill(QKV, kc, vc, ATT, S, NQ, c->max_seq, key0, qoff, SCALE,
+                                static_cast<float*>(s->p_fpart.p), static_cast<int*>(s->p_fcnt.p), st));
     linear(ATT, L.o, nullptr, Y, S, st);
     HIP_OK(launch_residual_add(Y, Hd, n, st));
     HIP_OK(launch_rmsnorm_rows(Hd, L.norms + H, Xn, S, H, EPS, st));
@@ -260,6 +262,12 @@ void ensure_prefill_buffers(DecoderScratch* s, int S) {
   s->p_gu.ensure((size_t)S * 2 * FF * 4, s->st);
   s->p_mlp.ensure((size_t)S * FF * 4, s->st);
   s->p_y.ensure((size_t)S * H * 4, s->st);
+  s->p_fpart.ensure(flash_split_floats(S, NQ) * 4, s->st);
+  const size_t cb = flash_split_counters(S, NQ) * sizeof(int);
+  if (cb > s->p_fcnt.n) {
+    s->p_fcnt.ensure(cb, s->st);
+    HIP_OK(hipMemset(s->p_fcnt.p, 0, s->p_fcnt.n));
+  }
 }
 
 // host copy between the caller's (pageable) rows and the pinned staging
@@ -515,7 +523,8 @@ void decoder_scratch_free_fn(DecoderScratch* s) {
   for (float* p : {s->hidden, s->qkv, s->attn, s->mlp, s->pm, s->pl, s->po})
     if (p) (void)hipFree(p);
   if (s->count) (void)hipFree(s->count);
-  for (DevBuf* b : {&s->p_h, &s->p_xn, &s->p_qkv, &s->p_att, &s->p_gu, &s->p_mlp, &s->p_y, &s->p_cos, &s->p_sin})
+  for (DevBuf* b : {&s->p_h, &s->p_xn, &s->p_qkv, &s->p_att, &s->p_gu, &s->p_mlp, &s->p_y, &s->p_cos, &s->p_sin,
+                    &s->p_fpart, &s->p_fcnt})
     if (b->p) (void)hipFree(b->p);
   if (s->keys.p) (void)hipFree(s->keys.p);
   if (s->tokens.p) (void)hipFree(s->tokens.p);

@@ -32,16 +32,6 @@ constexpr int ATT_T = 64;        // positions per attention work-group
 
 
 
-// Loads of the partials.  The merge runs in the same launch that wrote them,
-// possibly on another XCD, so it reads them with agent-scope atomic loads
-// (coherent across the XCDs' L2 caches) and they were stored with
-// agent-scope atomic stores.
-__device__ __forceinline__ float ld_agent(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_agent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c over the nc live chunks
 // of q head qh, element d; chunks in batches of 32 (all loads of a batch in

@@ -13,6 +13,8 @@
 // [S][2048], qkv [S][4096] (q | k | v), attention output [S][2048], gate/up
 // [S][12288] in the decoder's per-16-row interleave, mlp [S][6144].  The KV
 // cache is [kv head][max_seq][128] per layer.
+#include <algorithm>
+
 #include "tl_common.h"
 #include "tl_kernels.h"
 
@@ -147,15 +149,54 @@ constexpr int FT = 64;          // queries / keys per tile
 // the LDS rate; the swizzle and the 4-row pattern run at full rate.)
 // Each 16-key block's K operands, and each 4-key group's V operands, are read
 // into registers one block ahead of their MFMAs.
+//
+// Split keys: the causal work of a query tile grows with its index, so the
+// last tile's work-group alone would set the kernel's length.  A query tile
+// whose key tiles exceed half of the longest tile's (and number at least 4)
+// becomes two work items over the two halves of its key range.  Each half
+// stores its unnormalised output, running max and sum (agent-scope stores,
+// acknowledged before its arrival count), and the second to arrive combines
+// the two in a fixed order (half 0, then half 1) and writes the output, so
+// the result does not depend on which half finishes first.  Work items run
+// longest first (the unsplit tiles and the split tiles' halves, each list
+// already in decreasing length, merged); the host picks how many of the
+// longest tiles to split from the makespan of that order on the GPU's CUs.
+constexpr int FPART = 32 * 256 + 2 * 256;   // floats of one half's partials: O (32 per lane), m, l
+
+// Work items of one q head with query tiles qs .. ntq-1 split: list A holds
+// the unsplit tiles qs-1 .. 0, list B the halves (tile ntq-1 half 0, half 1,
+// tile ntq-2 half 0, ...); both are in non-increasing length (a tile's key
+// tiles grow by at most one per query tile) and the launch order merges
+// them, longest first, ties to A.
+struct FlashPlan {
+  int S, qoff, qs, ntq;
+  __host__ __device__ int nkt(int t) const { return (qoff + t * FT + min(FT, S - t * FT) - 1) / FT + 1; }
+  __host__ __device__ int len_a(int a) const { return nkt(qs - 1 - a); }
+  __host__ __device__ int len_b(int b) const {
+    const int n = nkt(ntq - 1 - (b >> 1));
+    return (b & 1) ? n >> 1 : (n + 1) >> 1;
+  }
+  // the next item comes from A after a items of A and b of B
+  __host__ __device__ bool take_a(int a, int b) const {
+    return a < qs && (b >= 2 * (ntq - qs) || len_a(a) >= len_b(b));
+  }
+};
 
 __global__ __launch_bounds__(256) void flash_prefill_mfma_kernel(const float* __restrict__ qkv,
                                                                  const float* __restrict__ kc,
                                                                  const float* __restrict__ vc, float* __restrict__ out,
                                                                  int S, int max_seq, int key0, int qoff, float scale,
-                                                                 int nheads) {
-  // longest first over all heads: work-group L takes query tile ntq-1-L/nheads
-  const int ntq = cdiv(S, FT);
-  const int qt = ntq - 1 - (int)blockIdx.x / nheads;
+                                                                 int nheads, int qs, float* __restrict__ part,
+                                                                 int* __restrict__ cnt) {
+  // work item L / nheads of q head L % nheads in the launch order above;
+  // query tiles qs .. ntq-1 are split into two halves of their key range
+  const FlashPlan plan{S, qoff, qs, cdiv(S, FT)};
+  const int item = (int)blockIdx.x / nheads;
+  int ia = 0, ib = 0;
+  for (int k = 0; k < item; k++) plan.take_a(ia, ib) ? ia++ : ib++;
+  const bool unsplit = plan.take_a(ia, ib);
+  const int qt = unsplit ? qs - 1 - ia : plan.ntq - 1 - (ib >> 1);
+  const int half = unsplit ? -1 : (ib & 1);
   const int qh = (int)blockIdx.x % nheads, h = qh >> 1;
   const int q0 = qt * FT;
   const int nq = min(FT, S - q0);
@@ -186,6 +227,9 @@ __global__ __launch_bounds__(256) void flash_prefill_mfma_kernel(const float* __
   float m = -3.0e38f, l = 0.0f;
 
   const int nkt = (qoff + q0 + nq - 1) / FT + 1;
+  const int kmid = (nkt + 1) / 2;
+  const int kt_begin = half == 1 ? kmid : 0;
+  const int kt_end = half == 0 ? kmid : nkt;
   // copy q (0..7) of this wave: tile rows R = 16 wv + 2q + (lane >> 5), slot
   // p = lane & 31 (every lane reads a valid row: keys past the end clamp)
   const int rsub = lane >> 5, p = lane & 31;
@@ -201,13 +245,13 @@ __global__ __launch_bounds__(256) void flash_prefill_mfma_kernel(const float* __
       dma_tile(reinterpret_cast<const uint4*>(vbase + (size_t)vkey * (PHD / 4) + p), vb + dst);
     }
   };
-  issue_tile(0, 0);
-  for (int kt = 0; kt < nkt; kt++) {
-    const int cb = kt & 1;
+  issue_tile(kt_begin, 0);
+  for (int kt = kt_begin; kt < kt_end; kt++) {
+    const int cb = (kt - kt_begin) & 1;
     wait_vm<0>();                           // this wave's copies of tile kt landed
     wait_lgkm0();                           // and its reads of tile kt - 1 are done
     stage_barrier();                        // every wave's: tile kt visible, buffer of kt - 1 free
-    if (kt + 1 < nkt) issue_tile(kt + 1, cb ^ 1);
+    if (kt + 1 < kt_end) issue_tile(kt + 1, cb ^ 1);
     const float* sK = reinterpret_cast<const float*>(&sKV[cb][0][0]);
     const float* sV = reinterpret_cast<const float*>(&sKV[cb][1][0]);
 
@@ -292,6 +336,42 @@ __global__ __launch_bounds__(256) void flash_prefill_mfma_kernel(const float* __
       o[7] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1.w, pk, o[7], 0, 0, 0);
     }
   }
+  if (half >= 0) {
+    // store this half's partials (layout: O element e of thread t at e 256 + t)
+    float* mine = part + ((size_t)(qt * nheads + qh) * 2 + half) * FPART;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) st_agent(mine + (4 * j + r) * 256 + tid, o[j][r]);
+    st_agent(mine + 32 * 256 + tid, m);
+    st_agent(mine + 33 * 256 + tid, l);
+    __shared__ int s_last;
+    asm volatile("" ::: "memory");
+    wait_vm<0>();                           // the stores are acknowledged
+    asm volatile("" ::: "memory");
+    __syncthreads();
+    int* c = cnt + qt * nheads + qh;
+    if (tid == 0) s_last = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
+    __syncthreads();
+    if (!s_last) return;
+    if (tid == 0) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // combine half 0 and half 1 in that order
+    const float* other = part + ((size_t)(qt * nheads + qh) * 2 + (1 - half)) * FPART;
+    const float mo = ld_agent(other + 32 * 256 + tid), lo = ld_agent(other + 33 * 256 + tid);
+    const float m0 = half == 0 ? m : mo, m1 = half == 0 ? mo : m;
+    const float l0 = half == 0 ? l : lo, l1 = half == 0 ? lo : l;
+    const float M = fmaxf(m0, m1);
+    const float a0 = expf(__fsub_rn(m0, M)), a1 = expf(__fsub_rn(m1, M));
+    l = __fadd_rn(__fmul_rn(l0, a0), __fmul_rn(l1, a1));
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float ov = ld_agent(other + (4 * j + r) * 256 + tid);
+        const float o0 = half == 0 ? o[j][r] : ov, o1 = half == 0 ? ov : o[j][r];
+        o[j][r] = __fadd_rn(__fmul_rn(o0, a0), __fmul_rn(o1, a1));
+      }
+  }
   if (qloc < nq) {
     const float inv = __fdiv_rn(1.0f, l);
     float* op = out + (size_t)(q0 + qloc) * 2048 + qh * PHD + 16 * g;
@@ -343,11 +423,51 @@ hipError_t launch_prefill_qk(float* qkv, const float* q_norm, const float* k_nor
   return hipGetLastError();
 }
 
+// First query tile whose key range is split (ntq: none): the qs whose launch
+// order has the shortest makespan under list scheduling on `mach` machines
+// (the CUs per q head: each item runs once per head), an item costing 4 per
+// key tile plus 1 for a half's partial hand-over.  Past 2 tiles per machine
+// the unsplit launch is balanced already.
+int flash_split_first(int S, int qoff, int mach) {
+  const int ntq = cdiv(S, FT);
+  if (mach < 1 || ntq > 2 * mach) return ntq;
+  auto makespan = [&](int qs) {
+    const FlashPlan p{S, qoff, qs, ntq};
+    int load[64] = {};
+    const int nm = std::min(mach, 64);
+    int a = 0, b = 0, worst = 0;
+    for (int k = 0; k < ntq + (ntq - qs); k++) {
+      const int cost = p.take_a(a, b) ? 4 * p.len_a(a++) : 4 * p.len_b(b++) + 1;
+      int* lo = std::min_element(load, load + nm);
+      *lo += cost;
+      worst = std::max(worst, *lo);
+    }
+    return worst;
+  };
+  int best_qs = ntq, best = makespan(ntq);
+  for (int qs = ntq - 1; qs >= 0 && FlashPlan{S, qoff, qs, ntq}.nkt(qs) >= 2; qs--) {
+    const int m = makespan(qs);
+    if (m < best) best = m, best_qs = qs;
+  }
+  return best_qs;
+}
+
+size_t flash_split_floats(int S, int nq) { return (size_t)cdiv(S, FT) * nq * 2 * FPART; }
+size_t flash_split_counters(int S, int nq) { return (size_t)cdiv(S, FT) * nq; }
+
 hipError_t launch_flash_prefill(const float* qkv, const float* kc, const float* vc, float* out, int S, int nq,
-                                int max_seq, int key0, int qoff, float scale, hipStream_t st) {
+                                int max_seq, int key0, int qoff, float scale, float* part, int* cnt,
+                                hipStream_t st) {
   if (S < 1 || key0 < 0 || qoff < 0 || key0 + qoff + S > max_seq) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(flash_prefill_mfma_kernel, dim3(cdiv(S, FT) * nq), dim3(256), 0, st, qkv, kc, vc, out, S,
-                     max_seq, key0, qoff, scale, nq);
+  const int ntq = cdiv(S, FT);
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return hipErrorInvalidDevice;
+  const int qs = (part && cnt) ? flash_split_first(S, qoff, cus / nq) : ntq;
+  const int items = ntq + (ntq - qs);
+  hipLaunchKernelGGL(flash_prefill_mfma_kernel, dim3(items * nq), dim3(256), 0, st, qkv, kc, vc, out, S,
+                     max_seq, key0, qoff, scale, nq, qs, part, cnt);
   return hipGetLastError();
 }
 

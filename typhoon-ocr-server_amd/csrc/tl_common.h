@@ -363,6 +363,17 @@ __device__ __forceinline__ void wait_vm() {
 }
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x3 << 14)); }
 
+// Partials handed between work-groups of one launch, which may sit on
+// different XCDs: stored with agent-scope atomic stores (they bypass the
+// XCD's non-coherent L2 path; a store is visible device-wide once vmcnt
+// acknowledges it) and read with agent-scope atomic loads.
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // One 1 KiB tile global -> LDS: lane l's 16 bytes land at lds_base + 16 l.
 // Issued as volatile asm with a memory clobber so the compiler neither moves
 // it across the stage barrier nor adds its own (conservative) vmcnt waits in

@@ -80,8 +80,14 @@ hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int r
 hipError_t launch_prefill_qk(float* qkv, const float* q_norm, const float* k_norm, const float* cos_t,
                              const float* sin_t, float* kc, float* vc, int max_seq, int row0, int S, int nkv,
                              float eps, hipStream_t st);
+// part / cnt: work-space for splitting the longest query tiles' key ranges in
+// two (flash_split_floats floats, flash_split_counters ints zeroed once: the
+// kernel leaves them zero); null: no split
+size_t flash_split_floats(int S, int nq);
+size_t flash_split_counters(int S, int nq);
 hipError_t launch_flash_prefill(const float* qkv, const float* kc, const float* vc, float* out, int S, int nq,
-                                int max_seq, int key0, int qoff, float scale, hipStream_t st);
+                                int max_seq, int key0, int qoff, float scale, float* part, int* cnt,
+                                hipStream_t st);
 hipError_t launch_swiglu_rows(const float* gu, float* mlp, int S, int ffn, hipStream_t st);
 hipError_t launch_residual_add(const float* y, float* h, long long n, hipStream_t st);
 
