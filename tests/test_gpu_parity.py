@@ -277,7 +277,7 @@ def test_small_m_wide_n(lin, orc, M, N, K):
     assert rel_l2(lin.w8a8_linear(xq, xs, w, s), orc.w8a8_linear(xq, xs, w, s)) <= 1e-5
 
 
-@pytest.mark.parametrize("M,N,K", [(40, 256, 2048), (3, 32800, 2048), (36, 300, 130)])
+@pytest.mark.parametrize("M,N,K", [(40, 256, 2048), (3, 32800, 2048), (7, 32800, 2048), (36, 300, 130)])
 def test_w8a32_planes_special_rows(lin, orc, M, N, K):
     """Batches that run on the int8 MFMA over four int8 planes per fp32 token
     (more than 32 tokens, or an lm_head-wide N): rows of zeros, of 1e-36 and

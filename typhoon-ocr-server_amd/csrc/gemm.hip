@@ -418,9 +418,13 @@ hipError_t launch_gemm(const GemmLaunch& L, hipStream_t st) {
   // int8 rows and 48 16-bit rows (measured at N = 2048 / 4096: 64 bf16 rows
   // 14.1 us here against 11.3 us tiled, 48 rows even, 32 rows 8.2 against
   // 11.4 us; int8 rows faster here up to 64); for wide N the activation
-  // fragments every work-group re-reads cost more than the tiled kernels' reuse
+  // fragments every work-group re-reads cost more than the tiled kernels' reuse,
+  // except up to 32 int8 rows at lm_head width (>= 2048 row groups, four per
+  // work-group share each fragment): the int8 planes of 5-8 fp32 tokens,
+  // 81 -> 70 us for the lm_head at 8 tokens
   const int small_rows = (L.amode == A_BF16 || L.amode == A_F16) ? 48 : 64;
-  if (gemm_small_supported(L) && (L.M <= 16 || (L.M <= small_rows && cdiv(L.N, 16) <= 256)))
+  const bool wide_i8 = L.amode == A_I8 && L.M <= 32 && cdiv(L.N, 16) >= 2048;
+  if (gemm_small_supported(L) && (L.M <= 16 || (L.M <= small_rows && cdiv(L.N, 16) <= 256) || wide_i8))
     return launch_gemm_small(L, st);
   if (L.amode == A_I8 && L.M > 16) return launch_gemm_i8(L, st);
   if (L.amode != A_I8 && L.M > 16 && gemm_b16_supported(L)) return launch_gemm_b16(L, st);
