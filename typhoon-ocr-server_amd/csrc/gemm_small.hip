@@ -204,16 +204,11 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
       const int t = min(t0 + u, last);
 #pragma unroll
       for (int r = 0; r < R; r++) {
-        if constexpr (R == 4) {
-          // four row groups per work-group: lm_head-wide N, whose weight
-          // stream goes through non-temporal (streaming) loads as the GEMV's
-          // (lm_head at M = 2: 66 -> 61 us)
-          typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
-          const v4u_t w = __builtin_nontemporal_load(reinterpret_cast<const v4u_t*>(wbase + (size_t)t * tstride + goff[r]));
-          b[u][r] = make_uint4(w.x, w.y, w.z, w.w);
-        } else {
-          b[u][r] = wbase[(size_t)t * tstride + goff[r]];
-        }
+        // each weight tile is read once per launch: non-temporal (streaming)
+        // loads, as the GEMV's (lm_head at M = 2: 66 -> 60 us)
+        typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
+        const v4u_t w = __builtin_nontemporal_load(reinterpret_cast<const v4u_t*>(wbase + (size_t)t * tstride + goff[r]));
+        b[u][r] = make_uint4(w.x, w.y, w.z, w.w);
       }
 #pragma unroll
       for (int g = 0; g < TG; g++) x[u][g] = load_a<AMODE>(a, min(kb0 + t, a.KB - 1), g, lane);
