@@ -312,6 +312,27 @@ int tl_decoder_generate(const ModelWeights *model, KVCache *cache, DecoderScratc
                         const tl_weights *lm_head, const float *final_norm, const float *embed, int first_token,
                         int n_steps, int32_t *tokens, const float *cos_tab, const float *sin_tab);
 
+/* Test hooks (device pointers, synchronous on `stream`): one launch of the
+ * decoder's attention kernels on caller buffers, so attention can be checked
+ * alone against the reference's attention (kernel/attention.c).
+ *   tl_attn_decode_dev: the decode-mode attention step of decoder.c:72-118
+ *     for one token: qkv [16*128 | 8*128 | 8*128] is the QKV projection;
+ *     q and k heads get their RMSNorm (q_norm, k_norm [128]) and the rotation
+ *     at row rope_pos of cos_tab / sin_tab ([max_seq x 64]); k and v go to
+ *     row pos of k_cache / v_cache ([8][max_seq][128]); out [16*128] is the
+ *     GQA attention over rows 0..pos (kernel/attention.c:172-224).
+ *   tl_attn_prefill_dev: the causal attention of S queries (q heads of the
+ *     token-major qkv [S x 4096], already normalised and rotated) over cache
+ *     rows key0 .. key0 + qoff + t for query t (PREFILL_MODE: key0 = row of
+ *     the first query, qoff = 0; CHUNKED_PREFILL_MODE: key0 = 0, qoff = rows
+ *     before the chunk); out [S x 2048].  split != 0 lets the longest query
+ *     tiles run as two halves of their key range (the decoder's default). */
+int tl_attn_decode_dev(const float *qkv, const float *q_norm, const float *k_norm, const float *cos_tab,
+                       const float *sin_tab, float *k_cache, float *v_cache, int max_seq, int pos, int rope_pos,
+                       float *out, void *stream);
+int tl_attn_prefill_dev(const float *qkv, const float *k_cache, const float *v_cache, float *out, int S,
+                        int max_seq, int key0, int qoff, int split, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

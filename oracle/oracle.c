@@ -22,10 +22,11 @@
  *       exact-tie cases (ties-to-even in the vector region, ties-away in the
  *       K%16 tail), x*fl(1/s) vs x/s discriminating cases, all-zero rows,
  *       NaN/Inf rows, and golden vectors computed independently in Python.
- *       One case is left unpinned: a row whose absmax is so small that
- *       absmax/127 underflows to 0 has inv = +inf, and its K%16 tail then
- *       evaluates (int)lroundf(+-inf), which C leaves unspecified (here:
- *       glibc's lroundf, 0 after the clamp; an AArch64 build may differ).
+ *       A row whose absmax is so small that fl(absmax/127) < 2^-128 has
+ *       inv = +inf, and its K%16 tail evaluates (int)lroundf(+-inf), which C
+ *       leaves unspecified.  That value is taken from how the reference's
+ *       AArch64 build evaluates it (fcvtas_x_low32 below), pinned by the
+ *       Arm architecture's FCVTAS definition in tests/test_oracle.py.
  *   orc_int_acc        -- pinned: brute-force Python integer dot products.
  *   orc_w8a32_linear   -- batch==1 pinned: closed form
  *       fl(fl(fl(acc)*ws)*xs) (+ bias as its own rounding) recomputed in
@@ -68,6 +69,22 @@ static inline int32_t fcvtns(float v)
     if (r >= 2147483648.0f) return INT32_MAX;
     if (r < -2147483648.0f) return INT32_MIN;
     return (int32_t)r;
+}
+
+/* (int)lroundf(v) as the reference's AArch64 build evaluates it: clang
+ * lowers lroundf (long is 64-bit there, math-errno off) to FCVTAS Xd, Sn --
+ * round to nearest with ties away from zero, saturating to int64, NaN -> 0
+ * (Arm ARM FPToFixed) -- and the conversion to int keeps the low 32 bits of
+ * the register.  Every finite v has |v| <= 127 (1 + 2^-21) here, so only the
+ * non-finite cases of an overflowing reciprocal reach the saturation:
+ * +inf -> INT64_MAX -> -1, -inf -> INT64_MIN -> 0. */
+static inline int32_t fcvtas_x_low32(float v)
+{
+    if (v != v) return 0;
+    if (v >= 9223372036854775808.0f) return -1;           /* low half of INT64_MAX */
+    if (v < -9223372036854775808.0f) return 0;            /* low half of INT64_MIN */
+    int64_t r = (int64_t)roundf(v);                        /* exact: |v| < 2^63 */
+    return (int32_t)(uint32_t)(uint64_t)r;
 }
 
 /* SQXTN s32->s16 then s16->s8 (vqmovn_s32, vqmovn_s16): saturating narrow. */
@@ -134,7 +151,7 @@ void orc_quantize_rows(const float *src, int8_t *dst, float *scales,
         }
         for (int k = main_end; k < cols; k++) {
             float v = row[k] * inv;
-            int q = (v != v) ? 0 : (int)lroundf(v);
+            int q = fcvtas_x_low32(v);
             if (q > 127) q = 127;
             if (q < -127) q = -127;
             out[k] = (int8_t)q;

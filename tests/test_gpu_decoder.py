@@ -393,3 +393,37 @@ def test_prefill_then_greedy_decode_matches_oracle(lin, orc, dev):
     np.testing.assert_array_equal(toks, np.array(want, np.int32))
     lm_dev.close()
     d.close()
+
+
+def test_generate_after_lm_head_replaced(lin, orc, dev):
+    """The captured generate graph bakes in the lm_head's device memory, so a
+    new lm_head handle must be recaptured even where the allocator hands back
+    the freed handle's host address: generate with one lm_head, destroy it,
+    create another with different codes, generate again; the tokens equal
+    the host step path on the second lm_head."""
+    import torch
+    from typhoon_ocr_server_amd import decoder as dec
+    say("generate, replace lm_head, generate vs step path")
+    rng = np.random.default_rng(28)
+    V = 8192
+    layers, lm, nw = _model(rng, orc, 1, vocab=V)
+    embed = (rng.standard_normal((V, 2048)) * 1.5).astype(F)
+    d = dec.Decoder(layers, lm_head=lm, final_norm=nw, max_seq=64)
+    embed_dev = torch.from_numpy(embed).to(dev)
+    other = lin.DeviceWeights.from_codes(rng.integers(-127, 128, (V, 2048), dtype=np.int8),
+                                         rng.uniform(0.002, 0.02, V).astype(F))
+    first, n = 77, 10
+    d.reset()
+    d.generate_greedy(first, n, embed_dev, other)
+    other.close()
+    lm_dev = lin.DeviceWeights.from_codes(d._lm_head_w, d._lm_head_s)
+    d.reset()
+    toks = d.generate_greedy(first, n, embed_dev, lm_dev)
+    d.reset()
+    tok, ref = first, []
+    for _ in range(n):
+        tok = d.next_token(d.step(embed[tok][None]))
+        ref.append(tok)
+    np.testing.assert_array_equal(toks, np.array(ref, np.int32))
+    lm_dev.close()
+    d.close()

@@ -91,6 +91,54 @@ def test_quantizer_special_rows(orc):
     assert np.isinf(s[0]) and np.all(q == 0)
 
 
+def _arm_fcvtas_x(v: float) -> int:
+    """FCVTAS Xd, Sn per the Arm ARM (FPToFixed, rounding FPRounding_TIEAWAY,
+    64-bit signed destination): NaN -> 0, round half away from zero,
+    saturate to [-2^63, 2^63 - 1]."""
+    import math
+    if math.isnan(v):
+        return 0
+    if math.isinf(v):
+        return 2 ** 63 - 1 if v > 0 else -(2 ** 63)
+    r = math.floor(abs(v) + 0.5) * (1 if v >= 0 else -1)
+    return max(-(2 ** 63), min(2 ** 63 - 1, r))
+
+
+def _low32(r: int) -> int:
+    """C's conversion of a 64-bit integer to int on clang/AArch64: the low 32
+    bits, two's complement."""
+    u = r & 0xFFFFFFFF
+    return u - 2 ** 32 if u >= 2 ** 31 else u
+
+
+@pytest.mark.parametrize("clamp", [True, False])
+def test_quantizer_tail_overflowing_reciprocal(orc, clamp):
+    """absmax so small that fl(absmax/127) rounds to 0: inv = +inf.  The
+    16-aligned prefix saturates (FCVTNS, SQXTN: +inf -> 127, -inf -> -128,
+    clamped to -127 by the weight quantizers, NaN = 0*inf -> 0); the scalar
+    tail evaluates (int)lroundf(x*inv), which the reference's AArch64 build
+    computes as FCVTAS into a 64-bit register, keeping the low 32 bits, then
+    clamps to [-127, 127].  Expected codes come from the Arm definition
+    (_arm_fcvtas_x); glibc's lroundf (+inf -> 0) or a 32-bit FCVTAS
+    (+inf -> 127) would fail the positive tail elements."""
+    x = np.array([1.4e-45, -2.8e-45, 0.0, 4.2e-45] * 4 + [2.8e-45, -1.4e-45, 0.0, 4.2e-45, -4.2e-45], F)
+    assert x[0] > 0 and x[1] < 0                       # denormals, not flushed
+    q, s = orc.quantize_rows(x, clamp_main=clamp)
+    assert s[0] == F(np.abs(x).max()) / F(127) == 0.0
+    inv = F(1) / s[0] if s[0] != 0 else np.float32(np.inf)
+    want = []
+    for k, v in enumerate(x):
+        with np.errstate(invalid="ignore", over="ignore"):
+            p = float(np.float32(v) * inv)
+        if k < 16:
+            c = 0 if np.isnan(p) else (127 if p > 0 else (-127 if clamp else -128))
+        else:
+            c = min(127, max(-127, _low32(_arm_fcvtas_x(p))))
+        want.append(c)
+    assert want[16:] == [-1, 0, 0, -1, 0]
+    assert list(q[0]) == want
+
+
 def test_activation_quantizer_matches_weight_quantizer(orc):
     # |x*inv| <= 127 (1 + 3 eps) always rounds into [-127, 127], so the
     # missing clamp of the activation quantizer never changes a code.
@@ -128,6 +176,24 @@ def test_gemv_golden(orc, golden, tag):
     np.testing.assert_array_equal(yb[0], g["ybias"])
     y8 = orc.w8a8_linear(codes[None], g["xs"], g["w"], g["ws"], bias=g["bias"])
     np.testing.assert_array_equal(y8[0], g["y8bias"])                 # fused epilogue
+
+
+@pytest.mark.parametrize("threads", [1, 3, 8])
+@pytest.mark.parametrize("N,K", [(6144, 2048), (2048, 6144), (37, 50), (1000, 1021)])
+def test_cpu_baseline_gemv_equals_oracle(orc, N, K, threads):
+    """The timed CPU-baseline GEMV (orc_w8a32_gemv_timed: the reference's
+    row-chunk fan-out) computes exactly orc_w8a32_linear at batch 1, for any
+    thread count, in both builds (x86-64-v3 and -march=native), so the GB/s
+    it reports are for the reference's arithmetic."""
+    rng = np.random.default_rng(N + K + threads)
+    x = rng.standard_normal((1, K)).astype(F)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    s = rng.uniform(0.002, 0.02, N).astype(F)
+    want = orc.w8a32_linear(x, w, s)[0]
+    for native in (False, True):
+        y = np.full(N, np.nan, F)
+        orc.w8a32_gemv_timed(x, w, s, y, threads, native=native)
+        np.testing.assert_array_equal(y, want)
 
 
 def test_gemv_epilogue_order(orc):

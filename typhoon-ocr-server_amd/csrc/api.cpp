@@ -49,9 +49,15 @@ int current_device() {
   return d;
 }
 
+uint64_t next_uid() {
+  static std::atomic<uint64_t> counter{1};
+  return counter.fetch_add(1, std::memory_order_relaxed);
+}
+
 tl_weights* weights_alloc(int rows, int cols) {
   REQUIRE(rows > 0 && cols > 0, "rows and cols must be positive");
   tl_weights* W = new tl_weights();
+  W->uid = next_uid();
   W->dev = current_device();
   W->rows = rows;
   W->cols = cols;

@@ -66,6 +66,7 @@ struct RopeDev {
   float* cos = nullptr;
   float* sin = nullptr;
   uint64_t fp = 0;
+  uint64_t uid = 0;             // process-unique (next_uid), drawn at allocation
 };
 
 uint64_t mix(uint64_t h, uint64_t v) {
@@ -92,7 +93,7 @@ uint64_t rope_fp(const float* c, const float* s, int rows) {
 struct ModelWeights {
   int dev = -1;
   LayerDev layers[NL];
-  uint64_t version = 0;
+  uint64_t version = next_uid();   // process-unique, redrawn whenever a layer changes
   bool prefill_w8a8 = false;    // prefill linears on per-token int8 activations
   int num_layers() const {
     int n = 0;
@@ -108,6 +109,7 @@ struct KVCache {
   float* k = nullptr;
   float* v = nullptr;
   int* state = nullptr;                 // device: position, rotary position, token counter
+  uint64_t uid = next_uid();            // process-unique, never reused
   std::map<std::pair<const float*, const float*>, RopeDev> rope;   // device copies of host tables
   size_t layer_floats() const { return (size_t)NKV * max_seq * HDIM; }
 };
@@ -126,13 +128,14 @@ struct DecoderScratch {
   // prefill activations (token-major, grown to the longest prefill)
   DevBuf p_h, p_xn, p_qkv, p_att, p_gu, p_mlp, p_y, p_cos, p_sin;
   DevBuf p_fpart, p_fcnt;               // prefill attention's split-key partials and counters (zero between launches)
-  // captured graphs and what they were captured for
+  // captured graphs and what they were captured for: process-unique ids of
+  // the handles whose device memory they bake in (a freed handle's successor
+  // can reuse its host address, never its id) and the device pointers the
+  // scratch itself owns
   hipGraphExec_t layers_exec = nullptr;
-  const void* layers_key[4] = {nullptr, nullptr, nullptr, nullptr};
-  uint64_t layers_version = 0;
+  uint64_t layers_key[4] = {};
   hipGraphExec_t gen_exec = nullptr;
-  const void* gen_key[9] = {};
-  uint64_t gen_version = 0;
+  uint64_t gen_key[9] = {};
 };
 
 namespace {
@@ -149,6 +152,7 @@ const RopeDev& rope_device(KVCache* c, const float* cos_tab, const float* sin_ta
   if (!r.cos) {
     HIP_OK(hipMalloc(&r.cos, (size_t)c->max_seq * 64 * 4));
     HIP_OK(hipMalloc(&r.sin, (size_t)c->max_seq * 64 * 4));
+    r.uid = next_uid();
   }
   if (r.fp != fp) {
     HIP_OK(hipMemcpy(r.cos, cos_tab, (size_t)c->max_seq * 64 * 4, hipMemcpyHostToDevice));
@@ -266,7 +270,7 @@ void ensure_prefill_buffers(DecoderScratch* s, int S) {
   const size_t cb = flash_split_counters(S, NQ) * sizeof(int);
   if (cb > s->p_fcnt.n) {
     s->p_fcnt.ensure(cb, s->st);
-    HIP_OK(hipMemset(s->p_fcnt.p, 0, s->p_fcnt.n));
+    HIP_OK(hipMemsetAsync(s->p_fcnt.p, 0, s->p_fcnt.n, s->st));   // ordered before the prefill kernels
   }
 }
 
@@ -428,7 +432,7 @@ void set_layer(ModelWeights* m, int l, const int8_t* q_w, const float* q_s, cons
   }
   m->layers[l].release();
   m->layers[l] = L;
-  m->version++;
+  m->version = next_uid();
 }
 
 }  // namespace
@@ -462,7 +466,9 @@ KVCache* decoder_cache_alloc(int max_seq) {
     HIP_OK(hipMalloc(&p->k, bytes));
     HIP_OK(hipMalloc(&p->v, bytes));
     HIP_OK(hipMalloc(&p->state, 4 * sizeof(int)));
-    HIP_OK(hipMemset(p->state, 0, 4 * sizeof(int)));
+    // null stream, completed before return: the kernels run on other streams
+    HIP_OK(hipMemsetAsync(p->state, 0, 4 * sizeof(int), nullptr));
+    HIP_OK(hipStreamSynchronize(nullptr));
     c = p.release();
   });
   return c;
@@ -508,7 +514,8 @@ DecoderScratch* decoder_scratch_alloc_fn(int max_seq) {
     HIP_OK(hipMalloc(&p->pl, (size_t)NQ * p->C * 4));
     HIP_OK(hipMalloc(&p->po, (size_t)NQ * p->C * HDIM * 4));
     HIP_OK(hipMalloc(&p->count, (size_t)NKV * sizeof(int)));
-    HIP_OK(hipMemset(p->count, 0, (size_t)NKV * sizeof(int)));
+    HIP_OK(hipMemsetAsync(p->count, 0, (size_t)NKV * sizeof(int), p->st));
+    HIP_OK(hipStreamSynchronize(p->st));
     p->pin.ensure(kStageHidden + (size_t)H * 4);
     s = p.release();
   });
@@ -591,12 +598,11 @@ void decoder_decode_step(const ModelWeights* model, KVCache* cache, float* hidde
     REQUIRE(rope_pos(cache) < cache->max_seq, "rotary position past the rope tables");
     DecoderScratch* s = scratch;
     const RopeDev& r = rope_device(cache, cos_tab, sin_tab);
-    const void* key[4] = {model, cache, r.cos, (const void*)(uintptr_t)model->num_layers()};
-    if (!s->layers_exec || s->layers_version != model->version || std::memcmp(key, s->layers_key, sizeof key)) {
+    const uint64_t key[4] = {model->version, cache->uid, r.uid, (uint64_t)model->num_layers()};
+    if (!s->layers_exec || std::memcmp(key, s->layers_key, sizeof key)) {
       drop_graph(s->layers_exec);
       s->layers_exec = capture(s->st, [&] { enqueue_layers(model, cache, s, r, s->st); });
       std::memcpy(s->layers_key, key, sizeof key);
-      s->layers_version = model->version;
     }
     write_state(cache, s, 0);   // also leaves the stream idle
     char* stage = static_cast<char*>(s->pin.p) + kStageHidden;
@@ -718,9 +724,17 @@ int tl_decoder_generate(const ModelWeights* model, KVCache* cache, DecoderScratc
       fn = static_cast<const float*>(s->fnorm.p);
     }
     const int max_tokens = (int)(s->tokens.n / sizeof(int32_t));
-    const void* key[9] = {model, cache, r.cos, lm_head, fn, embed, s->tokens.p, s->keys.p,
-                          (const void*)(uintptr_t)(model->num_layers() * 1000003 + max_tokens)};
-    if (!s->gen_exec || s->gen_version != model->version || std::memcmp(key, s->gen_key, sizeof key)) {
+    // embed is the caller's device pointer: its contents are read at replay
+    const uint64_t key[9] = {model->version,
+                             cache->uid,
+                             r.uid,
+                             lm_head->uid,
+                             (uint64_t)(uintptr_t)fn,
+                             (uint64_t)(uintptr_t)embed,
+                             (uint64_t)(uintptr_t)s->tokens.p,
+                             (uint64_t)(uintptr_t)s->keys.p,
+                             (uint64_t)model->num_layers() * 1000003u + (uint64_t)max_tokens};
+    if (!s->gen_exec || std::memcmp(key, s->gen_key, sizeof key)) {
       drop_graph(s->gen_exec);
       s->gen_exec = capture(s->st, [&] {
         enqueue_layers(model, cache, s, r, s->st);
@@ -739,7 +753,6 @@ int tl_decoder_generate(const ModelWeights* model, KVCache* cache, DecoderScratc
                                cache->state, static_cast<int32_t*>(s->tokens.p), max_tokens, s->st));
       });
       std::memcpy(s->gen_key, key, sizeof key);
-      s->gen_version = model->version;
     }
     write_state(cache, s, 0);
     HIP_OK(hipMemcpyAsync(s->hidden, embed + (size_t)first_token * H, (size_t)H * 4, hipMemcpyDeviceToDevice,
@@ -748,6 +761,85 @@ int tl_decoder_generate(const ModelWeights* model, KVCache* cache, DecoderScratc
     HIP_OK(hipMemcpyAsync(tokens, s->tokens.p, (size_t)n_steps * sizeof(int32_t), hipMemcpyDeviceToHost, s->st));
     HIP_OK(hipStreamSynchronize(s->st));
     advance(cache, n_steps);
+  });
+}
+
+// ---- attention test hooks -----------------------------------------------------
+int tl_attn_decode_dev(const float* qkv, const float* q_norm, const float* k_norm, const float* cos_tab,
+                       const float* sin_tab, float* k_cache, float* v_cache, int max_seq, int pos, int rope_pos,
+                       float* out, void* stream) {
+  return guarded("tl_attn_decode_dev", [&] {
+    REQUIRE(qkv && q_norm && k_norm && cos_tab && sin_tab && k_cache && v_cache && out, "NULL argument");
+    REQUIRE(max_seq >= 1 && pos >= 0 && pos < max_seq && rope_pos >= 0 && rope_pos < max_seq, "bad positions");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int C = attn_chunks(max_seq);
+    DevBuf ws;
+    const size_t part = (size_t)NQ * C * (2 + HDIM) * 4;
+    ws.ensure(part + 64 + (size_t)NKV * 4, st);
+    struct Free {   // the stream drains before the work-space goes, also on errors
+      DevBuf& b;
+      hipStream_t st;
+      ~Free() {
+        (void)hipStreamSynchronize(st);
+        if (b.p) (void)hipFree(b.p);
+      }
+    } guard{ws, st};
+    char* base = static_cast<char*>(ws.p);
+    int* state = reinterpret_cast<int*>(base + part);
+    int* count = reinterpret_cast<int*>(base + part + 64);
+    const int hs[4] = {pos, rope_pos, 0, 0};
+    HIP_OK(hipMemcpyAsync(state, hs, sizeof hs, hipMemcpyHostToDevice, st));
+    HIP_OK(hipMemsetAsync(count, 0, (size_t)NKV * 4, st));
+    AttnDecodeArgs a;
+    a.qkv = qkv;
+    a.q_norm = q_norm;
+    a.k_norm = k_norm;
+    a.cos_tab = cos_tab;
+    a.sin_tab = sin_tab;
+    a.kc = k_cache;
+    a.vc = v_cache;
+    a.state = state;
+    a.pm = reinterpret_cast<float*>(base);
+    a.pl = a.pm + (size_t)NQ * C;
+    a.po = a.pl + (size_t)NQ * C;
+    a.count = count;
+    a.out = out;
+    a.nq = NQ;
+    a.nkv = NKV;
+    a.max_seq = max_seq;
+    a.C = C;
+    a.scale = SCALE;
+    a.eps = EPS;
+    HIP_OK(launch_attn_decode(a, st));
+    HIP_OK(hipStreamSynchronize(st));
+  });
+}
+
+int tl_attn_prefill_dev(const float* qkv, const float* k_cache, const float* v_cache, float* out, int S,
+                        int max_seq, int key0, int qoff, int split, void* stream) {
+  return guarded("tl_attn_prefill_dev", [&] {
+    REQUIRE(qkv && k_cache && v_cache && out, "NULL argument");
+    REQUIRE(S >= 1 && key0 >= 0 && qoff >= 0 && key0 + qoff + S <= max_seq, "bad sizes");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    DevBuf part, cnt;
+    struct Free {   // the stream drains before the work-space goes, also on errors
+      DevBuf& a;
+      DevBuf& b;
+      hipStream_t st;
+      ~Free() {
+        (void)hipStreamSynchronize(st);
+        if (a.p) (void)hipFree(a.p);
+        if (b.p) (void)hipFree(b.p);
+      }
+    } guard{part, cnt, st};
+    if (split) {
+      part.ensure(flash_split_floats(S, NQ) * 4, st);
+      cnt.ensure(flash_split_counters(S, NQ) * sizeof(int), st);
+      HIP_OK(hipMemsetAsync(cnt.p, 0, cnt.n, st));
+    }
+    HIP_OK(launch_flash_prefill(qkv, k_cache, v_cache, out, S, NQ, max_seq, key0, qoff, SCALE,
+                                static_cast<float*>(part.p), static_cast<int*>(cnt.p), st));
+    HIP_OK(hipStreamSynchronize(st));
   });
 }
 

@@ -18,6 +18,7 @@ struct tl_weights {
   uint8_t* tiles = nullptr;   // NG * KB * 1024 bytes
   float* scales = nullptr;    // NG * 16 floats, zero padded
   size_t bytes = 0;
+  uint64_t uid = 0;           // process-unique, never reused (graph cache keys)
 };
 
 namespace tlhost {
@@ -61,6 +62,10 @@ int guarded(const char* fn, F&& f) {
 }
 
 int current_device();
+
+// process-unique id, never reused: captured graphs are keyed on these rather
+// than on host addresses, which a freed handle's successor can reuse
+uint64_t next_uid();
 
 // --------------------------------------------------------------------------
 // buffers

@@ -151,9 +151,10 @@ constexpr int FT = 64;          // queries / keys per tile
 // into registers one block ahead of their MFMAs.
 //
 // Split keys: the causal work of a query tile grows with its index, so the
-// last tile's work-group alone would set the kernel's length.  A query tile
-// whose key tiles exceed half of the longest tile's (and number at least 4)
-// becomes two work items over the two halves of its key range.  Each half
+// last tile's work-group alone would set the kernel's length.  The longest
+// query tiles (those from index qs on, each with at least 2 key tiles) become
+// two work items over the two halves of their key ranges; the host picks qs
+// by list-scheduling makespan (flash_split_first).  Each half
 // stores its unnormalised output, running max and sum (agent-scope stores,
 // acknowledged before its arrival count), and the second to arrive combines
 // the two in a fixed order (half 0, then half 1) and writes the output, so

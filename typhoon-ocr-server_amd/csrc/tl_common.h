@@ -63,10 +63,17 @@ __device__ inline int code_rne(float v, bool clamp127) {
   return (int)r;
 }
 
-// lroundf + clamp to [-127, 127] (scalar tail k >= K & ~15): half away from 0.
+// (int)lroundf + clamp to [-127, 127] (scalar tail k >= K & ~15): half away
+// from 0.  lroundf is FCVTAS into a 64-bit register on the reference's
+// AArch64 build (NaN -> 0, saturating), and the conversion to int keeps the
+// low 32 bits; an overflowing reciprocal (fl(absmax/127) < 2^-128) makes
+// v = +-inf, so +inf -> low half of INT64_MAX = -1 and -inf -> 0.  Finite v
+// here has |v| <= 127 (1 + 2^-21).
 __device__ inline int code_tail(float v) {
   float r = __builtin_roundf(v);
   r = (v != v) ? 0.0f : r;
+  r = (v == __builtin_inff()) ? -1.0f : r;
+  r = (v == -__builtin_inff()) ? 0.0f : r;
   r = __builtin_fminf(__builtin_fmaxf(r, -127.0f), 127.0f);
   return (int)r;
 }

@@ -93,6 +93,8 @@ SIGNATURES = {
     "tl_lm_head_argmax_dev": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tl_lm_head_argmax": (_int, [_f32p, _f32p, _i8p, _f32p, _int, _int, _f32p, ctypes.POINTER(ctypes.c_int32)]),
     "tl_rmsnorm_np_dev": (_int, [_vp, _vp, _vp, _int, _vp]),
+    "tl_attn_decode_dev": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp, _vp]),
+    "tl_attn_prefill_dev": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _int, _vp]),
 }
 
 _LIB: Optional[ctypes.CDLL] = None
