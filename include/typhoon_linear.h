@@ -188,6 +188,16 @@ int tl_w8a16_linear_dev(const void *X, int x_type, const tl_weights *W, const fl
  * returns all 151936 logits to Python and takes the argmax there. */
 int tl_lm_head_argmax_dev(const float *h, const float *norm_w, const tl_weights *W, float *logits,
                           int32_t *token, float *max_logit, void *stream);
+/* No reference counterpart.  tl_lm_head_argmax_dev for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): the same launches and results, with the
+ * work-space in a device array inside the library -- the argmax keys of up to
+ * 262144 lm_head rows and one normalised row of up to 16384 floats, 192 KiB,
+ * one copy per device, held until the process ends.  The call allocates
+ * nothing; larger lm_heads are rejected with an error.  Calls that overlap on
+ * one device share the array and race. */
+int tl_lm_head_argmax_noalloc_dev(const float *h, const float *norm_w, const tl_weights *W, float *logits,
+                                  int32_t *token, float *max_logit, void *stream);
 /* The same on host pointers (weights through the registry, like
  * w8a32_linear); returns the token in *token, logits optional. */
 int tl_lm_head_argmax(const float *h, const float *norm_w, const int8_t *w_int8, const float *scales,

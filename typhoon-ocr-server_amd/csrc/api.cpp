@@ -1015,32 +1015,11 @@ int tl_rmsnorm_np_dev(const float* h, const float* norm_w, float* out, int K, vo
 // final RMSNorm, lm_head GEMV with per-work-group argmax keys, key reduction
 void op_lm_head_argmax(const float* h, const float* norm_w, const tl_weights* W, float* logits,
                        int32_t* token, float* max_logit, hipStream_t st) {
-  const int K = W->cols;
-  REQUIRE(K >= 128 && K <= 16384 && (K & (K - 1)) == 0, "K must be a power of two in [128, 16384]");
   Workspace& ws = workspace(W->dev, st);
-  const GemvPlan p = gemv_plan(W->rows, K);
-  ws.keys.ensure((size_t)p.blocks * sizeof(uint64_t), st);
-  GemvLaunch L;
-  if (gemv_fused_norm_ok(K, h, norm_w)) {
-    // every GEMV work-group normalises the row itself: one launch fewer
-    L.x = h;
-    L.norm = NORM_NUMPY;
-    L.norm_w = norm_w;
-  } else {
-    ws.xn.ensure((size_t)K * sizeof(float), st);
-    float* xn = static_cast<float*>(ws.xn.p);
-    HIP_OK(launch_rmsnorm_np(h, norm_w, xn, K, 1e-6f, st));
-    L.x = xn;
-  }
-  L.wt = W->tiles;
-  L.ws = W->scales;
-  L.y = logits;
-  L.keys = static_cast<uint64_t*>(ws.keys.p);
-  L.N = W->rows;
-  L.K = K;
-  L.epi = EPI_ARGMAX;
-  HIP_OK(launch_gemv_i8(L, st));
-  HIP_OK(launch_argmax_keys(L.keys, p.blocks, token, max_logit, st));
+  ws.keys.ensure(lm_head_argmax_keys(W->rows, W->cols) * sizeof(uint64_t), st);
+  ws.xn.ensure((size_t)W->cols * sizeof(float), st);
+  lm_head_argmax_enqueue(h, norm_w, W, logits, token, max_logit, static_cast<uint64_t*>(ws.keys.p),
+                         static_cast<float*>(ws.xn.p), st);
 }
 
 int tl_lm_head_argmax_dev(const float* h, const float* norm_w, const tl_weights* W, float* logits,

@@ -91,6 +91,7 @@ SIGNATURES = {
     "tl_w8a32_gemv_acc_dev": (_int, [_vp, _vp, _vp, _vp, _vp]),
     "tl_w8a8_gemm_acc_dev": (_int, [_vp, _vp, _vp, _int, _vp]),
     "tl_lm_head_argmax_dev": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "tl_lm_head_argmax_noalloc_dev": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tl_lm_head_argmax": (_int, [_f32p, _f32p, _i8p, _f32p, _int, _int, _f32p, ctypes.POINTER(ctypes.c_int32)]),
     "tl_rmsnorm_np_dev": (_int, [_vp, _vp, _vp, _int, _vp]),
     "tl_attn_decode_dev": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp, _vp]),
@@ -374,6 +375,15 @@ def lm_head_argmax_dev(h, norm_w, W: DeviceWeights, token, logits=None, max_logi
     lib = load_library()
     _rc(lib, lib.tl_lm_head_argmax_dev(h.data_ptr(), _ptr(norm_w), W.handle, _ptr(logits), token.data_ptr(),
                                        _ptr(max_logit), _stream(stream)), "tl_lm_head_argmax_dev")
+
+
+def lm_head_argmax_noalloc_dev(h, norm_w, W: DeviceWeights, token, logits=None, max_logit=None, stream=None):
+    """lm_head_argmax_dev with the library's fixed device work-space: no
+    device allocation, lm_heads of up to 262144 rows and K up to 16384."""
+    lib = load_library()
+    _rc(lib, lib.tl_lm_head_argmax_noalloc_dev(h.data_ptr(), _ptr(norm_w), W.handle, _ptr(logits),
+                                               token.data_ptr(), _ptr(max_logit), _stream(stream)),
+        "tl_lm_head_argmax_noalloc_dev")
 
 
 def lm_head_argmax(h: np.ndarray, norm_w: Optional[np.ndarray], w: np.ndarray, scales: np.ndarray,
