@@ -110,6 +110,11 @@ int tl_gemv_set_plan(int rows, int u);
  * prefetch 7). */
 int tl_gemm_i8_set_cfg(int cfg);
 
+/* Tuning override of the decode attention for every later launch or graph
+ * capture in the process: cache positions per work-group, 32, 64 or 128; 0
+ * restores the built-in choice. */
+int tl_attn_set_chunk(int positions);
+
 /* ---- device-resident weights ------------------------------------------- */
 typedef struct tl_weights tl_weights;
 

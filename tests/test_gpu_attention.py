@@ -72,13 +72,21 @@ def test_attn_decode_matches_oracle(lin, orc, dev, pos, rope_pos):
     want, kw, vw = _decode_reference(orc, qkv, qn, kn, cos, sin, kc, vc, pos, rope_pos)
 
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-    kd, vd = t(kc), t(vc)
-    out = torch.full((NQ * HD,), np.nan, dtype=torch.float32, device=dev)
     args = [t(qkv), t(qn), t(kn), t(cos), t(sin)]
-    rc = lib.tl_attn_decode_dev(*[a.data_ptr() for a in args], kd.data_ptr(), vd.data_ptr(), max_seq, pos,
-                                rope_pos, out.data_ptr(), None)
-    assert rc == 0, lin.check(lib, "tl_attn_decode_dev")
-    kg, vg, og = kd.cpu().numpy(), vd.cpu().numpy(), out.cpu().numpy()
+    for chunk in (32, 64, 128):              # positions per work-group, every kernel variant
+        assert lib.tl_attn_set_chunk(chunk) == 0
+        try:
+            kd, vd = t(kc), t(vc)
+            out = torch.full((NQ * HD,), np.nan, dtype=torch.float32, device=dev)
+            rc = lib.tl_attn_decode_dev(*[a.data_ptr() for a in args], kd.data_ptr(), vd.data_ptr(), max_seq,
+                                        pos, rope_pos, out.data_ptr(), None)
+            assert rc == 0, lin.check(lib, "tl_attn_decode_dev")
+        finally:
+            lib.tl_attn_set_chunk(0)
+        _check_decode(kd.cpu().numpy(), vd.cpu().numpy(), out.cpu().numpy(), kc, vc, kw, vw, want, pos)
+
+
+def _check_decode(kg, vg, og, kc, vc, kw, vw, want, pos):
     np.testing.assert_array_equal(vg[:, pos], vw[:, pos])              # V appended as is
     assert rel_l2(kg[:, pos], kw[:, pos]) <= 1e-6, rel_l2(kg[:, pos], kw[:, pos])
     np.testing.assert_array_equal(kg[:, :pos], kc[:, :pos])            # earlier rows untouched

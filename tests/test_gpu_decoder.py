@@ -123,10 +123,18 @@ def _oracle_layers(d, layers):
 
 
 def test_decode_step_matches_oracle(lin, orc, dev):
-    """decoder_decode_step over 2 layers and 6 steps (rope offset set as after
-    a multimodal prefill) against the oracle's decode_layer chain."""
+    """decoder_decode_step over 2 layers and 76 steps (the last 6 with the
+    rope offset set as after a multimodal prefill) against the oracle's
+    decode_layer chain.  Before each step the oracle takes the GPU's cache
+    rows, so every step's error is its own: hidden rows within 1e-5 and the
+    new K/V rows within 1e-6 (summation orders only; measured ~1e-7), earlier
+    cache rows unchanged.  The exception is the reference's fast-exp SiLU: its
+    exp term doubles when a gate value crosses a truncation step, so a
+    last-bit difference in a gate can double one mlp element, which moves the
+    down projection by about 1/sqrt(6144) = 1.3% (and layer 1's K/V after it).
+    Up to 2 of the 76 steps may show such a jump, within 3e-2."""
     from typhoon_ocr_server_amd import decoder as dec
-    say("decoder_decode_step vs oracle, 2 layers x 6 steps")
+    say("decoder_decode_step vs oracle, 2 layers x 76 steps")
     rng = np.random.default_rng(23)
     layers, _, _ = _model(rng, orc, 2)
     max_seq = 160
@@ -135,33 +143,29 @@ def test_decode_step_matches_oracle(lin, orc, dev):
     c, s = d._cos_tab, d._sin_tab
     kc = [np.zeros((8, max_seq, 128), F) for _ in ol]
     vc = [np.zeros((8, max_seq, 128), F) for _ in ol]
-    # start with a cache already holding 70 positions (written by both sides)
     d.reset()
-    warm = 70
-    for t in range(warm):
+    warm, jumps = 70, []
+    for t in range(warm + 6):
+        if t == warm:
+            d.set_rope_offset(100)
+        rope = t if t < warm else 100 + (t - warm)
         h = (rng.standard_normal((1, 2048)) * 2).astype(F)
         hg = d.step(h)
         ho = h[0]
         for l, layer in enumerate(ol):
-            ho = orc.decode_layer(layer, kc[l], vc[l], ho, c, s, cache_len=t, rope_pos=t)
-        assert rel_l2(hg[0], ho) <= 1e-3, t
-    # keep both caches identical from here (the GPU's), so each step's error is its own
-    for l in range(len(ol)):
-        kc[l], vc[l] = d.read_cache(l)
-    d.set_rope_offset(100)
-    for t in range(warm, warm + 6):
-        h = (rng.standard_normal((1, 2048)) * 2).astype(F)
-        hg = d.step(h)
-        ho = h[0]
-        for l, layer in enumerate(ol):
-            ho = orc.decode_layer(layer, kc[l], vc[l], ho, c, s, cache_len=t, rope_pos=100 + (t - warm))
-        assert rel_l2(hg[0], ho) <= 1e-3, t
+            ho = orc.decode_layer(layer, kc[l], vc[l], ho, c, s, cache_len=t, rope_pos=rope)
+        e = rel_l2(hg[0], ho)
+        ekv = 0.0
         for l in range(len(ol)):
             kg, vg = d.read_cache(l)
-            assert rel_l2(kg[:, t], kc[l][:, t]) <= 1e-4
-            assert rel_l2(vg[:, t], vc[l][:, t]) <= 1e-4
-            np.testing.assert_array_equal(kg[:, :t], kc[l][:, :t])
+            ekv = max(ekv, rel_l2(kg[:, t], kc[l][:, t]), rel_l2(vg[:, t], vc[l][:, t]))
+            np.testing.assert_array_equal(kg[:, :t], kc[l][:, :t])    # earlier rows untouched
+            np.testing.assert_array_equal(vg[:, :t], vc[l][:, :t])
             kc[l][:, t], vc[l][:, t] = kg[:, t], vg[:, t]
+        if e > 1e-5 or ekv > 1e-6:
+            jumps.append(t)
+            assert e <= 3e-2 and ekv <= 3e-2, (t, e, ekv)
+    assert len(jumps) <= 2, jumps
     assert d.cache_len == warm + 6
     d.close()
 

@@ -810,6 +810,14 @@ int tl_gemm_i8_set_cfg(int cfg) {
   });
 }
 
+int tl_attn_set_chunk(int positions) {
+  return guarded("tl_attn_set_chunk", [&] {
+    REQUIRE(positions == 0 || positions == 32 || positions == 64 || positions == 128,
+            "positions must be 0, 32, 64 or 128");
+    attn_set_chunk(positions);
+  });
+}
+
 int tl_register_weights(const int8_t* w_int8, const float* scales, int rows, int cols) {
   return guarded("tl_register_weights", [&] {
     std::lock_guard<std::mutex> lk(g_host_mu);

@@ -119,7 +119,7 @@ struct DecoderScratch {
   int max_seq = 0;
   hipStream_t st = nullptr;
   float *hidden = nullptr, *qkv = nullptr, *attn = nullptr, *mlp = nullptr;
-  float *pm = nullptr, *pl = nullptr, *po = nullptr;
+  float *pm = nullptr, *pl = nullptr, *po = nullptr;   // attention chunk partials [NQ][C](x128)
   int* count = nullptr;                 // attention arrival counters [NKV], zero between launches
   int C = 0;
   DevBuf keys, tokens, fnorm;
@@ -211,6 +211,7 @@ void enqueue_layers(const ModelWeights* m, const KVCache* c, DecoderScratch* s, 
     a.nq = NQ;
     a.nkv = NKV;
     a.max_seq = c->max_seq;
+    a.T = attn_chunk_size(c->max_seq);
     a.C = attn_chunks(c->max_seq);
     a.scale = SCALE;
     a.eps = EPS;
@@ -508,8 +509,8 @@ DecoderScratch* decoder_scratch_alloc_fn(int max_seq) {
     HIP_OK(hipStreamCreateWithFlags(&p->st, hipStreamNonBlocking));
     HIP_OK(hipMalloc(&p->hidden, (size_t)H * 4));
     HIP_OK(hipMalloc(&p->qkv, (size_t)QKVD * 4));
-    HIP_OK(hipMalloc(&p->attn, (size_t)H * 4));
     HIP_OK(hipMalloc(&p->mlp, (size_t)FF * 4));
+    HIP_OK(hipMalloc(&p->attn, (size_t)H * 4));
     HIP_OK(hipMalloc(&p->pm, (size_t)NQ * p->C * 4));
     HIP_OK(hipMalloc(&p->pl, (size_t)NQ * p->C * 4));
     HIP_OK(hipMalloc(&p->po, (size_t)NQ * p->C * HDIM * 4));
@@ -527,7 +528,9 @@ void decoder_scratch_free_fn(DecoderScratch* s) {
   if (s->st) (void)hipStreamSynchronize(s->st);
   drop_graph(s->layers_exec);
   drop_graph(s->gen_exec);
-  for (float* p : {s->hidden, s->qkv, s->attn, s->mlp, s->pm, s->pl, s->po})
+  for (float* p : {s->hidden, s->qkv, s->attn, s->mlp})
+    if (p) (void)hipFree(p);
+  for (float* p : {s->pm, s->pl, s->po})
     if (p) (void)hipFree(p);
   if (s->count) (void)hipFree(s->count);
   for (DevBuf* b : {&s->p_h, &s->p_xn, &s->p_qkv, &s->p_att, &s->p_gu, &s->p_mlp, &s->p_y, &s->p_cos, &s->p_sin,
@@ -774,8 +777,8 @@ int tl_attn_decode_dev(const float* qkv, const float* q_norm, const float* k_nor
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int C = attn_chunks(max_seq);
     DevBuf ws;
-    const size_t part = (size_t)NQ * C * (2 + HDIM) * 4;
-    ws.ensure(part + 64 + (size_t)NKV * 4, st);
+    const size_t part = (size_t)NQ * C * (2 + HDIM) * sizeof(float);
+    ws.ensure(part + 64 + (size_t)NKV * sizeof(int), st);
     struct Free {   // the stream drains before the work-space goes, also on errors
       DevBuf& b;
       hipStream_t st;
@@ -788,8 +791,8 @@ int tl_attn_decode_dev(const float* qkv, const float* q_norm, const float* k_nor
     int* state = reinterpret_cast<int*>(base + part);
     int* count = reinterpret_cast<int*>(base + part + 64);
     const int hs[4] = {pos, rope_pos, 0, 0};
+    HIP_OK(hipMemsetAsync(count, 0, (size_t)NKV * sizeof(int), st));
     HIP_OK(hipMemcpyAsync(state, hs, sizeof hs, hipMemcpyHostToDevice, st));
-    HIP_OK(hipMemsetAsync(count, 0, (size_t)NKV * 4, st));
     AttnDecodeArgs a;
     a.qkv = qkv;
     a.q_norm = q_norm;
@@ -807,6 +810,7 @@ int tl_attn_decode_dev(const float* qkv, const float* q_norm, const float* k_nor
     a.nq = NQ;
     a.nkv = NKV;
     a.max_seq = max_seq;
+    a.T = attn_chunk_size(max_seq);
     a.C = C;
     a.scale = SCALE;
     a.eps = EPS;

@@ -28,68 +28,38 @@
 namespace tl {
 
 constexpr int HD = 128;          // head dim
-constexpr int ATT_T = 64;        // positions per attention work-group
+constexpr int kMergeRound = 32;  // chunks whose partials the merger loads at once
 
-
-
-
-// out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c over the nc live chunks
-// of q head qh, element d; chunks in batches of 32 (all loads of a batch in
-// flight together), each batch rescaling what the earlier ones accumulated.
-__device__ __forceinline__ float merge_chunks(const float* pm, const float* pl, const float* po, int C, int nc,
-                                              int qh, int d) {
-  float L = 0.0f, acc = 0.0f, M = -3.0e38f;
-  for (int c0 = 0; c0 < nc; c0 += 32) {
-    float v[32], m[32], l[32];
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
-      const bool ok = c0 + i < nc;
-      const int cc = min(c0 + i, nc - 1);
-      v[i] = ld_agent(po + ((size_t)qh * C + cc) * HD + d);
-      m[i] = ok ? ld_agent(pm + qh * C + cc) : -3.0e38f;
-      l[i] = ld_agent(pl + qh * C + cc);
-    }
-    float Mb = M;
-#pragma unroll
-    for (int i = 0; i < 32; i++) Mb = fmaxf(Mb, m[i]);
-    const float r = expf(__fsub_rn(M, Mb));
-    L = __fmul_rn(L, r);
-    acc = __fmul_rn(acc, r);
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
-      if (c0 + i < nc) {
-        const float w = expf(__fsub_rn(m[i], Mb));
-        L = __fmaf_rn(w, l[i], L);
-        acc = __fmaf_rn(w, v[i], acc);
-      }
-    }
-    M = Mb;
-  }
-  return __fmul_rn(acc, __fdiv_rn(1.0f, L));
-}
-
-// Work-group (c, h): kv head h, positions [64 c, 64 c + 64) of the S = len + 1
-// that the new token attends to; two q heads (GQA group 2).  256 threads.
-// Every load of the chunk (its K and V rows, the q/k/v rows of the QKV
-// output, norm weights, rope row) is issued first, so the norm/rotation
-// prologue runs while they are in flight.  Positions past the chunk end read
-// a clamped valid row and are masked; position p (the new token, whose cache
-// row this work-group writes) is taken from LDS instead of memory.
+// Work-group (c, h): kv head h, positions [T c, T c + T) of the S = p + 1 that
+// the new token attends to; its two q heads (GQA group 2).  256 threads.
+// The loads are issued in the order the work-group consumes them (the memory
+// counter retires loads in issue order): the q/k/v row, norm weights and rope
+// row, then the K rows, then the V rows; the norm and rotation prologue
+// starts when the first ones land and each score step waits only for its own
+// K rows.  Positions past the chunk end read a clamped valid row and are
+// masked; position p (the new token, whose cache row this work-group writes)
+// is taken from LDS instead of memory.  Lane sums are DPP row and wave
+// reductions (no LDS permutes).
 //
-// Merge without a second launch: every work-group stores its partials with
-// agent-scope atomic stores, waits until they are acknowledged (vmcnt 0: the
-// stores bypass the non-coherent L2 path, so no L2 write-back is needed, which
-// a device-scope fence would do), then bumps the kv head's arrival counter.
-// The work-group that brings the counter to the number of live chunks merges
-// the two q heads and resets the counter for the next launch.  Nothing waits
-// on another work-group.
+// Merge without a second launch: every work-group stores its partials (m, l
+// and o of each q head) with agent-scope atomic stores, waits until they are
+// acknowledged (vmcnt 0: the stores bypass the non-coherent L2 path, so no L2
+// write-back is needed, which a device-scope fence would do), then bumps the
+// kv head's arrival counter.  The work-group that brings the counter to the
+// number of live chunks merges the two q heads: every partial of a round of
+// chunks is loaded at once (each thread its o values, the m and l values one
+// per lane of a wave and shared through LDS), merged in chunk order, and the
+// counter is reset for the next launch.  Nothing waits on another work-group.
+template <int T>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
+  constexpr int NK = T / 16;                // K iterations: 16 positions (4 waves x 4) each
+  constexpr int NV = T / 8;                 // V float4 per thread: positions pg + 8 i
   const int c = blockIdx.x, h = blockIdx.y;
   const int p = a.state[0];                 // position of the new token
   const int S = p + 1;
-  const int t0 = c * ATT_T;
-  if (t0 >= S) return;                      // uniform: the whole work-group leaves
-  const int t1 = min(t0 + ATT_T, S);
+  const int t0 = c * T;
+  if (t0 >= S) return;                      // uniform: the whole work-group leaves, no ticket
+  const int t1 = min(t0 + T, S);
   const int rp = a.state[1];
 
   __shared__ float s_x[2][HD];              // normalised q heads before the rotation
@@ -97,33 +67,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   __shared__ float s_q[2][HD];              // rotated q heads
   __shared__ float s_k[HD], s_v[HD];        // the new token's k (rotated) and v
   __shared__ float s_red[8];
-  __shared__ float s_p[2][ATT_T];           // scores, then probabilities
+  __shared__ float s_p[2][T];               // scores, then probabilities
+  __shared__ float s_ml[2][2];              // chunk max and sum per q head
   __shared__ float4 s_o[8][2][HD / 4];      // V partial sums of the 8 position groups
 
   const int tid = threadIdx.x, g = tid >> 7, d = tid & 127;
   const int lane = tid & 63, wv = tid >> 6;
   const bool has_new = p < t1;              // this chunk holds position p
 
-  // ---- loads ---------------------------------------------------------------
-  // scores: 16 lanes per position (8 elements each), wave w takes positions
-  // t0 + 16 w + 4 it + (lane >> 4), it = 0..3
-  const int seg = lane & 15;
-  const float* kbase = a.kc + (size_t)h * a.max_seq * HD;
-  float4 kr[4][2];
-#pragma unroll
-  for (int it = 0; it < 4; it++) {
-    const int t = min(t0 + wv * 16 + it * 4 + (lane >> 4), t1 - 1);
-    const float4* kp = reinterpret_cast<const float4*>(kbase + (size_t)t * HD + seg * 8);
-    kr[it][0] = kp[0];
-    kr[it][1] = kp[1];
-  }
-  // V: thread (pg = tid >> 5, d4 = tid & 31) reads float4 d4 of positions
-  // t0 + pg + 8 i, i = 0..7
-  const int pg = tid >> 5, d4 = tid & 31;
-  const float4* vbase = reinterpret_cast<const float4*>(a.vc + (size_t)h * a.max_seq * HD) + d4;
-  float4 vr[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) vr[i] = vbase[(size_t)min(t0 + pg + 8 * i, t1 - 1) * (HD / 4)];
+  // ---- loads, in the order they are needed ----------------------------------
   const float qraw = a.qkv[(2 * h + g) * HD + d];
   const float qw = a.q_norm[d];
   const float* kv_src = a.qkv + a.nq * HD + (g == 0 ? h * HD : a.nkv * HD + h * HD);
@@ -131,16 +83,31 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   const float kw = a.k_norm[d];
   const int j = d & 63;
   const float co = a.cos_tab[(size_t)rp * 64 + j], si = a.sin_tab[(size_t)rp * 64 + j];
+  // scores: 16 lanes per position, lane seg holds dimensions 4 seg .. 4 seg + 3
+  // and 64 + 4 seg .. + 3 (each load instruction reads four 256-byte row halves);
+  // wave w takes positions t0 + 16 it + 4 w + (lane >> 4)
+  const int seg = lane & 15;
+  const float* kbase = a.kc + (size_t)h * a.max_seq * HD;
+  float4 kr[NK][2];
+#pragma unroll
+  for (int it = 0; it < NK; it++) {
+    const int t = min(t0 + it * 16 + wv * 4 + (lane >> 4), t1 - 1);
+    const float4* kp = reinterpret_cast<const float4*>(kbase + (size_t)t * HD);
+    kr[it][0] = kp[seg];
+    kr[it][1] = kp[16 + seg];
+  }
+  // V: thread (pg = tid >> 5, d4 = tid & 31) reads float4 d4 of positions
+  // t0 + pg + 8 i
+  const int pg = tid >> 5, d4 = tid & 31;
+  const float4* vbase = reinterpret_cast<const float4*>(a.vc + (size_t)h * a.max_seq * HD) + d4;
+  float4 vr[NV];
+#pragma unroll
+  for (int i = 0; i < NV; i++) vr[i] = vbase[(size_t)min(t0 + pg + 8 * i, t1 - 1) * (HD / 4)];
 
   // ---- q and the new k: RMSNorm (q_norm / k_norm) in one reduction pass, then
   //      the rotation; threads 0-127 also hold element d of k, 128-255 of v
   {
-    float sq = __fmul_rn(qraw, qraw), sk = __fmul_rn(kvraw, kvraw);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      sq = __fadd_rn(sq, __shfl_xor(sq, o, 64));
-      sk = __fadd_rn(sk, __shfl_xor(sk, o, 64));
-    }
+    const float sq = wave_sum(__fmul_rn(qraw, qraw)), sk = wave_sum(__fmul_rn(kvraw, kvraw));
     if (lane == 0) {
       s_red[wv] = sq;
       s_red[4 + wv] = sk;
@@ -175,18 +142,23 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   // ---- scores ----------------------------------------------------------------
   float q0[8], q1[8];
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    q0[i] = s_q[0][seg * 8 + i];
-    q1[i] = s_q[1][seg * 8 + i];
+  for (int i = 0; i < 4; i++) {
+    q0[i] = s_q[0][4 * seg + i];
+    q1[i] = s_q[1][4 * seg + i];
+    q0[4 + i] = s_q[0][64 + 4 * seg + i];
+    q1[4 + i] = s_q[1][64 + 4 * seg + i];
   }
 #pragma unroll
-  for (int it = 0; it < 4; it++) {
-    const int t = t0 + wv * 16 + it * 4 + (lane >> 4);
+  for (int it = 0; it < NK; it++) {
+    const int t = t0 + it * 16 + wv * 4 + (lane >> 4);
     float kv8[8] = {kr[it][0].x, kr[it][0].y, kr[it][0].z, kr[it][0].w,
                     kr[it][1].x, kr[it][1].y, kr[it][1].z, kr[it][1].w};
     if (t == p) {
 #pragma unroll
-      for (int i = 0; i < 8; i++) kv8[i] = s_k[seg * 8 + i];
+      for (int i = 0; i < 4; i++) {
+        kv8[i] = s_k[4 * seg + i];
+        kv8[4 + i] = s_k[64 + 4 * seg + i];
+      }
     }
     float d0 = 0.0f, d1 = 0.0f;
 #pragma unroll
@@ -194,11 +166,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
       d0 = __fmaf_rn(q0[i], kv8[i], d0);
       d1 = __fmaf_rn(q1[i], kv8[i], d1);
     }
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-      d0 = __fadd_rn(d0, __shfl_xor(d0, o, 64));
-      d1 = __fadd_rn(d1, __shfl_xor(d1, o, 64));
-    }
+    d0 = row16_sum(d0);                     // the 16 lanes of a position are one DPP row
+    d1 = row16_sum(d1);
     if (seg == 0 && t < t1) {
       s_p[0][t - t0] = __fmul_rn(d0, a.scale);
       s_p[1][t - t0] = __fmul_rn(d1, a.scale);
@@ -209,19 +178,28 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   // ---- chunk softmax statistics: wave g for q head 2h + g ---------------------
   const int n = t1 - t0;
   if (wv < 2) {
-    const float sc = lane < n ? s_p[wv][lane] : -3.0e38f;
-    float m = sc;
+    constexpr int PL = T >= 64 ? T / 64 : 1;   // scores per lane
+    float sc[PL];
+    float m = -3.0e38f;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    const float e = lane < n ? expf(__fsub_rn(sc, m)) : 0.0f;
-    float l = e;
+    for (int i = 0; i < PL; i++) {
+      const int t = lane + 64 * i;
+      sc[i] = t < n ? s_p[wv][t] : -3.0e38f;
+      m = fmaxf(m, sc[i]);
+    }
+    m = wave_fmax(m);
+    float l = 0.0f;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) l = __fadd_rn(l, __shfl_xor(l, o, 64));
-    s_p[wv][lane] = e;                      // zero past the chunk end
+    for (int i = 0; i < PL; i++) {
+      const int t = lane + 64 * i;
+      const float e = t < n ? expf(__fsub_rn(sc[i], m)) : 0.0f;
+      if (t < T) s_p[wv][t] = e;            // zero past the chunk end
+      l = __fadd_rn(l, e);
+    }
+    l = wave_sum(l);
     if (lane == 0) {
-      const int qh = 2 * h + wv;
-      st_agent(a.pm + qh * a.C + c, m);
-      st_agent(a.pl + qh * a.C + c, l);
+      s_ml[wv][0] = m;
+      s_ml[wv][1] = l;
     }
   }
   __syncthreads();
@@ -229,7 +207,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   // ---- unnormalised output of the chunk ------------------------------------------
   float4 o0 = make_float4(0.f, 0.f, 0.f, 0.f), o1 = o0;
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
+  for (int i = 0; i < NV; i++) {
     const int t = t0 + pg + 8 * i;
     float4 v = vr[i];
     if (t == p) v = reinterpret_cast<const float4*>(s_v)[d4];
@@ -247,7 +225,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   float o = 0.0f;
 #pragma unroll
   for (int q = 0; q < 8; q++) o = __fadd_rn(o, so[(q * 2 + g) * HD + d]);
-  st_agent(a.po + ((size_t)(2 * h + g) * a.C + c) * HD + d, o);
+  const int qh = 2 * h + g;
+  const int nc = cdiv(S, T);
+  if (d < 2) st_agent((d == 0 ? a.pm : a.pl) + (size_t)qh * a.C + c, s_ml[g][d]);
+  st_agent(a.po + ((size_t)qh * a.C + c) * HD + d, o);
 
   // ---- arrival; the last work-group of kv head h merges ----------------------
   __shared__ int s_last;
@@ -255,12 +236,43 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   wait_vm<0>();                             // this thread's partial stores are acknowledged
   asm volatile("" ::: "memory");
   __syncthreads();
-  const int nc = cdiv(S, ATT_T);
   if (tid == 0) s_last = __hip_atomic_fetch_add(a.count + h, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nc - 1;
   __syncthreads();
   if (!s_last) return;
+
+  // out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c, M = max_c m_c, in
+  // chunk order over rounds of kMergeRound chunks (one round up to 2048
+  // positions at 64 per chunk), each round rescaling the earlier ones
+  __shared__ float s_w[2][2][kMergeRound];  // m and l of q heads 2h, 2h + 1
+  const int wg = wv >> 1, ww = wv & 1;      // wave: q head 2h + wg, word ww (m or l)
+  const float* src_w = (ww == 0 ? a.pm : a.pl) + (size_t)(2 * h + wg) * a.C;
+  float M = -3.0e38f, L = 0.0f, acc = 0.0f;
+  for (int c0 = 0; c0 < nc; c0 += kMergeRound) {
+    if (lane < kMergeRound) s_w[wg][ww][lane] = ld_agent(src_w + min(c0 + lane, nc - 1));
+    float v[kMergeRound];
+#pragma unroll
+    for (int i = 0; i < kMergeRound; i++) v[i] = ld_agent(a.po + ((size_t)qh * a.C + min(c0 + i, nc - 1)) * HD + d);
+    __syncthreads();
+    float Mb = M;
+#pragma unroll
+    for (int i = 0; i < kMergeRound; i++)
+      if (c0 + i < nc) Mb = fmaxf(Mb, s_w[g][0][i]);
+    const float r = expf(__fsub_rn(M, Mb));
+    L = __fmul_rn(L, r);
+    acc = __fmul_rn(acc, r);
+#pragma unroll
+    for (int i = 0; i < kMergeRound; i++) {
+      if (c0 + i < nc) {
+        const float w = expf(__fsub_rn(s_w[g][0][i], Mb));
+        L = __fmaf_rn(w, s_w[g][1][i], L);
+        acc = __fmaf_rn(w, v[i], acc);
+      }
+    }
+    M = Mb;
+    __syncthreads();                        // s_w is rewritten by the next round
+  }
+  a.out[qh * HD + d] = __fmul_rn(acc, __fdiv_rn(1.0f, L));
   if (tid == 0) __hip_atomic_store(a.count + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  a.out[(2 * h + g) * HD + d] = merge_chunks(a.pm, a.pl, a.po, a.C, nc, 2 * h + g, d);
 }
 
 // greedy token (largest argmax key: largest logit, lowest index on ties),
@@ -298,9 +310,28 @@ __global__ __launch_bounds__(1024) void step_end_kernel(const uint64_t* __restri
   }
 }
 
+static int g_attn_t = 0;   // positions per work-group override (tuning), 0 = planner
+
+void attn_set_chunk(int t) { g_attn_t = (t == 32 || t == 64 || t == 128) ? t : 0; }
+
+int attn_chunk_size(int max_seq) {
+  (void)max_seq;
+  return g_attn_t ? g_attn_t : 64;
+}
+
+int attn_chunks(int max_seq) { return cdiv(max_seq, 32); }   // records per q head for the smallest chunks
+
 hipError_t launch_attn_decode(const AttnDecodeArgs& a, hipStream_t st) {
-  if (a.nq != 2 * a.nkv || a.C * ATT_T < a.max_seq || !a.count || !a.out) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(attn_decode_kernel, dim3(a.C, a.nkv), dim3(256), 0, st, a);
+  if (a.nq != 2 * a.nkv || a.T * a.C < a.max_seq || a.max_seq < 1 || !a.pm || !a.pl || !a.po || !a.count ||
+      !a.out)
+    return hipErrorInvalidValue;
+  const dim3 grid(cdiv(a.max_seq, a.T), a.nkv);
+  switch (a.T) {
+    case 32: hipLaunchKernelGGL(attn_decode_kernel<32>, grid, dim3(256), 0, st, a); break;
+    case 64: hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(256), 0, st, a); break;
+    case 128: hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(256), 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
@@ -310,7 +341,5 @@ hipError_t launch_step_end(const uint64_t* keys, int n, const float* embed, int 
                      max_tokens);
   return hipGetLastError();
 }
-
-int attn_chunks(int max_seq) { return cdiv(max_seq, ATT_T); }
 
 }  // namespace tl

@@ -160,8 +160,11 @@ __device__ void final_rmsnorm(float4 (&xv)[XV], const float4 (&nwv)[XV], bool ha
 #pragma unroll
       for (int i = 1; i < 16; i++) r = __fadd_rn(r, src[8 * i]);
     }
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) r = __fadd_rn(r, __shfl_xor(r, o, 64));
+    // xor butterflies over lanes 1, 2, 4, 8 then 16, 32: numpy's order.  The
+    // DPP quad permutes and row mirrors of wave_sum meet the same partner
+    // values (each step's inputs are uniform over the previous step's group)
+    // and its (r0 + r1) + (r2 + r3) is the last two steps, so the bits agree.
+    r = wave_sum(r);
     if ((threadIdx.x & 63) == 0 && (p >> 6) < ngrp) s_grp[p >> 6] = r;
   }
   __syncthreads();
@@ -209,8 +212,7 @@ __device__ void decoder_rmsnorm(float4 (&xv)[XV], const float4 (&nwv)[XV], bool 
     sq = __fmaf_rn(xv[i].z, xv[i].z, sq);
     sq = __fmaf_rn(xv[i].w, xv[i].w, sq);
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) sq = __fadd_rn(sq, __shfl_xor(sq, o, 64));
+  sq = wave_sum(sq);
   if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = sq;
   __syncthreads();
   const float tot = __fadd_rn(__fadd_rn(s_part[0], s_part[1]), __fadd_rn(s_part[2], s_part[3]));

@@ -56,8 +56,7 @@ __global__ __launch_bounds__(256) void rmsnorm_np_kernel(const float* __restrict
 #pragma unroll
       for (int i = 1; i < 16; i++) r = __fadd_rn(r, __fmul_rn(v[i], v[i]));
     }
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) r = __fadd_rn(r, __shfl_xor(r, o, 64));
+    r = wave_sum(r);   // numpy's xor-butterfly order, through DPP (see final_rmsnorm in gemv.hip)
     if ((threadIdx.x & 63) == 0 && (p >> 6) < ngrp) s_grp[p >> 6] = r;
   }
   __syncthreads();

@@ -161,6 +161,44 @@ __device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
   return m > r3 ? m : r3;
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __uint_as_float(dpp_u32<CTRL>(__float_as_uint(v)));
+}
+
+// sum over each row of 16 lanes, returned to every lane of the row: quad
+// pairs, quads, then the two halves of each 8 and of the row, all through DPP
+// (a fixed order, the same in every row)
+__device__ __forceinline__ float row16_sum(float v) {
+  v = __fadd_rn(v, dpp_f32<DPP_QP_1032>(v));
+  v = __fadd_rn(v, dpp_f32<DPP_QP_2301>(v));
+  v = __fadd_rn(v, dpp_f32<DPP_ROW_HALF_MIRROR>(v));
+  return __fadd_rn(v, dpp_f32<DPP_ROW_MIRROR>(v));
+}
+
+// wave-wide sum, returned wave-uniform: row sums, then (r0 + r1) + (r2 + r3)
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  const float r0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
+  const float r1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 16));
+  const float r2 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 32));
+  const float r3 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 48));
+  return __fadd_rn(__fadd_rn(r0, r1), __fadd_rn(r2, r3));
+}
+
+// wave-wide fmaxf, returned wave-uniform
+__device__ __forceinline__ float wave_fmax(float v) {
+  v = fmaxf(v, dpp_f32<DPP_QP_1032>(v));
+  v = fmaxf(v, dpp_f32<DPP_QP_2301>(v));
+  v = fmaxf(v, dpp_f32<DPP_ROW_HALF_MIRROR>(v));
+  v = fmaxf(v, dpp_f32<DPP_ROW_MIRROR>(v));
+  const float r0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
+  const float r1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 16));
+  const float r2 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 32));
+  const float r3 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 // max ignoring NaN (the tail scan), for non-negative inputs
 __device__ __forceinline__ float wave_fmax_nonnan(float v) {
   float t;

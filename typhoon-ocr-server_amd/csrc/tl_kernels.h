@@ -61,15 +61,21 @@ struct AttnDecodeArgs {
   float* kc = nullptr;             // this layer's cache [nkv][max_seq][128]
   float* vc = nullptr;
   const int* state = nullptr;      // device decode state (position, rotary position, counter)
-  float* pm = nullptr;             // partial maxima [nq][C]
-  float* pl = nullptr;             // partial sums [nq][C]
-  float* po = nullptr;             // partial outputs [nq][C][128]
+  float* pm = nullptr;             // chunk maxima [nq][C]
+  float* pl = nullptr;             // chunk sums [nq][C]
+  float* po = nullptr;             // chunk outputs [nq][C][128]
   int* count = nullptr;            // arrival counters [nkv], zero between launches
-  float* out = nullptr;            // merged attention output [nq*128]
-  int nq = 16, nkv = 8, max_seq = 0, C = 0;
+  float* out = nullptr;            // merged attention row [nq*128]
+  int nq = 16, nkv = 8, max_seq = 0;
+  int C = 0;                       // chunks per q head the partial arrays hold (>= ceil(max_seq / T))
+  int T = 64;                      // cache positions per work-group (attn_chunk_size)
   float scale = 0.0f, eps = 1e-6f;
 };
+// records per q head the work-space must hold for any chunk size
 int attn_chunks(int max_seq);
+// cache positions per work-group: 64, or the tuning override (32, 64, 128)
+int attn_chunk_size(int max_seq);
+void attn_set_chunk(int t);
 hipError_t launch_attn_decode(const AttnDecodeArgs& a, hipStream_t st);
 hipError_t launch_step_end(const uint64_t* keys, int n, const float* embed, int H, float* hidden, int* state,
                            int32_t* tokens, int max_tokens, hipStream_t st);
