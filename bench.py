@@ -161,6 +161,46 @@ def bench_lm_head_greedy(lin, torch, W, K, dev, stream, reps=20):
     return out
 
 
+def bench_single_gemv(lin, torch, dev, stream, N=6144, K=2048, reps=10):
+    """One W8A32 decode GEMV, x fp32 [1, K], W int8 [N, K] with per-row
+    scales: the launches over 41+ distinct weight copies (>= 512 MB, beyond
+    the 256 MB Infinity Cache) captured in one HIP graph and replayed."""
+    copies = max(41, int(np.ceil(512e6 / (N * K))))
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    Ws = []
+    for _ in range(copies):
+        w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+        Ws.append(lin.DeviceWeights.from_codes(w, torch.rand(N, device=dev, generator=g) * 0.018 + 0.002))
+        del w
+    x = torch.randn((1, K), device=dev, generator=g)
+    y = torch.empty((1, N), device=dev)
+    with torch.cuda.stream(stream):
+        for W in Ws:
+            lin.w8a32_linear_dev(x, W, y, stream=stream)
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for W in Ws:
+            lin.w8a32_linear_dev(x, W, y, stream=stream)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / (reps * copies)
+    b = gemv_bytes(N, K)
+    del graph
+    for W in Ws:
+        W.close()
+    return {"N": N, "K": K, "us": round(t * 1e6, 3), "GBps": round(b / t / 1e9, 1),
+            "frac_hbm": round(b / t / 1e9 / HBM_PEAK_GBS, 4), "bytes": b, "weight_copies": copies,
+            "timing": "graph of one launch per weight copy, replayed; HIP events; per-launch average"}
+
+
 def bench_w8a8_prefill(lin, torch, dev, reps=20):
     out = {}
     tot_ops, tot_t = 0.0, 0.0
@@ -310,24 +350,54 @@ def bench_decoder_generate(lin, torch, dev, n_layers=28, vocab=151936, prefix=12
     return out
 
 
-def cpu_baseline(seconds=10.0):
+def host_cores():
+    """Threads for the CPU baseline: every core this process may run on
+    (its affinity mask), capped by OMP_NUM_THREADS when the host sets it (the
+    GPU box gives one GPU's process a 16-core share and sets it to 16)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except Exception:
+        n = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def host_description():
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except Exception:
+        aff = None
+    return {"host_cpu": model, "nproc": os.cpu_count(), "affinity_cpus": aff,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
+def cpu_baseline(seconds=10.0, legs_seconds=20.0):
     """The oracle's M=1 GEMV (same formula as the reference's w8a32_gemv,
     OpenMP over row chunks like its GCD fan-out) on the host cores, over the
     same steps as the GPU: one layer's projection set (layer copy i % 28 of
     28 distinct ones) + the lm_head (one of two copies, alternating; 2.0 GB
-    of int8 weights in all, so no cache holds them).  Steps are timed until the time budget is spent; the
-    median step time gives GB/s."""
+    of int8 weights in all, so no cache holds them).  Steps are timed until
+    the time budget is spent; the median step time gives GB/s.  Beside it,
+    the reference's M>1 decompositions on the same cores (oracle/baseline.c:
+    dequantized 64/128-row weight tiles and a blocked fp32 SGEMM): W8A8 at
+    M=1024, the W8A16 sweep and w8a32_linear at the 1200-token prefill."""
     from oracle import oracle as orc
     native = True
     try:
         orc.build(native=True)
     except Exception:
         native = False
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except Exception:
-        cores = os.cpu_count() or 1
-    cores = max(1, min(cores, 16))
+    cores = host_cores()
     rng = np.random.default_rng(0)
     # two lm_head copies, alternating: a host last-level cache must not hold
     # the lm_head from one step to the next
@@ -352,22 +422,70 @@ def cpu_baseline(seconds=10.0):
         times.append(time.perf_counter() - t0)
         i += 1
     t_step = float(np.median(times))
-    model = "unknown"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    del mats
     step_bytes = sum(gemv_bytes(N, K) for (_, N, K) in LAYER_SHAPES + [LM_HEAD])
-    return {"value": round(step_bytes / t_step / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
-            "ms_per_step": round(t_step * 1e3, 3), "steps_timed": len(times),
-            "host_cpu": model, "nproc": os.cpu_count(),
-            "sample": f"oracle M=1 GEMV ({'-march=native' if native else 'x86-64-v3'}, OpenMP, "
-                      f"{cores} threads) over the benchmark's steps (one layer's projection set of 28 distinct "
-                      f"copies + one of two lm_head copies, 361.5 MB per step), median of {len(times)} steps "
-                      f"in ~{seconds:.0f} s"}
+    out = {"value": round(step_bytes / t_step / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
+           "ms_per_step": round(t_step * 1e3, 3), "steps_timed": len(times)}
+    out.update(host_description())
+    out["sample"] = (f"oracle M=1 GEMV ({'-march=native' if native else 'x86-64-v3'}, OpenMP, {cores} threads) "
+                     f"over the benchmark's steps (one layer's projection set of 28 distinct copies + one of two "
+                     f"lm_head copies, 361.5 MB per step), median of {len(times)} steps in ~{seconds:.0f} s")
+
+    # ---- the M>1 legs: each point timed on distinct weights, median of its calls
+    budget_end = time.perf_counter() + legs_seconds
+
+    def timed(fn, calls):
+        fn()                                          # warm-up (first touch, tile buffers)
+        ts = []
+        for _ in range(calls):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
+    legs = {}
+    w8 = {}
+    for (N, K) in [(6144, 2048), (2048, 6144)]:
+        M = 1024
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        xq, xs = orc.quantize_rows(x)
+        w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+        s = rng.uniform(0.002, 0.02, N).astype(np.float32)
+        t = timed(lambda: orc.base_w8a8_gemm(xq, xs, w, s, cores, native), 2)
+        w8[f"M{M}_N{N}_K{K}"] = {"ms": round(t * 1e3, 2), "GOPS": round(2.0 * M * N * K / t / 1e9, 1)}
+    legs["w8a8_m1024"] = w8
+    sw = {}
+    K = 2048
+    for N in (2048, 4096, 12288):
+        w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+        s = rng.uniform(0.002, 0.02, N).astype(np.float32)
+        for M in (1, 8, 64, 256, 1024):
+            if time.perf_counter() > budget_end:
+                break
+            xb = (rng.standard_normal((M, K), dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)
+            t = timed(lambda: orc.base_w8a16_linear(xb, w, s, cores, native), 5 if M <= 64 else 2)
+            b = N * K + 4 * N + 2 * M * K + 2 * M * N
+            sw[f"M{M}_N{N}"] = {"ms": round(t * 1e3, 3), "GFLOPS": round(2.0 * M * N * K / t / 1e9, 1),
+                                "GBps": round(b / t / 1e9, 1)}
+    legs["w8a16_sweep"] = sw
+    pre = {}
+    tot = 0.0
+    for (name, N, K) in LAYER_SHAPES:
+        if time.perf_counter() > budget_end:
+            break
+        M = 1200
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+        s = rng.uniform(0.002, 0.02, N).astype(np.float32)
+        t = timed(lambda: orc.base_w8a32_gemm(x, w, s, cores, native), 1)
+        pre[name] = {"ms": round(t * 1e3, 2), "GFLOPS": round(2.0 * M * N * K / t / 1e9, 1)}
+        tot += t
+    if len(pre) == len(LAYER_SHAPES):
+        pre["layer_ms"] = round(tot * 1e3, 2)
+    legs["w8a32_prefill_m1200"] = pre
+    legs["kind"] = "port: the reference's tile decompositions (oracle/baseline.c), blocked fp32 SGEMM"
+    out["m_gt_1_legs"] = legs
+    return out
 
 
 def rotating(lin, torch, dev, N, K, min_bytes=600e6):
@@ -380,18 +498,24 @@ def rotating(lin, torch, dev, N, K, min_bytes=600e6):
     return Ws
 
 
-def time_calls(torch, fn, n_w, reps=20):
+def time_calls(torch, fn, n_w, reps=20, rounds=3):
+    """Per-call time of fn(i % n_w, stream): the median over `rounds` timed
+    rounds of `reps` back-to-back calls (HIP events), after warm-up calls on
+    every weight copy."""
     st = torch.cuda.current_stream()
-    for i in range(3):
+    for i in range(max(3, n_w)):
         fn(i % n_w, st)
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    for i in range(reps):
-        fn(i % n_w, st)
-    e1.record(st)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e-3 / reps
+    ts = []
+    for r in range(rounds):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for i in range(reps):
+            fn((r * reps + i) % n_w, st)
+        e1.record(st)
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e-3 / reps)
+    return float(np.median(ts))
 
 
 def bench_decode_rows(lin, torch, dev):
@@ -637,6 +761,9 @@ def main():
         it[3].close()
     del items
 
+    log("single decode GEMV 6144x2048 over 41 weight copies")
+    single = bench_single_gemv(lin, torch, dev, stream)
+
     prefill = rows = sweep = pre32 = host = None
     if not args.quick:
         log("host-pointer ABI (PCIe-inclusive)")
@@ -683,6 +810,7 @@ def main():
         "roofline": roofline,
         "decode_step_28_layers": step28,
         "lm_head_greedy": greedy,
+        "gemv_6144x2048": single,
         "decoder_greedy": dec,
         "w8a8_prefill": prefill,
         "w8a32_decode_rows": rows,

@@ -96,6 +96,15 @@ void orc_prefill_layer(const int8_t *const *w, const float *const *s, const floa
                        const float *token_cos, const float *token_sin, int cache_len, int hidden_dim, int ffn_dim,
                        int num_q_heads, int num_kv_heads, int threads, int w8a8);
 
+/* CPU baseline (baseline.c): the reference's M>1 tile decompositions on a
+ * blocked fp32 SGEMM, and the W8A16 batch-1 GEMV, for timing beside the GPU. */
+void orc_base_w8a32_gemm(const float *X, const int8_t *w, const float *ws, const float *bias, float *Y,
+                         int M, int N, int K, int threads);
+void orc_base_w8a8_gemm(const int8_t *xq, const float *xs, const int8_t *w, const float *ws, const float *bias,
+                        float *Y, int M, int N, int K, int threads);
+void orc_base_w8a16_linear(const uint16_t *xb, const int8_t *w, const float *ws, const float *bias, float *Y,
+                           int M, int N, int K, int threads);
+
 #ifdef __cplusplus
 }
 #endif

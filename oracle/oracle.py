@@ -48,8 +48,15 @@ def load(native: bool = False) -> ctypes.CDLL:
                                      ctypes.c_int, ctypes.c_int, ctypes.c_int]
     lib.orc_w8a32_gemv_timed.argtypes = [_f32p, _i8p, _f32p, _f32p, ctypes.c_int, ctypes.c_int,
                                          ctypes.c_int]
+    lib.orc_base_w8a32_gemm.argtypes = [_f32p, _i8p, _f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int]
+    lib.orc_base_w8a8_gemm.argtypes = [_i8p, _f32p, _i8p, _f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_int, ctypes.c_int]
+    lib.orc_base_w8a16_linear.argtypes = [_u16p, _i8p, _f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int, ctypes.c_int]
     for f in ("orc_quantize_rows", "orc_int_acc", "orc_w8a32_linear", "orc_w8a8_linear",
-              "orc_w8a16_linear", "orc_w8a32_gemv_timed"):
+              "orc_w8a16_linear", "orc_w8a32_gemv_timed", "orc_base_w8a32_gemm", "orc_base_w8a8_gemm",
+              "orc_base_w8a16_linear"):
         getattr(lib, f).restype = None
     _f = ctypes.c_float
     _i = ctypes.c_int
@@ -174,6 +181,44 @@ def w8a32_gemv_timed(x: np.ndarray, w: np.ndarray, scales: np.ndarray, y: np.nda
     load(native).orc_w8a32_gemv_timed(_p(x, ctypes.c_float), _p(w, ctypes.c_int8),
                                       _p(scales, ctypes.c_float), _p(y, ctypes.c_float),
                                       n, k, threads)
+
+
+def base_w8a32_gemm(x, w, scales, threads: int, native: bool = False, bias=None) -> np.ndarray:
+    """The CPU baseline's w8a32_linear at batch > 1 (64-row dequantized tiles, blocked SGEMM)."""
+    x = np.ascontiguousarray(x, np.float32)
+    bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    m, k = x.shape
+    n = w.shape[0]
+    y = np.empty((m, n), np.float32)
+    load(native).orc_base_w8a32_gemm(_p(x, ctypes.c_float), _p(w, ctypes.c_int8), _p(scales, ctypes.c_float),
+                                     _p(bias, ctypes.c_float), _p(y, ctypes.c_float), m, n, k, threads)
+    return y
+
+
+def base_w8a8_gemm(x_q, x_scales, w, w_scales, threads: int, native: bool = False, bias=None) -> np.ndarray:
+    """The CPU baseline's w8a8_linear at batch > 1 (X dequantized, 128-row tiles, blocked SGEMM)."""
+    x_q = np.ascontiguousarray(x_q, np.int8)
+    bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    m, k = x_q.shape
+    n = w.shape[0]
+    y = np.empty((m, n), np.float32)
+    load(native).orc_base_w8a8_gemm(_p(x_q, ctypes.c_int8), _p(x_scales, ctypes.c_float), _p(w, ctypes.c_int8),
+                                    _p(w_scales, ctypes.c_float), _p(bias, ctypes.c_float),
+                                    _p(y, ctypes.c_float), m, n, k, threads)
+    return y
+
+
+def base_w8a16_linear(x_bf16, w, w_scales, threads: int, native: bool = False, bias=None) -> np.ndarray:
+    """The CPU baseline's w8a16_linear (batch 1: chunked GEMV; batch > 1: 128-row tiles, blocked SGEMM)."""
+    x_bf16 = np.ascontiguousarray(x_bf16, np.uint16)
+    bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    m, k = x_bf16.shape
+    n = w.shape[0]
+    y = np.empty((m, n), np.float32)
+    load(native).orc_base_w8a16_linear(_p(x_bf16, ctypes.c_uint16), _p(w, ctypes.c_int8),
+                                       _p(w_scales, ctypes.c_float), _p(bias, ctypes.c_float),
+                                       _p(y, ctypes.c_float), m, n, k, threads)
+    return y
 
 
 # ---------------------------------------------------------------------------

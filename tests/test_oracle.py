@@ -310,3 +310,31 @@ def test_numpy_mean_order_matches_kernel_model(K):
         s = _pairwise_model(h)
         assert s == np.add.reduce((h * h).astype(np.float32))
         assert np.mean(h * h) == np.float32(s / np.float32(K))
+
+
+@pytest.mark.parametrize("M,N,K", [(2, 130, 70), (37, 300, 257), (64, 256, 2048)])
+def test_cpu_baseline_gemms_match_checker(orc, M, N, K):
+    """The timed CPU-baseline legs (the reference's tile decompositions on a
+    blocked fp32 SGEMM) compute what the pinned checker computes: W8A32 and
+    W8A8 batch > 1 and W8A16 (batch 1 and > 1) within relative L2 1e-5 of
+    the float64-accumulated oracle, with and without bias, in both builds;
+    ragged shapes exercise the tile and register-block edges."""
+    rng = np.random.default_rng(M * 7 + N + K)
+    x = rng.standard_normal((M, K)).astype(F)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    s = rng.uniform(0.002, 0.02, N).astype(F)
+    b = rng.standard_normal(N).astype(F)
+    xq, xs = orc.quantize_rows(x)
+    u = x.view(np.uint32).astype(np.uint64)
+    xb = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+    def rel(a, r):
+        return float(np.linalg.norm(a.astype(np.float64) - r) / np.linalg.norm(r))
+    for native in (False, True):
+        for bias in (None, b):
+            assert rel(orc.base_w8a32_gemm(x, w, s, 3, native, bias), orc.w8a32_linear(x, w, s, bias=bias)) <= 1e-5
+            assert rel(orc.base_w8a8_gemm(xq, xs, w, s, 3, native, bias),
+                       orc.w8a8_linear(xq, xs, w, s, bias=bias)) <= 1e-5
+            assert rel(orc.base_w8a16_linear(xb, w, s, 3, native, bias), orc.w8a16_linear(xb, w, s, bias=bias)) <= 1e-5
+            assert rel(orc.base_w8a16_linear(xb[:1], w, s, 3, native, bias),
+                       orc.w8a16_linear(xb[:1], w, s, bias=bias)) <= 1e-5
