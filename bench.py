@@ -518,9 +518,42 @@ def time_calls(torch, fn, n_w, reps=20, rounds=3):
     return float(np.median(ts))
 
 
+def time_graph(torch, fn, n_w, min_calls=40, rounds=3):
+    """Per-call time of fn(i % n_w, stream) with the calls captured back to
+    back in one HIP graph (max(n_w, min_calls) calls: every weight copy once
+    or more) and replayed: the kernels' own time, without the host's launch
+    gaps (eager calls from Python are launch-bound below about 5 us).  Warm-up
+    calls first, so every work-space exists before the capture; the median
+    over `rounds` replays."""
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        for i in range(max(3, n_w)):
+            fn(i % n_w, st)
+    st.synchronize()
+    calls = max(n_w, min_calls)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        for i in range(calls):
+            fn(i % n_w, st)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(rounds):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e-3 / calls)
+    del g
+    return float(np.median(ts))
+
+
 def bench_decode_rows(lin, torch, dev):
-    """W8A32 decode rows M = 1, 2, 4, 8 (M = 1: int8 GEMV; M > 1: fp32
-    semantics on the MFMA small-M kernel) per decode shape, HBM GB/s."""
+    """W8A32 decode rows M = 1, 2, 4, 8 (M = 1: int8 GEMV; M = 2..8: fp32
+    semantics, int8 digit planes on the MFMA) per decode shape, HBM GB/s;
+    graph-replayed calls (time_graph)."""
     out = {}
     for (name, N, K) in LAYER_SHAPES + [LM_HEAD]:
         Ws = rotating(lin, torch, dev, N, K)
@@ -528,7 +561,7 @@ def bench_decode_rows(lin, torch, dev):
         for M in (1, 2, 4, 8):
             x = torch.randn((M, K), device=dev)
             y = torch.empty((M, N), device=dev)
-            t = time_calls(torch, lambda i, st: lin.w8a32_linear_dev(x, Ws[i], y, stream=st), len(Ws))
+            t = time_graph(torch, lambda i, st: lin.w8a32_linear_dev(x, Ws[i], y, stream=st), len(Ws))
             b = N * K + 4 * N + 4 * M * K + 4 * M * N
             row[f"M{M}"] = {"us": round(t * 1e6, 2), "GBps": round(b / t / 1e9, 1),
                             "frac_hbm": round(b / t / 1e9 / HBM_PEAK_GBS, 4)}
@@ -539,7 +572,8 @@ def bench_decode_rows(lin, torch, dev):
 
 
 def bench_w8a16_sweep(lin, torch, dev):
-    """W8A16 sweep: bf16 X [M, 2048], int8 W [N, 2048], bf16 out."""
+    """W8A16 sweep: bf16 X [M, 2048], int8 W [N, 2048], bf16 out; graph-replayed
+    calls (time_graph)."""
     out = {}
     K = 2048
     for N in (2048, 4096, 12288):
@@ -547,7 +581,7 @@ def bench_w8a16_sweep(lin, torch, dev):
         for M in (1, 8, 64, 256, 1024):
             x = torch.randn((M, K), device=dev).to(torch.bfloat16)
             y = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
-            t = time_calls(torch, lambda i, st: lin.w8a16_linear_dev(x, Ws[i], y, stream=st), len(Ws))
+            t = time_graph(torch, lambda i, st: lin.w8a16_linear_dev(x, Ws[i], y, stream=st), len(Ws))
             ops = 2.0 * M * N * K
             b = N * K + 4 * N + 2 * M * K + 2 * M * N
             hbm = M <= 64

@@ -110,6 +110,18 @@ int tl_gemv_set_plan(int rows, int u);
  * prefetch 7). */
 int tl_gemm_i8_set_cfg(int cfg);
 
+/* Tuning override of the 2..8-row kernel of w8a32_linear (int8 digit planes
+ * of the fp32 activations) for every later call in the process: 1..64 K
+ * slices per weight row group (at least as many as its LDS and registers
+ * need), 0 restores the planner, -1 switches the kernel off (the bf16-term
+ * small-batch kernel then takes those batches). */
+int tl_rows_set_split(int split);
+
+/* Tuning switch of w8a16_linear at batch 1 for every later call in the
+ * process: 1 (the default) runs it on the GEMV's weight stream with x as four
+ * int8 digit rows; 0 on the bf16 / fp16 MFMA small-batch kernel. */
+int tl_w8a16_set_gemv(int on);
+
 /* Tuning override of the decode attention for every later launch or graph
  * capture in the process: cache positions per work-group, 32, 64 or 128; 0
  * restores the built-in choice. */

@@ -345,6 +345,37 @@ def test_w8a32_small_batch_special_rows(lin, orc, M, N, K):
             assert rel_l2(got[r], want[r]) <= 1e-5, (r, rel_l2(got[r], want[r]))
 
 
+@pytest.mark.parametrize("M,N,K", [(2, 2048, 2048), (4, 2048, 6144), (5, 300, 2048), (8, 4096, 2048),
+                                   (7, 100, 68), (3, 20000, 2048), (8, 2048, 6144)])
+def test_rows_digit_planes_k_slices(lin, orc, M, N, K):
+    """w8a32_linear at 2..8 token rows as int8 digit planes (rows.hip) at
+    every K-slice count: one slice (outputs stored directly) and 2..5 slices
+    (partials merged by the row group's last work-group), each within
+    relative L2 1e-5 of the oracle's fp32 GEMM, bias included; a row holding
+    NaN gives NaN outputs and leaves the other rows' bits unchanged, and two
+    calls in a row give the same bits (the arrival counters are back at
+    zero); the earlier small-batch kernel (split -1) agrees too."""
+    say(f"rows digit planes M={M} N={N} K={K}")
+    lib = lin.load_library()
+    rng = np.random.default_rng(M * 31 + N + K)
+    x, w, s = make(rng, M, N, K)
+    b = rng.standard_normal(N).astype(F)
+    want = orc.w8a32_linear(x, w, s, bias=b)
+    xn = x.copy()
+    xn[M - 1, K // 3] = np.nan
+    try:
+        for split in (1, 2, 3, 5, -1, 0):
+            assert lib.tl_rows_set_split(split) == 0
+            got = lin.w8a32_linear(x, w, s, bias=b)
+            assert rel_l2(got, want) <= 1e-5, (split, rel_l2(got, want))
+            np.testing.assert_array_equal(lin.w8a32_linear(x, w, s, bias=b), got)
+            gn = lin.w8a32_linear(xn, w, s, bias=b)
+            assert np.isnan(gn[M - 1]).all(), split
+            np.testing.assert_array_equal(gn[:M - 1], got[:M - 1])
+    finally:
+        lib.tl_rows_set_split(0)
+
+
 def test_w8a32_prefill_rows_consistent(lin, orc):
     """1200-token prefill (fused QKV shape): rows are independent, so a
     subset computed alone matches the corresponding rows of the full call."""
@@ -514,6 +545,58 @@ def test_w8a16_fp32_out(lin, orc, M, N, K):
     assert rel_l2(lin.w8a16_linear(xb, w, s), want) <= 1e-5
     b = rng.standard_normal(N).astype(F)
     assert rel_l2(lin.w8a16_linear(xb, w, s, bias=b), orc.w8a16_linear(xb, w, s, bias=b)) <= 1e-5
+
+
+@pytest.mark.parametrize("N,K", [(4096, 2048), (2048, 6144), (151936, 2048), (300, 16384), (37, 50), (70, 1000)])
+def test_w8a16_batch1_gemv_digit_rows(lin, orc, dev, N, K):
+    """w8a16_linear at batch 1 on the GEMV's weight stream with x as four int8
+    digit rows (gemv.hip plane mode): within relative L2 1e-5 of the oracle
+    (the reference's bf16 dot products) with and without bias, also with the
+    bf16 / fp16 MFMA kernel switched in (tl_w8a16_set_gemv(0)) for the same
+    inputs; bf16 and fp16 outputs within 2e-3; a zero row gives the bias
+    exactly, a row of 1e-30 magnitude stays within 1e-5, and NaN or Inf in x
+    gives NaN outputs."""
+    import torch
+    say(f"w8a16 batch-1 GEMV N={N} K={K}")
+    lib = lin.load_library()
+    rng = np.random.default_rng(N + K)
+    x, w, s = make(rng, 1, N, K)
+    xb = bf16_bits(x)
+    b = rng.standard_normal(N).astype(F)
+    want = orc.w8a16_linear(xb, w, s)
+    wantb = orc.w8a16_linear(xb, w, s, bias=b)
+    try:
+        for on in (1, 0):
+            assert lib.tl_w8a16_set_gemv(on) == 0
+            assert rel_l2(lin.w8a16_linear(xb, w, s), want) <= 1e-5, on
+            assert rel_l2(lin.w8a16_linear(xb, w, s, bias=b), wantb) <= 1e-5, on
+    finally:
+        lib.tl_w8a16_set_gemv(1)
+    z = np.zeros_like(xb)
+    np.testing.assert_array_equal(lin.w8a16_linear(z, w, s, bias=b), b[None, :])
+    tiny = bf16_bits(x * F(1e-30))
+    assert rel_l2(lin.w8a16_linear(tiny, w, s), orc.w8a16_linear(tiny, w, s)) <= 1e-5
+    for bad in (np.nan, np.inf):
+        xx = x.copy()
+        xx[0, K // 2] = bad
+        assert np.isnan(lin.w8a16_linear(bf16_bits(xx), w, s)).all(), bad
+    # device path: bf16 / fp16 x with bf16 / fp16 out
+    W = lin.DeviceWeights.from_codes(w, s)
+    xt = torch.from_numpy(x).to(dev).to(torch.bfloat16)
+    y = torch.empty((1, N), dtype=torch.bfloat16, device=dev)
+    lin.w8a16_linear_dev(xt, W, y)
+    torch.cuda.synchronize()
+    assert rel_l2(y.float().cpu().numpy(), want) <= 2e-3
+    xh = x.astype(np.float16)
+    wantf = (xh.astype(np.float64) @ w.astype(np.float64).T) * s.astype(np.float64)
+    yh = torch.empty((1, N), dtype=torch.float16, device=dev)
+    lin.w8a16_linear_dev(torch.from_numpy(xh).to(dev), W, yh)
+    yf = torch.empty((1, N), dtype=torch.float32, device=dev)
+    lin.w8a16_linear_dev(torch.from_numpy(xh).to(dev), W, yf)
+    torch.cuda.synchronize()
+    assert rel_l2(yh.float().cpu().numpy(), wantf) <= 2e-3
+    assert rel_l2(yf.cpu().numpy(), wantf) <= 1e-5
+    W.close()
 
 
 @pytest.mark.parametrize("M", [1, 8, 64, 256, 1024])

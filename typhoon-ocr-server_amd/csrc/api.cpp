@@ -367,6 +367,23 @@ void run_gemm(Workspace& ws, GemmLaunch& L, hipStream_t st) {
   HIP_OK(launch_gemm(L, st));
 }
 
+// 1..8 rows with fp32 semantics as int8 digit planes (rows.hip); false when
+// the shape or alignment is not one it takes, or the path is switched off
+bool g_rows_off = false;
+bool g_gemv_w8a16_off = false;   // tuning: W8A16 batch 1 on the bf16 / fp16 MFMA kernel instead
+
+bool run_rows(Workspace& ws, GemmLaunch& L, hipStream_t st) {
+  if (g_rows_off || !rows_supported(L)) return false;
+  const RowsPlan p = rows_plan(L.M, L.N, L.K);
+  if (p.split > 1) {
+    ws.part.ensure(rows_workspace_bytes(L.M, L.N, L.K), st);
+    L.part = ws.part.p;
+    L.cnt = ensure_counters(ws, rows_counter_count(L.N), st);
+  }
+  HIP_OK(launch_rows(L, st));
+  return true;
+}
+
 void op_w8a32(const float* X, const tl_weights* W, const float* bias, float* Y, int batch,
               hipStream_t st) {
   Workspace& ws = workspace(W->dev, st);
@@ -387,26 +404,33 @@ void op_w8a32(const float* X, const tl_weights* W, const float* bias, float* Y, 
       L.xs_in = xs;
     }
     run_gemv(ws, L, st);
-  } else if ((batch <= 16 && W->NG < 2048) || (batch <= 32 && W->NG <= 256)) {
+    return;
+  }
+  GemmLaunch L;
+  L.amode = A_F32X3;
+  L.A = X;
+  L.lda = W->cols;
+  L.Bt = W->tiles;
+  L.ws = W->scales;
+  L.bias = bias;
+  L.Y = Y;
+  L.ldy = W->rows;
+  L.M = batch;
+  L.N = W->rows;
+  L.K = W->cols;
+  L.ep = EP_SCALE;
+  L.out = OUT_F32;
+  // 2..8 token rows over a weight of fewer than 32768 rows: int8 digit planes
+  // of the fp32 rows, made inside the one launch (rows.hip; every work-group
+  // splits its activation slice, which an lm_head-wide grid repeats too
+  // often: 2 tokens 62.5 us there against 58.6 us below)
+  if (batch <= 8 && W->NG < 2048 && run_rows(ws, L, st)) return;
+  if ((batch <= 16 && W->NG < 2048) || (batch <= 32 && W->NG <= 256)) {
     // a few token rows over a narrow weight: the small-M kernel splits the
     // fp32 rows into three bf16 terms as it loads them (one launch; a
     // separate plane split costs more than it saves at these sizes: at
     // N <= 4096, 24-32 tokens 13.7-15.1 us here against 16.6-17.0 us on the
     // planes, which win from 48 tokens)
-    GemmLaunch L;
-    L.amode = A_F32X3;
-    L.A = X;
-    L.lda = W->cols;
-    L.Bt = W->tiles;
-    L.ws = W->scales;
-    L.bias = bias;
-    L.Y = Y;
-    L.ldy = W->rows;
-    L.M = batch;
-    L.N = W->rows;
-    L.K = W->cols;
-    L.ep = EP_SCALE;
-    L.out = OUT_F32;
     run_gemm(ws, L, st);
   } else {
     // fp32 rows as four int8 planes each (x = 2^e (q0 + q1/254 + q2/254^2 +
@@ -421,20 +445,20 @@ void op_w8a32(const float* X, const tl_weights* W, const float* bias, float* Y, 
     uint8_t* tiles = static_cast<uint8_t*>(ws.planes.p);
     int* xe = reinterpret_cast<int*>(tiles + xe_off);
     HIP_OK(launch_split_i8x4(X, K, batch, K, tiles, xe, st));
-    GemmLaunch L;
-    L.amode = A_I8;
-    L.A = tiles;
-    L.Bt = W->tiles;
-    L.ws = W->scales;
-    L.xe = xe;
-    L.bias = bias;
-    L.Y = Y;
-    L.ldy = W->rows;
-    L.M = M4;
-    L.N = W->rows;
-    L.K = K;
-    L.out = OUT_F32_X4;
-    run_gemm(ws, L, st);
+    GemmLaunch P;
+    P.amode = A_I8;
+    P.A = tiles;
+    P.Bt = W->tiles;
+    P.ws = W->scales;
+    P.xe = xe;
+    P.bias = bias;
+    P.Y = Y;
+    P.ldy = W->rows;
+    P.M = M4;
+    P.N = W->rows;
+    P.K = K;
+    P.out = OUT_F32_X4;
+    run_gemm(ws, P, st);
   }
 }
 
@@ -502,6 +526,24 @@ void op_w8a16(const void* X, int x_type, const tl_weights* W, const float* bias,
   // adds it after the product (:193-200)
   L.ep = (batch == 1) ? EP_SCALE_FMA : EP_SCALE;
   L.out = (y_type == TL_F32) ? OUT_F32 : (y_type == TL_BF16 ? OUT_BF16 : OUT_F16);
+  if (batch == 1 && gemv_fused_xv(W->cols) > 0 && !g_gemv_w8a16_off) {
+    // one token: the GEMV's weight stream with x as four int8 digit rows
+    // (fp32-accurate products, y = fma(sum, ws, bias) as the reference's
+    // r * ws + b)
+    GemvLaunch G;
+    G.x = static_cast<const float*>(X);
+    G.x_type = x_type == TL_BF16 ? 1 : 2;
+    G.wt = W->tiles;
+    G.ws = W->scales;
+    G.bias = bias;
+    G.y = static_cast<float*>(Y);
+    G.N = W->rows;
+    G.K = W->cols;
+    G.epi = EPI_W8A16;
+    G.out = L.out;
+    run_gemv(ws, G, st);
+    return;
+  }
   run_gemm(ws, L, st);
 }
 
@@ -800,6 +842,21 @@ int tl_gemv_set_plan(int rows, int u) {
     REQUIRE(u == 0 || u == 2 || u == 4 || u == 6 || u == 8 || u == 12, "u must be 0, 2, 4, 6, 8 or 12");
     REQUIRE(u == 0 || rows == 0 || (rows == 16 ? u != 6 : u != 12), "u = 6 needs rows 8, u = 12 rows 16");
     gemv_set_plan(rows, u);
+  });
+}
+
+int tl_rows_set_split(int split) {
+  return guarded("tl_rows_set_split", [&] {
+    REQUIRE(split >= -1 && split <= 64, "split must be -1 (path off), 0 (planner) or 1..64");
+    g_rows_off = split < 0;
+    rows_set_split(split > 0 ? split : 0);
+  });
+}
+
+int tl_w8a16_set_gemv(int on) {
+  return guarded("tl_w8a16_set_gemv", [&] {
+    REQUIRE(on == 0 || on == 1, "on must be 0 or 1");
+    g_gemv_w8a16_off = on == 0;
   });
 }
 

@@ -54,7 +54,9 @@ struct GemvArgs {
   float norm_eps;
   int norm;            // NORM_*
   int N, K, KB, NG, epi;
-  int x_vec;           // 2: K == 1024*XV and x 16-byte aligned (unguarded loads)
+  int x_vec;           // 2: K == 1024*XV and x aligned to 4 elements (unguarded loads)
+  int x_type = 0;      // EPI_W8A16: 0 fp32, 1 bf16, 2 fp16
+  int out = OUT_F32;   // EPI_W8A16: output type
 };
 
 __device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, int n, int acc, float xs,
@@ -87,24 +89,29 @@ struct WStream {
   __device__ __forceinline__ int kb_clamped(int i) const { return min(kb_of(i), kbmax); }
 };
 
-// acc += dot(tiles, codes) for U load instructions starting at i0; k-blocks at
-// or beyond kb1 were loaded from a clamped address and are dropped.
-template <int XV, int U, int RH>
-__device__ __forceinline__ int consume_batch(const uint4 (&b)[U], const uint4 (&c)[XV == 0 ? U : 1],
-                                             const uint4* s_codes, const WStream<RH>& ws, int i0, int lg,
-                                             int acc) {
-  uint4 cv[U];
+// acc[p] += dot(tiles, codes of row p) for U load instructions starting at
+// i0 (NP = 1 code row, or the 4 digit rows of the plane mode, each XV KiB of
+// LDS); k-blocks at or beyond kb1 were loaded from a clamped address and are
+// dropped.
+template <int XV, int U, int RH, int NP>
+__device__ __forceinline__ void consume_batch(const uint4 (&b)[U], const uint4 (&c)[XV == 0 ? U : 1],
+                                              const uint4* s_codes, const WStream<RH>& ws, int i0, int lg,
+                                              int (&acc)[NP]) {
+  uint4 cv[U][NP];
 #pragma unroll
-  for (int u = 0; u < U; u++) {
-    if constexpr (XV > 0) cv[u] = s_codes[ws.kb_clamped(i0 + u) * 4 + lg];
-    else cv[u] = c[u];
-  }
+  for (int u = 0; u < U; u++)
 #pragma unroll
-  for (int u = 0; u < U; u++) {
-    const int d = dot16(b[u], cv[u], 0);
-    acc += (ws.kb_of(i0 + u) < ws.kb1) ? d : 0;
-  }
-  return acc;
+    for (int p = 0; p < NP; p++) {
+      if constexpr (XV > 0) cv[u][p] = s_codes[p * XV * 64 + ws.kb_clamped(i0 + u) * 4 + lg];
+      else cv[u][p] = c[u];
+    }
+#pragma unroll
+  for (int u = 0; u < U; u++)
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+      const int d = dot16(b[u], cv[u][p], 0);
+      acc[p] += (ws.kb_of(i0 + u) < ws.kb1) ? d : 0;
+    }
 }
 
 template <int XV, int U, int RH>
@@ -234,12 +241,39 @@ __device__ void decoder_rmsnorm(float4 (&xv)[XV], const float4 (&nwv)[XV], bool 
   }
 }
 
+// 4 activations at k of a row of fp32 (xt 0), bf16 (1) or fp16 (2), as fp32
+__device__ __forceinline__ float4 gemv_x4(const float* x, int xt, int k) {
+  if (xt == 0) return *reinterpret_cast<const float4*>(x + k);
+  const uint2 u = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(x) + k);
+  if (xt == 1)
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                       __uint_as_float(u.y & 0xffff0000u));
+  return make_float4((float)__builtin_bit_cast(_Float16, (uint16_t)(u.x & 0xffff)),
+                     (float)__builtin_bit_cast(_Float16, (uint16_t)(u.x >> 16)),
+                     (float)__builtin_bit_cast(_Float16, (uint16_t)(u.y & 0xffff)),
+                     (float)__builtin_bit_cast(_Float16, (uint16_t)(u.y >> 16)));
+}
+__device__ __forceinline__ float gemv_x1(const float* x, int xt, int k) {
+  if (xt == 0) return x[k];
+  const uint16_t h = reinterpret_cast<const uint16_t*>(x)[k];
+  return xt == 1 ? __uint_as_float((uint32_t)h << 16) : (float)__builtin_bit_cast(_Float16, h);
+}
+
 // Arguments are scalars so that the leading ones (through `flags`) are
 // preloaded into SGPRs at wave launch (kernarg preload, -amdgpu-kernarg-
 // preload-count in the build): the first loads need no kernarg fetch.
 // flags: bits 0-1 x_vec, bits 2-4 epilogue, bit 5 bias present, bits 6-7
-// RMSNorm of x first (NORM_*; K == 1024 XV a power of two, x_vec 2).
-template <int XV, int U, int RH>
+// RMSNorm of x first (NORM_*; K == 1024 XV a power of two, x_vec 2); plane
+// mode (PL, EPI_W8A16): bits 8-9 x type (0 fp32, 1 bf16, 2 fp16), bits 10-11
+// output type (OUT_F32, OUT_BF16, OUT_F16).
+//
+// Plane mode: x (any of the three types, held as fp32) becomes four int8
+// digit rows in LDS (digit_word / digit_planes: the row's absmax exponent
+// e, q = x 2^(30-e) truncated), each weight dword meets all four through
+// v_dot4, and y = fma(2^(e-6) t, ws, bias) with t the digit sums' Horner
+// combination: fp32-accurate products (w8a16_linear batch 1,
+// kernel/w8a16_kernel.c:90-182) on the GEMV's weight stream.
+template <int XV, int U, int RH, int PL>
 __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint8_t* wt, const float* ws,
                                                       float* y, int N, int K, int NG, int KB, int flags,
                                                       const uint8_t* xq, const float* xs_in, const float* bias,
@@ -266,10 +300,12 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
   a.NG = NG;
   a.epi = (flags >> 2) & 7;
   a.x_vec = flags & 3;
-  __shared__ uint4 s_codes[XV > 0 ? XV * 64 : 1];
+  constexpr int NP = PL ? 4 : 1;        // code rows: the activation codes, or its 4 digit rows
+  const int xt = PL ? (flags >> 8) & 3 : 0;
+  __shared__ uint4 s_codes[XV > 0 ? XV * 64 * NP : 1];
   __shared__ uint32_t s_mx[4];
   __shared__ float s_tail[4];
-  __shared__ int s_red[RH * 4 * SL];
+  __shared__ int s_red[NP][RH * 4 * SL];
 
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // k slice of this wave
@@ -302,7 +338,7 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
   if constexpr (XV > 0) {
     if (a.x_vec == 2) {
 #pragma unroll
-      for (int i = 0; i < XV; i++) xv[i] = *reinterpret_cast<const float4*>(a.x + 4 * (threadIdx.x + 256 * i));
+      for (int i = 0; i < XV; i++) xv[i] = gemv_x4(a.x, xt, 4 * (threadIdx.x + 256 * i));
       if (norm) {
 #pragma unroll
         for (int i = 0; i < XV; i++)
@@ -314,10 +350,10 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
       for (int i = 0; i < XV; i++) {
         const int k0 = 4 * (threadIdx.x + 256 * i);
         float4 v;
-        v.x = (k0 < K) ? a.x[k0] : 0.f;
-        v.y = (k0 + 1 < K) ? a.x[k0 + 1] : 0.f;
-        v.z = (k0 + 2 < K) ? a.x[k0 + 2] : 0.f;
-        v.w = (k0 + 3 < K) ? a.x[k0 + 3] : 0.f;
+        v.x = (k0 < K) ? gemv_x1(a.x, xt, k0) : 0.f;
+        v.y = (k0 + 1 < K) ? gemv_x1(a.x, xt, k0 + 1) : 0.f;
+        v.z = (k0 + 2 < K) ? gemv_x1(a.x, xt, k0 + 2) : 0.f;
+        v.w = (k0 + 3 < K) ? gemv_x1(a.x, xt, k0 + 3) : 0.f;
         xv[i] = v;
       }
     }
@@ -330,7 +366,35 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
   const float bv = a.bias ? a.bias[nr] : 0.0f;
 
   float xs;
-  if constexpr (XV > 0) {
+  int px = 0;                            // plane mode: the row's absmax exponent, or kXeNonFinite
+  if constexpr (PL) {
+    // ---- digit rows of x (every element: no scalar tail in this mode) ------
+    uint32_t mx = 0;
+#pragma unroll
+    for (int i = 0; i < XV; i++) {
+      const uint32_t m01 = max(abs_bits(xv[i].x), abs_bits(xv[i].y));
+      const uint32_t m23 = max(abs_bits(xv[i].z), abs_bits(xv[i].w));
+      mx = max(mx, max(m01, m23));
+    }
+    mx = wave_umax(mx);
+    if (lane == 0) s_mx[wv] = mx;
+    __syncthreads();
+    const uint32_t m = max(max(s_mx[0], s_mx[1]), max(s_mx[2], s_mx[3]));
+    int ex = 0;
+    if (m < 0x7f800000u && m != 0) (void)frexpf(__uint_as_float(m), &ex);
+    px = m < 0x7f800000u ? ex : kXeNonFinite;
+    uint32_t* sc = reinterpret_cast<uint32_t*>(s_codes);
+#pragma unroll
+    for (int i = 0; i < XV; i++) {
+      uint32_t d[4];
+      digit_planes(digit_word(xv[i].x, 30 - ex), digit_word(xv[i].y, 30 - ex), digit_word(xv[i].z, 30 - ex),
+                   digit_word(xv[i].w, 30 - ex), d);
+#pragma unroll
+      for (int p = 0; p < 4; p++) sc[p * XV * 256 + threadIdx.x + 256 * i] = d[p];
+    }
+    xs = 1.0f;
+    __syncthreads();
+  } else if constexpr (XV > 0) {
     if (a.norm == NORM_NUMPY) final_rmsnorm<XV>(xv, nwv, norm_w != nullptr, K, norm_eps);
     else if (a.norm == NORM_DECODER) decoder_rmsnorm<XV>(xv, nwv, norm_w != nullptr, K, norm_eps);
     // ---- fused per-token activation quantization --------------------------
@@ -416,33 +480,56 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
   // Both batches were issued before the prologue.  The loop body is
   // straight-line code that enters and leaves with the 2U loads of b0 and b1
   // outstanding, so the compiler keeps the wait counts exact.
-  int acc = 0;
+  int acc[NP];
+#pragma unroll
+  for (int p = 0; p < NP; p++) acc[p] = 0;
   int i = 0;
   for (; i + 2 * U < n_i; i += 2 * U) {
-    acc = consume_batch<XV, U, RH>(b0, c0, s_codes, st, i, lg, acc);
+    consume_batch<XV, U, RH, NP>(b0, c0, s_codes, st, i, lg, acc);
     load_batch<XV, U, RH>(b0, c0, st, cg, i + 2 * U, lg);
-    acc = consume_batch<XV, U, RH>(b1, c1, s_codes, st, i + U, lg, acc);
+    consume_batch<XV, U, RH, NP>(b1, c1, s_codes, st, i + U, lg, acc);
     load_batch<XV, U, RH>(b1, c1, st, cg, i + 3 * U, lg);
   }
-  acc = consume_batch<XV, U, RH>(b0, c0, s_codes, st, i, lg, acc);
-  acc = consume_batch<XV, U, RH>(b1, c1, s_codes, st, i + U, lg, acc);
+  consume_batch<XV, U, RH, NP>(b0, c0, s_codes, st, i, lg, acc);
+  consume_batch<XV, U, RH, NP>(b1, c1, s_codes, st, i + U, lg, acc);
 
   // ---- reduction: row r's 4*SL partials (wave w, lane slot q) at
-  //      s_red[r*4*SL + w*SL + q], summed in that order by wave 0 ------------
-  s_red[r * 4 * SL + wv * SL + slot] = acc;
+  //      s_red[p][r*4*SL + w*SL + q], summed in that order by wave 0 ---------
+#pragma unroll
+  for (int p = 0; p < NP; p++) s_red[p][r * 4 * SL + wv * SL + slot] = acc[p];
   __syncthreads();
   if (wv != 0) return;
   uint64_t key = 0;
   if (lane < RH) {
-    const int4* p = reinterpret_cast<const int4*>(s_red + lane * 4 * SL);
-    int tot = 0;
+    int tots[NP];
 #pragma unroll
-    for (int q = 0; q < SL; q++) {
-      const int4 v = p[q];
-      tot += (v.x + v.y) + (v.z + v.w);
+    for (int pp = 0; pp < NP; pp++) {
+      const int4* p = reinterpret_cast<const int4*>(s_red[pp] + lane * 4 * SL);
+      int t = 0;
+#pragma unroll
+      for (int q = 0; q < SL; q++) {
+        const int4 v = p[q];
+        t += (v.x + v.y) + (v.z + v.w);
+      }
+      tots[pp] = t;
     }
+    const int tot = tots[0];
     const int n = row0 + lane;
-    if (a.epi == EPI_SWIGLU) {
+    if constexpr (PL) {
+      if (n < a.N) {
+        const float t = digits_sum(tots[0], tots[1], tots[2], tots[3]);
+        const float v = px == kXeNonFinite ? __builtin_nanf("") : __fmaf_rn(ldexpf(t, px - 6), wsv, bv);
+        const int out = (flags >> 10) & 3;
+        if (out == OUT_F32) {
+          a.y[n] = v;
+        } else if (out == OUT_BF16) {
+          reinterpret_cast<uint16_t*>(a.y)[n] = (uint16_t)f32_to_bf16_rne(v);
+        } else {
+          const _Float16 h = (_Float16)v;
+          reinterpret_cast<uint16_t*>(a.y)[n] = __builtin_bit_cast(uint16_t, h);
+        }
+      }
+    } else if (a.epi == EPI_SWIGLU) {
       // RH == 16: lanes 0-7 hold gate rows 8b + lane, lanes 8-15 the matching
       // up rows; rows past N are zero rows (their value is never stored)
       const float g = __fmul_rn(__fmul_rn((float)tot, wsv), xs);
@@ -477,31 +564,32 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
 // ---------------------------------------------------------------------------
 // launcher
 // ---------------------------------------------------------------------------
-template <int XV, int U, int RH>
+template <int XV, int U, int RH, int PL>
 static void launch_one(const GemvArgs& a, int blocks, hipStream_t st) {
-  const int flags = (a.x_vec & 3) | ((a.epi & 7) << 2) | (a.bias ? 32 : 0) | ((a.norm & 3) << 6);
+  const int flags = (a.x_vec & 3) | ((a.epi & 7) << 2) | (a.bias ? 32 : 0) | ((a.norm & 3) << 6) |
+                    ((a.x_type & 3) << 8) | ((a.out & 3) << 10);
   const size_t dyn = a.norm == NORM_NUMPY ? (size_t)(a.K / 128) * kNpNormStride * sizeof(float) : 0;
-  hipLaunchKernelGGL((gemv_i8_kernel<XV, U, RH>), dim3(blocks), dim3(256), dyn, st, a.x, a.wt, a.ws, a.y,
+  hipLaunchKernelGGL((gemv_i8_kernel<XV, U, RH, PL>), dim3(blocks), dim3(256), dyn, st, a.x, a.wt, a.ws, a.y,
                      a.N, a.K, a.NG, a.KB, flags, a.xq, a.xs_in, a.bias, a.acc_out, a.xs_out, a.keys,
                      a.norm_w, a.norm_eps);
 }
 
-template <int XV>
+template <int XV, int PL = 0>
 static hipError_t launch_xv(const GemvArgs& a, const GemvPlan& p, hipStream_t st) {
   if (p.rows == 16) {
     switch (p.u) {
-      case 2: launch_one<XV, 2, 16>(a, p.blocks, st); break;
-      case 4: launch_one<XV, 4, 16>(a, p.blocks, st); break;
-      case 8: launch_one<XV, 8, 16>(a, p.blocks, st); break;
-      case 12: launch_one<XV, 12, 16>(a, p.blocks, st); break;
+      case 2: launch_one<XV, 2, 16, PL>(a, p.blocks, st); break;
+      case 4: launch_one<XV, 4, 16, PL>(a, p.blocks, st); break;
+      case 8: launch_one<XV, 8, 16, PL>(a, p.blocks, st); break;
+      case 12: launch_one<XV, 12, 16, PL>(a, p.blocks, st); break;
       default: return hipErrorInvalidValue;
     }
   } else if (p.rows == 8) {
     switch (p.u) {
-      case 2: launch_one<XV, 2, 8>(a, p.blocks, st); break;
-      case 4: launch_one<XV, 4, 8>(a, p.blocks, st); break;
-      case 6: launch_one<XV, 6, 8>(a, p.blocks, st); break;
-      case 8: launch_one<XV, 8, 8>(a, p.blocks, st); break;
+      case 2: launch_one<XV, 2, 8, PL>(a, p.blocks, st); break;
+      case 4: launch_one<XV, 4, 8, PL>(a, p.blocks, st); break;
+      case 6: launch_one<XV, 6, 8, PL>(a, p.blocks, st); break;
+      case 8: launch_one<XV, 8, 8, PL>(a, p.blocks, st); break;
       default: return hipErrorInvalidValue;
     }
   } else {
@@ -610,6 +698,23 @@ hipError_t launch_gemv_i8(const GemvLaunch& L, hipStream_t st) {
       }
   }
   const int xv = L.x ? gemv_fused_xv(L.K) : 0;
+  if (L.epi == EPI_W8A16) {
+    // digit-plane mode: fused x only, no RMSNorm; y of type L.out
+    if (!L.x || xv == 0 || L.norm != NORM_NONE || L.x_type < 0 || L.x_type > 2) return hipErrorInvalidValue;
+    if (L.out != OUT_F32 && L.out != OUT_BF16 && L.out != OUT_F16) return hipErrorInvalidValue;
+    a.x_type = L.x_type;
+    a.out = L.out;
+    const uintptr_t align = L.x_type == 0 ? 15 : 7;
+    if (L.K == 1024 * xv && (((uintptr_t)L.x) & align) == 0) a.x_vec = 2;
+    switch (xv) {
+      case 2: return launch_xv<2, 1>(a, p, st);
+      case 4: return launch_xv<4, 1>(a, p, st);
+      case 6: return launch_xv<6, 1>(a, p, st);
+      case 8: return launch_xv<8, 1>(a, p, st);
+      case 16: return launch_xv<16, 1>(a, p, st);
+      default: return hipErrorInvalidValue;
+    }
+  }
   if (L.x && xv == 0) return hipErrorInvalidValue;  // caller must quantize first
   if (L.x && L.K == 1024 * xv && (((uintptr_t)L.x) & 15) == 0) a.x_vec = 2;
   if (L.norm && (!gemv_fused_norm_ok(L.K, L.x, L.norm_w) || a.x_vec != 2)) return hipErrorInvalidValue;

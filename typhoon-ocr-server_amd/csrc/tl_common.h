@@ -252,6 +252,44 @@ __device__ __forceinline__ float planes_scale(float t, float ws, int e) {
 }
 
 // ---------------------------------------------------------------------------
+// fp32 activations as four int8 digit rows (fp32-semantics products on int8
+// dot products): q = x 2^sh truncated (|q| < 2^30 for |x| < 2^(30 - sh)) is
+// d0 2^24 + d1 2^16 + d2 2^8 + d3 with signed digits d1..d3 in [-128, 127]
+// and d0 in [-64, 64]: the bytes of q + 0x808080, the low three flipped by
+// 0x80.  Digit sums a_p = sum_k w_k d_p,k are exact int32, and
+// sum_k w_k x_k = 2^(24 - sh) (a0 + 2^-8 (a1 + 2^-8 (a2 + 2^-8 a3))).
+// ---------------------------------------------------------------------------
+// biased digit word of one activation: (q + 0x808080) with q = x 2^sh
+// truncated toward zero (x 2^sh is exact in fp32, |x 2^sh| < 2^30 for a
+// finite slice; the clamp keeps Inf and NaN, whose token's outputs are NaN
+// anyway, in the int range)
+__device__ __forceinline__ uint32_t digit_word(float x, int sh) {
+  return (uint32_t)(int)__builtin_amdgcn_fmed3f(ldexpf(x, sh), -0x1p30f, 0x1p30f) + 0x808080u;
+}
+
+// four biased digit words (k .. k+3) -> the four digit-plane dwords:
+// plane p holds byte 3 - p of each word (p = 0 the most significant digit);
+// the low three bytes are flipped by 0x80 back to signed digits
+__device__ __forceinline__ void digit_planes(uint32_t y0, uint32_t y1, uint32_t y2, uint32_t y3, uint32_t (&pl)[4]) {
+  const uint32_t t0 = __builtin_amdgcn_perm(y1, y0, 0x05010400u);   // y0.b0 y1.b0 y0.b1 y1.b1
+  const uint32_t t1 = __builtin_amdgcn_perm(y1, y0, 0x07030602u);   // y0.b2 y1.b2 y0.b3 y1.b3
+  const uint32_t t2 = __builtin_amdgcn_perm(y3, y2, 0x05010400u);
+  const uint32_t t3 = __builtin_amdgcn_perm(y3, y2, 0x07030602u);
+  pl[3] = __builtin_amdgcn_perm(t2, t0, 0x05040100u) ^ 0x80808080u;  // byte 0 of each word
+  pl[2] = __builtin_amdgcn_perm(t2, t0, 0x07060302u) ^ 0x80808080u;  // byte 1
+  pl[1] = __builtin_amdgcn_perm(t3, t1, 0x05040100u) ^ 0x80808080u;  // byte 2
+  pl[0] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);                // byte 3 (top digit)
+}
+
+// a0 + 2^-8 (a1 + 2^-8 (a2 + 2^-8 a3)), each step rounded
+__device__ __forceinline__ float digits_sum(int a0, int a1, int a2, int a3) {
+  float t = __fadd_rn(__fmul_rn((float)a3, 0x1p-8f), (float)a2);
+  t = __fadd_rn(__fmul_rn(t, 0x1p-8f), (float)a1);
+  return __fadd_rn(__fmul_rn(t, 0x1p-8f), (float)a0);
+}
+
+
+// ---------------------------------------------------------------------------
 // argmax keys: the float's bits made monotonic in the high word, the index
 // complemented in the low word, so the largest key is the largest value and,
 // among equal values, the lowest index (torch.argmax's first-max rule)

@@ -15,7 +15,9 @@ __host__ __device__ inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 // EPI_SWIGLU: W8A32 outputs of a gate/up weight interleaved per 16-row group
 // (rows 16b..16b+7 = gate rows 8b.., rows 16b+8.. = up rows 8b..), written as
 // y[8b + r] = fl(silu(gate) * up) with the reference's fast-exp silu
-enum { EPI_W8A32 = 0, EPI_W8A8 = 1, EPI_ACC = 2, EPI_ARGMAX = 3, EPI_SWIGLU = 4 };
+// EPI_W8A16: fp32-semantics products of a bf16 / fp16 / fp32 x (x_type) as
+// four int8 digit rows, y = fma(sum, ws, bias) stored as `out`
+enum { EPI_W8A32 = 0, EPI_W8A8 = 1, EPI_ACC = 2, EPI_ARGMAX = 3, EPI_SWIGLU = 4, EPI_W8A16 = 5 };
 // GEMV x prologues: the numpy final RMSNorm (decoder.py:444-446) or the
 // decoder's RMSNorm (kernel/ops.c:22-56, estimate-based rsqrt)
 enum { NORM_NONE = 0, NORM_NUMPY = 1, NORM_DECODER = 2 };
@@ -117,6 +119,8 @@ struct GemvLaunch {
   const float* norm_w = nullptr;  //   its weights (null: none)
   float norm_eps = 1e-6f;
   int N = 0, K = 0, epi = EPI_W8A32;
+  int x_type = 0;                 // EPI_W8A16: x is 0 fp32, 1 bf16, 2 fp16
+  int out = OUT_F32;              // EPI_W8A16: y is OUT_F32 / OUT_BF16 / OUT_F16
 };
 GemvPlan gemv_plan(int N, int K);
 int gemv_fused_xv(int K);
@@ -165,5 +169,18 @@ bool gemm_b16_supported(const GemmLaunch& L);
 bool gemm_small_supported(const GemmLaunch& L);
 hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st);
 hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st);
+
+// ---- 2..8 rows of fp32 activations as int8 digit planes (rows.hip): amode
+//      A_F32X3; fp32 sums of w * x, y = 2^e fl(t * ws) summed over K slices,
+//      then + bias -----------------------------------------------------------
+struct RowsPlan {
+  int tg = 1, nkb = 16, cpt = 1, kbs = 1, split = 1, blocks = 0;
+};
+bool rows_supported(const GemmLaunch& L);
+RowsPlan rows_plan(int M, int N, int K);
+size_t rows_workspace_bytes(int M, int N, int K);   // partials when split > 1
+size_t rows_counter_count(int N);                   // zeroed arrival counters
+void rows_set_split(int s);                         // tuning override (0 = planner)
+hipError_t launch_rows(const GemmLaunch& L, hipStream_t st);
 
 }  // namespace tl

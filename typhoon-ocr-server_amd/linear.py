@@ -41,6 +41,8 @@ SIGNATURES = {
     "tl_device_count": (_int, []),
     "tl_gemv_set_plan": (_int, [_int, _int]),
     "tl_gemm_i8_set_cfg": (_int, [_int]),
+    "tl_rows_set_split": (_int, [_int]),
+    "tl_w8a16_set_gemv": (_int, [_int]),
     "tl_attn_set_chunk": (_int, [_int]),
     "tl_gemv_fused_dev": (_int, [_vp, _vp, _vp, _vp, _int, _int, _vp, _vp]),
     # decoder loop (Part 3), reference argtypes (decoder.py:86-143)
