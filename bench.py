@@ -90,29 +90,29 @@ def run_step(lin, items, stream):
         lin.w8a32_linear_dev(x, W, y, stream=stream)
 
 
-def time_shapes(lin, torch, items, stream, reps):
-    """Average launch duration per decode shape: the launches of one shape in
-    a step (28 distinct matrices, or the lm_head) captured back-to-back in a
-    HIP graph and replayed; HIP events on the replay stream."""
+def time_shapes(lin, torch, items, dev):
+    """Average launch duration per decode shape: the launches of one shape
+    (its 28 distinct matrices; the lm_head alternating with a second copy of
+    it, so that every launch reads HBM) captured back to back in a HIP graph
+    of >= 40 launches and replayed (time_graph)."""
     by = {}
     for it in items:
         by.setdefault(it[0].split(".")[-1], []).append(it)
     out = {}
     for key, its in by.items():
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=stream):
-            for (_, _, _, W, x, y) in its:
-                lin.w8a32_linear_dev(x, W, y, stream=stream)
-        g.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        out[key] = (its[0][1], its[0][2], e0.elapsed_time(e1) * 1e-3 / (reps * len(its)))
-        del g
+        extra = []
+        if len(its) == 1:
+            (_, N, K, W, x, y) = its[0]
+            w2 = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev)
+            s2 = torch.rand(N, device=dev) * 0.018 + 0.002
+            extra = [lin.DeviceWeights.from_codes(w2, s2)]
+            del w2
+        Ws = [it[3] for it in its] + extra
+        x, y = its[0][4], its[0][5]
+        t = time_graph(torch, lambda i, st: lin.w8a32_linear_dev(x, Ws[i], y, stream=st), len(Ws))
+        out[key] = (its[0][1], its[0][2], t)
+        for W in extra:
+            W.close()
     return out
 
 
@@ -550,6 +550,39 @@ def time_graph(torch, fn, n_w, min_calls=40, rounds=3):
     return float(np.median(ts))
 
 
+def read_floor(lin, torch, dev, nbytes, min_bytes=640e6):
+    """The launch-time floor of reading `nbytes` once: tl_stream_read_dev (a
+    grid-stride read with the GEMV's non-temporal 16-byte loads and nothing
+    else) over rotating buffers (> 640 MB, past the 256 MB MALL), graph-replayed,
+    best over grids of 256..2048 work-groups and 4 or 8 loads in flight."""
+    lib = lin.load_library()
+    n = (int(nbytes) + 15) // 16 * 16
+    copies = max(2, int(np.ceil(min_bytes / n)))
+    bufs = [torch.empty(n, dtype=torch.uint8, device=dev).fill_(1) for _ in range(copies)]
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    best = None
+    for u in (4, 8):
+        for grid in (256, 512, 1024, 2048):
+            if grid * 256 * u * 16 > n:
+                continue
+
+            def fn(i, st, grid=grid, u=u):
+                rc = lib.tl_stream_read_dev(bufs[i].data_ptr(), n, grid, u, sink.data_ptr(), st.cuda_stream)
+                assert rc == 0, lin.check(lib, "tl_stream_read_dev")
+            t = time_graph(torch, fn, copies)
+            if best is None or t < best[0]:
+                best = (t, grid, u)
+    if best is None:          # fewer bytes than one full pass of 256 work-groups
+        def fn(i, st):
+            rc = lib.tl_stream_read_dev(bufs[i].data_ptr(), n, 256, 4, sink.data_ptr(), st.cuda_stream)
+            assert rc == 0, lin.check(lib, "tl_stream_read_dev")
+        best = (time_graph(torch, fn, copies), 256, 4)
+    del bufs
+    t, grid, u = best
+    return {"bytes": n, "us": round(t * 1e6, 2), "GBps": round(n / t / 1e9, 1),
+            "frac_hbm": round(n / t / 1e9 / HBM_PEAK_GBS, 4), "grid": grid, "u": u}
+
+
 def bench_decode_rows(lin, torch, dev):
     """W8A32 decode rows M = 1, 2, 4, 8 (M = 1: int8 GEMV; M = 2..8: fp32
     semantics, int8 digit planes on the MFMA) per decode shape, HBM GB/s;
@@ -657,7 +690,6 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the W8A8 prefill timing")
-    ap.add_argument("--kernel-reps", type=int, default=5)
     ap.add_argument("--quick", action="store_true",
                     help="decode set only (no prefill, sweeps or CPU baseline)")
     ap.add_argument("--prefill-only", action="store_true",
@@ -769,12 +801,20 @@ def main():
     del graph28
 
     log("per-shape launch timing (graph replay)")
-    per = time_shapes(lin, torch, items, stream, max(5, args.kernel_reps))
+    per = time_shapes(lin, torch, items, dev)
     per_shape = {}
     for key, (N, K, t) in per.items():
         b = gemv_bytes(N, K)
         per_shape[key] = {"N": N, "K": K, "us": round(t * 1e6, 2), "GBps": round(b / t / 1e9, 1),
                           "frac_hbm": round(b / t / 1e9 / HBM_PEAK_GBS, 4)}
+    if not args.quick:
+        # what a launch that only reads the same bytes takes on this device
+        log("read floor per shape (plain streaming read of the same bytes)")
+        for key, (N, K, t) in per.items():
+            f = read_floor(lin, torch, dev, gemv_bytes(N, K))
+            per_shape[key]["read_floor_us"] = f["us"]
+            per_shape[key]["read_floor_frac_hbm"] = f["frac_hbm"]
+            per_shape[key]["vs_read_floor"] = round(f["us"] * 1e-6 / t, 4)
     # every launch is the GEMV kernel and the replays run them back to back,
     # so its average launch duration is the step time over the launches per step
     n_per_step = len(LAYER_SHAPES) + 1

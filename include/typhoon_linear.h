@@ -122,6 +122,15 @@ int tl_rows_set_split(int split);
  * int8 digit rows; 0 on the bf16 / fp16 MFMA small-batch kernel. */
 int tl_w8a16_set_gemv(int on);
 
+/* Measurement aid, no counterpart in the reference: one streaming read of
+ * `bytes` device bytes (a multiple of 16, p 16-byte aligned) by `grid`
+ * work-groups with u (4 or 8) 16-byte loads in flight per lane, the loads
+ * of the GEMV weight stream and nothing else.  Its launch time is the floor
+ * a launch reading that many bytes reaches on the device, against which the
+ * GEMV times are set (bench.py).  sink: one device word, written only if the
+ * bytes fold to a fixed improbable value. */
+int tl_stream_read_dev(const void *p, size_t bytes, int grid, int u, uint32_t *sink, void *stream);
+
 /* Tuning override of the decode attention for every later launch or graph
  * capture in the process: cache positions per work-group, 32, 64 or 128; 0
  * restores the built-in choice. */

@@ -867,6 +867,17 @@ int tl_gemm_i8_set_cfg(int cfg) {
   });
 }
 
+int tl_stream_read_dev(const void* p, size_t bytes, int grid, int u, uint32_t* sink, void* stream) {
+  return guarded("tl_stream_read_dev", [&] {
+    REQUIRE(p && sink, "NULL pointer");
+    REQUIRE(bytes > 0 && bytes % 16 == 0 && (((uintptr_t)p) & 15) == 0,
+            "bytes must be a positive multiple of 16 and p 16-byte aligned");
+    REQUIRE(grid >= 1 && grid <= 65536, "grid must be 1..65536");
+    REQUIRE(u == 4 || u == 8, "u must be 4 or 8");
+    HIP_OK(launch_stream_read(p, bytes, grid, u, sink, static_cast<hipStream_t>(stream)));
+  });
+}
+
 int tl_attn_set_chunk(int positions) {
   return guarded("tl_attn_set_chunk", [&] {
     REQUIRE(positions == 0 || positions == 32 || positions == 64 || positions == 128,

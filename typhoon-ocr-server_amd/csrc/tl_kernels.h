@@ -50,6 +50,10 @@ hipError_t launch_argmax_keys(const uint64_t* keys, int n, int32_t* token, float
 // q3/254^3) up to 2^-32 of the row's absmax; a row holding Inf or NaN gets
 // xe = kXeNonFinite (tl_common.h; its outputs are NaN)
 hipError_t launch_split_i8x4(const float* X, int ldx, int M, int K, uint8_t* tiles, int* xe, hipStream_t st);
+// one streaming read of `bytes` (a multiple of 16, 16-byte aligned) by grid
+// work-groups of 256 lanes with u (4 or 8) 16-byte loads in flight each
+// (stream.hip): the read floor of a launch that moves those bytes
+hipError_t launch_stream_read(const void* p, size_t bytes, int grid, int u, uint32_t* sink, hipStream_t st);
 // 4-byte-word copy by a kernel (bytes % 4 == 0), e.g. from mapped pinned host memory
 hipError_t launch_copy_words(const void* src, void* dst, size_t bytes, hipStream_t st);
 
