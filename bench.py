@@ -678,8 +678,46 @@ def bench_host_abi(lin, reps=200):
         b = gemv_bytes(N, K)
         out[f"{name}_{N}x{K}"] = {"us": round(t * 1e6, 2), "GBps": round(b / t / 1e9, 1)}
         lib.tl_evict_weights(lin._p(w, lin.ctypes.c_int8))
+    # the same QKV call from 1 and from 4 threads (one ctypes call each, which
+    # releases the interpreter lock; every thread on its own weights)
+    import threading
+    calls, keep = [], []
+    for _ in range(4):
+        N, K = 4096, 2048
+        w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+        s = rng.uniform(0.002, 0.02, N).astype(np.float32)
+        x = rng.standard_normal((1, K), dtype=np.float32)
+        y = np.empty((1, N), np.float32)
+        keep.append((w, s, x, y))
+        calls.append((lin._p(x, lin.ctypes.c_float), lin._p(w, lin.ctypes.c_int8), lin._p(s, lin.ctypes.c_float),
+                      lin._p(y, lin.ctypes.c_float), N, K))
+
+    def work(c, n):
+        xp, wp, sp, yp, N, K = c
+        for _ in range(n):
+            lib.w8a32_linear(xp, wp, sp, None, yp, None, 1, N, K)
+
+    for c in calls:
+        work(c, 10)
+    n = 1000
+    t0 = time.perf_counter()
+    for c in calls:
+        work(c, n)
+    t1 = (time.perf_counter() - t0) / (4 * n)
+    ths = [threading.Thread(target=work, args=(c, n)) for c in calls]
+    t0 = time.perf_counter()
+    for th in ths:
+        th.start()
+    for th in ths:
+        th.join()
+    t4 = (time.perf_counter() - t0) / (4 * n)
+    for (w, *_r) in keep:
+        lib.tl_evict_weights(lin._p(w, lin.ctypes.c_int8))
+    out["qkv_threads"] = {"threads1_us_per_call": round(t1 * 1e6, 2), "threads4_us_per_call": round(t4 * 1e6, 2),
+                          "speedup": round(t1 / t4, 2)}
     out["includes"] = ("median per call: host x -> HBM, GEMV, HBM -> host y, stream sync; "
-                       "weights already resident")
+                       "weights already resident; qkv_threads: aggregate time per call of 4000 calls "
+                       "from 1 thread and from 4 threads")
     return out
 
 

@@ -24,6 +24,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <utility>
@@ -178,8 +179,14 @@ struct RegKey {
     return dev < o.dev;
   }
 };
+// entries are shared: a call holds its weights until it returns, so an
+// eviction by another thread (LRU, tl_evict_weights, a changed array)
+// only drops the registry's reference
+using WeightsRef = std::shared_ptr<tl_weights>;
+inline WeightsRef own_weights(tl_weights* W) { return WeightsRef(W, weights_free); }
+
 struct RegEntry {
-  tl_weights* W = nullptr;
+  WeightsRef W;
   uint64_t fp = 0;
   uint64_t tick = 0;
 };
@@ -234,12 +241,11 @@ void registry_evict_lru_locked(size_t need) {
     for (auto it = g_reg.begin(); it != g_reg.end(); ++it)
       if (it->second.tick < victim->second.tick) victim = it;
     g_reg_bytes -= victim->second.W->bytes;
-    weights_free(victim->second.W);
     g_reg.erase(victim);
   }
 }
 
-const tl_weights* registry_get(const int8_t* w, const float* s, int rows, int cols, hipStream_t st) {
+WeightsRef registry_get(const int8_t* w, const float* s, int rows, int cols, hipStream_t st) {
   REQUIRE(w && s, "weight and scale pointers must be non-NULL");
   const int dev = current_device();
   const uint64_t fp = fingerprint(w, s, rows, cols);
@@ -252,12 +258,11 @@ const tl_weights* registry_get(const int8_t* w, const float* s, int rows, int co
       return it->second.W;
     }
     g_reg_bytes -= it->second.W->bytes;  // contents changed in place: re-upload
-    weights_free(it->second.W);
     g_reg.erase(it);
   }
   const size_t need = (size_t)cdiv(rows, 16) * 16 * (size_t)cdiv(cols, 64) * 64 + (size_t)rows * 4;
   registry_evict_lru_locked(need);
-  tl_weights* W = weights_from_codes(w, s, rows, cols, false, st);
+  WeightsRef W = own_weights(weights_from_codes(w, s, rows, cols, false, st));
   g_reg[key] = RegEntry{W, fp, ++g_tick};
   g_reg_bytes += W->bytes;
   return W;
@@ -270,35 +275,62 @@ void registry_put(const int8_t* w, const float* s, tl_weights* W) {
   std::lock_guard<std::mutex> lk(g_reg_mu);
   RegKey key{w, s, W->rows, W->cols, W->dev};
   auto it = g_reg.find(key);
+  WeightsRef ref;
   if (it != g_reg.end()) {
     g_reg_bytes -= it->second.W->bytes;
-    if (it->second.W != W) weights_free(it->second.W);
+    if (it->second.W.get() == W) ref = it->second.W;   // re-adopting the same matrix
     g_reg.erase(it);
   }
+  if (!ref) ref = own_weights(W);
   registry_evict_lru_locked(W->bytes);
-  g_reg[key] = RegEntry{W, fp, ++g_tick};
+  g_reg[key] = RegEntry{ref, fp, ++g_tick};
   g_reg_bytes += W->bytes;
 }
 
 // --------------------------------------------------------------------------
-// host-call context (Part 1): one per device, calls serialized
+// host-call contexts (Part 1): a call leases one for its duration (its own
+// stream, staging and pinned buffers), so calls from different threads run
+// concurrently; contexts return to a per-device pool, which holds as many as
+// calls ever overlapped
 // --------------------------------------------------------------------------
 struct HostCtx {
   hipStream_t st = nullptr;
   DevBuf x, y, bias, xs;
   PinnedBuf hin, hout, htok;
 };
-std::mutex g_host_mu;
-std::map<int, HostCtx*> g_host;
+std::mutex g_host_mu;                             // guards the pool only
+std::map<int, std::vector<HostCtx*>> g_host_free;
 
-HostCtx& host_ctx(int dev) {
-  auto it = g_host.find(dev);
-  if (it != g_host.end()) return *it->second;
-  HostCtx* c = new HostCtx();
-  HIP_OK(hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking));
-  g_host[dev] = c;
-  return *c;
-}
+struct HostLease {
+  int dev;
+  HostCtx* c = nullptr;
+  HostLease() : dev(current_device()) {
+    {
+      std::lock_guard<std::mutex> lk(g_host_mu);
+      auto& pool = g_host_free[dev];
+      if (!pool.empty()) {
+        c = pool.back();
+        pool.pop_back();
+      }
+    }
+    if (!c) {
+      auto* n = new HostCtx();
+      if (hipStreamCreateWithFlags(&n->st, hipStreamNonBlocking) != hipSuccess) {
+        delete n;
+        throw Fail{"hipStreamCreateWithFlags failed"};
+      }
+      c = n;
+    }
+  }
+  // back to the pool, also after an error: its next user waits on its stream
+  // before reusing a staging buffer
+  ~HostLease() {
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    g_host_free[dev].push_back(c);
+  }
+  HostLease(const HostLease&) = delete;
+  HostLease& operator=(const HostLease&) = delete;
+};
 
 void h2d(HostCtx& c, DevBuf& d, const void* src, size_t bytes) {
   c.hin.ensure(bytes);
@@ -559,8 +591,8 @@ void host_quantize(const char* fn, const float* src, int8_t* dst, float* scales,
   (void)fn;
   REQUIRE(src && dst && scales, "NULL pointer");
   REQUIRE(rows >= 1 && cols >= 1, "rows and cols must be >= 1");
-  std::lock_guard<std::mutex> lk(g_host_mu);
-  HostCtx& c = host_ctx(current_device());
+  HostLease lease;
+  HostCtx& c = *lease.c;
   // chunks of at most 64 MiB of fp32 input, whole 16-row groups when packing
   int chunk = (int)std::max<size_t>(1, ((size_t)64 << 20) / ((size_t)cols * 4));
   if (pack) chunk = std::max(16, chunk & ~15);
@@ -746,9 +778,10 @@ void w8a32_linear(const float* X, const int8_t* w_int8, const float* scales, con
   guarded("w8a32_linear", [&] {
     check_shape(batch, M, K);
     REQUIRE(X && Y, "X and Y must be non-NULL");
-    std::lock_guard<std::mutex> lk(g_host_mu);
-    HostCtx& c = host_ctx(current_device());
-    const tl_weights* W = registry_get(w_int8, scales, M, K, c.st);
+    HostLease lease;
+    HostCtx& c = *lease.c;
+    const WeightsRef Wr = registry_get(w_int8, scales, M, K, c.st);
+    const tl_weights* W = Wr.get();
     const float* b = nullptr;
     if (bias) {
       c.bias.ensure((size_t)M * sizeof(float), c.st);
@@ -783,9 +816,10 @@ void w8a8_linear(const int8_t* x_int8, const float* x_scales, const int8_t* w_in
   guarded("w8a8_linear", [&] {
     check_shape(batch, M, K);
     REQUIRE(x_int8 && x_scales && Y, "x_int8, x_scales and Y must be non-NULL");
-    std::lock_guard<std::mutex> lk(g_host_mu);
-    HostCtx& c = host_ctx(current_device());
-    const tl_weights* W = registry_get(w_int8, w_scales, M, K, c.st);
+    HostLease lease;
+    HostCtx& c = *lease.c;
+    const WeightsRef Wr = registry_get(w_int8, w_scales, M, K, c.st);
+    const tl_weights* W = Wr.get();
     h2d(c, c.x, x_int8, (size_t)batch * K);
     c.xs.ensure((size_t)batch * sizeof(float), c.st);
     HIP_OK(hipMemcpyAsync(c.xs.p, x_scales, (size_t)batch * sizeof(float), hipMemcpyHostToDevice, c.st));
@@ -807,9 +841,10 @@ void w8a16_linear(const uint16_t* x_bf16_raw, const int8_t* w_int8, const float*
   guarded("w8a16_linear", [&] {
     check_shape(batch, M, K);
     REQUIRE(x_bf16_raw && Y, "x and Y must be non-NULL");
-    std::lock_guard<std::mutex> lk(g_host_mu);
-    HostCtx& c = host_ctx(current_device());
-    const tl_weights* W = registry_get(w_int8, w_scales, M, K, c.st);
+    HostLease lease;
+    HostCtx& c = *lease.c;
+    const WeightsRef Wr = registry_get(w_int8, w_scales, M, K, c.st);
+    const tl_weights* W = Wr.get();
     h2d(c, c.x, x_bf16_raw, (size_t)batch * K * sizeof(uint16_t));
     const float* b = nullptr;
     if (bias) {
@@ -888,9 +923,8 @@ int tl_attn_set_chunk(int positions) {
 
 int tl_register_weights(const int8_t* w_int8, const float* scales, int rows, int cols) {
   return guarded("tl_register_weights", [&] {
-    std::lock_guard<std::mutex> lk(g_host_mu);
-    HostCtx& c = host_ctx(current_device());
-    (void)registry_get(w_int8, scales, rows, cols, c.st);
+    HostLease lease;
+    (void)registry_get(w_int8, scales, rows, cols, lease.c->st);
   });
 }
 
@@ -900,7 +934,6 @@ int tl_evict_weights(const int8_t* w_int8) {
     for (auto it = g_reg.begin(); it != g_reg.end();) {
       if (it->first.w == (const void*)w_int8) {
         g_reg_bytes -= it->second.W->bytes;
-        weights_free(it->second.W);
         it = g_reg.erase(it);
       } else {
         ++it;
@@ -911,7 +944,6 @@ int tl_evict_weights(const int8_t* w_int8) {
 
 void tl_registry_clear(void) {
   std::lock_guard<std::mutex> lk(g_reg_mu);
-  for (auto& kv : g_reg) weights_free(kv.second.W);
   g_reg.clear();
   g_reg_bytes = 0;
 }
@@ -1112,9 +1144,10 @@ int tl_lm_head_argmax(const float* h, const float* norm_w, const int8_t* w_int8,
   return guarded("tl_lm_head_argmax", [&] {
     check_shape(1, N, K);
     REQUIRE(h && token, "h and token must be non-NULL");
-    std::lock_guard<std::mutex> lk(g_host_mu);
-    HostCtx& c = host_ctx(current_device());
-    const tl_weights* W = registry_get(w_int8, scales, N, K, c.st);
+    HostLease lease;
+    HostCtx& c = *lease.c;
+    const WeightsRef Wr = registry_get(w_int8, scales, N, K, c.st);
+    const tl_weights* W = Wr.get();
     // h and the norm weights in one staging copy: [h | norm_w]
     const size_t kb = (size_t)K * sizeof(float);
     const size_t inb = norm_w ? 2 * kb : kb;
