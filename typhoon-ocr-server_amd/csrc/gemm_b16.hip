@@ -279,7 +279,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
       const bool full = vec_ok && n + 4 <= a.N;
       if (a.out == OUT_F32) {
         float* yp = reinterpret_cast<float*>(a.Y) + o;
-        if (full) *reinterpret_cast<float4*>(yp) = make_float4(y[0], y[1], y[2], y[3]);
+        if (full) st_stream(yp, make_float4(y[0], y[1], y[2], y[3]));   // streaming, as the int8 GEMM's
         else for (int r = 0; r < 4 && n + r < a.N; r++) yp[r] = y[r];
       } else {
         uint16_t hv[4];

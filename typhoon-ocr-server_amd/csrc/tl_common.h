@@ -446,6 +446,18 @@ __device__ __forceinline__ void wait_vm() {
 }
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x3 << 14)); }
 
+// 16-byte output store that streams past the caches (non-temporal): large
+// GEMM outputs are written once and read by the next launch, so keeping them
+// out of L2 saves the write-back of dirty lines at the kernel's end
+__device__ __forceinline__ void st_stream(float* p, float4 v) {
+  typedef float v4f_t __attribute__((ext_vector_type(4)));
+  __builtin_nontemporal_store(v4f_t{v.x, v.y, v.z, v.w}, reinterpret_cast<v4f_t*>(p));
+}
+__device__ __forceinline__ void st_stream(int32_t* p, int4 v) {
+  typedef int v4i_t __attribute__((ext_vector_type(4)));
+  __builtin_nontemporal_store(v4i_t{v.x, v.y, v.z, v.w}, reinterpret_cast<v4i_t*>(p));
+}
+
 // Partials handed between work-groups of one launch, which may sit on
 // different XCDs: stored with agent-scope atomic stores (they bypass the
 // XCD's non-coherent L2 path; a store is visible device-wide once vmcnt
