@@ -281,6 +281,40 @@ def test_prefill_matches_oracle(lin, orc, dev, w8a8):
     d.close()
 
 
+@pytest.mark.parametrize("S", [130, 1200])
+def test_w8a8_prefill_fused_quantization_bit_identical(lin, orc, dev, S):
+    """W8A8 prefill with the per-token quantization fused into the layer's
+    RMSNorm and SwiGLU kernels (they write int8 tiles and scales; the fp32
+    rows are never stored) gives, bit for bit, the hidden rows and K/V cache
+    of the prefill that quantizes each linear's stored fp32 input in its own
+    launch (tl_prefill_set_fused_quant(0)): the codes are the same."""
+    from typhoon_ocr_server_amd import decoder as dec
+    say(f"W8A8 prefill fused vs separate quantization, 2 layers x {S} tokens")
+    lib = lin.load_library()
+    rng = np.random.default_rng(31 + S)
+    layers, _, _ = _model(rng, orc, 2)
+    d = dec.Decoder(layers, max_seq=S + 64)
+    d.set_prefill_w8a8(True)
+    h0 = (rng.standard_normal((S, 2048)) * 2).astype(F)
+    h0[S // 2] *= F(1e4)                        # a row far from the others: its own scale
+    outs = []
+    try:
+        for fused in (1, 0):
+            assert lib.tl_prefill_set_fused_quant(fused) == 0
+            d.reset()
+            hg = d.prefill(h0)
+            caches = [d.read_cache(l) for l in range(2)]
+            outs.append((hg, caches))
+    finally:
+        lib.tl_prefill_set_fused_quant(1)
+    (h1, c1), (h2, c2) = outs
+    np.testing.assert_array_equal(h1, h2)
+    for (k1, v1), (k2, v2) in zip(c1, c2):
+        np.testing.assert_array_equal(k1[:, :S], k2[:, :S])
+        np.testing.assert_array_equal(v1[:, :S], v2[:, :S])
+    d.close()
+
+
 def test_chunked_prefill_equals_full_prefill(lin, orc, dev):
     """Chunks that attend to the whole cache (decoder_chunked_prefill_step)
     give the full causal prefill (relative L2 <= 1e-3: the chunks' GEMMs run

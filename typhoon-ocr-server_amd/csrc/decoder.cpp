@@ -127,6 +127,7 @@ struct DecoderScratch {
   PinnedBuf pin_rows;                   // prefill hidden rows on their way to / from HBM
   // prefill activations (token-major, grown to the longest prefill)
   DevBuf p_h, p_xn, p_qkv, p_att, p_gu, p_mlp, p_y, p_cos, p_sin;
+  DevBuf p_q, p_qs;                     // W8A8 prefill: int8 activation tiles and per-token scales
   DevBuf p_fpart, p_fcnt;               // prefill attention's split-key partials and counters (zero between launches)
   // captured graphs and what they were captured for: process-unique ids of
   // the handles whose device memory they bake in (a freed handle's successor
@@ -224,6 +225,10 @@ void enqueue_layers(const ModelWeights* m, const KVCache* c, DecoderScratch* s, 
 
 void advance(KVCache* c, int n);
 
+// W8A8 prefill with the quantization fused into the RMSNorm / SwiGLU kernels
+// (default), or each linear's own quantization launch (tl_prefill_set_fused_quant)
+bool g_prefill_fused_quant = true;
+
 // Prefill of S tokens through every layer (decoder.c:33-157 with seq_len > 1):
 // token t is rotated with rows t of cos_rows / sin_rows, its K/V go to cache
 // row row0 + t, and it attends cache rows key0 .. key0 + qoff + t.
@@ -237,24 +242,42 @@ void enqueue_prefill(const ModelWeights* m, KVCache* c, DecoderScratch* s, int S
   float* MLP = static_cast<float*>(s->p_mlp.p);
   float* Y = static_cast<float*>(s->p_y.p);
   const long long n = (long long)S * H;
-  // w8a32_linear at batch S (decoder.c), or W8A8 with per-token activation codes
+  // w8a32_linear at batch S (decoder.c), or W8A8 with per-token activation
+  // codes; in W8A8 the layer's two RMSNorms and the SwiGLU write the codes of
+  // their output rows directly (the fp32 rows are never stored), and only the
+  // attention output goes through a separate quantization
   auto linear = m->prefill_w8a8 ? linear_w8a8 : linear_w8a32;
+  const bool fused_q = m->prefill_w8a8 && g_prefill_fused_quant;
+  uint8_t* Aq = static_cast<uint8_t*>(s->p_q.p);
+  float* As = static_cast<float*>(s->p_qs.p);
   for (int l = 0; l < m->num_layers(); l++) {
     const LayerDev& L = m->layers[l];
     float* kc = c->k + (size_t)l * c->layer_floats();
     float* vc = c->v + (size_t)l * c->layer_floats();
-    HIP_OK(launch_rmsnorm_rows(Hd, L.norms, Xn, S, H, EPS, st));
-    linear(Xn, L.qkv, nullptr, QKV, S, st);
+    if (fused_q) {
+      HIP_OK(launch_rmsnorm_rows_q(Hd, L.norms, Aq, As, S, H, EPS, st));
+      linear_w8a8_tiles(Aq, As, L.qkv, QKV, S, st);
+    } else {
+      HIP_OK(launch_rmsnorm_rows(Hd, L.norms, Xn, S, H, EPS, st));
+      linear(Xn, L.qkv, nullptr, QKV, S, st);
+    }
     HIP_OK(launch_prefill_qk(QKV, L.norms + 2 * H, L.norms + 2 * H + HDIM, cos_rows, sin_rows, kc, vc, c->max_seq,
                              row0, S, NKV, EPS, st));
     HIP_OK(launch_flash_prefill(QKV, kc, vc, ATT, S, NQ, c->max_seq, key0, qoff, SCALE,
                                 static_cast<float*>(s->p_fpart.p), static_cast<int*>(s->p_fcnt.p), st));
     linear(ATT, L.o, nullptr, Y, S, st);
     HIP_OK(launch_residual_add(Y, Hd, n, st));
-    HIP_OK(launch_rmsnorm_rows(Hd, L.norms + H, Xn, S, H, EPS, st));
-    linear(Xn, L.gu, nullptr, GU, S, st);
-    HIP_OK(launch_swiglu_rows(GU, MLP, S, FF, st));
-    linear(MLP, L.down, nullptr, Y, S, st);
+    if (fused_q) {
+      HIP_OK(launch_rmsnorm_rows_q(Hd, L.norms + H, Aq, As, S, H, EPS, st));
+      linear_w8a8_tiles(Aq, As, L.gu, GU, S, st);
+      HIP_OK(launch_swiglu_rows_q(GU, Aq, As, S, FF, st));
+      linear_w8a8_tiles(Aq, As, L.down, Y, S, st);
+    } else {
+      HIP_OK(launch_rmsnorm_rows(Hd, L.norms + H, Xn, S, H, EPS, st));
+      linear(Xn, L.gu, nullptr, GU, S, st);
+      HIP_OK(launch_swiglu_rows(GU, MLP, S, FF, st));
+      linear(MLP, L.down, nullptr, Y, S, st);
+    }
     HIP_OK(launch_residual_add(Y, Hd, n, st));
   }
 }
@@ -267,6 +290,8 @@ void ensure_prefill_buffers(DecoderScratch* s, int S) {
   s->p_gu.ensure((size_t)S * 2 * FF * 4, s->st);
   s->p_mlp.ensure((size_t)S * FF * 4, s->st);
   s->p_y.ensure((size_t)S * H * 4, s->st);
+  s->p_q.ensure((size_t)cdiv(S, 16) * 16 * FF, s->st);        // tiles of the widest input (K = FF)
+  s->p_qs.ensure((size_t)cdiv(S, 16) * 16 * sizeof(float), s->st);
   s->p_fpart.ensure(flash_split_floats(S, NQ) * 4, s->st);
   const size_t cb = flash_split_counters(S, NQ) * sizeof(int);
   if (cb > s->p_fcnt.n) {
@@ -534,6 +559,7 @@ void decoder_scratch_free_fn(DecoderScratch* s) {
     if (p) (void)hipFree(p);
   if (s->count) (void)hipFree(s->count);
   for (DevBuf* b : {&s->p_h, &s->p_xn, &s->p_qkv, &s->p_att, &s->p_gu, &s->p_mlp, &s->p_y, &s->p_cos, &s->p_sin,
+                    &s->p_q, &s->p_qs,
                     &s->p_fpart, &s->p_fcnt})
     if (b->p) (void)hipFree(b->p);
   if (s->keys.p) (void)hipFree(s->keys.p);
@@ -696,6 +722,13 @@ int tl_decoder_read_cache(const KVCache* cache, int layer, float* k, float* v) {
 }
 
 int tl_decoder_cache_len(const KVCache* cache) { return cache ? cache->seq_len : -1; }
+
+int tl_prefill_set_fused_quant(int on) {
+  return guarded("tl_prefill_set_fused_quant", [&] {
+    REQUIRE(on == 0 || on == 1, "on must be 0 or 1");
+    g_prefill_fused_quant = on != 0;
+  });
+}
 
 int tl_decoder_set_prefill_w8a8(ModelWeights* model, int on) {
   return guarded("tl_decoder_set_prefill_w8a8", [&] {

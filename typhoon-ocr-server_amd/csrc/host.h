@@ -121,6 +121,10 @@ void check_weights(const tl_weights* W);
 void linear_w8a32(const float* X, const tl_weights* W, const float* bias, float* Y, int batch, hipStream_t st);
 // per-token int8 activations of fp32 X, int8 GEMM, fp32 out (tl_w8a8_linear_f32_dev)
 void linear_w8a8(const float* X, const tl_weights* W, const float* bias, float* Y, int batch, hipStream_t st);
+// the W8A8 GEMM on activations already quantized into int8 tiles (row groups
+// of 16 tokens, ceil(K / 64) k-blocks) with their per-token scales
+void linear_w8a8_tiles(const uint8_t* tiles, const float* xs, const tl_weights* W, float* Y, int batch,
+                       hipStream_t st);
 // greedy lm_head step (lmhead.hip): final RMSNorm, GEMV with argmax keys, key
 // reduction; keys: lm_head_argmax_keys(N, K) entries, xn: K floats
 size_t lm_head_argmax_keys(int N, int K);

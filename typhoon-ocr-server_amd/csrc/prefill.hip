@@ -59,6 +59,101 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restri
   }
 }
 
+// Per-token int8 codes of a row held in registers (float4 f = tid + 256 j of
+// the row), written straight into the int8 tile layout with the row's scale:
+// the arithmetic of quantize_rows_tiled_vec_kernel (quant.hip) on the same
+// values, so the codes equal those of quantizing the stored row afterwards.
+template <int NV>
+__device__ __forceinline__ void quantize_row_to_tiles(const float4 (&v)[NV], int n4, int row, int MG,
+                                                      uint8_t* __restrict__ tiles, float* __restrict__ scales,
+                                                      uint32_t* s_mx) {
+  const int tid = threadIdx.x;
+  uint32_t mx = 0;
+#pragma unroll
+  for (int j = 0; j < NV; j++)
+    if (tid + 256 * j < n4)
+      mx = max(mx, max(max(abs_bits(v[j].x), abs_bits(v[j].y)), max(abs_bits(v[j].z), abs_bits(v[j].w))));
+  mx = wave_umax(mx);
+  if ((tid & 63) == 0) s_mx[tid >> 6] = mx;
+  __syncthreads();
+  mx = max(max(s_mx[0], s_mx[1]), max(s_mx[2], s_mx[3]));
+  const float scale = quant_scale(__uint_as_float(mx));
+  const float inv = quant_inv(scale);
+  if (tid == 0) scales[row] = scale;
+  const bool fast = mx < 0x7f800000u && (__float_as_uint(inv) & 0x7f800000u) != 0x7f800000u;
+  uint32_t* t32 = reinterpret_cast<uint32_t*>(tiles) + ((size_t)(row >> 4) * 64 + (row & 15)) * 4;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int f = tid + 256 * j;          // float4 index: k = 4f .. 4f+3
+    if (f >= n4) continue;
+    const uint32_t code = fast ? codes4_rne(v[j], inv)
+                               : pack4(code_rne(v[j].x * inv, true), code_rne(v[j].y * inv, true),
+                                       code_rne(v[j].z * inv, true), code_rne(v[j].w * inv, true));
+    t32[((size_t)(f >> 4) * MG) * 256 + ((f >> 2) & 3) * 64 + (f & 3)] = code;
+  }
+}
+
+// The layer's RMSNorm followed by the W8A8 per-token quantization of its
+// output, one work-group per token: the normalised values of
+// rmsnorm_rows_kernel, quantized in registers and written as int8 tiles and
+// scales (the fp32 row is never stored; K % 64 == 0, K <= 2048).
+__global__ __launch_bounds__(256) void rmsnorm_rows_q_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                             int K, float eps, int MG, uint8_t* __restrict__ tiles,
+                                                             float* __restrict__ scales) {
+  __shared__ float s_part[4];
+  __shared__ uint32_t s_mx[4];
+  const size_t row = blockIdx.x;
+  const float4* xr = reinterpret_cast<const float4*>(x + row * K);
+  const float4* wr = reinterpret_cast<const float4*>(w);
+  const int n4 = K >> 2;
+  float4 v[2], wv[2];
+  float sq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int f = threadIdx.x + 256 * i;
+    v[i] = f < n4 ? xr[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+    wv[i] = f < n4 ? wr[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+    sq = __fmaf_rn(v[i].x, v[i].x, sq);
+    sq = __fmaf_rn(v[i].y, v[i].y, sq);
+    sq = __fmaf_rn(v[i].z, v[i].z, sq);
+    sq = __fmaf_rn(v[i].w, v[i].w, sq);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sq = __fadd_rn(sq, __shfl_xor(sq, o, 64));
+  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = sq;
+  __syncthreads();
+  const float tot = __fadd_rn(__fadd_rn(s_part[0], s_part[1]), __fadd_rn(s_part[2], s_part[3]));
+  const float r = ref_rsqrt(__fadd_rn(__fdiv_rn(tot, (float)K), eps));
+  float4 y[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+    y[i] = make_float4(__fmul_rn(__fmul_rn(v[i].x, r), wv[i].x), __fmul_rn(__fmul_rn(v[i].y, r), wv[i].y),
+                       __fmul_rn(__fmul_rn(v[i].z, r), wv[i].z), __fmul_rn(__fmul_rn(v[i].w, r), wv[i].w));
+  quantize_row_to_tiles<2>(y, n4, (int)row, MG, tiles, scales, s_mx);
+}
+
+// SwiGLU of one token's interleaved gate/up row (the values of
+// swiglu_rows_kernel) followed by the W8A8 per-token quantization, written as
+// int8 tiles and the token's scale; one work-group per token, ffn = 1024 NV.
+template <int NV>
+__global__ __launch_bounds__(256) void swiglu_rows_q_kernel(const float* __restrict__ gu, int ffn, int MG,
+                                                            uint8_t* __restrict__ tiles, float* __restrict__ scales) {
+  __shared__ uint32_t s_mx[4];
+  const size_t t = blockIdx.x;
+  const float* row = gu + t * 2 * ffn;
+  float4 y[NV];
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int c = 4 * (threadIdx.x + 256 * j);    // outputs c .. c+3: gate 16b + r.., up 16b + 8 + r..
+    const int b = c >> 3, r = c & 7;
+    const float4 g = *reinterpret_cast<const float4*>(row + 16 * b + r);
+    const float4 u = *reinterpret_cast<const float4*>(row + 16 * b + 8 + r);
+    y[j] = make_float4(__fmul_rn(ref_silu(g.x), u.x), __fmul_rn(ref_silu(g.y), u.y), __fmul_rn(ref_silu(g.z), u.z),
+                       __fmul_rn(ref_silu(g.w), u.w));
+  }
+  quantize_row_to_tiles<NV>(y, ffn >> 2, (int)t, MG, tiles, scales, s_mx);
+}
+
 // Work-group (t, h): token t, kv head h.  q heads 2h, 2h+1 (RMSNorm with
 // q_norm, rotation, written back in place in qkv), k head h (k_norm,
 // rotation) and v head h to cache row `row0 + t`.  The rotation uses row t of
@@ -412,6 +507,23 @@ hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int r
                                hipStream_t st) {
   if (K % 4 != 0 || K > 2048 || rows < 1) return hipErrorInvalidValue;
   hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(256), 0, st, x, w, out, K, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_rows_q(const float* x, const float* w, uint8_t* tiles, float* scales, int rows, int K,
+                                 float eps, hipStream_t st) {
+  if (K % 64 != 0 || K > 2048 || rows < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(rmsnorm_rows_q_kernel, dim3(rows), dim3(256), 0, st, x, w, K, eps, cdiv(rows, 16), tiles,
+                     scales);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu_rows_q(const float* gu, uint8_t* tiles, float* scales, int S, int ffn, hipStream_t st) {
+  if (S < 1) return hipErrorInvalidValue;
+  const int MG = cdiv(S, 16);
+  if (ffn == 6144) hipLaunchKernelGGL(swiglu_rows_q_kernel<6>, dim3(S), dim3(256), 0, st, gu, ffn, MG, tiles, scales);
+  else if (ffn == 2048) hipLaunchKernelGGL(swiglu_rows_q_kernel<2>, dim3(S), dim3(256), 0, st, gu, ffn, MG, tiles, scales);
+  else return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

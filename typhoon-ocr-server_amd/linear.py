@@ -44,6 +44,7 @@ SIGNATURES = {
     "tl_rows_set_split": (_int, [_int]),
     "tl_w8a16_set_gemv": (_int, [_int]),
     "tl_attn_set_chunk": (_int, [_int]),
+    "tl_prefill_set_fused_quant": (_int, [_int]),
     "tl_stream_read_dev": (_int, [_vp, ctypes.c_size_t, _int, _int, _vp, _vp]),
     "tl_gemv_fused_dev": (_int, [_vp, _vp, _vp, _vp, _int, _int, _vp, _vp]),
     # decoder loop (Part 3), reference argtypes (decoder.py:86-143)
