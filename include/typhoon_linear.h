@@ -334,10 +334,12 @@ int tl_decoder_cache_len(const KVCache *cache);
  * int8 activations (w8a8_quantize_activations, kernel/w8a8_kernel.c:109-114)
  * and the exact int8 GEMM. */
 int tl_decoder_set_prefill_w8a8(ModelWeights *model, int on);
-/* Tuning switch of the W8A8 prefill for every later prefill in the process:
- * 1 (default) the layer's RMSNorms and SwiGLU write the int8 codes and scales
- * of their output rows directly; 0 each linear quantizes its fp32 input in
- * its own launch.  The codes are the same either way. */
+/* Tuning switch of the prefill for every later prefill in the process: 1
+ * (default) the layer's RMSNorms and SwiGLU write their output rows directly
+ * as the linears' activations (W8A8: int8 codes and scales; fp32 linears at
+ * more than 32 tokens: the four int8 planes per row and their exponents); 0
+ * each linear converts its stored fp32 input in its own launch.  The
+ * activations are the same either way. */
 int tl_prefill_set_fused_quant(int on);
 /* Copies one layer's K and V cache ([8][max_seq][128] fp32 each; either may
  * be NULL) to host memory. */

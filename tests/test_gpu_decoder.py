@@ -282,19 +282,21 @@ def test_prefill_matches_oracle(lin, orc, dev, w8a8):
 
 
 @pytest.mark.parametrize("S", [130, 1200])
-def test_w8a8_prefill_fused_quantization_bit_identical(lin, orc, dev, S):
-    """W8A8 prefill with the per-token quantization fused into the layer's
-    RMSNorm and SwiGLU kernels (they write int8 tiles and scales; the fp32
-    rows are never stored) gives, bit for bit, the hidden rows and K/V cache
-    of the prefill that quantizes each linear's stored fp32 input in its own
-    launch (tl_prefill_set_fused_quant(0)): the codes are the same."""
+@pytest.mark.parametrize("w8a8", [True, False], ids=["w8a8", "w8a32"])
+def test_prefill_fused_activations_bit_identical(lin, orc, dev, S, w8a8):
+    """The prefill with the linears' activations written by the layer's
+    RMSNorm and SwiGLU kernels (W8A8: int8 tiles and per-token scales; fp32
+    linears: the four int8 planes per row and their exponents; the fp32 rows
+    are never stored) gives, bit for bit, the hidden rows and K/V cache of the
+    prefill whose linears convert their stored fp32 input in their own launch
+    (tl_prefill_set_fused_quant(0)): the activations are the same."""
     from typhoon_ocr_server_amd import decoder as dec
-    say(f"W8A8 prefill fused vs separate quantization, 2 layers x {S} tokens")
+    say(f"prefill fused vs separate activations, w8a8={w8a8}, 2 layers x {S} tokens")
     lib = lin.load_library()
     rng = np.random.default_rng(31 + S)
     layers, _, _ = _model(rng, orc, 2)
     d = dec.Decoder(layers, max_seq=S + 64)
-    d.set_prefill_w8a8(True)
+    d.set_prefill_w8a8(w8a8)
     h0 = (rng.standard_normal((S, 2048)) * 2).astype(F)
     h0[S // 2] *= F(1e4)                        # a row far from the others: its own scale
     outs = []

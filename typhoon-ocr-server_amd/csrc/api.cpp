@@ -746,6 +746,23 @@ void linear_w8a32(const float* X, const tl_weights* W, const float* bias, float*
 void linear_w8a8(const float* X, const tl_weights* W, const float* bias, float* Y, int batch, hipStream_t st) {
   if (tl_w8a8_linear_f32_dev(X, W, bias, Y, batch, st) != 0) throw Fail{t_err};
 }
+void linear_w8a32_planes(const uint8_t* tiles, const int* xe, const tl_weights* W, float* Y, int batch,
+                         hipStream_t st) {
+  Workspace& ws = workspace(W->dev, st);
+  GemmLaunch L;
+  L.amode = A_I8;
+  L.A = tiles;
+  L.Bt = W->tiles;
+  L.ws = W->scales;
+  L.xe = xe;
+  L.Y = Y;
+  L.ldy = W->rows;
+  L.M = 4 * batch;
+  L.N = W->rows;
+  L.K = W->cols;
+  L.out = OUT_F32_X4;
+  run_gemm(ws, L, st);
+}
 void linear_w8a8_tiles(const uint8_t* tiles, const float* xs, const tl_weights* W, float* Y, int batch,
                        hipStream_t st) {
   Workspace& ws = workspace(W->dev, st);

@@ -127,7 +127,7 @@ struct DecoderScratch {
   PinnedBuf pin_rows;                   // prefill hidden rows on their way to / from HBM
   // prefill activations (token-major, grown to the longest prefill)
   DevBuf p_h, p_xn, p_qkv, p_att, p_gu, p_mlp, p_y, p_cos, p_sin;
-  DevBuf p_q, p_qs;                     // W8A8 prefill: int8 activation tiles and per-token scales
+  DevBuf p_q, p_qs;                     // int8 activation tiles, per-token scales (W8A8) or exponents (planes)
   DevBuf p_fpart, p_fcnt;               // prefill attention's split-key partials and counters (zero between launches)
   // captured graphs and what they were captured for: process-unique ids of
   // the handles whose device memory they bake in (a freed handle's successor
@@ -225,8 +225,9 @@ void enqueue_layers(const ModelWeights* m, const KVCache* c, DecoderScratch* s, 
 
 void advance(KVCache* c, int n);
 
-// W8A8 prefill with the quantization fused into the RMSNorm / SwiGLU kernels
-// (default), or each linear's own quantization launch (tl_prefill_set_fused_quant)
+// prefill with the activation quantization / plane split fused into the
+// RMSNorm and SwiGLU kernels (default), or each linear's own launch
+// (tl_prefill_set_fused_quant)
 bool g_prefill_fused_quant = true;
 
 // Prefill of S tokens through every layer (decoder.c:33-157 with seq_len > 1):
@@ -243,20 +244,28 @@ void enqueue_prefill(const ModelWeights* m, KVCache* c, DecoderScratch* s, int S
   float* Y = static_cast<float*>(s->p_y.p);
   const long long n = (long long)S * H;
   // w8a32_linear at batch S (decoder.c), or W8A8 with per-token activation
-  // codes; in W8A8 the layer's two RMSNorms and the SwiGLU write the codes of
-  // their output rows directly (the fp32 rows are never stored), and only the
-  // attention output goes through a separate quantization
+  // codes.  The layer's two RMSNorms and the SwiGLU write their output rows
+  // directly as the GEMM's activations (the fp32 rows are never stored): the
+  // W8A8 codes and scales, or, for w8a32_linear's fp32 semantics, the four
+  // int8 planes and exponents it splits a batch of more than 32 rows into
+  // (S <= 32 keeps the fp32 rows: w8a32_linear takes other kernels there).
+  // Only the attention output goes through its linear's own quantization.
   auto linear = m->prefill_w8a8 ? linear_w8a8 : linear_w8a32;
-  const bool fused_q = m->prefill_w8a8 && g_prefill_fused_quant;
+  const bool fused_q = g_prefill_fused_quant && (m->prefill_w8a8 || S > 32);
   uint8_t* Aq = static_cast<uint8_t*>(s->p_q.p);
-  float* As = static_cast<float*>(s->p_qs.p);
+  float* As = m->prefill_w8a8 ? static_cast<float*>(s->p_qs.p) : nullptr;
+  int* Ae = m->prefill_w8a8 ? nullptr : static_cast<int*>(s->p_qs.p);
+  auto linear_q = [&](const tl_weights* W, float* out) {
+    if (m->prefill_w8a8) linear_w8a8_tiles(Aq, As, W, out, S, st);
+    else linear_w8a32_planes(Aq, Ae, W, out, S, st);
+  };
   for (int l = 0; l < m->num_layers(); l++) {
     const LayerDev& L = m->layers[l];
     float* kc = c->k + (size_t)l * c->layer_floats();
     float* vc = c->v + (size_t)l * c->layer_floats();
     if (fused_q) {
-      HIP_OK(launch_rmsnorm_rows_q(Hd, L.norms, Aq, As, S, H, EPS, st));
-      linear_w8a8_tiles(Aq, As, L.qkv, QKV, S, st);
+      HIP_OK(launch_rmsnorm_rows_q(Hd, L.norms, Aq, As, Ae, S, H, EPS, st));
+      linear_q(L.qkv, QKV);
     } else {
       HIP_OK(launch_rmsnorm_rows(Hd, L.norms, Xn, S, H, EPS, st));
       linear(Xn, L.qkv, nullptr, QKV, S, st);
@@ -268,10 +277,10 @@ void enqueue_prefill(const ModelWeights* m, KVCache* c, DecoderScratch* s, int S
     linear(ATT, L.o, nullptr, Y, S, st);
     HIP_OK(launch_residual_add(Y, Hd, n, st));
     if (fused_q) {
-      HIP_OK(launch_rmsnorm_rows_q(Hd, L.norms + H, Aq, As, S, H, EPS, st));
-      linear_w8a8_tiles(Aq, As, L.gu, GU, S, st);
-      HIP_OK(launch_swiglu_rows_q(GU, Aq, As, S, FF, st));
-      linear_w8a8_tiles(Aq, As, L.down, Y, S, st);
+      HIP_OK(launch_rmsnorm_rows_q(Hd, L.norms + H, Aq, As, Ae, S, H, EPS, st));
+      linear_q(L.gu, GU);
+      HIP_OK(launch_swiglu_rows_q(GU, Aq, As, Ae, S, FF, st));
+      linear_q(L.down, Y);
     } else {
       HIP_OK(launch_rmsnorm_rows(Hd, L.norms + H, Xn, S, H, EPS, st));
       linear(Xn, L.gu, nullptr, GU, S, st);
@@ -290,7 +299,7 @@ void ensure_prefill_buffers(DecoderScratch* s, int S) {
   s->p_gu.ensure((size_t)S * 2 * FF * 4, s->st);
   s->p_mlp.ensure((size_t)S * FF * 4, s->st);
   s->p_y.ensure((size_t)S * H * 4, s->st);
-  s->p_q.ensure((size_t)cdiv(S, 16) * 16 * FF, s->st);        // tiles of the widest input (K = FF)
+  s->p_q.ensure((size_t)cdiv(4 * S, 16) * 16 * FF, s->st);    // plane tiles of the widest input (K = FF)
   s->p_qs.ensure((size_t)cdiv(S, 16) * 16 * sizeof(float), s->st);
   s->p_fpart.ensure(flash_split_floats(S, NQ) * 4, s->st);
   const size_t cb = flash_split_counters(S, NQ) * sizeof(int);

@@ -125,6 +125,10 @@ void linear_w8a8(const float* X, const tl_weights* W, const float* bias, float* 
 // of 16 tokens, ceil(K / 64) k-blocks) with their per-token scales
 void linear_w8a8_tiles(const uint8_t* tiles, const float* xs, const tl_weights* W, float* Y, int batch,
                        hipStream_t st);
+// the fp32-semantics GEMM (w8a32_linear at batch > 32) on activations already
+// split into four int8 planes per token (code rows 4t + p) with their exponents
+void linear_w8a32_planes(const uint8_t* tiles, const int* xe, const tl_weights* W, float* Y, int batch,
+                         hipStream_t st);
 // greedy lm_head step (lmhead.hip): final RMSNorm, GEMV with argmax keys, key
 // reduction; keys: lm_head_argmax_keys(N, K) entries, xn: K floats
 size_t lm_head_argmax_keys(int N, int K);

@@ -63,10 +63,14 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restri
 // the row), written straight into the int8 tile layout with the row's scale:
 // the arithmetic of quantize_rows_tiled_vec_kernel (quant.hip) on the same
 // values, so the codes equal those of quantizing the stored row afterwards.
-template <int NV>
+//
+// PLANES: instead, the four int8 planes of the row as code rows 4 row + p
+// (MG = ceil(4 rows / 16)) and its exponent in `xe` (split_i8x4_kernel's
+// arithmetic, quant.hip), the activations of the fp32-semantics GEMM.
+template <int NV, bool PLANES>
 __device__ __forceinline__ void quantize_row_to_tiles(const float4 (&v)[NV], int n4, int row, int MG,
                                                       uint8_t* __restrict__ tiles, float* __restrict__ scales,
-                                                      uint32_t* s_mx) {
+                                                      int* __restrict__ xe, uint32_t* s_mx) {
   const int tid = threadIdx.x;
   uint32_t mx = 0;
 #pragma unroll
@@ -77,6 +81,27 @@ __device__ __forceinline__ void quantize_row_to_tiles(const float4 (&v)[NV], int
   if ((tid & 63) == 0) s_mx[tid >> 6] = mx;
   __syncthreads();
   mx = max(max(s_mx[0], s_mx[1]), max(s_mx[2], s_mx[3]));
+  if constexpr (PLANES) {
+    const int ee = planes_exponent(mx);
+    const bool finite = ee != kXeNonFinite;
+    const int e = finite ? ee : 0;
+    if (tid == 0) xe[row] = ee;
+    uint32_t* t32 = reinterpret_cast<uint32_t*>(tiles);
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      const int f = tid + 256 * j;
+      if (f >= n4) continue;
+      const float w4[4] = {finite ? v[j].x : 0.f, finite ? v[j].y : 0.f, finite ? v[j].z : 0.f, finite ? v[j].w : 0.f};
+      uint32_t code[4];
+      planes4_i8(w4, e, code);
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const int rr = 4 * row + p;
+        t32[(((size_t)(f >> 4) * MG + (rr >> 4)) * 64 + (rr & 15) + 16 * ((f >> 2) & 3)) * 4 + (f & 3)] = code[p];
+      }
+    }
+    return;
+  }
   const float scale = quant_scale(__uint_as_float(mx));
   const float inv = quant_inv(scale);
   if (tid == 0) scales[row] = scale;
@@ -97,9 +122,10 @@ __device__ __forceinline__ void quantize_row_to_tiles(const float4 (&v)[NV], int
 // output, one work-group per token: the normalised values of
 // rmsnorm_rows_kernel, quantized in registers and written as int8 tiles and
 // scales (the fp32 row is never stored; K % 64 == 0, K <= 2048).
+template <bool PLANES>
 __global__ __launch_bounds__(256) void rmsnorm_rows_q_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                              int K, float eps, int MG, uint8_t* __restrict__ tiles,
-                                                             float* __restrict__ scales) {
+                                                             float* __restrict__ scales, int* __restrict__ xe) {
   __shared__ float s_part[4];
   __shared__ uint32_t s_mx[4];
   const size_t row = blockIdx.x;
@@ -129,15 +155,16 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_q_kernel(const float* __rest
   for (int i = 0; i < 2; i++)
     y[i] = make_float4(__fmul_rn(__fmul_rn(v[i].x, r), wv[i].x), __fmul_rn(__fmul_rn(v[i].y, r), wv[i].y),
                        __fmul_rn(__fmul_rn(v[i].z, r), wv[i].z), __fmul_rn(__fmul_rn(v[i].w, r), wv[i].w));
-  quantize_row_to_tiles<2>(y, n4, (int)row, MG, tiles, scales, s_mx);
+  quantize_row_to_tiles<2, PLANES>(y, n4, (int)row, MG, tiles, scales, xe, s_mx);
 }
 
 // SwiGLU of one token's interleaved gate/up row (the values of
 // swiglu_rows_kernel) followed by the W8A8 per-token quantization, written as
 // int8 tiles and the token's scale; one work-group per token, ffn = 1024 NV.
-template <int NV>
+template <int NV, bool PLANES>
 __global__ __launch_bounds__(256) void swiglu_rows_q_kernel(const float* __restrict__ gu, int ffn, int MG,
-                                                            uint8_t* __restrict__ tiles, float* __restrict__ scales) {
+                                                            uint8_t* __restrict__ tiles, float* __restrict__ scales,
+                                                            int* __restrict__ xe) {
   __shared__ uint32_t s_mx[4];
   const size_t t = blockIdx.x;
   const float* row = gu + t * 2 * ffn;
@@ -151,7 +178,7 @@ __global__ __launch_bounds__(256) void swiglu_rows_q_kernel(const float* __restr
     y[j] = make_float4(__fmul_rn(ref_silu(g.x), u.x), __fmul_rn(ref_silu(g.y), u.y), __fmul_rn(ref_silu(g.z), u.z),
                        __fmul_rn(ref_silu(g.w), u.w));
   }
-  quantize_row_to_tiles<NV>(y, ffn >> 2, (int)t, MG, tiles, scales, s_mx);
+  quantize_row_to_tiles<NV, PLANES>(y, ffn >> 2, (int)t, MG, tiles, scales, xe, s_mx);
 }
 
 // Work-group (t, h): token t, kv head h.  q heads 2h, 2h+1 (RMSNorm with
@@ -510,20 +537,32 @@ hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int r
   return hipGetLastError();
 }
 
-hipError_t launch_rmsnorm_rows_q(const float* x, const float* w, uint8_t* tiles, float* scales, int rows, int K,
-                                 float eps, hipStream_t st) {
-  if (K % 64 != 0 || K > 2048 || rows < 1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(rmsnorm_rows_q_kernel, dim3(rows), dim3(256), 0, st, x, w, K, eps, cdiv(rows, 16), tiles,
-                     scales);
+hipError_t launch_rmsnorm_rows_q(const float* x, const float* w, uint8_t* tiles, float* scales, int* xe, int rows,
+                                 int K, float eps, hipStream_t st) {
+  if (K % 64 != 0 || K > 2048 || rows < 1 || (!scales == !xe)) return hipErrorInvalidValue;
+  if (xe)
+    hipLaunchKernelGGL(rmsnorm_rows_q_kernel<true>, dim3(rows), dim3(256), 0, st, x, w, K, eps, cdiv(4 * rows, 16),
+                       tiles, scales, xe);
+  else
+    hipLaunchKernelGGL(rmsnorm_rows_q_kernel<false>, dim3(rows), dim3(256), 0, st, x, w, K, eps, cdiv(rows, 16),
+                       tiles, scales, xe);
   return hipGetLastError();
 }
 
-hipError_t launch_swiglu_rows_q(const float* gu, uint8_t* tiles, float* scales, int S, int ffn, hipStream_t st) {
-  if (S < 1) return hipErrorInvalidValue;
-  const int MG = cdiv(S, 16);
-  if (ffn == 6144) hipLaunchKernelGGL(swiglu_rows_q_kernel<6>, dim3(S), dim3(256), 0, st, gu, ffn, MG, tiles, scales);
-  else if (ffn == 2048) hipLaunchKernelGGL(swiglu_rows_q_kernel<2>, dim3(S), dim3(256), 0, st, gu, ffn, MG, tiles, scales);
-  else return hipErrorInvalidValue;
+hipError_t launch_swiglu_rows_q(const float* gu, uint8_t* tiles, float* scales, int* xe, int S, int ffn,
+                                hipStream_t st) {
+  if (S < 1 || (!scales == !xe)) return hipErrorInvalidValue;
+  const int MG = xe ? cdiv(4 * S, 16) : cdiv(S, 16);
+  if (ffn == 6144 && xe)
+    hipLaunchKernelGGL((swiglu_rows_q_kernel<6, true>), dim3(S), dim3(256), 0, st, gu, ffn, MG, tiles, scales, xe);
+  else if (ffn == 6144)
+    hipLaunchKernelGGL((swiglu_rows_q_kernel<6, false>), dim3(S), dim3(256), 0, st, gu, ffn, MG, tiles, scales, xe);
+  else if (ffn == 2048 && xe)
+    hipLaunchKernelGGL((swiglu_rows_q_kernel<2, true>), dim3(S), dim3(256), 0, st, gu, ffn, MG, tiles, scales, xe);
+  else if (ffn == 2048)
+    hipLaunchKernelGGL((swiglu_rows_q_kernel<2, false>), dim3(S), dim3(256), 0, st, gu, ffn, MG, tiles, scales, xe);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

@@ -244,13 +244,9 @@ __global__ __launch_bounds__(256) void split_i8x4_kernel(const float* __restrict
   }
   mx = wave_umax(mx);
   const bool finite = mx < 0x7f800000u;
-  int e = 0;
-  if (finite && mx != 0) {
-    int ex;
-    (void)frexpf(__uint_as_float(mx), &ex);
-    e = ex - 6;
-  }
-  if (lane == 0) xe[t] = finite ? e : kXeNonFinite;
+  const int ee = planes_exponent(mx);
+  const int e = finite ? ee : 0;
+  if (lane == 0) xe[t] = ee;
   // tile dword of plane p for float4 group f: row 4t + p of group (4t + p) >> 4
   uint32_t* t32 = reinterpret_cast<uint32_t*>(tiles);
   const int r0 = 4 * t;
@@ -266,26 +262,8 @@ __global__ __launch_bounds__(256) void split_i8x4_kernel(const float* __restrict
         for (int q = 0; q < 4; q++) v[q] = (k + q < K) ? row[k + q] : 0.0f;
       }
     }
-    uint32_t code[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      float r = ldexpf(v[q], -e);
-      float c = rintf(r);
-      uint32_t b0 = (uint32_t)((int)c & 0xff);
-      r = __fsub_rn(r, c);
-      uint32_t bp[3];
-#pragma unroll
-      for (int p = 0; p < 3; p++) {
-        const float s = __fmul_rn(r, 254.0f);
-        c = rintf(s);
-        bp[p] = (uint32_t)((int)c & 0xff);
-        r = __fsub_rn(s, c);
-      }
-      code[0] |= b0 << (8 * q);
-      code[1] |= bp[0] << (8 * q);
-      code[2] |= bp[1] << (8 * q);
-      code[3] |= bp[2] << (8 * q);
-    }
+    uint32_t code[4];
+    planes4_i8(v, e, code);
 #pragma unroll
     for (int p = 0; p < 4; p++) {
       const int rr = r0 + p;

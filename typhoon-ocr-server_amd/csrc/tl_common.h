@@ -237,6 +237,44 @@ __device__ __forceinline__ uint32_t codes4_rne(float4 v, float inv) {
 // ---------------------------------------------------------------------------
 constexpr int kXeNonFinite = -100000;   // exponent marking a row with Inf / NaN
 
+// the four int8 planes of 4 values of a row with exponent e (v = x 2^-e
+// exact, |v| < 64): dword p holds plane p of the 4 values, one byte each
+__device__ __forceinline__ void planes4_i8(const float (&v)[4], int e, uint32_t (&code)[4]) {
+#pragma unroll
+  for (int p = 0; p < 4; p++) code[p] = 0u;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    float r = ldexpf(v[q], -e);
+    float c = rintf(r);
+    const uint32_t b0 = (uint32_t)((int)c & 0xff);
+    r = __fsub_rn(r, c);
+    uint32_t bp[3];
+#pragma unroll
+    for (int p = 0; p < 3; p++) {
+      const float sv = __fmul_rn(r, 254.0f);
+      c = rintf(sv);
+      bp[p] = (uint32_t)((int)c & 0xff);
+      r = __fsub_rn(sv, c);
+    }
+    code[0] |= b0 << (8 * q);
+    code[1] |= bp[0] << (8 * q);
+    code[2] |= bp[1] << (8 * q);
+    code[3] |= bp[2] << (8 * q);
+  }
+}
+// the row exponent of the planes: frexp exponent of the absmax - 6 (0 for a
+// zero row), or kXeNonFinite when the row holds Inf or NaN
+__device__ __forceinline__ int planes_exponent(uint32_t absmax_bits) {
+  if (absmax_bits >= 0x7f800000u) return kXeNonFinite;
+  int e = 0;
+  if (absmax_bits != 0) {
+    int ex;
+    (void)frexpf(__uint_as_float(absmax_bits), &ex);
+    e = ex - 6;
+  }
+  return e;
+}
+
 // the four plane accumulators of one output: a0 + a1/254 + a2/254^2 +
 // a3/254^3, Horner from the smallest term, each step rounded
 __device__ __forceinline__ float planes_sum(int a0, int a1, int a2, int a3) {

@@ -101,13 +101,17 @@ hipError_t launch_flash_prefill(const float* qkv, const float* kc, const float* 
                                 int max_seq, int key0, int qoff, float scale, float* part, int* cnt,
                                 hipStream_t st);
 hipError_t launch_swiglu_rows(const float* gu, float* mlp, int S, int ffn, hipStream_t st);
-// the same two steps followed by the W8A8 per-token quantization of their
-// output, written as int8 code tiles (MG = ceil(rows / 16) row groups) and
-// per-token scales instead of fp32 rows: the codes of quantizing the stored
-// rows, bit for bit (K % 64 == 0, K <= 2048; ffn 2048 or 6144)
-hipError_t launch_rmsnorm_rows_q(const float* x, const float* w, uint8_t* tiles, float* scales, int rows, int K,
-                                 float eps, hipStream_t st);
-hipError_t launch_swiglu_rows_q(const float* gu, uint8_t* tiles, float* scales, int S, int ffn, hipStream_t st);
+// the same two steps with their output rows written as GEMM activations
+// instead of fp32 rows (K % 64 == 0, K <= 2048; ffn 2048 or 6144), one of:
+//   scales: the W8A8 per-token quantization, int8 code tiles (ceil(rows / 16)
+//           row groups) and per-token scales, the codes of
+//           launch_quantize_rows_tiled on the stored rows, bit for bit;
+//   xe:     the four int8 planes per row (code rows 4t + p, ceil(4 rows / 16)
+//           row groups) and exponents of launch_split_i8x4, bit for bit
+hipError_t launch_rmsnorm_rows_q(const float* x, const float* w, uint8_t* tiles, float* scales, int* xe, int rows,
+                                 int K, float eps, hipStream_t st);
+hipError_t launch_swiglu_rows_q(const float* gu, uint8_t* tiles, float* scales, int* xe, int S, int ffn,
+                                hipStream_t st);
 hipError_t launch_residual_add(const float* y, float* h, long long n, hipStream_t st);
 
 // ---- M=1 GEMV (gemv.hip) --------------------------------------------------
