@@ -74,7 +74,9 @@ __device__ inline v4f mfma16(uint4 w, uint4 x, v4f c) {
   else return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(w), as_bf(x), c, 0, 0, 0);
 }
 
-template <int AMODE, int MT, int NT, int NST, int WM, int WN>
+// KF: K is a multiple of 64 (every copy a per-lane offset from a uniform
+// per-stage base; the general path masks pieces past K and rows past M)
+template <int AMODE, int MT, int NT, int NST, int WM, int WN, bool KF>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args a) {
   constexpr int NW = WM * WN;
   constexpr int AP = 2;                                // A copies per (row group, K block)
@@ -145,7 +147,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
   // K a multiple of 64 (no piece past K): each copy is a per-lane byte offset
   // from a uniform per-stage base (rows past M read row M - 1; their outputs
   // are never stored)
-  const bool kfull = (a.K % 64) == 0;
+  constexpr bool kfull = KF;
   uint32_t qvo[PW];
 #pragma unroll
   for (int p = 0; p < PW; p++)
@@ -153,23 +155,23 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
   auto issue = [&](int st, uint4* buf) {
     const int sc = min(st, nst - 1);
     const uint32_t base = lds_addr(buf);
-    if (kfull) {
+    if constexpr (kfull) {
       const char* sa = Xb + (size_t)sc * 64 * ESZ;
       const char* sb = reinterpret_cast<const char*>(a.Bt) + (size_t)sc * bstride;
 #pragma unroll
       for (int p = 0; p < PW; p++) dma_tile_s(qvo[p], (wv + NW * p < TA) ? sa : sb, base + qlds[p]);
-      return;
-    }
+    } else {
 #pragma unroll
-    for (int p = 0; p < PW; p++) {
-      const uint4* g;
-      if (qkoff[p] >= 0) {
-        const int k = sc * 64 + qkoff[p];
-        g = (qrow_ok[p] && k < a.K) ? reinterpret_cast<const uint4*>(qsrc[p] + (size_t)sc * 64 * ESZ) : Z4;
-      } else {
-        g = reinterpret_cast<const uint4*>(qsrc[p] + (size_t)sc * bstride);
+      for (int p = 0; p < PW; p++) {
+        const uint4* g;
+        if (qkoff[p] >= 0) {
+          const int k = sc * 64 + qkoff[p];
+          g = (qrow_ok[p] && k < a.K) ? reinterpret_cast<const uint4*>(qsrc[p] + (size_t)sc * 64 * ESZ) : Z4;
+        } else {
+          g = reinterpret_cast<const uint4*>(qsrc[p] + (size_t)sc * bstride);
+        }
+        dma_tile(g, base + qlds[p]);
       }
-      dma_tile(g, base + qlds[p]);
     }
   };
 
@@ -207,18 +209,30 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
     for (int j = 0; j < FN; j++) fb[c][j] = buf[(TA + wn * FN + j) * 64 + lane];
   };
 
+  // Column by column: the MFMAs of weight column j (both K halves of every
+  // row group) run interleaved with the widening of column j + 1, so the
+  // VALU work of the int8 -> 16-bit conversion hides under the matrix pipe
+  // (all widening first, then all MFMAs, left them back to back).
   auto compute = [&](int c) {
-    uint4 wb[FN][2];
+    uint4 wcur[2], wnxt[2];
+    widen<AMODE>(fb[c][0], wcur[0], wcur[1]);
 #pragma unroll
-    for (int j = 0; j < FN; j++) widen<AMODE>(fb[c][j], wb[j][0], wb[j][1]);
+    for (int j = 0; j < FN; j++) {
+      if (j + 1 < FN) widen<AMODE>(fb[c][j + 1], wnxt[0], wnxt[1]);
 #pragma unroll
-    for (int i = 0; i < FM; i++) {
-      const uint4* f = &fa[c][i * AP];
+      for (int h = 0; h < 2; h++)
 #pragma unroll
-      for (int j = 0; j < FN; j++) {
-        acc[i][j] = mfma16<AMODE>(wb[j][0], f[0], acc[i][j]);
-        acc[i][j] = mfma16<AMODE>(wb[j][1], f[1], acc[i][j]);
+        for (int i = 0; i < FM; i++) acc[i][j] = mfma16<AMODE>(wcur[h], fa[c][i * AP + h], acc[i][j]);
+      if (j + 1 < FN) {
+#pragma unroll
+        for (int q = 0; q < 2 * FM; q++) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // then three VALU
+        }
       }
+      __builtin_amdgcn_sched_barrier(0);
+      wcur[0] = wnxt[0];
+      wcur[1] = wnxt[1];
     }
   };
 
@@ -331,6 +345,13 @@ static int b16_pick_cfg(int MG, int NG) {
   return best;
 }
 
+template <int AMODE, bool KF>
+static void launch_b16(const GemmB16Args& a, int cfg, dim3 grid, dim3 block, hipStream_t st) {
+  if (cfg == 0) hipLaunchKernelGGL((gemm_b16_lds_kernel<AMODE, 8, 12, 4, 2, 2, KF>), grid, block, 0, st, a);
+  else if (cfg == 1) hipLaunchKernelGGL((gemm_b16_lds_kernel<AMODE, 4, 8, 8, 2, 2, KF>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((gemm_b16_lds_kernel<AMODE, 2, 4, 8, 2, 2, KF>), grid, block, 0, st, a);
+}
+
 bool gemm_b16_supported(const GemmLaunch& L) {
   if (L.amode != A_BF16 && L.amode != A_F16) return false;
   if (L.K % 8 != 0 || L.lda % 8 != 0) return false;   // 8 elements per 16-byte copy
@@ -363,17 +384,14 @@ hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st) {
   a.ntm = cdiv(a.MG, mt);
   a.ntn = cdiv(a.NG, nt);
   const int blocks = a.ntm * a.ntn;
-  switch (L.amode) {
-    case A_BF16:
-      if (best == 0) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_BF16, 8, 12, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
-      else if (best == 1) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_BF16, 4, 8, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
-      else hipLaunchKernelGGL((gemm_b16_lds_kernel<A_BF16, 2, 4, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
-      break;
-    default:
-      if (best == 0) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F16, 8, 12, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
-      else if (best == 1) hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F16, 4, 8, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
-      else hipLaunchKernelGGL((gemm_b16_lds_kernel<A_F16, 2, 4, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a);
-      break;
+  const bool kf = (L.K % 64) == 0;
+  const dim3 grid(blocks), block(256);
+  if (L.amode == A_BF16) {
+    if (kf) launch_b16<A_BF16, true>(a, best, grid, block, st);
+    else launch_b16<A_BF16, false>(a, best, grid, block, st);
+  } else {
+    if (kf) launch_b16<A_F16, true>(a, best, grid, block, st);
+    else launch_b16<A_F16, false>(a, best, grid, block, st);
   }
   return hipGetLastError();
 }
