@@ -311,22 +311,23 @@ bool rows_supported(const GemmLaunch& L) {
   return (((uintptr_t)L.A) & align) == 0;
 }
 
-// K slices: the fewest that keep a slice's code tiles within 64 KiB of LDS
-// (64 k-blocks for one token group, 32 for two) and its activation chunks
-// within 4 per thread (MP * kbs <= 256, MP = M rounded up to a power of 2).  One slice needs no merge, and
-// splitting further was measured slower on every decode shape but the
-// 6144-deep down projection, where 2..3 slices balance the grid.
+// K slices: the fewest that keep a slice's code tiles within LDS (96 k-blocks
+// for up to 2 tokens, 64 for one token group, 32 for two) and its activation
+// chunks within 4 per thread (MP * kbs <= 256, MP = M rounded up to a power
+// of 2).  One slice needs no merge; splitting further was measured slower on
+// every decode shape (the down projection at 2 tokens: 7.7 us in one slice,
+// 8.2 / 8.5 / 8.9 us in 2 / 3 / 4).
 RowsPlan rows_plan(int M, int N, int K) {
   RowsPlan p;
   p.tg = M <= 4 ? 1 : 2;
   const int NG = cdiv(N, 16), KB = cdiv(K, 64);
   const int mp = M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8));
-  const int kmax = min(p.tg == 1 ? 64 : 32, 256 / mp);
+  const int kmax = min(p.tg == 1 ? (mp <= 2 ? 96 : 64) : 32, 256 / mp);
   int s = cdiv(KB, kmax);
   if (g_rows_force_split > 0) s = max(s, min(g_rows_force_split, KB));
   p.kbs = cdiv(KB, s);
   p.split = cdiv(KB, p.kbs);                // every slice holds >= 1 k-block
-  p.nkb = p.kbs <= 16 ? 16 : (p.kbs <= 32 ? 32 : 64);
+  p.nkb = p.kbs <= 16 ? 16 : (p.kbs <= 32 ? 32 : (p.kbs <= 64 ? 64 : 96));
   const int nch = p.kbs * mp * 4;
   p.cpt = nch <= 256 ? 1 : (nch <= 512 ? 2 : 4);
   p.blocks = NG * p.split;
@@ -352,7 +353,8 @@ static void launch_rows_mode(const RowsArgs& a, const RowsPlan& p, hipStream_t s
   if (p.tg == 1) {
     if (p.nkb == 16) launch_rows_cpt<AMODE, 1, 16>(a, p, st);
     else if (p.nkb == 32) launch_rows_cpt<AMODE, 1, 32>(a, p, st);
-    else launch_rows_cpt<AMODE, 1, 64>(a, p, st);
+    else if (p.nkb == 64) launch_rows_cpt<AMODE, 1, 64>(a, p, st);
+    else launch_rows_cpt<AMODE, 1, 96>(a, p, st);
   } else {
     if (p.nkb == 16) launch_rows_cpt<AMODE, 2, 16>(a, p, st);
     else launch_rows_cpt<AMODE, 2, 32>(a, p, st);
