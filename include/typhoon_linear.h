@@ -117,6 +117,11 @@ int tl_gemm_i8_set_cfg(int cfg);
  * small-batch kernel then takes those batches). */
 int tl_rows_set_split(int split);
 
+/* Tuning override of the same kernel: 1..3 16-row weight groups per
+ * work-group, sharing one split of the activations (taken only where a K
+ * slice holds at most 32 k-blocks; 1 elsewhere), 0 restores the planner. */
+int tl_rows_set_groups(int groups);
+
 /* Tuning switch of w8a16_linear at batch 1 for every later call in the
  * process: 1 (the default) runs it on the GEMV's weight stream with x as four
  * int8 digit rows; 0 on the bf16 / fp16 MFMA small-batch kernel. */

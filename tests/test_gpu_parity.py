@@ -354,7 +354,10 @@ def test_rows_digit_planes_k_slices(lin, orc, M, N, K):
     relative L2 1e-5 of the oracle's fp32 GEMM, bias included; a row holding
     NaN gives NaN outputs and leaves the other rows' bits unchanged, and two
     calls in a row give the same bits (the arrival counters are back at
-    zero); the earlier small-batch kernel (split -1) agrees too."""
+    zero); the earlier small-batch kernel (split -1) agrees too.  Work-groups
+    of 2 and 3 weight row groups sharing one split of the activations
+    (including a last work-group whose row groups run past N) give the same
+    bits as one row group per work-group."""
     say(f"rows digit planes M={M} N={N} K={K}")
     lib = lin.load_library()
     rng = np.random.default_rng(M * 31 + N + K)
@@ -364,16 +367,24 @@ def test_rows_digit_planes_k_slices(lin, orc, M, N, K):
     xn = x.copy()
     xn[M - 1, K // 3] = np.nan
     try:
-        for split in (1, 2, 3, 5, -1, 0):
-            assert lib.tl_rows_set_split(split) == 0
-            got = lin.w8a32_linear(x, w, s, bias=b)
-            assert rel_l2(got, want) <= 1e-5, (split, rel_l2(got, want))
-            np.testing.assert_array_equal(lin.w8a32_linear(x, w, s, bias=b), got)
-            gn = lin.w8a32_linear(xn, w, s, bias=b)
-            assert np.isnan(gn[M - 1]).all(), split
-            np.testing.assert_array_equal(gn[:M - 1], got[:M - 1])
+        by_split = {}
+        for groups in (1, 2, 3, 0):
+            assert lib.tl_rows_set_groups(groups) == 0
+            for split in ((1, 2, 3, 5, -1, 0) if groups == 0 else (1, 3)):
+                say(f"  groups {groups} split {split}")
+                assert lib.tl_rows_set_split(split) == 0
+                got = lin.w8a32_linear(x, w, s, bias=b)
+                assert rel_l2(got, want) <= 1e-5, (groups, split, rel_l2(got, want))
+                np.testing.assert_array_equal(lin.w8a32_linear(x, w, s, bias=b), got)
+                if split in by_split:
+                    np.testing.assert_array_equal(got, by_split[split])
+                by_split.setdefault(split, got)
+                gn = lin.w8a32_linear(xn, w, s, bias=b)
+                assert np.isnan(gn[M - 1]).all(), (groups, split)
+                np.testing.assert_array_equal(gn[:M - 1], got[:M - 1])
     finally:
         lib.tl_rows_set_split(0)
+        lib.tl_rows_set_groups(0)
 
 
 def test_w8a32_prefill_rows_consistent(lin, orc):

@@ -455,7 +455,8 @@ void op_w8a32(const float* X, const tl_weights* W, const float* bias, float* Y, 
   // 2..8 token rows over a weight of fewer than 32768 rows: int8 digit planes
   // of the fp32 rows, made inside the one launch (rows.hip; every work-group
   // splits its activation slice, which an lm_head-wide grid repeats too
-  // often: 2 tokens 62.5 us there against 58.6 us below)
+  // often: 151936 rows at 2 tokens 60.1 us there against 57.0 us below, at 8
+  // tokens 133 against 68 us)
   if (batch <= 8 && W->NG < 2048 && run_rows(ws, L, st)) return;
   if ((batch <= 16 && W->NG < 2048) || (batch <= 32 && W->NG <= 256)) {
     // a few token rows over a narrow weight: the small-M kernel splits the
@@ -919,6 +920,13 @@ int tl_rows_set_split(int split) {
     REQUIRE(split >= -1 && split <= 64, "split must be -1 (path off), 0 (planner) or 1..64");
     g_rows_off = split < 0;
     rows_set_split(split > 0 ? split : 0);
+  });
+}
+
+int tl_rows_set_groups(int groups) {
+  return guarded("tl_rows_set_groups", [&] {
+    REQUIRE(groups >= 0 && groups <= 3, "groups must be 0 (planner) or 1..3");
+    rows_set_groups(groups);
   });
 }
 

@@ -16,10 +16,10 @@
 // one MFMA per 16x64 weight tile and 4-token group.
 //
 // Work decomposition (HBM-bound like the GEMV: the weight bytes dominate):
-//   * work-group (g, s) owns the 16 weight rows of row group g and the
-//     k-blocks of K slice s (S slices of kbs k-blocks); its 4 waves split the
-//     slice's k-blocks and issue every weight load of the slice first (all
-//     tiles in flight at once, non-temporal);
+//   * work-group (g, s) owns the 16 R weight rows of row groups gR .. gR+R-1
+//     (R = 1..3) and the k-blocks of K slice s (S slices of kbs k-blocks);
+//     its 4 waves split the slice's k-blocks and issue every weight load of
+//     the slice first (all tiles in flight at once, non-temporal);
 //   * meanwhile all 256 threads load the slice of the M token rows in
 //     chunks of 16 consecutive k (chunk c = (kbl MP + t) 4 + kq: k-block
 //     kbl, token t, k quarter kq, MP = M rounded up to a power of two;
@@ -33,7 +33,7 @@
 //   * wave 0 combines each token's four digit sums (lane quads), scales them
 //     (y_s = 2^(e-6) fl(t ws)), and either stores the outputs (S == 1) or
 //     stores its partials with agent-scope atomic stores, waits for their
-//     acknowledgement and bumps row group g's arrival counter; the work-group
+//     acknowledgement and bumps work-group column g's arrival counter; the work-group
 //     that brings it to S adds the S partials in slice order, adds the bias,
 //     stores, and resets the counter.  Nothing waits on another work-group.
 // A token whose slice holds Inf or NaN gets NaN outputs (the reference's
@@ -54,6 +54,7 @@ struct RowsArgs {
   float* part;          // [S][M][N] partial outputs (S > 1)
   uint32_t* cnt;        // [NG] arrival counters, zero at rest (S > 1)
   int M, N, K, KB, NG, S, kbs;
+  int NGR;              // work-groups per K slice: ceil(NG / R)
   int lmp;              // log2 of M rounded up to a power of two
   int out;
 };
@@ -90,19 +91,20 @@ __device__ __forceinline__ void store_out(const RowsArgs& a, size_t o, float y) 
 }
 
 // TG 4-token groups (M <= 4 TG); NKB k-blocks per slice at most (code tiles
-// in LDS); CPT chunks of 16 activations per thread (MP * nk * 4 <= 256 CPT)
-template <int AMODE, int TG, int NKB, int CPT>
+// in LDS); CPT chunks of 16 activations per thread (MP * nk * 4 <= 256 CPT);
+// R weight row groups per work-group, sharing one split of the activations
+template <int AMODE, int TG, int NKB, int CPT, int R>
 __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
-  constexpr int NT = NKB / 4;           // weight tiles per wave at most
+  constexpr int NT = NKB / 4;           // weight tiles per wave and row group at most
   __shared__ uint4 s_codes[NKB][TG][64];
   __shared__ uint32_t s_mx[TG * 4];
-  __shared__ v4i s_part[TG][4][64];
+  __shared__ v4i s_part[R][TG][4][64];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = blockIdx.x % a.NG;
-  const int s = blockIdx.x / a.NG;
+  const int gg = blockIdx.x % a.NGR;         // row groups gg R .. gg R + R - 1
+  const int s = blockIdx.x / a.NGR;
   const int kb_lo = s * a.kbs;
   const int nk = min(a.kbs, a.KB - kb_lo);   // >= 1 (the host sizes S so)
   // chunks (k-block, token, k quarter); tokens padded to MP = 2^lmp >= M so
@@ -128,17 +130,24 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- this wave's weight tiles, all in flight
+  // ---- this wave's weight tiles of every row group, all in flight (row
+  //      groups past NG re-read the last one; their outputs are never stored)
   const int kw0 = (wv * nk) >> 2, n_t = (((wv + 1) * nk) >> 2) - kw0;
-  const uint4* wbase = reinterpret_cast<const uint4*>(a.Bt) + (size_t)g * 64 + lane;
   const size_t tstride = (size_t)a.NG * 64;
-  uint4 wt[NT];
+  const uint4* wbase[R];
+#pragma unroll
+  for (int r = 0; r < R; r++)
+    wbase[r] = reinterpret_cast<const uint4*>(a.Bt) + (size_t)min(gg * R + r, a.NG - 1) * 64 + lane;
+  uint4 wt[R][NT];
 #pragma unroll
   for (int i = 0; i < NT; i++) {
     const int kb = n_t > 0 ? kb_lo + kw0 + min(i, n_t - 1) : kb_lo;   // clamped repeats are skipped
-    typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
-    const v4u_t w = __builtin_nontemporal_load(reinterpret_cast<const v4u_t*>(wbase + (size_t)kb * tstride));
-    wt[i] = make_uint4(w.x, w.y, w.z, w.w);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
+      const v4u_t w = __builtin_nontemporal_load(reinterpret_cast<const v4u_t*>(wbase[r] + (size_t)kb * tstride));
+      wt[r][i] = make_uint4(w.x, w.y, w.z, w.w);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();                           // s_mx cleared
@@ -191,9 +200,11 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
 
   // ---- one MFMA per weight tile and token group (code rows of tokens >= M
   //      are never written: their outputs are never stored)
-  v4i acc[TG];
+  v4i acc[R][TG];
 #pragma unroll
-  for (int tg = 0; tg < TG; tg++) acc[tg] = v4i{0, 0, 0, 0};
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int tg = 0; tg < TG; tg++) acc[r][tg] = v4i{0, 0, 0, 0};
   const int rslot = lane ^ ((lane >> 4) & 3);   // this lane's code row, as stored
 #pragma unroll
   for (int i = 0; i < NT; i++) {
@@ -201,57 +212,68 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
 #pragma unroll
       for (int tg = 0; tg < TG; tg++) {
         const uint4 c = s_codes[kw0 + i][tg][rslot];
-        acc[tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, wt[i]), __builtin_bit_cast(v4i, c),
-                                                       acc[tg], 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < R; r++)
+          acc[r][tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, wt[r][i]),
+                                                             __builtin_bit_cast(v4i, c), acc[r][tg], 0, 0, 0);
       }
     }
   }
 #pragma unroll
-  for (int tg = 0; tg < TG; tg++) s_part[tg][wv][lane] = acc[tg];
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int tg = 0; tg < TG; tg++) s_part[r][tg][wv][lane] = acc[r][tg];
   __syncthreads();
   if (wv != 0) return;
 
-  // ---- wave 0: lane holds D[n0 .. n0+3][m], m = lane & 15 = 4 tq + p
-  //      (digit row p of token 4 tg + tq), n0 = 16 g + 4 (lane >> 4)
+  // ---- wave 0: lane holds D[n0 .. n0+3][m] of row group g, m = lane & 15 =
+  //      4 tq + p (digit row p of token 4 tg + tq), n0 = 16 g + 4 (lane >> 4)
   const int tq = (lane >> 2) & 3;
-  const int n0 = 16 * g + 4 * (lane >> 4);
   const bool owner = (lane & 3) == 0;
-  float y[TG][4];
+  float y[R][TG][4];
 #pragma unroll
-  for (int tg = 0; tg < TG; tg++) {
-    v4i tot = s_part[tg][0][lane];
+  for (int r = 0; r < R; r++) {
+    const int n0 = 16 * (gg * R + r) + 4 * (lane >> 4);
 #pragma unroll
-    for (int w = 1; w < 4; w++) {
-      const v4i p = s_part[tg][w][lane];
+    for (int tg = 0; tg < TG; tg++) {
+      v4i tot = s_part[r][tg][0][lane];
 #pragma unroll
-      for (int q = 0; q < 4; q++) tot[q] += p[q];
-    }
-    const int t = min(4 * tg + tq, a.M - 1);
-    const uint32_t mx = s_mx[t];
-    int ex = 0;
-    if (mx < 0x7f800000u && mx != 0) (void)frexpf(__uint_as_float(mx), &ex);
+      for (int w = 1; w < 4; w++) {
+        const v4i p = s_part[r][tg][w][lane];
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const int a1 = __shfl_xor(tot[q], 1, 64), a2 = __shfl_xor(tot[q], 2, 64), a3 = __shfl_xor(tot[q], 3, 64);
-      const float sum = digits_sum(tot[q], a1, a2, a3);
-      const int n = min(n0 + q, a.N - 1);
-      y[tg][q] = mx >= 0x7f800000u ? __builtin_nanf("") : ldexpf(__fmul_rn(sum, a.ws[n]), ex - 6);
+        for (int q = 0; q < 4; q++) tot[q] += p[q];
+      }
+      const int t = min(4 * tg + tq, a.M - 1);
+      const uint32_t mx = s_mx[t];
+      int ex = 0;
+      if (mx < 0x7f800000u && mx != 0) (void)frexpf(__uint_as_float(mx), &ex);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int a1 = __shfl_xor(tot[q], 1, 64), a2 = __shfl_xor(tot[q], 2, 64), a3 = __shfl_xor(tot[q], 3, 64);
+        const float sum = digits_sum(tot[q], a1, a2, a3);
+        const int n = min(n0 + q, a.N - 1);
+        y[r][tg][q] = mx >= 0x7f800000u ? __builtin_nanf("") : ldexpf(__fmul_rn(sum, a.ws[n]), ex - 6);
+      }
     }
   }
 
   if (a.S == 1) {
     if (!owner) return;
 #pragma unroll
-    for (int tg = 0; tg < TG; tg++) {
-      const int t = 4 * tg + tq;
-      if (t >= a.M) continue;
+    for (int r = 0; r < R; r++) {
+      const int n0 = 16 * (gg * R + r) + 4 * (lane >> 4);
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int n = n0 + q;
-        if (n >= a.N) continue;
-        float v = y[tg][q];
-        if (a.bias) v = __fadd_rn(v, a.bias[n]);
-        store_out(a, (size_t)t * a.ldy + n, v);
+      for (int tg = 0; tg < TG; tg++) {
+        const int t = 4 * tg + tq;
+        if (t >= a.M) continue;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int n = n0 + q;
+          if (n >= a.N) continue;
+          float v = y[r][tg][q];
+          if (a.bias) v = __fadd_rn(v, a.bias[n]);
+          store_out(a, (size_t)t * a.ldy + n, v);
+        }
       }
     }
     return;
@@ -260,46 +282,56 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
   // ---- S > 1: partials, arrival, and the last work-group's merge
   if (owner) {
 #pragma unroll
-    for (int tg = 0; tg < TG; tg++) {
-      const int t = 4 * tg + tq;
-      if (t >= a.M) continue;
+    for (int r = 0; r < R; r++) {
+      const int n0 = 16 * (gg * R + r) + 4 * (lane >> 4);
 #pragma unroll
-      for (int q = 0; q < 4; q++)
-        if (n0 + q < a.N) st_agent(a.part + ((size_t)s * a.M + t) * a.N + n0 + q, y[tg][q]);
+      for (int tg = 0; tg < TG; tg++) {
+        const int t = 4 * tg + tq;
+        if (t >= a.M) continue;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+          if (n0 + q < a.N) st_agent(a.part + ((size_t)s * a.M + t) * a.N + n0 + q, y[r][tg][q]);
+      }
     }
   }
   asm volatile("" ::: "memory");
   wait_vm<0>();                                // this wave's partial stores are acknowledged
   asm volatile("" ::: "memory");
   int last = 0;
-  if (lane == 0) last = __hip_atomic_fetch_add(a.cnt + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.S - 1);
+  if (lane == 0) last = __hip_atomic_fetch_add(a.cnt + gg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.S - 1);
   last = __shfl(last, 0, 64);
   if (!last) return;
   asm volatile("" ::: "memory");
   if (owner) {
 #pragma unroll
-    for (int tg = 0; tg < TG; tg++) {
-      const int t = 4 * tg + tq;
-      if (t >= a.M) continue;
+    for (int r = 0; r < R; r++) {
+      const int n0 = 16 * (gg * R + r) + 4 * (lane >> 4);
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int n = n0 + q;
-        if (n >= a.N) continue;
-        float v = ld_agent(a.part + (size_t)t * a.N + n);
-        for (int ss = 1; ss < a.S; ss++) v = __fadd_rn(v, ld_agent(a.part + ((size_t)ss * a.M + t) * a.N + n));
-        if (a.bias) v = __fadd_rn(v, a.bias[n]);
-        store_out(a, (size_t)t * a.ldy + n, v);
+      for (int tg = 0; tg < TG; tg++) {
+        const int t = 4 * tg + tq;
+        if (t >= a.M) continue;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int n = n0 + q;
+          if (n >= a.N) continue;
+          float v = ld_agent(a.part + (size_t)t * a.N + n);
+          for (int ss = 1; ss < a.S; ss++) v = __fadd_rn(v, ld_agent(a.part + ((size_t)ss * a.M + t) * a.N + n));
+          if (a.bias) v = __fadd_rn(v, a.bias[n]);
+          store_out(a, (size_t)t * a.ldy + n, v);
+        }
       }
     }
   }
-  if (lane == 0) __hip_atomic_store(a.cnt + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0) __hip_atomic_store(a.cnt + gg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
 // planner and launcher
 // ---------------------------------------------------------------------------
 static int g_rows_force_split = 0;
+static int g_rows_force_groups = 0;
 void rows_set_split(int s) { g_rows_force_split = s > 0 ? s : 0; }
+void rows_set_groups(int r) { g_rows_force_groups = r > 0 ? r : 0; }
 
 bool rows_supported(const GemmLaunch& L) {
   if (L.M < 1 || L.M > 8 || L.N < 1 || L.K < 1) return false;
@@ -317,6 +349,13 @@ bool rows_supported(const GemmLaunch& L) {
 // of 2).  One slice needs no merge; splitting further was measured slower on
 // every decode shape (the down projection at 2 tokens: 7.7 us in one slice,
 // 8.2 / 8.5 / 8.9 us in 2 / 3 / 4).
+// Row groups per work-group: each work-group loads and splits its slice of
+// the activations once for R 16-row weight groups.  R > 1 only for two token
+// groups (5..8 tokens, where the split costs twice as much) and only where
+// the grid still holds >= 256 work-groups, one per CU: the gate/up
+// projection (12288 x 2048) at 5..8 tokens 13.4-14.4 us with R = 1, 12.7-12.9
+// with R = 3; at 2..4 tokens R = 1 is fastest on every decode shape (gate/up
+// 7.5 against 8.5 us at 2 tokens).
 RowsPlan rows_plan(int M, int N, int K) {
   RowsPlan p;
   p.tg = M <= 4 ? 1 : 2;
@@ -330,7 +369,17 @@ RowsPlan rows_plan(int M, int N, int K) {
   p.nkb = p.kbs <= 16 ? 16 : (p.kbs <= 32 ? 32 : (p.kbs <= 64 ? 64 : 96));
   const int nch = p.kbs * mp * 4;
   p.cpt = nch <= 256 ? 1 : (nch <= 512 ? 2 : 4);
-  p.blocks = NG * p.split;
+  p.r = 1;
+  if (p.nkb <= 32) {   // the instances built for R > 1
+    if (g_rows_force_groups > 0) p.r = g_rows_force_groups;
+    else if (p.tg == 2)
+      for (int r = 3; r > 1; r--)
+        if (cdiv(NG, r) * p.split >= 256) {
+          p.r = r;
+          break;
+        }
+  }
+  p.blocks = cdiv(NG, p.r) * p.split;
   return p;
 }
 
@@ -340,24 +389,31 @@ size_t rows_workspace_bytes(int M, int N, int K) {
 }
 size_t rows_counter_count(int N) { return (size_t)cdiv(N, 16); }
 
-template <int AMODE, int TG, int NKB>
+template <int AMODE, int TG, int NKB, int R>
 static void launch_rows_cpt(const RowsArgs& a, const RowsPlan& p, hipStream_t st) {
   const dim3 grid(p.blocks), block(256);
-  if (p.cpt == 1) hipLaunchKernelGGL((rows_planes_kernel<AMODE, TG, NKB, 1>), grid, block, 0, st, a);
-  else if (p.cpt == 2) hipLaunchKernelGGL((rows_planes_kernel<AMODE, TG, NKB, 2>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((rows_planes_kernel<AMODE, TG, NKB, 4>), grid, block, 0, st, a);
+  if (p.cpt == 1) hipLaunchKernelGGL((rows_planes_kernel<AMODE, TG, NKB, 1, R>), grid, block, 0, st, a);
+  else if (p.cpt == 2) hipLaunchKernelGGL((rows_planes_kernel<AMODE, TG, NKB, 2, R>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((rows_planes_kernel<AMODE, TG, NKB, 4, R>), grid, block, 0, st, a);
+}
+
+template <int AMODE, int TG, int NKB>
+static void launch_rows_r(const RowsArgs& a, const RowsPlan& p, hipStream_t st) {
+  if (p.r == 1) launch_rows_cpt<AMODE, TG, NKB, 1>(a, p, st);
+  else if (p.r == 2) launch_rows_cpt<AMODE, TG, NKB, 2>(a, p, st);
+  else launch_rows_cpt<AMODE, TG, NKB, 3>(a, p, st);
 }
 
 template <int AMODE>
 static void launch_rows_mode(const RowsArgs& a, const RowsPlan& p, hipStream_t st) {
   if (p.tg == 1) {
-    if (p.nkb == 16) launch_rows_cpt<AMODE, 1, 16>(a, p, st);
-    else if (p.nkb == 32) launch_rows_cpt<AMODE, 1, 32>(a, p, st);
-    else if (p.nkb == 64) launch_rows_cpt<AMODE, 1, 64>(a, p, st);
-    else launch_rows_cpt<AMODE, 1, 96>(a, p, st);
+    if (p.nkb == 16) launch_rows_r<AMODE, 1, 16>(a, p, st);
+    else if (p.nkb == 32) launch_rows_r<AMODE, 1, 32>(a, p, st);
+    else if (p.nkb == 64) launch_rows_cpt<AMODE, 1, 64, 1>(a, p, st);
+    else launch_rows_cpt<AMODE, 1, 96, 1>(a, p, st);
   } else {
-    if (p.nkb == 16) launch_rows_cpt<AMODE, 2, 16>(a, p, st);
-    else launch_rows_cpt<AMODE, 2, 32>(a, p, st);
+    if (p.nkb == 16) launch_rows_r<AMODE, 2, 16>(a, p, st);
+    else launch_rows_r<AMODE, 2, 32>(a, p, st);
   }
 }
 
@@ -366,6 +422,8 @@ hipError_t launch_rows(const GemmLaunch& L, hipStream_t st) {
   const RowsPlan p = rows_plan(L.M, L.N, L.K);
   const int lmp = L.M <= 1 ? 0 : (L.M <= 2 ? 1 : (L.M <= 4 ? 2 : 3));
   if ((p.tg == 2 && p.nkb > 32) || p.split < 1 || (p.kbs << lmp) * 4 > 256 * p.cpt) return hipErrorInvalidValue;
+  if (p.r < 1 || p.r > 3 || (p.r > 1 && p.nkb > 32) || p.blocks != cdiv(cdiv(L.N, 16), p.r) * p.split)
+    return hipErrorInvalidValue;
   if (p.split > 1 && (!L.part || !L.cnt)) return hipErrorInvalidValue;
   RowsArgs a;
   a.X = L.A;
@@ -384,6 +442,7 @@ hipError_t launch_rows(const GemmLaunch& L, hipStream_t st) {
   a.NG = cdiv(L.N, 16);
   a.S = p.split;
   a.kbs = p.kbs;
+  a.NGR = cdiv(a.NG, p.r);
   a.lmp = lmp;
   a.out = L.out;
   launch_rows_mode<A_F32X3>(a, p, st);

@@ -189,13 +189,14 @@ hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st);
 //      A_F32X3; fp32 sums of w * x, y = 2^e fl(t * ws) summed over K slices,
 //      then + bias -----------------------------------------------------------
 struct RowsPlan {
-  int tg = 1, nkb = 16, cpt = 1, kbs = 1, split = 1, blocks = 0;
+  int tg = 1, nkb = 16, cpt = 1, kbs = 1, split = 1, r = 1, blocks = 0;
 };
 bool rows_supported(const GemmLaunch& L);
 RowsPlan rows_plan(int M, int N, int K);
 size_t rows_workspace_bytes(int M, int N, int K);   // partials when split > 1
 size_t rows_counter_count(int N);                   // zeroed arrival counters
 void rows_set_split(int s);                         // tuning override (0 = planner)
+void rows_set_groups(int r);                        // tuning override (0 = planner)
 hipError_t launch_rows(const GemmLaunch& L, hipStream_t st);
 
 }  // namespace tl
