@@ -124,11 +124,14 @@ __device__ __forceinline__ void quantize_row_to_tiles(const float4 (&v)[NV], int
 // scales (the fp32 row is never stored; K % 64 == 0, K <= 2048).
 template <bool PLANES>
 __global__ __launch_bounds__(256) void rmsnorm_rows_q_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                             int K, float eps, int MG, uint8_t* __restrict__ tiles,
-                                                             float* __restrict__ scales, int* __restrict__ xe) {
+                                                             int rows, int K, float eps, int MG,
+                                                             uint8_t* __restrict__ tiles, float* __restrict__ scales,
+                                                             int* __restrict__ xe) {
   __shared__ float s_part[4];
   __shared__ uint32_t s_mx[4];
-  const size_t row = blockIdx.x;
+  const int rr = xcd_grouped_row(blockIdx.x);
+  if (rr >= rows) return;                   // the whole work-group
+  const size_t row = rr;
   const float4* xr = reinterpret_cast<const float4*>(x + row * K);
   const float4* wr = reinterpret_cast<const float4*>(w);
   const int n4 = K >> 2;
@@ -161,23 +164,45 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_q_kernel(const float* __rest
 // SwiGLU of one token's interleaved gate/up row (the values of
 // swiglu_rows_kernel) followed by the W8A8 per-token quantization, written as
 // int8 tiles and the token's scale; one work-group per token, ffn = 1024 NV.
+// The SwiGLU values wait in LDS (each thread reads back its own) while the row
+// is computed in two halves: holding a whole 6144-wide row's loads and values
+// in registers took 127 VGPRs, 4 work-groups per CU, and a 1200-token batch
+// then ran in two rounds; at 24 KB of LDS per work-group all 1200 are resident.
 template <int NV, bool PLANES>
-__global__ __launch_bounds__(256) void swiglu_rows_q_kernel(const float* __restrict__ gu, int ffn, int MG,
+__global__ __launch_bounds__(256) void swiglu_rows_q_kernel(const float* __restrict__ gu, int S, int ffn, int MG,
                                                             uint8_t* __restrict__ tiles, float* __restrict__ scales,
                                                             int* __restrict__ xe) {
   __shared__ uint32_t s_mx[4];
-  const size_t t = blockIdx.x;
+  __shared__ float4 s_y[NV][256];
+  const int tt = xcd_grouped_row(blockIdx.x);
+  if (tt >= S) return;                      // the whole work-group
+  const size_t t = tt;
   const float* row = gu + t * 2 * ffn;
+  constexpr int H = (NV + 1) / 2;
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    float4 g[H], u[H];
+#pragma unroll
+    for (int i = 0; i < H; i++) {
+      const int j = h * H + i;
+      if (j >= NV) continue;
+      const int c = 4 * (threadIdx.x + 256 * j);  // outputs c .. c+3: gate 16b + r.., up 16b + 8 + r..
+      const int b = c >> 3, r = c & 7;
+      g[i] = *reinterpret_cast<const float4*>(row + 16 * b + r);
+      u[i] = *reinterpret_cast<const float4*>(row + 16 * b + 8 + r);
+    }
+#pragma unroll
+    for (int i = 0; i < H; i++) {
+      const int j = h * H + i;
+      if (j >= NV) continue;
+      s_y[j][threadIdx.x] = make_float4(__fmul_rn(ref_silu(g[i].x), u[i].x), __fmul_rn(ref_silu(g[i].y), u[i].y),
+                                        __fmul_rn(ref_silu(g[i].z), u[i].z), __fmul_rn(ref_silu(g[i].w), u[i].w));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
   float4 y[NV];
 #pragma unroll
-  for (int j = 0; j < NV; j++) {
-    const int c = 4 * (threadIdx.x + 256 * j);    // outputs c .. c+3: gate 16b + r.., up 16b + 8 + r..
-    const int b = c >> 3, r = c & 7;
-    const float4 g = *reinterpret_cast<const float4*>(row + 16 * b + r);
-    const float4 u = *reinterpret_cast<const float4*>(row + 16 * b + 8 + r);
-    y[j] = make_float4(__fmul_rn(ref_silu(g.x), u.x), __fmul_rn(ref_silu(g.y), u.y), __fmul_rn(ref_silu(g.z), u.z),
-                       __fmul_rn(ref_silu(g.w), u.w));
-  }
+  for (int j = 0; j < NV; j++) y[j] = s_y[j][threadIdx.x];
   quantize_row_to_tiles<NV, PLANES>(y, ffn >> 2, (int)t, MG, tiles, scales, xe, s_mx);
 }
 
@@ -540,11 +565,12 @@ hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int r
 hipError_t launch_rmsnorm_rows_q(const float* x, const float* w, uint8_t* tiles, float* scales, int* xe, int rows,
                                  int K, float eps, hipStream_t st) {
   if (K % 64 != 0 || K > 2048 || rows < 1 || (!scales == !xe)) return hipErrorInvalidValue;
+  const dim3 grid(cdiv(rows, 64) * 64);     // xcd_grouped_row: whole groups of 64 rows
   if (xe)
-    hipLaunchKernelGGL(rmsnorm_rows_q_kernel<true>, dim3(rows), dim3(256), 0, st, x, w, K, eps, cdiv(4 * rows, 16),
+    hipLaunchKernelGGL(rmsnorm_rows_q_kernel<true>, grid, dim3(256), 0, st, x, w, rows, K, eps, cdiv(4 * rows, 16),
                        tiles, scales, xe);
   else
-    hipLaunchKernelGGL(rmsnorm_rows_q_kernel<false>, dim3(rows), dim3(256), 0, st, x, w, K, eps, cdiv(rows, 16),
+    hipLaunchKernelGGL(rmsnorm_rows_q_kernel<false>, grid, dim3(256), 0, st, x, w, rows, K, eps, cdiv(rows, 16),
                        tiles, scales, xe);
   return hipGetLastError();
 }
@@ -553,14 +579,15 @@ hipError_t launch_swiglu_rows_q(const float* gu, uint8_t* tiles, float* scales, 
                                 hipStream_t st) {
   if (S < 1 || (!scales == !xe)) return hipErrorInvalidValue;
   const int MG = xe ? cdiv(4 * S, 16) : cdiv(S, 16);
+  const dim3 grid(cdiv(S, 64) * 64);        // xcd_grouped_row: whole groups of 64 rows
   if (ffn == 6144 && xe)
-    hipLaunchKernelGGL((swiglu_rows_q_kernel<6, true>), dim3(S), dim3(256), 0, st, gu, ffn, MG, tiles, scales, xe);
+    hipLaunchKernelGGL((swiglu_rows_q_kernel<6, true>), grid, dim3(256), 0, st, gu, S, ffn, MG, tiles, scales, xe);
   else if (ffn == 6144)
-    hipLaunchKernelGGL((swiglu_rows_q_kernel<6, false>), dim3(S), dim3(256), 0, st, gu, ffn, MG, tiles, scales, xe);
+    hipLaunchKernelGGL((swiglu_rows_q_kernel<6, false>), grid, dim3(256), 0, st, gu, S, ffn, MG, tiles, scales, xe);
   else if (ffn == 2048 && xe)
-    hipLaunchKernelGGL((swiglu_rows_q_kernel<2, true>), dim3(S), dim3(256), 0, st, gu, ffn, MG, tiles, scales, xe);
+    hipLaunchKernelGGL((swiglu_rows_q_kernel<2, true>), grid, dim3(256), 0, st, gu, S, ffn, MG, tiles, scales, xe);
   else if (ffn == 2048)
-    hipLaunchKernelGGL((swiglu_rows_q_kernel<2, false>), dim3(S), dim3(256), 0, st, gu, ffn, MG, tiles, scales, xe);
+    hipLaunchKernelGGL((swiglu_rows_q_kernel<2, false>), grid, dim3(256), 0, st, gu, S, ffn, MG, tiles, scales, xe);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

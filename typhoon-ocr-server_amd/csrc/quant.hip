@@ -177,7 +177,12 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_vec_kernel(const floa
                                                                       uint8_t* __restrict__ tiles,
                                                                       float* __restrict__ scales, int clamp127) {
   const int lane = threadIdx.x & 63;
-  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  // rows 4 quad .. 4 quad + 3; the two quads whose codes share each 128-byte
+  // tile line (8 rows) run on one XCD (work-group b on XCD b % 8), so their
+  // partial-line stores merge in its L2; a bijection of [0, 16 n) work-groups
+  const int x = blockIdx.x & 7, jj = blockIdx.x >> 3;
+  const int quad = 16 * (jj >> 1) + 2 * x + (jj & 1);
+  const int r = quad * 4 + (threadIdx.x >> 6);
   if (r >= rows) return;
   const float4* row = reinterpret_cast<const float4*>(src + (size_t)r * cols);
   float4 v[NV];
@@ -385,14 +390,15 @@ hipError_t launch_quantize_rows_tiled(const float* src, int rows, int cols, uint
   const int c = clamp127 ? 1 : 0;
   const bool aligned = (((uintptr_t)src) & 15) == 0;
   const int MG = cdiv(rows, 16);
+  const dim3 vgrid(cdiv(rows, 64) * 16);   // whole groups of 16 quads of rows
   if (aligned && cols == 2048)
-    hipLaunchKernelGGL(quantize_rows_tiled_vec_kernel<8>, grid, block, 0, st, src, rows, cols, MG, tiles, scales, c);
+    hipLaunchKernelGGL(quantize_rows_tiled_vec_kernel<8>, vgrid, block, 0, st, src, rows, cols, MG, tiles, scales, c);
   else if (aligned && cols == 6144)
-    hipLaunchKernelGGL(quantize_rows_tiled_vec_kernel<24>, grid, block, 0, st, src, rows, cols, MG, tiles, scales, c);
+    hipLaunchKernelGGL(quantize_rows_tiled_vec_kernel<24>, vgrid, block, 0, st, src, rows, cols, MG, tiles, scales, c);
   else if (aligned && cols == 1024)
-    hipLaunchKernelGGL(quantize_rows_tiled_vec_kernel<4>, grid, block, 0, st, src, rows, cols, MG, tiles, scales, c);
+    hipLaunchKernelGGL(quantize_rows_tiled_vec_kernel<4>, vgrid, block, 0, st, src, rows, cols, MG, tiles, scales, c);
   else if (aligned && cols == 4096)
-    hipLaunchKernelGGL(quantize_rows_tiled_vec_kernel<16>, grid, block, 0, st, src, rows, cols, MG, tiles, scales, c);
+    hipLaunchKernelGGL(quantize_rows_tiled_vec_kernel<16>, vgrid, block, 0, st, src, rows, cols, MG, tiles, scales, c);
   else
     hipLaunchKernelGGL(quantize_rows_tiled_kernel<0>, grid, block, 0, st, src, rows, cols, KB, tiles, scales, c);
   return hipGetLastError();

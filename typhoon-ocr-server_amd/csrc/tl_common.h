@@ -528,6 +528,18 @@ __device__ __forceinline__ void dma_tile_s(uint32_t voff, const void* sbase, uin
 }
 __device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
+// Work-group b -> token row for kernels that write one token's int8 codes
+// per work-group into the 16x64 tile layout.  A 128-byte line of a tile holds
+// tile lanes 8i .. 8i+7, i.e. 8 consecutive code rows (8 tokens, or 2 tokens
+// of four planes each); dispatch is round-robin over the 8 XCDs (work-group b
+// on XCD b % 8), so rows 8g .. 8g+7 go to work-groups of one XCD and their
+// partial-line stores merge in that XCD's L2 instead of reaching memory as 8
+// partial writes.  A bijection of [0, 64 n); grids are rounded up to 64.
+__device__ __forceinline__ int xcd_grouped_row(int b) {
+  const int x = b & 7, j = b >> 3;
+  return 64 * (j >> 3) + 8 * x + (j & 7);
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) void*)p));
