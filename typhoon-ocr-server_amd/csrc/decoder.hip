@@ -343,3 +343,17 @@ hipError_t launch_step_end(const uint64_t* keys, int n, const float* embed, int 
 }
 
 }  // namespace tl
+
+// ---------------------------------------------------------------------------
+// C ABI of the launchers above (tl_kernels.h)
+// ---------------------------------------------------------------------------
+extern "C" {
+int tlk_attn_chunks(int max_seq) { return tl::attn_chunks(max_seq); }
+int tlk_attn_chunk_size(int max_seq) { return tl::attn_chunk_size(max_seq); }
+void tlk_attn_set_chunk(int t) { tl::attn_set_chunk(t); }
+hipError_t tlk_launch_attn_decode(const AttnDecodeArgs* a, hipStream_t st) { return tl::launch_attn_decode(*a, st); }
+hipError_t tlk_launch_step_end(const uint64_t* keys, int n, const float* embed, int H, float* hidden, int* state,
+                               int32_t* tokens, int max_tokens, hipStream_t st) {
+  return tl::launch_step_end(keys, n, embed, H, hidden, state, tokens, max_tokens, st);
+}
+}  // extern "C"

@@ -438,3 +438,15 @@ hipError_t launch_gemm(const GemmLaunch& L, hipStream_t st) {
 }
 
 }  // namespace tl
+
+// ---------------------------------------------------------------------------
+// C ABI of the launchers above (tl_kernels.h)
+// ---------------------------------------------------------------------------
+extern "C" {
+void tlk_gemm_plan(int amode, int M, int N, int K, GemmPlan* plan) { *plan = tl::gemm_plan(amode, M, N, K); }
+size_t tlk_gemm_workspace_bytes(int amode, int M, int N, int K) {
+  return tl::gemm_workspace_bytes(amode, M, N, K);
+}
+size_t tlk_gemm_counter_count(int amode, int M, int N, int K) { return tl::gemm_counter_count(amode, M, N, K); }
+hipError_t tlk_launch_gemm(const GemmLaunch* L, hipStream_t st) { return tl::launch_gemm(*L, st); }
+}  // extern "C"

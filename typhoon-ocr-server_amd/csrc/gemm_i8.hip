@@ -612,3 +612,5 @@ hipError_t launch_gemm_i8(const GemmLaunch& L, hipStream_t st) {
 }
 
 }  // namespace tl
+
+extern "C" void tlk_gemm_i8_set_cfg(int cfg) { tl::gemm_i8_set_cfg(cfg); }

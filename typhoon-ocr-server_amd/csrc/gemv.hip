@@ -731,3 +731,16 @@ hipError_t launch_gemv_i8(const GemvLaunch& L, hipStream_t st) {
 }
 
 }  // namespace tl
+
+// ---------------------------------------------------------------------------
+// C ABI of the launchers above (tl_kernels.h)
+// ---------------------------------------------------------------------------
+extern "C" {
+void tlk_gemv_plan(int N, int K, GemvPlan* plan) { *plan = tl::gemv_plan(N, K); }
+int tlk_gemv_fused_xv(int K) { return tl::gemv_fused_xv(K); }
+bool tlk_gemv_fused_norm_ok(int K, const float* x, const float* norm_w) {
+  return tl::gemv_fused_norm_ok(K, x, norm_w);
+}
+hipError_t tlk_launch_gemv_i8(const GemvLaunch* L, hipStream_t st) { return tl::launch_gemv_i8(*L, st); }
+void tlk_gemv_set_plan(int rows, int u) { tl::gemv_set_plan(rows, u); }
+}  // extern "C"

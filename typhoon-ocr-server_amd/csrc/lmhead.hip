@@ -18,7 +18,6 @@
 //
 // The GEMV's EPI_ARGMAX epilogue leaves one key per work-group (tl_common.h
 // argmax_key); argmax_keys_kernel reduces them to the token.
-#include "host.h"
 #include "tl_common.h"
 #include "tl_kernels.h"
 
@@ -26,7 +25,7 @@
 
 namespace tl {
 
-constexpr int kRmsMaxK = 16384;
+constexpr int kRmsMaxK = TLK_RMS_MAX_K;
 
 // One work-group.  Thread p = 8b + j owns accumulator j of block b: its 16
 // terms x[128b + 8i + j]^2 are loaded at once and added in order i = 0..15.
@@ -127,92 +126,51 @@ hipError_t launch_argmax_keys(const uint64_t* keys, int n, int32_t* token, float
 
 }  // namespace tl
 
-namespace tlhost {
-using namespace tl;
-
-size_t lm_head_argmax_keys(int N, int K) { return (size_t)gemv_plan(N, K).blocks; }
-
-// The greedy step's launches on caller-provided work-space: keys (one 8-byte
-// key per GEMV work-group, 16-byte aligned) and xn (K floats, used only when
-// the final RMSNorm cannot run inside the GEMV's prologue).
-void lm_head_argmax_enqueue(const float* h, const float* norm_w, const tl_weights* W, float* logits,
-                            int32_t* token, float* max_logit, uint64_t* keys, float* xn, hipStream_t st) {
-  const int K = W->cols;
-  REQUIRE(K >= 128 && K <= kRmsMaxK && (K & (K - 1)) == 0, "K must be a power of two in [128, 16384]");
-  GemvLaunch L;
-  if (gemv_fused_norm_ok(K, h, norm_w)) {
-    // every GEMV work-group normalises the row itself: one launch fewer
-    L.x = h;
-    L.norm = NORM_NUMPY;
-    L.norm_w = norm_w;
-  } else {
-    HIP_OK(launch_rmsnorm_np(h, norm_w, xn, K, 1e-6f, st));
-    L.x = xn;
-  }
-  L.wt = W->tiles;
-  L.ws = W->scales;
-  L.y = logits;
-  L.keys = keys;
-  L.N = W->rows;
-  L.K = K;
-  L.epi = EPI_ARGMAX;
-  HIP_OK(launch_gemv_i8(L, st));
-  HIP_OK(launch_argmax_keys(keys, (int)lm_head_argmax_keys(W->rows, K), token, max_logit, st));
-}
-
-}  // namespace tlhost
-
 // --------------------------------------------------------------------------
-// tl_lm_head_argmax_noalloc_dev: the greedy step with its work-space in a
-// file-scope device array, for callers that cannot allocate (HIP graph
-// capture, serving loops).  The array holds the argmax keys of up to
-// kNaMaxRows lm_head rows (16-row work-groups) and one normalised row of
-// kRmsMaxK floats.  Every device the library runs on keeps its own copy
-// until the process ends; host code reaches it only through the address
+// The no-allocation work-space of tl_lm_head_argmax_noalloc_dev (api.c): a
+// file-scope device array for callers that cannot allocate (HIP graph
+// capture, serving loops).  It holds the argmax keys of up to
+// TLK_NA_MAX_ROWS lm_head rows (16-row work-groups) and one normalised row of
+// kRmsMaxK floats.  Every device the library runs on keeps its own copy until
+// the process ends; host code reaches it only through the address
 // hipGetSymbolAddress returns for the current device (the array's name is a
-// host-side stand-in, not a device address).  Nothing in it needs to start
-// at zero: each call writes every key and element it reads.  Calls that
-// overlap on one device share the array and race.
+// host-side stand-in, not a device address), looked up once per device here.
+// Nothing in it needs to start at zero: each call writes every key and
+// element it reads.  Calls that overlap on one device share the array and
+// race.
 // --------------------------------------------------------------------------
 namespace {
-constexpr int kNaMaxRows = 262144;
-constexpr size_t kNaKeyBytes = (size_t)kNaMaxRows / 16 * sizeof(uint64_t);   // 128 KiB
-constexpr size_t kNaBytes = kNaKeyBytes + (size_t)tl::kRmsMaxK * sizeof(float);   // + 64 KiB
+constexpr size_t kNaBytes = (size_t)TLK_NA_KEY_BYTES + (size_t)tl::kRmsMaxK * sizeof(float);   // 192 KiB
 constexpr int kNaMaxDevices = 64;
+static_assert((size_t)TLK_NA_KEY_BYTES == (size_t)TLK_NA_MAX_ROWS / 16 * sizeof(uint64_t), "key bytes");
 }  // namespace
 
 static __device__ __align__(256) uint8_t scratch[kNaBytes];
 
 namespace {
-using tlhost::Fail;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kNaMaxDevices] = {};
+}  // namespace
 
-// the device address of `scratch` on the current device, looked up once per device
-uint8_t* scratch_on(int dev) {
-  REQUIRE(dev >= 0 && dev < kNaMaxDevices, "device index out of range");
+extern "C" {
+hipError_t tlk_launch_rmsnorm_np(const float* h, const float* w, float* out, int K, float eps, hipStream_t st) {
+  return tl::launch_rmsnorm_np(h, w, out, K, eps, st);
+}
+hipError_t tlk_launch_argmax_keys(const uint64_t* keys, int n, int32_t* token, float* value, hipStream_t st) {
+  return tl::launch_argmax_keys(keys, n, token, value, st);
+}
+// the device address of `scratch` on device `dev` (current), looked up once
+hipError_t tlk_noalloc_workspace(int dev, uint8_t** base) {
+  if (dev < 0 || dev >= kNaMaxDevices || !base) return hipErrorInvalidValue;
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
     void* p = nullptr;
-    HIP_OK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
-    REQUIRE(p != nullptr, "hipGetSymbolAddress returned NULL for the scratch array");
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
     g_scratch_ptr[dev] = p;
   }
-  return static_cast<uint8_t*>(g_scratch_ptr[dev]);
+  *base = static_cast<uint8_t*>(g_scratch_ptr[dev]);
+  return hipSuccess;
 }
-}  // namespace
-
-extern "C" int tl_lm_head_argmax_noalloc_dev(const float* h, const float* norm_w, const tl_weights* W,
-                                             float* logits, int32_t* token, float* max_logit, void* stream) {
-  using namespace tlhost;
-  return guarded("tl_lm_head_argmax_noalloc_dev", [&] {
-    check_weights(W);
-    REQUIRE(h && token, "h and token must be non-NULL");
-    REQUIRE(W->rows <= kNaMaxRows, "lm_head has more rows than the no-allocation work-space holds (262144)");
-    REQUIRE(lm_head_argmax_keys(W->rows, W->cols) * sizeof(uint64_t) <= kNaKeyBytes,
-            "the GEMV plan needs more argmax keys than the no-allocation work-space holds");
-    uint8_t* base = scratch_on(W->dev);
-    lm_head_argmax_enqueue(h, norm_w, W, logits, token, max_logit, reinterpret_cast<uint64_t*>(base),
-                           reinterpret_cast<float*>(base + kNaKeyBytes), static_cast<hipStream_t>(stream));
-  });
-}
+}  // extern "C"

@@ -665,3 +665,39 @@ hipError_t launch_residual_add(const float* y, float* h, long long n, hipStream_
 }
 
 }  // namespace tl
+
+// ---------------------------------------------------------------------------
+// C ABI of the launchers above (tl_kernels.h)
+// ---------------------------------------------------------------------------
+extern "C" {
+hipError_t tlk_launch_rmsnorm_rows(const float* x, const float* w, float* out, int rows, int K, float eps,
+                                   hipStream_t st) {
+  return tl::launch_rmsnorm_rows(x, w, out, rows, K, eps, st);
+}
+hipError_t tlk_launch_prefill_qk(float* qkv, const float* q_norm, const float* k_norm, const float* cos_t,
+                                 const float* sin_t, float* kc, float* vc, int max_seq, int row0, int S, int nkv,
+                                 float eps, hipStream_t st) {
+  return tl::launch_prefill_qk(qkv, q_norm, k_norm, cos_t, sin_t, kc, vc, max_seq, row0, S, nkv, eps, st);
+}
+size_t tlk_flash_split_floats(int S, int nq) { return tl::flash_split_floats(S, nq); }
+size_t tlk_flash_split_counters(int S, int nq) { return tl::flash_split_counters(S, nq); }
+hipError_t tlk_launch_flash_prefill(const float* qkv, const float* kc, const float* vc, float* out, int S, int nq,
+                                    int max_seq, int key0, int qoff, float scale, float* part, int* cnt,
+                                    hipStream_t st) {
+  return tl::launch_flash_prefill(qkv, kc, vc, out, S, nq, max_seq, key0, qoff, scale, part, cnt, st);
+}
+hipError_t tlk_launch_swiglu_rows(const float* gu, float* mlp, int S, int ffn, hipStream_t st) {
+  return tl::launch_swiglu_rows(gu, mlp, S, ffn, st);
+}
+hipError_t tlk_launch_rmsnorm_rows_q(const float* x, const float* w, uint8_t* tiles, float* scales, int* xe,
+                                     int rows, int K, float eps, hipStream_t st) {
+  return tl::launch_rmsnorm_rows_q(x, w, tiles, scales, xe, rows, K, eps, st);
+}
+hipError_t tlk_launch_swiglu_rows_q(const float* gu, uint8_t* tiles, float* scales, int* xe, int S, int ffn,
+                                    hipStream_t st) {
+  return tl::launch_swiglu_rows_q(gu, tiles, scales, xe, S, ffn, st);
+}
+hipError_t tlk_launch_residual_add(const float* y, float* h, long long n, hipStream_t st) {
+  return tl::launch_residual_add(y, h, n, st);
+}
+}  // extern "C"

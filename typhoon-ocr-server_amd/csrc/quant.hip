@@ -431,3 +431,33 @@ hipError_t launch_unpack_tiles(const uint8_t* tiles, int rows, int cols, int8_t*
 }
 
 }  // namespace tl
+
+// ---------------------------------------------------------------------------
+// C ABI of the launchers above (tl_kernels.h)
+// ---------------------------------------------------------------------------
+extern "C" {
+hipError_t tlk_launch_quantize_rows(const float* src, int8_t* dst, float* scales, int rows, int cols,
+                                    bool clamp127, hipStream_t st) {
+  return tl::launch_quantize_rows(src, dst, scales, rows, cols, clamp127, st);
+}
+hipError_t tlk_launch_quantize_rows_tiled(const float* src, int rows, int cols, uint8_t* tiles, float* scales,
+                                          bool clamp127, hipStream_t st) {
+  return tl::launch_quantize_rows_tiled(src, rows, cols, tiles, scales, clamp127, st);
+}
+hipError_t tlk_launch_pack_tiles(const int8_t* w, int rows, int cols, uint8_t* tiles, hipStream_t st) {
+  return tl::launch_pack_tiles(w, rows, cols, tiles, st);
+}
+hipError_t tlk_launch_pack_tiles_rows(const int8_t* w, int rows, int cols, int NGt, int g0, uint8_t* tiles,
+                                      hipStream_t st) {
+  return tl::launch_pack_tiles_rows(w, rows, cols, NGt, g0, tiles, st);
+}
+hipError_t tlk_launch_unpack_tiles(const uint8_t* tiles, int rows, int cols, int8_t* w, hipStream_t st) {
+  return tl::launch_unpack_tiles(tiles, rows, cols, w, st);
+}
+hipError_t tlk_launch_split_i8x4(const float* X, int ldx, int M, int K, uint8_t* tiles, int* xe, hipStream_t st) {
+  return tl::launch_split_i8x4(X, ldx, M, K, tiles, xe, st);
+}
+hipError_t tlk_launch_copy_words(const void* src, void* dst, size_t bytes, hipStream_t st) {
+  return tl::launch_copy_words(src, dst, bytes, st);
+}
+}  // extern "C"

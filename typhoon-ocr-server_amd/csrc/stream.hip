@@ -47,3 +47,8 @@ hipError_t launch_stream_read(const void* p, size_t bytes, int grid, int u, uint
 }
 
 }  // namespace tl
+
+extern "C" hipError_t tlk_launch_stream_read(const void* p, size_t bytes, int grid, int u, uint32_t* sink,
+                                             hipStream_t st) {
+  return tl::launch_stream_read(p, bytes, grid, u, sink, st);
+}
