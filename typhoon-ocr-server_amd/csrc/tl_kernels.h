@@ -1,6 +1,6 @@
 // tl_kernels.h -- the launch interface of the INT8 linear kernels: a C ABI
 // (tlk_* functions, plain structs, device pointers, asynchronous on `st`)
-// that the C host layer (api.c, decoder.c) calls, and below it, for C++
+// that the C host layer (api.c, decoder_host.c) calls, and below it, for C++
 // only, the same launchers in namespace tl as the kernel sources call each
 // other.  Each tlk_* function forwards to its tl:: counterpart in the source
 // file that defines it; no allocation, no synchronisation.
