@@ -44,17 +44,36 @@ COPY_PROBE_BYTES = 512 << 20
 TRAFFIC_SUMMARY = ROOT / "profiles" / "gemv_decode_step_traffic.md"
 
 
+# the GEMV kernel's sources: the traffic figure holds for the build it was measured on
+GEMV_SOURCES = [ROOT / "typhoon-ocr-server_amd" / "csrc" / "gemv.hip", ROOT / "typhoon-ocr-server_amd" / "csrc" / "tl_common.h"]
+
+
+def gemv_sources_sha256():
+    h = hashlib.sha256()
+    for p in GEMV_SOURCES:
+        h.update(p.read_bytes())
+    return h.hexdigest()
+
+
 def measured_traffic():
     """HBM bytes per GEMV launch measured with rocprofv3 --pmc FETCH_SIZE and
     WRITE_SIZE on `bench.py --traffic-probe` (counters scaled by what they
-    read for a 512 MiB copy), recorded in the profile summary; None if absent."""
+    read for a 512 MiB copy), recorded in the profile summary together with
+    the SHA-256 of the GEMV sources it was measured on.  Returns (bytes, note):
+    bytes is None when the summary is absent or the sources changed since."""
+    rec = {}
     try:
         for line in TRAFFIC_SUMMARY.read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch:"):
-                return float(line.split(":", 1)[1].strip())
+            if ":" in line and line.split(":", 1)[0] in ("traffic_bytes_per_launch", "gemv_sources_sha256"):
+                k, v = line.split(":", 1)
+                rec[k] = v.strip()
     except OSError:
-        pass
-    return None
+        return None, "no traffic summary"
+    if "traffic_bytes_per_launch" not in rec:
+        return None, "no traffic figure in the summary"
+    if rec.get("gemv_sources_sha256") != gemv_sources_sha256():
+        return None, "stale: the GEMV sources changed since the counters were taken"
+    return float(rec["traffic_bytes_per_launch"]), "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, same GEMV sources"
 LAYERS = 28
 LAYER_SHAPES = [("qkv", 4096, 2048), ("o", 2048, 2048), ("gate_up", 12288, 2048), ("down", 2048, 6144)]
 LM_HEAD = ("lm_head", 151936, 2048)
@@ -859,8 +878,9 @@ def main():
     avg_bytes = step_bytes / n_per_step
     avg_t = t_step / n_per_step
     achieved = avg_bytes / avg_t / 1e9
+    traffic, traffic_note = measured_traffic()
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_note,
                 "kernel": f"gemv_i8_kernel (all {n_per_step} launches of a step)",
                 "bytes_per_launch": round(avg_bytes), "avg_launch_us": round(avg_t * 1e6, 3),
                 "per_shape": per_shape}
