@@ -99,8 +99,13 @@ int tlh_pinned_ensure(PinnedBuf* b, size_t bytes) {
   }
   const size_t want = bytes < 4096 ? 4096 : bytes;
   HIP_TRY(hipHostMalloc(&b->p, want, hipHostMallocDefault));
+  const hipError_t e = hipHostGetDevicePointer(&b->dp, b->p, 0);
+  if (e != hipSuccess) {   /* never leave a buffer without its device mapping */
+    (void)hipHostFree(b->p);
+    b->p = b->dp = NULL;
+    return tlh_fail_hip("hipHostGetDevicePointer", e);
+  }
   b->n = want;
-  HIP_TRY(hipHostGetDevicePointer(&b->dp, b->p, 0));
   return 0;
 }
 
@@ -203,13 +208,18 @@ typedef struct Workspace {
   DevBuf xn;         /* normalised hidden row (lm_head argmax) */
   DevBuf keys;       /* per-work-group argmax keys */
   DevBuf planes;     /* W8A32 batches: int8 plane tiles of the fp32 rows and their exponents */
+  pthread_mutex_t mu;   /* held by one operation from its first buffer use to its last launch */
   struct Workspace* next;
 } Workspace;
 
 static pthread_mutex_t g_ws_mu = PTHREAD_MUTEX_INITIALIZER;
 static Workspace* g_ws = NULL;
 
-static int workspace(int dev, hipStream_t st, Workspace** out) {
+/* The work-space of (dev, st), returned locked: threads that enqueue on the
+ * same stream (the null stream, say) take turns, so one never grows or frees
+ * a buffer that another has just bound into its launches.  The caller unlocks
+ * it after its last launch. */
+static int workspace_lock(int dev, hipStream_t st, Workspace** out) {
   pthread_mutex_lock(&g_ws_mu);
   Workspace* w = g_ws;
   while (w && !(w->dev == dev && w->st == st)) w = w->next;
@@ -218,15 +228,26 @@ static int workspace(int dev, hipStream_t st, Workspace** out) {
     if (w) {
       w->dev = dev;
       w->st = st;
+      pthread_mutex_init(&w->mu, NULL);
       w->next = g_ws;
       g_ws = w;
     }
   }
   pthread_mutex_unlock(&g_ws_mu);
   REQ(w, "out of host memory");
+  pthread_mutex_lock(&w->mu);
   *out = w;
   return 0;
 }
+
+#define WS_CALL(dev, st, call)               \
+  do {                                       \
+    Workspace* ws_;                          \
+    TRY(workspace_lock((dev), (st), &ws_));  \
+    const int rc_ = call;                    \
+    pthread_mutex_unlock(&ws_->mu);          \
+    return rc_;                              \
+  } while (0)
 
 static int ensure_counters(Workspace* w, size_t n, hipStream_t st, uint32_t** out) {
   if (n > w->cnt_n) {
@@ -595,9 +616,7 @@ static int run_rows(Workspace* ws, GemmLaunch* L, hipStream_t st, bool* done) {
   return 0;
 }
 
-static int op_w8a32(const float* X, const tl_weights* W, const float* bias, float* Y, int batch, hipStream_t st) {
-  Workspace* ws;
-  TRY(workspace(W->dev, st, &ws));
+static int op_w8a32_ws(Workspace* ws, const float* X, const tl_weights* W, const float* bias, float* Y, int batch, hipStream_t st) {
   if (batch == 1) {
     GemvLaunch L = tlk_gemv_launch_init();
     L.wt = W->tiles;
@@ -679,11 +698,13 @@ static int op_w8a32(const float* X, const tl_weights* W, const float* bias, floa
   return run_gemm(ws, &P, st);
 }
 
+static int op_w8a32(const float* X, const tl_weights* W, const float* bias, float* Y, int batch, hipStream_t st) {
+  WS_CALL(W->dev, st, op_w8a32_ws(ws_, X, W, bias, Y, batch, st));
+}
+
 /* W8A8 on row-major device codes */
-static int op_w8a8_codes(const int8_t* xq, const float* xs, const tl_weights* W, const float* bias, void* Y, int out,
+static int op_w8a8_codes_ws(Workspace* ws, const int8_t* xq, const float* xs, const tl_weights* W, const float* bias, void* Y, int out,
                          int batch, hipStream_t st) {
-  Workspace* ws;
-  TRY(workspace(W->dev, st, &ws));
   const int K = W->cols, KB = W->KB;
   if (batch == 1 && out != OUT_I32) {
     /* codes must be zero padded to KB*64 for the GEMV */
@@ -723,11 +744,14 @@ static int op_w8a8_codes(const int8_t* xq, const float* xs, const tl_weights* W,
   return run_gemm(ws, &L, st);
 }
 
+static int op_w8a8_codes(const int8_t* xq, const float* xs, const tl_weights* W, const float* bias, void* Y, int out,
+                         int batch, hipStream_t st) {
+  WS_CALL(W->dev, st, op_w8a8_codes_ws(ws_, xq, xs, W, bias, Y, out, batch, st));
+}
+
 /* per-token int8 activations of fp32 X (the GEMV quantizes inside its
  * prologue at batch 1), int8 GEMM, fp32 out */
-static int op_w8a8_f32(const float* X, const tl_weights* W, const float* bias, float* Y, int batch, hipStream_t st) {
-  Workspace* ws;
-  TRY(workspace(W->dev, st, &ws));
+static int op_w8a8_f32_ws(Workspace* ws, const float* X, const tl_weights* W, const float* bias, float* Y, int batch, hipStream_t st) {
   if (batch == 1) {
     GemvLaunch L = tlk_gemv_launch_init();
     L.wt = W->tiles;
@@ -769,12 +793,14 @@ static int op_w8a8_f32(const float* X, const tl_weights* W, const float* bias, f
   return run_gemm(ws, &L, st);
 }
 
-static int op_w8a16(const void* X, int x_type, const tl_weights* W, const float* bias, void* Y, int y_type, int batch,
+static int op_w8a8_f32(const float* X, const tl_weights* W, const float* bias, float* Y, int batch, hipStream_t st) {
+  WS_CALL(W->dev, st, op_w8a8_f32_ws(ws_, X, W, bias, Y, batch, st));
+}
+
+static int op_w8a16_ws(Workspace* ws, const void* X, int x_type, const tl_weights* W, const float* bias, void* Y, int y_type, int batch,
                     hipStream_t st) {
   REQ(x_type == TL_BF16 || x_type == TL_F16, "x_type must be TL_BF16 or TL_F16");
   REQ(y_type == TL_F32 || y_type == TL_BF16 || y_type == TL_F16, "bad y_type");
-  Workspace* ws;
-  TRY(workspace(W->dev, st, &ws));
   GemmLaunch L = tlk_gemm_launch_init();
   L.amode = (x_type == TL_BF16) ? A_BF16 : A_F16;
   L.A = X;
@@ -812,6 +838,11 @@ static int op_w8a16(const void* X, int x_type, const tl_weights* W, const float*
   return run_gemm(ws, &L, st);
 }
 
+static int op_w8a16(const void* X, int x_type, const tl_weights* W, const float* bias, void* Y, int y_type, int batch,
+                    hipStream_t st) {
+  WS_CALL(W->dev, st, op_w8a16_ws(ws_, X, x_type, W, bias, Y, y_type, batch, st));
+}
+
 int tlh_linear_w8a32(const float* X, const tl_weights* W, const float* bias, float* Y, int batch, hipStream_t st) {
   return op_w8a32(X, W, bias, Y, batch, st);
 }
@@ -820,10 +851,8 @@ int tlh_linear_w8a8(const float* X, const tl_weights* W, const float* bias, floa
   return op_w8a8_f32(X, W, bias, Y, batch, st);
 }
 
-int tlh_linear_w8a32_planes(const uint8_t* tiles, const int* xe, const tl_weights* W, float* Y, int batch,
+static int linear_w8a32_planes_ws(Workspace* ws, const uint8_t* tiles, const int* xe, const tl_weights* W, float* Y, int batch,
                             hipStream_t st) {
-  Workspace* ws;
-  TRY(workspace(W->dev, st, &ws));
   GemmLaunch L = tlk_gemm_launch_init();
   L.amode = A_I8;
   L.A = tiles;
@@ -839,10 +868,13 @@ int tlh_linear_w8a32_planes(const uint8_t* tiles, const int* xe, const tl_weight
   return run_gemm(ws, &L, st);
 }
 
-int tlh_linear_w8a8_tiles(const uint8_t* tiles, const float* xs, const tl_weights* W, float* Y, int batch,
+int tlh_linear_w8a32_planes(const uint8_t* tiles, const int* xe, const tl_weights* W, float* Y, int batch,
+                            hipStream_t st) {
+  WS_CALL(W->dev, st, linear_w8a32_planes_ws(ws_, tiles, xe, W, Y, batch, st));
+}
+
+static int linear_w8a8_tiles_ws(Workspace* ws, const uint8_t* tiles, const float* xs, const tl_weights* W, float* Y, int batch,
                           hipStream_t st) {
-  Workspace* ws;
-  TRY(workspace(W->dev, st, &ws));
   GemmLaunch L = tlk_gemm_launch_init();
   L.amode = A_I8;
   L.A = tiles;
@@ -856,6 +888,11 @@ int tlh_linear_w8a8_tiles(const uint8_t* tiles, const float* xs, const tl_weight
   L.K = W->cols;
   L.out = OUT_F32;
   return run_gemm(ws, &L, st);
+}
+
+int tlh_linear_w8a8_tiles(const uint8_t* tiles, const float* xs, const tl_weights* W, float* Y, int batch,
+                          hipStream_t st) {
+  WS_CALL(W->dev, st, linear_w8a8_tiles_ws(ws_, tiles, xs, W, Y, batch, st));
 }
 
 /* Quantizes rows of host fp32 on the GPU and returns codes and scales to the
@@ -1501,13 +1538,16 @@ static int lm_head_argmax_enqueue(const float* h, const float* norm_w, const tl_
   return 0;
 }
 
-static int op_lm_head_argmax(const float* h, const float* norm_w, const tl_weights* W, float* logits, int32_t* token,
+static int op_lm_head_argmax_ws(Workspace* ws, const float* h, const float* norm_w, const tl_weights* W, float* logits, int32_t* token,
                              float* max_logit, hipStream_t st) {
-  Workspace* ws;
-  TRY(workspace(W->dev, st, &ws));
   TRY(tlh_devbuf_ensure(&ws->keys, lm_head_argmax_keys(W->rows, W->cols) * sizeof(uint64_t), st));
   TRY(tlh_devbuf_ensure(&ws->xn, (size_t)W->cols * sizeof(float), st));
   return lm_head_argmax_enqueue(h, norm_w, W, logits, token, max_logit, (uint64_t*)ws->keys.p, (float*)ws->xn.p, st);
+}
+
+static int op_lm_head_argmax(const float* h, const float* norm_w, const tl_weights* W, float* logits, int32_t* token,
+                             float* max_logit, hipStream_t st) {
+  WS_CALL(W->dev, st, op_lm_head_argmax_ws(ws_, h, norm_w, W, logits, token, max_logit, st));
 }
 
 static int lm_head_argmax_dev_impl(const float* h, const float* norm_w, const tl_weights* W, float* logits,
