@@ -206,51 +206,57 @@ __global__ __launch_bounds__(256) void swiglu_rows_q_kernel(const float* __restr
   quantize_row_to_tiles<NV, PLANES>(y, ffn >> 2, (int)t, MG, tiles, scales, xe, s_mx);
 }
 
-// Work-group (t, h): token t, kv head h.  q heads 2h, 2h+1 (RMSNorm with
-// q_norm, rotation, written back in place in qkv), k head h (k_norm,
-// rotation) and v head h to cache row `row0 + t`.  The rotation uses row t of
-// cos / sin (the caller points them at the token's first row).
+// One wave per 128-wide head vector of a token: the token's nq = 2 nkv q
+// heads (RMSNorm with q_norm, rotation, written back in place in qkv), then
+// its nkv kv heads (k: k_norm and rotation to cache row `row0 + t`; v copied
+// there), so 3 nkv waves per token and no work-group barrier.  Lane l holds
+// elements l and l + 64, the two halves the rotation pairs: the squares of
+// each half are summed by a butterfly over the wave and the halves added low
+// half first (the order of the decode attention kernel's two-wave sum).  The
+// rotation uses row t of cos / sin (the caller points them at the token's
+// first row).
 __global__ __launch_bounds__(256) void prefill_qk_kernel(float* __restrict__ qkv, const float* __restrict__ q_norm,
                                                          const float* __restrict__ k_norm, const float* __restrict__ cos_t,
                                                          const float* __restrict__ sin_t, float* __restrict__ kc,
-                                                         float* __restrict__ vc, int max_seq, int row0, float eps) {
-  const int t = blockIdx.x, h = blockIdx.y;
-  const int tid = threadIdx.x, g = tid >> 7, d = tid & 127, lane = tid & 63, wv = tid >> 6;
-  __shared__ float s_x[2][PHD], s_xk[PHD], s_red[8];
+                                                         float* __restrict__ vc, int max_seq, int row0, int S, int nkv,
+                                                         float eps) {
+  const int lane = threadIdx.x & 63;
+  const int unit = blockIdx.x * 4 + (threadIdx.x >> 6);   // uniform per wave
+  const int per_tok = 3 * nkv;
+  const int t = unit / per_tok, k = unit - t * per_tok;
+  if (t >= S) return;
   float* row = qkv + (size_t)t * 4096;
-  const float qraw = row[(2 * h + g) * PHD + d];
-  const float kvraw = row[2048 + (g == 0 ? h * PHD : 1024 + h * PHD) + d];
-  const float qw = q_norm[d], kw = k_norm[d];
-  const int j = d & 63;
-  const float co = cos_t[(size_t)t * 64 + j], si = sin_t[(size_t)t * 64 + j];
-  float sq = __fmul_rn(qraw, qraw), sk = __fmul_rn(kvraw, kvraw);
+  const bool is_q = k < 2 * nkv;
+  const int h = is_q ? k : k - 2 * nkv;                     // q head, or kv head
+  const float* src = row + (is_q ? h * PHD : 2048 + h * PHD);
+  const float* nw = is_q ? q_norm : k_norm;
+  const float xl = src[lane], xh = src[lane + 64];
+  const float wl = nw[lane], wh = nw[lane + 64];
+  const float co = cos_t[(size_t)t * 64 + lane], si = sin_t[(size_t)t * 64 + lane];
+  float vl = 0.f, vh = 0.f;
+  if (!is_q) {
+    vl = row[3072 + h * PHD + lane];
+    vh = row[3072 + h * PHD + lane + 64];
+  }
+  float sl = __fmul_rn(xl, xl), sh = __fmul_rn(xh, xh);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
-    sq = __fadd_rn(sq, __shfl_xor(sq, o, 64));
-    sk = __fadd_rn(sk, __shfl_xor(sk, o, 64));
+    sl = __fadd_rn(sl, __shfl_xor(sl, o, 64));
+    sh = __fadd_rn(sh, __shfl_xor(sh, o, 64));
   }
-  if (lane == 0) {
-    s_red[wv] = sq;
-    s_red[4 + wv] = sk;
-  }
-  __syncthreads();
-  const int w0 = wv & ~1;
-  const float rq = ref_rsqrt(__fadd_rn(__fdiv_rn(__fadd_rn(s_red[w0], s_red[w0 + 1]), (float)PHD), eps));
-  s_x[g][d] = __fmul_rn(__fmul_rn(qraw, rq), qw);
-  if (g == 0) {
-    const float rk = ref_rsqrt(__fadd_rn(__fdiv_rn(__fadd_rn(s_red[4], s_red[5]), (float)PHD), eps));
-    s_xk[d] = __fmul_rn(__fmul_rn(kvraw, rk), kw);
-  }
-  __syncthreads();
-  const float lo = s_x[g][j], hi = s_x[g][j + 64];
-  row[(2 * h + g) * PHD + d] =
-      d < 64 ? __fsub_rn(__fmul_rn(lo, co), __fmul_rn(hi, si)) : __fadd_rn(__fmul_rn(hi, co), __fmul_rn(lo, si));
-  const size_t off = ((size_t)h * max_seq + row0 + t) * PHD + d;
-  if (g == 0) {
-    const float klo = s_xk[j], khi = s_xk[j + 64];
-    kc[off] = d < 64 ? __fsub_rn(__fmul_rn(klo, co), __fmul_rn(khi, si)) : __fadd_rn(__fmul_rn(khi, co), __fmul_rn(klo, si));
+  const float r = ref_rsqrt(__fadd_rn(__fdiv_rn(__fadd_rn(sl, sh), (float)PHD), eps));
+  const float nl = __fmul_rn(__fmul_rn(xl, r), wl), nh = __fmul_rn(__fmul_rn(xh, r), wh);
+  const float ol = __fsub_rn(__fmul_rn(nl, co), __fmul_rn(nh, si));
+  const float oh = __fadd_rn(__fmul_rn(nh, co), __fmul_rn(nl, si));
+  if (is_q) {
+    row[h * PHD + lane] = ol;
+    row[h * PHD + lane + 64] = oh;
   } else {
-    vc[off] = kvraw;
+    const size_t off = ((size_t)h * max_seq + row0 + t) * PHD;
+    kc[off + lane] = ol;
+    kc[off + lane + 64] = oh;
+    vc[off + lane] = vl;
+    vc[off + lane + 64] = vh;
   }
 }
 
@@ -596,9 +602,10 @@ hipError_t launch_swiglu_rows_q(const float* gu, uint8_t* tiles, float* scales, 
 hipError_t launch_prefill_qk(float* qkv, const float* q_norm, const float* k_norm, const float* cos_t,
                              const float* sin_t, float* kc, float* vc, int max_seq, int row0, int S, int nkv,
                              float eps, hipStream_t st) {
-  if (S < 1 || row0 < 0 || row0 + S > max_seq) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(prefill_qk_kernel, dim3(S, nkv), dim3(256), 0, st, qkv, q_norm, k_norm, cos_t, sin_t, kc, vc,
-                     max_seq, row0, eps);
+  if (S < 1 || row0 < 0 || row0 + S > max_seq || nkv != 8) return hipErrorInvalidValue;   // rows of 4096: 16 q + 8 k + 8 v heads
+  const long long waves = (long long)S * 3 * nkv;
+  hipLaunchKernelGGL(prefill_qk_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, qkv, q_norm, k_norm,
+                     cos_t, sin_t, kc, vc, max_seq, row0, S, nkv, eps);
   return hipGetLastError();
 }
 
