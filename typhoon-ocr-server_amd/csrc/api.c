@@ -681,7 +681,10 @@ static int op_w8a32_ws(Workspace* ws, const float* X, const tl_weights* W, const
   TRY(tlh_devbuf_ensure(&ws->planes, xe_off + (size_t)batch * sizeof(int), st));
   uint8_t* tiles = (uint8_t*)ws->planes.p;
   int* xe = (int*)(tiles + xe_off);
-  HIP_TRY(tlk_launch_split_i8x4(X, K, batch, K, tiles, xe, st));
+  /* one work-group per row where the shape allows it (the same planes) */
+  const bool by_rows = (K == 1024 || K == 2048 || K == 4096 || K == 6144) && (((uintptr_t)X) & 15) == 0;
+  if (by_rows) HIP_TRY(tlk_launch_split_rows_planes(X, K, batch, K, tiles, xe, st));
+  else HIP_TRY(tlk_launch_split_i8x4(X, K, batch, K, tiles, xe, st));
   GemmLaunch P = tlk_gemm_launch_init();
   P.amode = A_I8;
   P.A = tiles;

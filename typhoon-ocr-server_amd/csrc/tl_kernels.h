@@ -145,6 +145,11 @@ hipError_t tlk_launch_swiglu_rows(const float* gu, float* mlp, int S, int ffn, h
 //           row groups) and exponents of launch_split_i8x4, bit for bit
 hipError_t tlk_launch_rmsnorm_rows_q(const float* x, const float* w, uint8_t* tiles, float* scales, int* xe,
                                      int rows, int K, float eps, hipStream_t st);
+// the result of tlk_launch_split_i8x4 with one work-group per row, for
+// K = 1024, 2048, 4096 or 6144 and 16-byte aligned rows (else
+// hipErrorInvalidValue)
+hipError_t tlk_launch_split_rows_planes(const float* x, int ldx, int rows, int K, uint8_t* tiles, int* xe,
+                                        hipStream_t st);
 hipError_t tlk_launch_swiglu_rows_q(const float* gu, uint8_t* tiles, float* scales, int* xe, int S, int ffn,
                                     hipStream_t st);
 hipError_t tlk_launch_residual_add(const float* y, float* h, long long n, hipStream_t st);
@@ -286,6 +291,8 @@ hipError_t launch_flash_prefill(const float* qkv, const float* kc, const float* 
                                 int max_seq, int key0, int qoff, float scale, float* part, int* cnt,
                                 hipStream_t st);
 hipError_t launch_swiglu_rows(const float* gu, float* mlp, int S, int ffn, hipStream_t st);
+hipError_t launch_split_rows_planes(const float* x, int ldx, int rows, int K, uint8_t* tiles, int* xe,
+                                    hipStream_t st);
 hipError_t launch_rmsnorm_rows_q(const float* x, const float* w, uint8_t* tiles, float* scales, int* xe, int rows,
                                  int K, float eps, hipStream_t st);
 hipError_t launch_swiglu_rows_q(const float* gu, uint8_t* tiles, float* scales, int* xe, int S, int ffn,
