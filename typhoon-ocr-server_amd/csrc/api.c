@@ -779,7 +779,14 @@ static int op_w8a8_f32_ws(Workspace* ws, const float* X, const tl_weights* W, co
   const int MG = tlk_cdiv(batch, 16);
   TRY(tlh_devbuf_ensure(&ws->act, (size_t)MG * W->KB * 1024, st));
   TRY(tlh_devbuf_ensure(&ws->act_s, (size_t)MG * 16 * sizeof(float), st));
-  HIP_TRY(tlk_launch_quantize_rows_tiled(X, batch, W->cols, (uint8_t*)ws->act.p, (float*)ws->act_s.p, true, st));
+  {
+    const int K = W->cols;
+    const bool by_rows = (K == 1024 || K == 2048 || K == 4096 || K == 6144) && (((uintptr_t)X) & 15) == 0;
+    if (by_rows)
+      HIP_TRY(tlk_launch_quantize_rows_by_row(X, batch, K, (uint8_t*)ws->act.p, (float*)ws->act_s.p, st));
+    else
+      HIP_TRY(tlk_launch_quantize_rows_tiled(X, batch, K, (uint8_t*)ws->act.p, (float*)ws->act_s.p, true, st));
+  }
   GemmLaunch L = tlk_gemm_launch_init();
   L.amode = A_I8;
   L.A = ws->act.p;

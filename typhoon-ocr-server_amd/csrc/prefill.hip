@@ -165,10 +165,12 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_q_kernel(const float* __rest
 // result, quant.hip), one work-group per row: the row is loaded once into
 // registers (float4 tid + 256 j) and quantize_row_to_tiles writes the planes,
 // where split_i8x4_kernel makes one wave walk the row twice.  K = 1024 NV.
-template <int NV>
+// PLANES false: the W8A8 per-token codes and scales instead
+// (quantize_rows_tiled's result).
+template <int NV, bool PLANES>
 __global__ __launch_bounds__(256) void split_rows_planes_kernel(const float* __restrict__ x, int ldx, int rows,
                                                                 int MG, uint8_t* __restrict__ tiles,
-                                                                int* __restrict__ xe) {
+                                                                float* __restrict__ scales, int* __restrict__ xe) {
   __shared__ uint32_t s_mx[4];
   const int rr = xcd_grouped_row(blockIdx.x);
   if (rr >= rows) return;                   // the whole work-group
@@ -176,7 +178,7 @@ __global__ __launch_bounds__(256) void split_rows_planes_kernel(const float* __r
   float4 v[NV];
 #pragma unroll
   for (int j = 0; j < NV; j++) v[j] = xr[threadIdx.x + 256 * j];
-  quantize_row_to_tiles<NV, true>(v, 256 * NV, rr, MG, tiles, nullptr, xe, s_mx);
+  quantize_row_to_tiles<NV, PLANES>(v, 256 * NV, rr, MG, tiles, scales, xe, s_mx);
 }
 
 // SwiGLU of one token's interleaved gate/up row (the values of
@@ -599,19 +601,30 @@ hipError_t launch_rmsnorm_rows_q(const float* x, const float* w, uint8_t* tiles,
   return hipGetLastError();
 }
 
-hipError_t launch_split_rows_planes(const float* x, int ldx, int rows, int K, uint8_t* tiles, int* xe,
-                                    hipStream_t st) {
+template <bool PLANES>
+static hipError_t launch_rows_q(const float* x, int ldx, int rows, int K, uint8_t* tiles, float* scales, int* xe,
+                                hipStream_t st) {
   if (rows < 1 || ldx < K || ldx % 4 != 0 || (((uintptr_t)x) & 15) != 0) return hipErrorInvalidValue;
   const dim3 grid(cdiv(rows, 64) * 64);     // xcd_grouped_row: whole groups of 64 rows
-  const int MG = cdiv(4 * rows, 16);
+  const int MG = cdiv(PLANES ? 4 * rows : rows, 16);
   switch (K) {
-    case 1024: hipLaunchKernelGGL(split_rows_planes_kernel<1>, grid, dim3(256), 0, st, x, ldx, rows, MG, tiles, xe); break;
-    case 2048: hipLaunchKernelGGL(split_rows_planes_kernel<2>, grid, dim3(256), 0, st, x, ldx, rows, MG, tiles, xe); break;
-    case 4096: hipLaunchKernelGGL(split_rows_planes_kernel<4>, grid, dim3(256), 0, st, x, ldx, rows, MG, tiles, xe); break;
-    case 6144: hipLaunchKernelGGL(split_rows_planes_kernel<6>, grid, dim3(256), 0, st, x, ldx, rows, MG, tiles, xe); break;
+    case 1024: hipLaunchKernelGGL((split_rows_planes_kernel<1, PLANES>), grid, dim3(256), 0, st, x, ldx, rows, MG, tiles, scales, xe); break;
+    case 2048: hipLaunchKernelGGL((split_rows_planes_kernel<2, PLANES>), grid, dim3(256), 0, st, x, ldx, rows, MG, tiles, scales, xe); break;
+    case 4096: hipLaunchKernelGGL((split_rows_planes_kernel<4, PLANES>), grid, dim3(256), 0, st, x, ldx, rows, MG, tiles, scales, xe); break;
+    case 6144: hipLaunchKernelGGL((split_rows_planes_kernel<6, PLANES>), grid, dim3(256), 0, st, x, ldx, rows, MG, tiles, scales, xe); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+hipError_t launch_split_rows_planes(const float* x, int ldx, int rows, int K, uint8_t* tiles, int* xe,
+                                    hipStream_t st) {
+  return launch_rows_q<true>(x, ldx, rows, K, tiles, nullptr, xe, st);
+}
+
+hipError_t launch_quantize_rows_by_row(const float* x, int rows, int K, uint8_t* tiles, float* scales,
+                                       hipStream_t st) {
+  return launch_rows_q<false>(x, K, rows, K, tiles, scales, nullptr, st);
 }
 
 hipError_t launch_swiglu_rows_q(const float* gu, uint8_t* tiles, float* scales, int* xe, int S, int ffn,
@@ -732,6 +745,10 @@ hipError_t tlk_launch_swiglu_rows(const float* gu, float* mlp, int S, int ffn, h
 hipError_t tlk_launch_split_rows_planes(const float* x, int ldx, int rows, int K, uint8_t* tiles, int* xe,
                                         hipStream_t st) {
   return tl::launch_split_rows_planes(x, ldx, rows, K, tiles, xe, st);
+}
+hipError_t tlk_launch_quantize_rows_by_row(const float* x, int rows, int K, uint8_t* tiles, float* scales,
+                                           hipStream_t st) {
+  return tl::launch_quantize_rows_by_row(x, rows, K, tiles, scales, st);
 }
 hipError_t tlk_launch_rmsnorm_rows_q(const float* x, const float* w, uint8_t* tiles, float* scales, int* xe,
                                      int rows, int K, float eps, hipStream_t st) {

@@ -150,6 +150,10 @@ hipError_t tlk_launch_rmsnorm_rows_q(const float* x, const float* w, uint8_t* ti
 // hipErrorInvalidValue)
 hipError_t tlk_launch_split_rows_planes(const float* x, int ldx, int rows, int K, uint8_t* tiles, int* xe,
                                         hipStream_t st);
+// the result of tlk_launch_quantize_rows_tiled (clamp127) with one
+// work-group per row, for the same K and alignment
+hipError_t tlk_launch_quantize_rows_by_row(const float* x, int rows, int K, uint8_t* tiles, float* scales,
+                                           hipStream_t st);
 hipError_t tlk_launch_swiglu_rows_q(const float* gu, uint8_t* tiles, float* scales, int* xe, int S, int ffn,
                                     hipStream_t st);
 hipError_t tlk_launch_residual_add(const float* y, float* h, long long n, hipStream_t st);
@@ -293,6 +297,8 @@ hipError_t launch_flash_prefill(const float* qkv, const float* kc, const float* 
 hipError_t launch_swiglu_rows(const float* gu, float* mlp, int S, int ffn, hipStream_t st);
 hipError_t launch_split_rows_planes(const float* x, int ldx, int rows, int K, uint8_t* tiles, int* xe,
                                     hipStream_t st);
+hipError_t launch_quantize_rows_by_row(const float* x, int rows, int K, uint8_t* tiles, float* scales,
+                                       hipStream_t st);
 hipError_t launch_rmsnorm_rows_q(const float* x, const float* w, uint8_t* tiles, float* scales, int* xe, int rows,
                                  int K, float eps, hipStream_t st);
 hipError_t launch_swiglu_rows_q(const float* gu, uint8_t* tiles, float* scales, int* xe, int S, int ffn,
