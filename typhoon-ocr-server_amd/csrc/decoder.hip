@@ -243,33 +243,48 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   // out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c, M = max_c m_c, in
   // chunk order over rounds of kMergeRound chunks (one round up to 2048
   // positions at 64 per chunk), each round rescaling the earlier ones
+  // The round's maximum and the chunk weights e^(m_c - M) are made once per
+  // chunk (lane c of the wave that loaded the m values) and shared through
+  // LDS; every thread then folds them in chunk order (the values and the
+  // order of the sequential fold, without its serial exponentials).
   __shared__ float s_w[2][2][kMergeRound];  // m and l of q heads 2h, 2h + 1
+  __shared__ float s_e[2][kMergeRound + 1]; // e^(m_c - M) of the round, then e^(M_prev - M)
+  __shared__ float s_mb[2];                 // the running maximum M of each q head
   const int wg = wv >> 1, ww = wv & 1;      // wave: q head 2h + wg, word ww (m or l)
   const float* src_w = (ww == 0 ? a.pm : a.pl) + (size_t)(2 * h + wg) * a.C;
   float M = -3.0e38f, L = 0.0f, acc = 0.0f;
   for (int c0 = 0; c0 < nc; c0 += kMergeRound) {
-    if (lane < kMergeRound) s_w[wg][ww][lane] = ld_agent(src_w + min(c0 + lane, nc - 1));
+    float wm = -3.0e38f;                    // this lane's m (wave ww == 0 of head wg)
+    if (lane < kMergeRound) {
+      wm = ld_agent(src_w + min(c0 + lane, nc - 1));
+      s_w[wg][ww][lane] = wm;
+    }
     float v[kMergeRound];
 #pragma unroll
     for (int i = 0; i < kMergeRound; i++) v[i] = ld_agent(a.po + ((size_t)qh * a.C + min(c0 + i, nc - 1)) * HD + d);
+    if (ww == 0) {                          // wave-uniform: the wave holding the m values
+      const float mb = fmaxf(M, wave_fmax(lane < kMergeRound && c0 + lane < nc ? wm : -3.0e38f));
+      if (lane < kMergeRound) s_e[wg][lane] = expf(__fsub_rn(wm, mb));
+      if (lane == 0) {
+        s_e[wg][kMergeRound] = expf(__fsub_rn(M, mb));
+        s_mb[wg] = mb;
+      }
+    }
     __syncthreads();
-    float Mb = M;
-#pragma unroll
-    for (int i = 0; i < kMergeRound; i++)
-      if (c0 + i < nc) Mb = fmaxf(Mb, s_w[g][0][i]);
-    const float r = expf(__fsub_rn(M, Mb));
+    const float Mb = s_mb[g];
+    const float r = s_e[g][kMergeRound];
     L = __fmul_rn(L, r);
     acc = __fmul_rn(acc, r);
 #pragma unroll
     for (int i = 0; i < kMergeRound; i++) {
       if (c0 + i < nc) {
-        const float w = expf(__fsub_rn(s_w[g][0][i], Mb));
+        const float w = s_e[g][i];
         L = __fmaf_rn(w, s_w[g][1][i], L);
         acc = __fmaf_rn(w, v[i], acc);
       }
     }
     M = Mb;
-    __syncthreads();                        // s_w is rewritten by the next round
+    __syncthreads();                        // s_w and s_e are rewritten by the next round
   }
   a.out[qh * HD + d] = __fmul_rn(acc, __fdiv_rn(1.0f, L));
   if (tid == 0) __hip_atomic_store(a.count + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
