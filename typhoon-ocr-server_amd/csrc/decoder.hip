@@ -299,7 +299,24 @@ __global__ __launch_bounds__(1024) void step_end_kernel(const uint64_t* __restri
   __shared__ uint64_t s_k[16];
   __shared__ int s_tok;
   uint64_t k = 0;
-  for (int i = threadIdx.x; i < n; i += 1024) k = keys[i] > k ? keys[i] : k;
+  // keys in pairs, eight 16-byte loads in flight per thread (the keys buffer
+  // is 16-byte aligned); an odd last key separately
+  const int n2 = n >> 1;
+  const ulonglong2* k2 = reinterpret_cast<const ulonglong2*>(keys);
+  for (int i0 = threadIdx.x; i0 < n2; i0 += 1024 * 8) {
+    ulonglong2 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int i = i0 + 1024 * u;
+      v[u] = i < n2 ? k2[i] : make_ulonglong2(0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      k = v[u].x > k ? v[u].x : k;
+      k = v[u].y > k ? v[u].y : k;
+    }
+  }
+  if ((n & 1) && threadIdx.x == 0) k = keys[n - 1] > k ? keys[n - 1] : k;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const uint64_t t = __shfl_xor(k, o, 64);
@@ -352,6 +369,7 @@ hipError_t launch_attn_decode(const AttnDecodeArgs& a, hipStream_t st) {
 
 hipError_t launch_step_end(const uint64_t* keys, int n, const float* embed, int H, float* hidden, int* state,
                            int32_t* tokens, int max_tokens, hipStream_t st) {
+  if (n < 1 || (((uintptr_t)keys) & 15) != 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(step_end_kernel, dim3(1), dim3(1024), 0, st, keys, n, embed, H, hidden, state, tokens,
                      max_tokens);
   return hipGetLastError();
