@@ -412,7 +412,11 @@ __device__ __forceinline__ float arm_frecpe(float x) {
   const uint32_t u = __float_as_uint(x);
   const int e = (int)((u >> 23) & 0xff);
   const uint32_t a = 2u * (256u + ((u & 0x7fffffu) >> 15)) + 1u;   // midpoint, units of 1/1024
-  uint32_t b = (uint32_t)(524288.0f / (float)a);                     // floor(2^19 / a), fixed below
+  // floor(2^19 / a) from the hardware reciprocal: for odd a in [513, 1023]
+  // the quotient's fraction is at least 1/a, far above the product's error
+  // (< 2e-4), so the truncation is the floor (the two checks below keep it
+  // exact regardless)
+  uint32_t b = (uint32_t)(524288.0f * __builtin_amdgcn_rcpf((float)a));
   if (b * a > 524288u) b--;
   if ((b + 1u) * a <= 524288u) b++;
   const uint32_t est = ((b + 1u) >> 1) & 0xffu;
