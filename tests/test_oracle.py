@@ -338,3 +338,16 @@ def test_cpu_baseline_gemms_match_checker(orc, M, N, K):
             assert rel(orc.base_w8a16_linear(xb, w, s, 3, native, bias), orc.w8a16_linear(xb, w, s, bias=bias)) <= 1e-5
             assert rel(orc.base_w8a16_linear(xb[:1], w, s, 3, native, bias),
                        orc.w8a16_linear(xb[:1], w, s, bias=bias)) <= 1e-5
+
+
+def test_frecpe_quotient_from_any_faithful_reciprocal():
+    """The device restatement of FRECPE takes floor(2^19 / a), for the odd
+    a = 2 (256 + m) + 1 in [513, 1023] that the estimate's eight mantissa
+    bits give, as trunc(2^19 * rcp(a)) with the hardware reciprocal, which is
+    within one ulp of 1/a.  Every float within one ulp of 1/a, scaled by 2^19
+    (exact), truncates to the same integer as the integer quotient: the
+    quotient's fraction is at least 1/a, far above the scaled error."""
+    for a in range(513, 1024, 2):
+        r = np.float32(1.0) / np.float32(a)           # correctly rounded 1/a
+        for rr in (np.nextafter(r, np.float32(0)), r, np.nextafter(r, np.float32(1))):
+            assert int(np.float32(524288.0) * rr) == 524288 // a, a
