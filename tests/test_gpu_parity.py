@@ -247,7 +247,9 @@ def test_registry_detects_in_place_update(lin, orc):
 # W8A32 batch > 1 (fp32 semantics)
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("M,N,K", [(2, 2048, 2048), (4, 6144, 2048), (8, 2048, 6144), (3, 100, 70),
-                                   (17, 512, 2048), (64, 1024, 2048), (200, 4096, 2048)])
+                                   (17, 512, 2048), (64, 1024, 2048), (200, 4096, 2048),
+                                   # the row-wise plane split's other widths (K = 1024 NV)
+                                   (40, 300, 1024), (70, 256, 4096), (33, 130, 6144)])
 def test_w8a32_batch_fp32(lin, orc, M, N, K):
     say(f"w8a32 batch M={M} N={N} K={K}")
     rng = np.random.default_rng(M * 13 + N + K)
@@ -452,7 +454,9 @@ def test_w8a8_m1_bit_exact(lin, orc, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(2, 512, 2048), (16, 6144, 2048), (100, 2048, 6144), (256, 6144, 2048),
-                                   (45, 130, 300)])
+                                   (45, 130, 300),
+                                   # the row-wise per-token quantizer's other widths
+                                   (40, 300, 1024), (70, 256, 4096)])
 def test_w8a8_gemm(lin, orc, dev, M, N, K):
     import torch
     say(f"w8a8 gemm M={M} N={N} K={K}")
