@@ -4,11 +4,13 @@ Workload (the metric's configuration; a "step" = W8A32 batch==1 GEMVs):
   the decode projection set of one Qwen3-VL-2B text layer plus the lm_head,
   QKV 4096x2048, O 2048x2048, gate_up 12288x2048, down 2048x6144, lm_head
   151936x2048 (361.5 MB of int8 weights and scales), per-row fp32 scales,
-  fp32 activations ~N(0,1) resident in HBM, synthetic data.  Each step (5
-  GEMV launches) is captured in a HIP graph; step i replays the graph of layer
-  copy i % 28 of 28 distinct ones plus the lm_head, so every step's weights
-  come from HBM (1.72 GB in all, far beyond the 256 MB Infinity Cache; the
-  311 MB lm_head passes through it between steps).
+  fp32 activations ~N(0,1) resident in HBM, synthetic data.  Step i (5 GEMV
+  launches) runs layer copy i % 28 of 28 distinct ones plus the lm_head, so
+  every step's weights come from HBM (1.72 GB in all, far beyond the 256 MB
+  Infinity Cache; the 311 MB lm_head passes through it between steps).  The
+  timed steps are captured back to back in one HIP graph, as the decoder
+  captures its layers; the same steps replayed as one graph each (a graph
+  launch per 5 kernels) are reported as `graph_per_step`.
 Also the full decoder's step, 28 layers + lm_head (113 launches, one graph):
   `decode_step_28_layers`.
 
@@ -829,23 +831,59 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e-3 / reps, time.perf_counter() - t0
 
-    log("warm-up (eager) and graph capture: one graph per step (layer copy l + lm_head)")
-    graphs = [capture(seq[(nl + 1) * l:(nl + 1) * (l + 1)]) for l in range(LAYERS)]
-    for i in range(args.warmup):
-        graphs[i % LAYERS].replay()
+    # The timed steps run as the decoder runs its layers: captured back to
+    # back in one HIP graph (step i = layer copy i % 28 + the lm_head), so a
+    # step pays kernel boundaries only, not a graph launch of its own.  The
+    # same steps as one graph each are timed beside it (graph_per_step).
+    def step_items(i):
+        l = i % LAYERS
+        return seq[(nl + 1) * l:(nl + 1) * (l + 1)]
+
+    log(f"warm-up (eager) and graph capture: {args.steps} steps in one graph")
+    with torch.cuda.stream(stream):
+        for l in range(LAYERS):
+            run_step(lin, step_items(l), stream)
+    stream.synchronize()
+    g_steps = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_steps, stream=stream):
+        for i in range(args.steps):
+            run_step(lin, step_items(i), stream)
+    g_warm = None
+    if args.warmup > 0:
+        g_warm = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_warm, stream=stream):
+            for i in range(args.warmup):
+                run_step(lin, step_items(i), stream)
+    torch.cuda.synchronize()
+    if g_warm is not None:
+        g_warm.replay()
     torch.cuda.synchronize()
     log(f"timing {args.steps} steps")
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     e0.record()
-    for i in range(args.steps):
-        graphs[i % LAYERS].replay()
+    g_steps.replay()
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     t_step = e0.elapsed_time(e1) * 1e-3 / args.steps
     value = step_bytes / t_step / 1e9
+    del g_steps, g_warm
+
+    log("the same steps as one graph launch each")
+    graphs = [capture(step_items(l)) for l in range(LAYERS)]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for i in range(args.steps):
+        graphs[i % LAYERS].replay()
+    e1.record()
+    torch.cuda.synchronize()
+    t_step_graphs = e0.elapsed_time(e1) * 1e-3 / args.steps
+    graph_per_step = {"ms_per_step": round(t_step_graphs * 1e3, 5),
+                      "GBps": round(step_bytes / t_step_graphs / 1e9, 1),
+                      "frac_hbm": round(step_bytes / t_step_graphs / 1e9 / HBM_PEAK_GBS, 4)}
     del graphs
 
     log("the full decoder step: 28 layers + lm_head in one graph")
@@ -935,11 +973,12 @@ def main():
         "data": "synthetic",
         "config": {"workload": "batch-1 decode projection set of one Qwen3-VL-2B text layer + lm_head, "
                                "W8A32: QKV 4096x2048, O 2048x2048, gate_up 12288x2048, down 2048x6144, "
-                               "lm_head 151936x2048; one HIP graph per step, step i on layer copy i % 28 "
-                               "of 28 distinct ones (every step's weights from HBM)",
+                               "lm_head 151936x2048; the timed steps in one HIP graph, step i on layer "
+                               "copy i % 28 of 28 distinct ones (every step's weights from HBM)",
                    "step_bytes": step_bytes, "launches_per_step": len(LAYER_SHAPES) + 1},
         "wall_s": round(wall, 3),
         "roofline": roofline,
+        "graph_per_step": graph_per_step,
         "decode_step_28_layers": step28,
         "lm_head_greedy": greedy,
         "gemv_6144x2048": single,
