@@ -50,17 +50,22 @@ constexpr int kMergeRound = 32;  // chunks whose partials the merger loads at on
 // chunks is loaded at once (each thread its o values, the m and l values one
 // per lane of a wave and shared through LDS), merged in chunk order, and the
 // counter is reset for the next launch.  Nothing waits on another work-group.
+// The state pointer and the q/k/v row come first among the arguments, so
+// that they arrive in SGPRs at wave launch (kernarg preload in the build) and
+// the state read, the first link of the kernel's dependent chain, waits for
+// no kernarg fetch.
 template <int T>
-__global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
+__global__ __launch_bounds__(256) void attn_decode_kernel(const int* __restrict__ state, const float* __restrict__ qkv,
+                                                          AttnDecodeArgs a) {
   constexpr int NK = T / 16;                // K iterations: 16 positions (4 waves x 4) each
   constexpr int NV = T / 8;                 // V float4 per thread: positions pg + 8 i
   const int c = blockIdx.x, h = blockIdx.y;
-  const int p = a.state[0];                 // position of the new token
+  const int p = state[0];                   // position of the new token
   const int S = p + 1;
   const int t0 = c * T;
   if (t0 >= S) return;                      // uniform: the whole work-group leaves, no ticket
   const int t1 = min(t0 + T, S);
-  const int rp = a.state[1];
+  const int rp = state[1];
 
   __shared__ float s_x[2][HD];              // normalised q heads before the rotation
   __shared__ float s_xk[HD];                // normalised new k before the rotation
@@ -76,9 +81,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   const bool has_new = p < t1;              // this chunk holds position p
 
   // ---- loads, in the order they are needed ----------------------------------
-  const float qraw = a.qkv[(2 * h + g) * HD + d];
+  const float qraw = qkv[(2 * h + g) * HD + d];
   const float qw = a.q_norm[d];
-  const float* kv_src = a.qkv + a.nq * HD + (g == 0 ? h * HD : a.nkv * HD + h * HD);
+  const float* kv_src = qkv + a.nq * HD + (g == 0 ? h * HD : a.nkv * HD + h * HD);
   const float kvraw = has_new ? kv_src[d] : 0.0f;
   const float kw = a.k_norm[d];
   const int j = d & 63;
@@ -359,9 +364,9 @@ hipError_t launch_attn_decode(const AttnDecodeArgs& a, hipStream_t st) {
     return hipErrorInvalidValue;
   const dim3 grid(cdiv(a.max_seq, a.T), a.nkv);
   switch (a.T) {
-    case 32: hipLaunchKernelGGL(attn_decode_kernel<32>, grid, dim3(256), 0, st, a); break;
-    case 64: hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(256), 0, st, a); break;
-    case 128: hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(256), 0, st, a); break;
+    case 32: hipLaunchKernelGGL(attn_decode_kernel<32>, grid, dim3(256), 0, st, a.state, a.qkv, a); break;
+    case 64: hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(256), 0, st, a.state, a.qkv, a); break;
+    case 128: hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(256), 0, st, a.state, a.qkv, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
