@@ -5,11 +5,12 @@ Workload (the metric's configuration; a "step" = W8A32 batch==1 GEMVs):
   QKV 4096x2048, O 2048x2048, gate_up 12288x2048, down 2048x6144, lm_head
   151936x2048 (361.5 MB of int8 weights and scales), per-row fp32 scales,
   fp32 activations ~N(0,1) resident in HBM, synthetic data.  Step i (5 GEMV
-  launches) runs layer copy i % 28 of 28 distinct ones plus the lm_head, so
-  every step's weights come from HBM (1.72 GB in all, far beyond the 256 MB
-  Infinity Cache; the 311 MB lm_head passes through it between steps).  The
-  timed steps are captured back to back in one HIP graph, as the decoder
-  captures its layers; the same steps replayed as one graph each (a graph
+  launches) runs layer copy i % 28 of 28 distinct ones plus lm_head copy
+  i % 2 of two, so every step's weights come from HBM (1.72 GB of layers and
+  622 MB of lm_heads, far beyond the 256 MB Infinity Cache).  The timed steps
+  are captured back to back in one HIP graph, as the decoder captures its
+  layers; the graph is replayed 5 times, each replay timed on its own, and the
+  median is the figure.  The same steps replayed as one graph each (a graph
   launch per 5 kernels) are reported as `graph_per_step`.
 Also the full decoder's step, 28 layers + lm_head (113 launches, one graph):
   `decode_step_28_layers`.
@@ -17,9 +18,13 @@ Also the full decoder's step, 28 layers + lm_head (113 launches, one graph):
 value   = algorithmic bytes of one step / step time (GB/s); bytes per GEMV
           launch are N*K + 4N + 4K + 4N (weights, scales, x, y).
 roofline: the GEMV kernel family (every launch is a GEMV), average bytes per
-          launch over its average launch duration (HIP events on the replay
-          stream around the timed steps, divided by the 5 launches of each),
-          against the 8 TB/s HBM peak.
+          launch over its average launch duration, against the 8 TB/s HBM
+          peak.  The duration comes from the committed rocprofv3 kernel trace
+          of this command (profiles/gemv_timed_steps_kernel_trace.md, written
+          by --summarize-trace: the GEMV durations between the marker launches
+          that bracket each timed replay) while it was taken on the current
+          GEMV sources; `roofline.live` holds the same ratio on this run's
+          HIP-event step time (launch gaps included).
 Also: W8A8 prefill TOPS (M=1024; N=6144,K=2048 and N=2048,K=6144; includes
 the per-token quantization kernel), and the CPU baseline (the oracle's M=1
 GEMV, OpenMP on the host cores) on a bounded sample.
@@ -76,9 +81,123 @@ def measured_traffic():
     if rec.get("gemv_sources_sha256") != gemv_sources_sha256():
         return None, "stale: the GEMV sources changed since the counters were taken"
     return float(rec["traffic_bytes_per_launch"]), "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, same GEMV sources"
+
+
+# The timed steps' kernel trace: `bench.py --summarize-trace` writes this
+# summary from a rocprofv3 --kernel-trace run of the benchmark's own command.
+TRACE_SUMMARY = ROOT / "profiles" / "gemv_timed_steps_kernel_trace.md"
+TIMED_REPLAYS = 5
+MARKER_BYTES = 4096        # the trace marker: one 256-thread work-group reading 4 KiB
+
+
+class TraceMarker:
+    """A launch that brackets each timed replay in a kernel trace: the plain
+    streaming read kernel on one work-group (every other launch of it in
+    this benchmark uses 256 or more), outside the HIP events."""
+
+    def __init__(self, lin, torch, dev):
+        self.lib = lin.load_library()
+        self.lin = lin
+        self.buf = torch.ones(MARKER_BYTES, dtype=torch.uint8, device=dev)
+        self.sink = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def launch(self, stream):
+        rc = self.lib.tl_stream_read_dev(self.buf.data_ptr(), MARKER_BYTES, 1, 4, self.sink.data_ptr(),
+                                         stream.cuda_stream)
+        assert rc == 0, self.lin.check(self.lib, "tl_stream_read_dev")
+
+
+def read_summary_fields(path, keys):
+    rec = {}
+    for line in path.read_text().splitlines():
+        if ":" in line and line.split(":", 1)[0] in keys:
+            k, v = line.split(":", 1)
+            rec[k] = v.strip()
+    return rec
+
+
+def profiled_step_kernel_us(steps):
+    """GEMV kernel time of one benchmark step (us) from the committed kernel
+    trace summary, or None with the reason: absent, taken on other GEMV
+    sources, or at another step count."""
+    try:
+        rec = read_summary_fields(TRACE_SUMMARY, ("kernel_us_per_step", "gemv_sources_sha256", "steps",
+                                                  "timed_replays", "lm_head_copies"))
+    except OSError:
+        return None, "no kernel trace summary"
+    if "kernel_us_per_step" not in rec:
+        return None, "no kernel_us_per_step in the trace summary"
+    if rec.get("gemv_sources_sha256") != gemv_sources_sha256():
+        return None, "trace summary stale: the GEMV sources changed since it was taken"
+    if rec.get("steps") != str(steps) or rec.get("lm_head_copies") != str(LM_COPIES):
+        return None, f"trace summary taken at steps={rec.get('steps')}, not {steps}"
+    return float(rec["kernel_us_per_step"]), (f"median over its {rec.get('timed_replays')} timed replays of "
+                                              f"the summed GEMV durations per step")
+
+
+def summarize_trace(csv_path, steps, cmd):
+    """Markdown summary of the timed replays in a rocprofv3 kernel trace of
+    this benchmark: the launches between each pair of marker launches, per
+    shape (told apart by grid size) and per step."""
+    import csv
+    rows = list(csv.DictReader(open(csv_path)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    n_per = len(LAYER_SHAPES) + 1
+    marks = [i for i, r in enumerate(rows)
+             if "stream_read_kernel" in r["Kernel_Name"] and int(r["Grid_Size_X"]) == 256]
+    if len(marks) < 2 or len(marks) % 2:
+        raise SystemExit(f"{len(marks)} marker launches in the trace; expected pairs")
+    grid_shape = {}
+    for (name, N, K) in LAYER_SHAPES + [LM_HEAD]:
+        grid_shape.setdefault(name, N)
+    reps, per = [], {}
+    for a, b in zip(marks[0::2], marks[1::2]):
+        seg = [r for r in rows[a + 1:b] if "gemv_i8_kernel" in r["Kernel_Name"]]
+        if len(seg) != steps * n_per or len(seg) != b - a - 1:
+            raise SystemExit(f"timed replay holds {b - a - 1} launches ({len(seg)} GEMV); expected {steps * n_per}")
+        durs = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3 for r in seg]
+        span = (int(seg[-1]["End_Timestamp"]) - int(seg[0]["Start_Timestamp"])) * 1e-3
+        reps.append((sum(durs) / steps, span / steps))
+        for j, (r, d) in enumerate(zip(seg, durs)):
+            shape = (LAYER_SHAPES + [LM_HEAD])[j % n_per]
+            per.setdefault(shape, {"kernel": r["Kernel_Name"], "grid": int(r["Grid_Size_X"]), "d": []})["d"].append(d)
+    k_step = float(np.median([k for k, _ in reps]))
+    s_step = float(np.median([s for _, s in reps]))
+    step_bytes = sum(gemv_bytes(N, K) for (_, N, K) in LAYER_SHAPES + [LM_HEAD])
+    out = ["# GEMV timed steps: kernel durations (rocprofv3 --kernel-trace)", "",
+           "Command (MI355X, one GPU):", "", "```", cmd, "```", "",
+           f"Workload: the benchmark's timed steps. Step i is layer copy i % {LAYERS}'s projection set "
+           "(QKV 4096x2048, O 2048x2048, gate_up 12288x2048, down 2048x6144) plus lm_head 151936x2048 "
+           f"copy i % {LM_COPIES}, W8A32 batch 1, {steps} steps captured back to back in one HIP graph; "
+           f"{len(reps)} timed replays, each bracketed by a one-work-group `stream_read_kernel` marker "
+           "launch outside the HIP events. This summary counts the launches between each pair of "
+           "markers only (every one a `gemv_i8_kernel`).", "",
+           "| shape | kernel | grid threads | launches | avg us | median us | min us |",
+           "|---|---|---|---|---|---|---|"]
+    for (name, N, K), rec in per.items():
+        d = rec["d"]
+        kname = rec["kernel"].split("(")[0].replace("tl::", "")
+        out.append(f"| {name} {N}x{K} | `{kname}` | {rec['grid']} | {len(d)} | {np.mean(d):.2f} | "
+                   f"{np.median(d):.2f} | {np.min(d):.2f} |")
+    out += ["", "Per timed replay (us per step): GEMV kernel time summed / span from the first launch's "
+            "start to the last launch's end:", ""]
+    out += [f"- replay {i}: {k:.2f} / {s:.2f}" for i, (k, s) in enumerate(reps)]
+    out += ["", "Figures bench.py reads (median over the timed replays):", "",
+            f"kernel_us_per_step: {k_step:.3f}",
+            f"span_us_per_step: {s_step:.3f}",
+            f"bytes_per_step: {step_bytes}",
+            f"frac_hbm_from_kernel_time: {step_bytes / (k_step * 1e-6) / 1e9 / HBM_PEAK_GBS:.4f}",
+            f"steps: {steps}",
+            f"timed_replays: {len(reps)}",
+            f"lm_head_copies: {LM_COPIES}",
+            f"gemv_sources_sha256: {gemv_sources_sha256()}", ""]
+    return "\n".join(out)
+
+
 LAYERS = 28
 LAYER_SHAPES = [("qkv", 4096, 2048), ("o", 2048, 2048), ("gate_up", 12288, 2048), ("down", 2048, 6144)]
 LM_HEAD = ("lm_head", 151936, 2048)
+LM_COPIES = 2
 METRIC = "INT8 GEMV HBM GB/s + decode tok/s; W8A8 prefill TOPS (Qwen3-VL-2B decoder)"
 
 
@@ -94,7 +213,9 @@ def build_decode_set(lin, torch, dev, seed=0):
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     items = []
-    shapes = [(f"l{l}.{n}", N, K) for l in range(LAYERS) for (n, N, K) in LAYER_SHAPES] + [LM_HEAD]
+    # two lm_head copies: the timed steps alternate them (step i reads copy
+    # i % 2), so no step finds its lm_head lines left in the Infinity Cache
+    shapes = [(f"l{l}.{n}", N, K) for l in range(LAYERS) for (n, N, K) in LAYER_SHAPES] + [LM_HEAD] * LM_COPIES
     for name, N, K in shapes:
         w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
         s = torch.rand(N, device=dev, generator=g) * 0.018 + 0.002
@@ -651,7 +772,8 @@ def bench_w8a16_sweep(lin, torch, dev):
 def bench_w8a32_prefill(lin, torch, dev, M=1200):
     """The reference decoder's prefill linear path, w8a32_linear(batch=S)
     (fp32 X times dequantized weights), at S = 1200 on the fused layer shapes;
-    computed as three bf16 MFMA passes (fp32-accurate)."""
+    computed fp32-accurately on the int8 MFMA, each token split into four int8
+    planes (the plane split launch included)."""
     out = {}
     tot_f, tot_t = 0.0, 0.0
     for (name, N, K) in LAYER_SHAPES:
@@ -762,7 +884,15 @@ def main():
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run a 512 MiB device copy (counter calibration) and one eager decode "
                          "step, then exit; used under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--summarize-trace", metavar="CSV",
+                    help="write the timed steps' summary of a rocprofv3 kernel_trace.csv of this "
+                         "benchmark (run with the same --steps) to stdout, then exit (no GPU use)")
+    ap.add_argument("--trace-command", default="",
+                    help="the profiling command, recorded in the --summarize-trace output")
     args = ap.parse_args()
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace, args.steps, args.trace_command))
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1"}))
         sys.exit(2)
@@ -785,13 +915,17 @@ def main():
         print(json.dumps({"decoder_greedy": bench_decoder_generate(lin, torch, dev, n_layers=args.decoder_layers,
                                                                    steps=args.decoder_steps)}), flush=True)
         return
-    log("building the decode set (1.72 GB of int8 weights)")
+    log("building the decode set (1.72 GB of layer weights, two 311 MB lm_head copies)")
     items = build_decode_set(lin, torch, dev)
-    # the benchmark's steps: layer copy l's projection set + the lm_head, l = 0..27
     nl = len(LAYER_SHAPES)
-    seq = []
-    for l in range(LAYERS):
-        seq += items[nl * l:nl * l + nl] + [items[-1]]
+    layers = [items[nl * l:nl * l + nl] for l in range(LAYERS)]
+    lm_heads = items[nl * LAYERS:]
+
+    # the benchmark's step i: layer copy i % 28's projection set + lm_head copy i % 2
+    def step_items(i):
+        return layers[i % LAYERS] + [lm_heads[i % LM_COPIES]]
+
+    seq = [it for i in range(LAYERS) for it in step_items(i)]
     if args.traffic_probe:
         src = torch.empty(COPY_PROBE_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
@@ -805,6 +939,7 @@ def main():
         return
     step_bytes = sum(gemv_bytes(N, K) for (_, N, K) in LAYER_SHAPES + [LM_HEAD])
     stream = torch.cuda.Stream()
+    marker = TraceMarker(lin, torch, dev)
 
     def capture(its):
         with torch.cuda.stream(stream):
@@ -832,17 +967,13 @@ def main():
         return e0.elapsed_time(e1) * 1e-3 / reps, time.perf_counter() - t0
 
     # The timed steps run as the decoder runs its layers: captured back to
-    # back in one HIP graph (step i = layer copy i % 28 + the lm_head), so a
-    # step pays kernel boundaries only, not a graph launch of its own.  The
-    # same steps as one graph each are timed beside it (graph_per_step).
-    def step_items(i):
-        l = i % LAYERS
-        return seq[(nl + 1) * l:(nl + 1) * (l + 1)]
-
+    # back in one HIP graph, so a step pays kernel boundaries only, not a graph
+    # launch of its own.  The same steps as one graph each are timed beside it
+    # (graph_per_step).
     log(f"warm-up (eager) and graph capture: {args.steps} steps in one graph")
     with torch.cuda.stream(stream):
-        for l in range(LAYERS):
-            run_step(lin, step_items(l), stream)
+        for i in range(LAYERS):
+            run_step(lin, step_items(i), stream)
     stream.synchronize()
     g_steps = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g_steps, stream=stream):
@@ -858,40 +989,56 @@ def main():
     if g_warm is not None:
         g_warm.replay()
     torch.cuda.synchronize()
-    log(f"timing {args.steps} steps")
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0.record()
-    g_steps.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    t_step = e0.elapsed_time(e1) * 1e-3 / args.steps
+    # TIMED_REPLAYS replays of the K-step graph, each timed on its own (HIP
+    # events on the replay stream, synchronised before and after); the median
+    # is the figure.  A marker launch (outside the events) brackets every timed
+    # replay, so a kernel trace of this run can find the timed launches.
+    log(f"timing {args.steps} steps, {TIMED_REPLAYS} replays")
+    t_reps, wall = [], 0.0
+    replay_stream = torch.cuda.current_stream()      # CUDAGraph.replay() launches on the current stream
+    for _ in range(TIMED_REPLAYS):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        marker.launch(replay_stream)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(replay_stream)
+        g_steps.replay()
+        e1.record(replay_stream)
+        torch.cuda.synchronize()
+        wall += time.perf_counter() - t0
+        marker.launch(replay_stream)
+        torch.cuda.synchronize()
+        t_reps.append(e0.elapsed_time(e1) * 1e-3 / args.steps)
+    t_step = float(np.median(t_reps))
     value = step_bytes / t_step / 1e9
     del g_steps, g_warm
 
     log("the same steps as one graph launch each")
-    graphs = [capture(step_items(l)) for l in range(LAYERS)]
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for i in range(args.steps):
-        graphs[i % LAYERS].replay()
-    e1.record()
-    torch.cuda.synchronize()
-    t_step_graphs = e0.elapsed_time(e1) * 1e-3 / args.steps
+    graphs = [capture(step_items(i)) for i in range(LAYERS)]
+    t_gs = []
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for i in range(args.steps):
+            graphs[i % LAYERS].replay()
+        e1.record()
+        torch.cuda.synchronize()
+        t_gs.append(e0.elapsed_time(e1) * 1e-3 / args.steps)
+    t_step_graphs = float(np.median(t_gs))
     graph_per_step = {"ms_per_step": round(t_step_graphs * 1e3, 5),
                       "GBps": round(step_bytes / t_step_graphs / 1e9, 1),
-                      "frac_hbm": round(step_bytes / t_step_graphs / 1e9 / HBM_PEAK_GBS, 4)}
+                      "frac_hbm": round(step_bytes / t_step_graphs / 1e9 / HBM_PEAK_GBS, 4),
+                      "timing": "one graph launch per step, median of 3 rounds of --steps steps"}
     del graphs
 
     log("the full decoder step: 28 layers + lm_head in one graph")
-    graph28 = capture(items)
+    full = [it for l in layers for it in l] + [lm_heads[0]]
+    graph28 = capture(full)
     t28, _ = time_replays(graph28, max(5, args.steps // 5))
-    bytes28 = sum(gemv_bytes(N, K) for (_, N, K, *_r) in items)
+    bytes28 = sum(gemv_bytes(N, K) for (_, N, K, *_r) in full)
     step28 = {"ms": round(t28 * 1e3, 4), "GBps": round(bytes28 / t28 / 1e9, 1),
-              "frac_hbm": round(bytes28 / t28 / 1e9 / HBM_PEAK_GBS, 4), "launches": len(items),
+              "frac_hbm": round(bytes28 / t28 / 1e9 / HBM_PEAK_GBS, 4), "launches": len(full),
               "bytes": bytes28, "tok_s_linear_layers": round(1.0 / t28, 1)}
     del graph28
 
@@ -910,18 +1057,34 @@ def main():
             per_shape[key]["read_floor_us"] = f["us"]
             per_shape[key]["read_floor_frac_hbm"] = f["frac_hbm"]
             per_shape[key]["vs_read_floor"] = round(f["us"] * 1e-6 / t, 4)
-    # every launch is the GEMV kernel and the replays run them back to back,
-    # so its average launch duration is the step time over the launches per step
+    # Every launch of a step is the GEMV kernel.  `achieved` is the step's
+    # algorithmic bytes over the GEMV kernel time of a step in the committed
+    # rocprofv3 kernel trace of this command (the timed replays' launches,
+    # End - Start summed per step), while that trace was taken on the current
+    # GEMV sources; `live` is the same ratio on this run's HIP-event step time
+    # (launch gaps included).
     n_per_step = len(LAYER_SHAPES) + 1
     avg_bytes = step_bytes / n_per_step
-    avg_t = t_step / n_per_step
-    achieved = avg_bytes / avg_t / 1e9
+    live_achieved = step_bytes / t_step / 1e9
+    live = {"achieved": round(live_achieved, 1), "frac": round(live_achieved / HBM_PEAK_GBS, 4),
+            "avg_launch_us": round(t_step / n_per_step * 1e6, 3),
+            "replay_ms_per_step": [round(t * 1e3, 5) for t in t_reps],
+            "source": f"HIP events on the replay stream, median of {TIMED_REPLAYS} replays of the "
+                      f"{args.steps}-step graph, step time / {n_per_step} launches"}
+    prof_us, prof_note = profiled_step_kernel_us(args.steps)
+    if prof_us is not None:
+        achieved = step_bytes / (prof_us * 1e-6) / 1e9
+        avg_launch_us = prof_us / n_per_step
+        src = f"rocprofv3 kernel trace of this command ({TRACE_SUMMARY.relative_to(ROOT)}): {prof_note}"
+    else:
+        achieved, avg_launch_us = live_achieved, t_step / n_per_step * 1e6
+        src = f"HIP events of this run ({prof_note})"
     traffic, traffic_note = measured_traffic()
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_note,
                 "kernel": f"gemv_i8_kernel (all {n_per_step} launches of a step)",
-                "bytes_per_launch": round(avg_bytes), "avg_launch_us": round(avg_t * 1e6, 3),
-                "per_shape": per_shape}
+                "bytes_per_launch": round(avg_bytes), "avg_launch_us": round(avg_launch_us, 3),
+                "achieved_source": src, "live": live, "per_shape": per_shape}
 
     log("fused greedy lm_head step")
     greedy = bench_lm_head_greedy(lin, torch, items[-1][3], items[-1][2], dev, stream)
