@@ -286,8 +286,10 @@ void decoder_set_layer_weights(ModelWeights *model, int layer_idx, const int8_t 
                                const int8_t *up_w, const float *up_s, const int8_t *down_w, const float *down_s,
                                const float *input_ln, const float *post_attn_ln, const float *q_norm,
                                const float *k_norm);
-/* decoder.c:393-424: as above, with the fused Q||K||V given directly (the
- * fused gate||up is accepted and re-laid out from gate and up). */
+/* decoder.c:393-424: as above, with the fused Q||K||V [4096 x 2048] and
+ * gate||up [12288 x 2048] (decoder.py:290-302); when given, the fused arrays
+ * are the source of those rows (gate||up re-laid out per 16-row group) and
+ * the separate q/k/v and gate/up arrays are not read. */
 void decoder_set_layer_weights_v32(ModelWeights *model, int layer_idx, const int8_t *q_w, const float *q_s,
                                    const int8_t *k_w, const float *k_s, const int8_t *v_w, const float *v_s,
                                    const int8_t *o_w, const float *o_s, const int8_t *gate_w,

@@ -214,6 +214,59 @@ def test_generate_greedy_matches_step_path_and_oracle(lin, orc, dev):
     d.close()
 
 
+def test_v32_registration_equals_separate_matrices(lin, orc, dev):
+    """The Decoder hands its layers to the device loop through
+    decoder_set_layer_weights_v32 with the fused Q||K||V and gate||up arrays,
+    as the reference's _register_layer does (decoder.py:304-317 ->
+    decoder.c:393-423); the oracle tests in this file therefore run on that
+    path.  The same layers re-registered through decoder_set_layer_weights
+    (the separate matrices), and through _v32 with only the fused arrays
+    (separate q/k/v and gate/up pointers NULL), give bit-identical prefill
+    rows, K/V cache rows and decode steps."""
+    import ctypes
+    from typhoon_ocr_server_amd import decoder as dec
+    say("decoder_set_layer_weights_v32 vs decoder_set_layer_weights, 2 layers")
+    rng = np.random.default_rng(29)
+    layers, _, _ = _model(rng, orc, 2)
+    d = dec.Decoder(layers, max_seq=96)
+    lib = d._lib
+    h0 = (rng.standard_normal((40, 2048)) * 2).astype(F)
+    steps = (rng.standard_normal((6, 2048)) * 2).astype(F)
+
+    def run():
+        d.reset()
+        hp = d.prefill(h0)
+        hs = [d.step(h[None]) for h in steps]
+        return [hp] + hs + [a for l in range(2) for a in d.read_cache(l)]
+
+    def i8(a):
+        return None if a is None else a.ctypes.data_as(ctypes.POINTER(ctypes.c_int8))
+
+    def f32(a):
+        return None if a is None else a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+    norms = [[np.ascontiguousarray(layer[n], dtype=F) for n in dec.NORMS] for layer in layers]
+    a = run()
+    for l, e in enumerate(d.layers):
+        args = [p for n in dec.PROJECTIONS for p in (i8(e[n][0]), f32(e[n][1]))] + [f32(n) for n in norms[l]]
+        lib.decoder_set_layer_weights(d._c_model, l, *args)
+        lin.check(lib, "decoder_set_layer_weights")
+    b = run()
+    for l, e in enumerate(d.layers):
+        sep = [p for n in dec.PROJECTIONS
+               for p in ((i8(e[n][0]), f32(e[n][1])) if n in ("o_proj", "down_proj") else (None, None))]
+        args = sep + [f32(n) for n in norms[l]]
+        args += [i8(e["qkv_proj"][0]), f32(e["qkv_proj"][1]), i8(e["gate_up_proj"][0]), f32(e["gate_up_proj"][1])]
+        lib.decoder_set_layer_weights_v32(d._c_model, l, *args)
+        lin.check(lib, "decoder_set_layer_weights_v32")
+    c = run()
+    assert len(a) == len(b) == len(c) == 1 + len(steps) + 4
+    for x, y, z in zip(a, b, c):
+        np.testing.assert_array_equal(x, y)
+        np.testing.assert_array_equal(x, z)
+    d.close()
+
+
 # ---------------------------------------------------------------------------
 # prefill (survey row f-4): decoder.c:33-157 with seq_len > 1, decoder.c:437-507
 # ---------------------------------------------------------------------------

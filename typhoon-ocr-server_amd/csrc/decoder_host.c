@@ -31,6 +31,7 @@
 #include <math.h>
 #include <unistd.h>
 #include <pthread.h>
+#include <stdatomic.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -243,7 +244,8 @@ static void advance(KVCache* c, int n) {   /* kv_cache_advance (kernel/kv_cache.
 /* prefill with the activation quantization / plane split fused into the
  * RMSNorm and SwiGLU kernels (default), or each linear's own launch
  * (tl_prefill_set_fused_quant) */
-static bool g_prefill_fused_quant = true;
+/* atomic, since a setter may run while other threads enqueue prefills */
+static atomic_bool g_prefill_fused_quant = true;
 
 /* Prefill of S tokens through every layer (decoder.c:33-157 with seq_len > 1):
  * token t is rotated with rows t of cos_rows / sin_rows, its K/V go to cache
@@ -266,7 +268,7 @@ static int enqueue_prefill(const ModelWeights* m, KVCache* c, DecoderScratch* s,
    * (S <= 32 keeps the fp32 rows: w8a32_linear takes other kernels there).
    * Only the attention output goes through its linear's own quantization. */
   const bool w8 = m->prefill_w8a8;
-  const bool fused_q = g_prefill_fused_quant && (w8 || S > 32);
+  const bool fused_q = atomic_load_explicit(&g_prefill_fused_quant, memory_order_relaxed) && (w8 || S > 32);
   uint8_t* Aq = (uint8_t*)s->p_q.p;
   float* As = w8 ? (float*)s->p_qs.p : NULL;
   int* Ae = w8 ? NULL : (int*)s->p_qs.p;
@@ -450,9 +452,13 @@ static int write_state(KVCache* c, DecoderScratch* s, int counter) {
   return 0;
 }
 
+/* One layer's host arrays.  qkv_w / gate_up_w are the fused row
+ * concatenations Q||K||V [4096 x 2048] and gate||up [12288 x 2048]
+ * (decoder.py:290-302); when given they are the source of those rows, and
+ * the separate q/k/v or gate/up arrays are not read. */
 typedef struct LayerSources {
-  const int8_t *q_w, *k_w, *v_w, *o_w, *gate_w, *up_w, *down_w, *qkv_w;
-  const float *q_s, *k_s, *v_s, *o_s, *gate_s, *up_s, *down_s, *qkv_s;
+  const int8_t *q_w, *k_w, *v_w, *o_w, *gate_w, *up_w, *down_w, *qkv_w, *gate_up_w;
+  const float *q_s, *k_s, *v_s, *o_s, *gate_s, *up_s, *down_s, *qkv_s, *gate_up_s;
   const float *input_ln, *post_attn_ln, *q_norm, *k_norm;
 } LayerSources;
 
@@ -484,6 +490,11 @@ static int build_layer(const LayerSources* w, LayerDev* L) {
   {
     /* gate and up interleaved per 16-row group: rows 16b..16b+7 are gate
      * rows 8b.., rows 16b+8.. the up rows 8b.. (EPI_SWIGLU) */
+    const bool fused = w->gate_up_w && w->gate_up_s;
+    const int8_t* gate_w = fused ? w->gate_up_w : w->gate_w;
+    const int8_t* up_w = fused ? w->gate_up_w + (size_t)FF * H : w->up_w;
+    const float* gate_s = fused ? w->gate_up_s : w->gate_s;
+    const float* up_s = fused ? w->gate_up_s + FF : w->up_s;
     int8_t* gw = (int8_t*)malloc((size_t)2 * FF * H);
     float* gs = (float*)malloc((size_t)2 * FF * 4);
     if (!gw || !gs) {
@@ -492,10 +503,10 @@ static int build_layer(const LayerSources* w, LayerDev* L) {
       return tlh_fail("out of host memory");
     }
     for (int b = 0; b < FF / 8; b++) {
-      memcpy(gw + (size_t)(16 * b) * H, w->gate_w + (size_t)(8 * b) * H, (size_t)8 * H);
-      memcpy(gw + (size_t)(16 * b + 8) * H, w->up_w + (size_t)(8 * b) * H, (size_t)8 * H);
-      memcpy(gs + 16 * b, w->gate_s + 8 * b, 8 * 4);
-      memcpy(gs + 16 * b + 8, w->up_s + 8 * b, 8 * 4);
+      memcpy(gw + (size_t)(16 * b) * H, gate_w + (size_t)(8 * b) * H, (size_t)8 * H);
+      memcpy(gw + (size_t)(16 * b + 8) * H, up_w + (size_t)(8 * b) * H, (size_t)8 * H);
+      memcpy(gs + 16 * b, gate_s + 8 * b, 8 * 4);
+      memcpy(gs + 16 * b + 8, up_s + 8 * b, 8 * 4);
     }
     const int rc = tlh_weights_from_codes(gw, gs, 2 * FF, H, false, st, &L->gu);
     free(gw);
@@ -517,10 +528,10 @@ static int set_layer(ModelWeights* m, int l, const LayerSources* w) {
   int dev;
   TRY(tlh_current_device(&dev));
   REQ(m->dev == dev, "model lives on another device");
-  REQ(w->o_w && w->o_s && w->gate_w && w->gate_s && w->up_w && w->up_s && w->down_w && w->down_s,
-      "NULL weight pointer");
+  REQ(w->o_w && w->o_s && w->down_w && w->down_s, "NULL weight pointer");
   REQ(w->input_ln && w->post_attn_ln && w->q_norm && w->k_norm, "NULL norm pointer");
   REQ((w->qkv_w && w->qkv_s) || (w->q_w && w->q_s && w->k_w && w->k_s && w->v_w && w->v_s), "NULL q/k/v pointer");
+  REQ((w->gate_up_w && w->gate_up_s) || (w->gate_w && w->gate_s && w->up_w && w->up_s), "NULL gate/up pointer");
   LayerDev L;
   memset(&L, 0, sizeof L);
   if (build_layer(w, &L) != 0) {
@@ -681,8 +692,8 @@ void decoder_set_layer_weights(ModelWeights* model, int layer_idx, const int8_t*
                                const float* input_ln, const float* post_attn_ln, const float* q_norm,
                                const float* k_norm) {
   tlh_begin();
-  const LayerSources w = {q_w, k_w, v_w, o_w, gate_w, up_w, down_w, NULL,
-                          q_s, k_s, v_s, o_s, gate_s, up_s, down_s, NULL,
+  const LayerSources w = {q_w, k_w, v_w, o_w, gate_w, up_w, down_w, NULL, NULL,
+                          q_s, k_s, v_s, o_s, gate_s, up_s, down_s, NULL, NULL,
                           input_ln, post_attn_ln, q_norm, k_norm};
   tlh_finish("decoder_set_layer_weights", set_layer(model, layer_idx, &w));
 }
@@ -694,11 +705,9 @@ void decoder_set_layer_weights_v32(ModelWeights* model, int layer_idx, const int
                                    const float* input_ln, const float* post_attn_ln, const float* q_norm,
                                    const float* k_norm, const int8_t* qkv_w, const float* qkv_s,
                                    const int8_t* gate_up_w, const float* gate_up_s) {
-  (void)gate_up_w;   /* gate and up are re-laid out from the separate matrices */
-  (void)gate_up_s;
   tlh_begin();
-  const LayerSources w = {q_w, k_w, v_w, o_w, gate_w, up_w, down_w, qkv_w,
-                          q_s, k_s, v_s, o_s, gate_s, up_s, down_s, qkv_s,
+  const LayerSources w = {q_w, k_w, v_w, o_w, gate_w, up_w, down_w, qkv_w, gate_up_w,
+                          q_s, k_s, v_s, o_s, gate_s, up_s, down_s, qkv_s, gate_up_s,
                           input_ln, post_attn_ln, q_norm, k_norm};
   tlh_finish("decoder_set_layer_weights_v32", set_layer(model, layer_idx, &w));
 }
@@ -857,7 +866,7 @@ int tl_decoder_cache_len(const KVCache* cache) { return cache ? cache->seq_len :
 int tl_prefill_set_fused_quant(int on) {
   tlh_begin();
   if (on != 0 && on != 1) return tlh_finish("tl_prefill_set_fused_quant", tlh_fail("on must be 0 or 1"));
-  g_prefill_fused_quant = on != 0;
+  atomic_store_explicit(&g_prefill_fused_quant, on != 0, memory_order_relaxed);
   return 0;
 }
 

@@ -14,8 +14,9 @@ error behaviour, on the MI355X library:
   * Decoder quantizes on the GPU (w8a32_quantize packs the HBM tiles in the
     same pass and keeps them for the returned host arrays), packs the fused
     matrices, and registers every quantized matrix with tl_register_weights
-    (the step the reference's decoder_set_layer_weights_v32 performs by
-    pointer; only the fused copies upload anything there);
+    (only the fused copies upload anything there); with the layer norms it
+    hands the layer, fused matrices included, to the device loop through
+    decoder_set_layer_weights_v32, as the reference does (:304-317);
   * save_cache() / from_cache() write and read a packed-weight cache file,
     so a later load copies the HBM tiles back with no quantization;
   * project() runs one projection through w8a32_linear with the reference's
@@ -24,7 +25,7 @@ error behaviour, on the MI355X library:
 
 With the layer norms given (random_layer_weights(norms=True) or real
 weights), the Decoder also builds the device-resident layer loop through the
-reference's decoder C ABI (decoder_set_layer_weights, decoder_decode_step:
+reference's decoder C ABI (decoder_set_layer_weights_v32, decoder_decode_step:
 kernel/decoder.c:300-526): step() is the reference's Decoder.step, and
 generate_greedy() runs the greedy decode loop on the GPU.
 """
@@ -221,10 +222,6 @@ class Decoder:
 
     def _register_layer(self, l_idx: int, layer: Mapping[str, np.ndarray]) -> None:
         q = {name: self._quantize_and_keep(layer[name]) for name in PROJECTIONS}
-        if all(n in layer for n in NORMS):
-            norms = [np.ascontiguousarray(layer[n], dtype=np.float32) for n in NORMS]
-            self._weight_store.extend(norms)
-            self._set_device_layer(l_idx, q, norms)
         # fused Q||K||V [4096 x 2048] and gate||up [12288 x 2048] (reference :290-302)
         qkv_w = np.ascontiguousarray(np.concatenate([q["q_proj"][0], q["k_proj"][0], q["v_proj"][0]], axis=0))
         qkv_s = np.ascontiguousarray(np.concatenate([q["q_proj"][1], q["k_proj"][1], q["v_proj"][1]]))
@@ -234,6 +231,10 @@ class Decoder:
         entry = dict(q)
         entry["qkv_proj"] = (qkv_w, qkv_s)
         entry["gate_up_proj"] = (gu_w, gu_s)
+        if all(n in layer for n in NORMS):
+            norms = [np.ascontiguousarray(layer[n], dtype=np.float32) for n in NORMS]
+            self._weight_store.extend(norms)
+            self._set_device_layer(l_idx, entry, norms)
         for w, s in entry.values():
             self._register(w, s)
         self.layers.append(entry)
@@ -258,14 +259,19 @@ class Decoder:
         _lin.check(lib, "decoder_precompute_rope")
 
     def _set_device_layer(self, l_idx: int, q: Mapping[str, tuple], norms: List[np.ndarray]) -> None:
+        """The layer's seven projections, four norms and the fused Q||K||V and
+        gate||up, registered through decoder_set_layer_weights_v32 as the
+        reference's _register_layer does (decoder.py:304-317)."""
         self._init_device_loop()
         args = []
-        for name in PROJECTIONS:
+        for name in PROJECTIONS + ("qkv_proj", "gate_up_proj"):
             w, s_ = q[name]
-            args += [_np_ptr(w, ctypes.c_int8), _np_ptr(s_)]
-        args += [_np_ptr(n) for n in norms]
-        self._lib.decoder_set_layer_weights(self._c_model, l_idx, *args)
-        _lin.check(self._lib, "decoder_set_layer_weights")
+            args.append((_np_ptr(w, ctypes.c_int8), _np_ptr(s_)))
+        flat = [p for pair in args[:len(PROJECTIONS)] for p in pair]
+        flat += [_np_ptr(n) for n in norms]
+        flat += [p for pair in args[len(PROJECTIONS):] for p in pair]
+        self._lib.decoder_set_layer_weights_v32(self._c_model, l_idx, *flat)
+        _lin.check(self._lib, "decoder_set_layer_weights_v32")
 
     def reset(self) -> None:
         """Clear the KV cache for a new sequence (reference :322-323)."""
