@@ -407,43 +407,53 @@ static int reg_insert_locked(const void* w, const void* s, int dev, WRef* ref, u
 }
 
 /* the resident matrix of host arrays (w, s), uploaded and packed on first
- * use (or again when their contents changed); the caller drops *out */
+ * use (or again when their contents changed); the caller drops *out.
+ * A miss uploads without holding the registry lock, so calls whose weights
+ * are resident go on meanwhile (a first lm_head upload moves 311 MB); two
+ * threads that miss on the same arrays both upload, and the second to
+ * insert takes the first one's entry and frees its own copy.  The LRU
+ * eviction runs at the insert, so the budget can be exceeded by the matrices
+ * in flight. */
 static int registry_get(const int8_t* w, const float* s, int rows, int cols, hipStream_t st, WRef** out) {
   REQ(w && s, "weight and scale pointers must be non-NULL");
   int dev;
   TRY(tlh_current_device(&dev));
   const uint64_t fp = fingerprint(w, s, rows, cols);
-  int rc = 0;
   pthread_mutex_lock(&g_reg_mu);
   RegNode** pp = reg_find_locked(w, s, rows, cols, dev);
-  if (pp) {
-    if ((*pp)->fp == fp) {
-      (*pp)->tick = ++g_tick;
-      *out = wref_take((*pp)->ref);
-      pthread_mutex_unlock(&g_reg_mu);
-      return 0;
-    }
-    reg_erase_locked(pp);   /* contents changed in place: re-upload */
+  if (pp && (*pp)->fp == fp) {
+    (*pp)->tick = ++g_tick;
+    *out = wref_take((*pp)->ref);
+    pthread_mutex_unlock(&g_reg_mu);
+    return 0;
   }
-  const size_t need = (size_t)tlk_cdiv(rows, 16) * 16 * (size_t)tlk_cdiv(cols, 64) * 64 + (size_t)rows * 4;
-  registry_evict_lru_locked(need);
+  pthread_mutex_unlock(&g_reg_mu);
   tl_weights* W = NULL;
-  TRY_GO(tlh_weights_from_codes(w, s, rows, cols, false, st, &W), done);
+  TRY(tlh_weights_from_codes(w, s, rows, cols, false, st, &W));
   WRef* ref = wref_new(W);
   if (!ref) {
     tlh_weights_free(W);
-    rc = tlh_fail("out of host memory");
-    goto done;
+    return tlh_fail("out of host memory");
   }
-  if (reg_insert_locked(w, s, dev, ref, fp) != 0) {
+  pthread_mutex_lock(&g_reg_mu);
+  pp = reg_find_locked(w, s, rows, cols, dev);
+  if (pp && (*pp)->fp == fp) {              /* another thread's upload of the same contents won */
+    (*pp)->tick = ++g_tick;
+    *out = wref_take((*pp)->ref);
+    pthread_mutex_unlock(&g_reg_mu);
     wref_drop(ref);
-    rc = -1;
-    goto done;
+    return 0;
+  }
+  if (pp) reg_erase_locked(pp);             /* contents changed in place: replace */
+  registry_evict_lru_locked(W->bytes);
+  if (reg_insert_locked(w, s, dev, ref, fp) != 0) {
+    pthread_mutex_unlock(&g_reg_mu);
+    wref_drop(ref);
+    return -1;
   }
   *out = wref_take(ref);
-done:
   pthread_mutex_unlock(&g_reg_mu);
-  return rc;
+  return 0;
 }
 
 /* makes W (owned by the registry from here on) the entry of host arrays
@@ -552,7 +562,7 @@ static int quantize_padded(Workspace* ws, const float* x, int K, hipStream_t st,
   const int kpad = tlk_cdiv(K, 64) * 64;
   TRY(tlh_devbuf_ensure(&ws->act, (size_t)kpad, st));
   TRY(tlh_devbuf_ensure(&ws->act_s, sizeof(float), st));
-  HIP_TRY(hipMemsetAsync(ws->act.p, 0, (size_t)kpad, st));
+  HIP_TRY(tlk_launch_copy_pad_bytes(NULL, 0, ws->act.p, (size_t)kpad, st));   /* zero padding, a kernel node */
   HIP_TRY(tlk_launch_quantize_rows(x, (int8_t*)ws->act.p, (float*)ws->act_s.p, 1, K, false, st));
   *xs_dev = (float*)ws->act_s.p;
   *codes = (uint8_t*)ws->act.p;
@@ -598,12 +608,13 @@ static int run_gemm(Workspace* ws, GemmLaunch* L, hipStream_t st) {
 
 /* 1..8 rows with fp32 semantics as int8 digit planes (rows.hip); *done = false
  * when the shape or alignment is not one it takes, or the path is switched off */
-static bool g_rows_off = false;
-static bool g_gemv_w8a16_off = false;   /* tuning: W8A16 batch 1 on the bf16 / fp16 MFMA kernel instead */
+/* tuning switches; atomic, since a setter may run while other threads call */
+static atomic_bool g_rows_off = false;
+static atomic_bool g_gemv_w8a16_off = false;   /* W8A16 batch 1 on the bf16 / fp16 MFMA kernel instead */
 
 static int run_rows(Workspace* ws, GemmLaunch* L, hipStream_t st, bool* done) {
   *done = false;
-  if (g_rows_off || !tlk_rows_supported(L)) return 0;
+  if (atomic_load_explicit(&g_rows_off, memory_order_relaxed) || !tlk_rows_supported(L)) return 0;
   RowsPlan p;
   tlk_rows_plan(L->M, L->N, L->K, &p);
   if (p.split > 1) {
@@ -713,8 +724,7 @@ static int op_w8a8_codes_ws(Workspace* ws, const int8_t* xq, const float* xs, co
     /* codes must be zero padded to KB*64 for the GEMV */
     const int kpad = KB * 64;
     TRY(tlh_devbuf_ensure(&ws->act, (size_t)kpad, st));
-    if (kpad != K) HIP_TRY(hipMemsetAsync(ws->act.p, 0, (size_t)kpad, st));
-    HIP_TRY(hipMemcpyAsync(ws->act.p, xq, (size_t)K, hipMemcpyDeviceToDevice, st));
+    HIP_TRY(tlk_launch_copy_pad_bytes(xq, (size_t)K, ws->act.p, (size_t)kpad, st));
     GemvLaunch L = tlk_gemv_launch_init();
     L.xq = (const uint8_t*)ws->act.p;
     L.xs_in = xs;
@@ -827,7 +837,7 @@ static int op_w8a16_ws(Workspace* ws, const void* X, int x_type, const tl_weight
    * adds it after the product (:193-200) */
   L.ep = (batch == 1) ? EP_SCALE_FMA : EP_SCALE;
   L.out = (y_type == TL_F32) ? OUT_F32 : (y_type == TL_BF16 ? OUT_BF16 : OUT_F16);
-  if (batch == 1 && tlk_gemv_fused_xv(W->cols) > 0 && !g_gemv_w8a16_off) {
+  if (batch == 1 && tlk_gemv_fused_xv(W->cols) > 0 && !atomic_load_explicit(&g_gemv_w8a16_off, memory_order_relaxed)) {
     /* one token: the GEMV's weight stream with x as four int8 digit rows
      * (fp32-accurate products, y = fma(sum, ws, bias) as the reference's
      * r * ws + b) */
@@ -1253,7 +1263,7 @@ int tl_gemv_set_plan(int rows, int u) {
 
 static int rows_set_split_impl(int split) {
   REQ(split >= -1 && split <= 64, "split must be -1 (path off), 0 (planner) or 1..64");
-  g_rows_off = split < 0;
+  atomic_store_explicit(&g_rows_off, split < 0, memory_order_relaxed);
   tlk_rows_set_split(split > 0 ? split : 0);
   return 0;
 }
@@ -1274,7 +1284,7 @@ int tl_rows_set_groups(int groups) {
 
 static int w8a16_set_gemv_impl(int on) {
   REQ(on == 0 || on == 1, "on must be 0 or 1");
-  g_gemv_w8a16_off = on == 0;
+  atomic_store_explicit(&g_gemv_w8a16_off, on == 0, memory_order_relaxed);
   return 0;
 }
 int tl_w8a16_set_gemv(int on) {

@@ -359,9 +359,29 @@ __global__ __launch_bounds__(256) void copy_words_kernel(const uint32_t* __restr
   }
 }
 
+// Byte copy with zero padding: dst[i] = src[i] for i < n, 0 for n <= i < npad
+// (src may be null when n == 0).  Clears or pads a small code vector inside
+// the stream's kernel order, so that a caller capturing the call into a HIP
+// graph records a kernel node rather than a memset node.
+__global__ __launch_bounds__(256) void copy_pad_bytes_kernel(const uint8_t* __restrict__ src, long long n,
+                                                             uint8_t* __restrict__ dst, long long npad) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i < npad) dst[i] = i < n ? src[i] : (uint8_t)0;
+}
+
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
+hipError_t launch_copy_pad_bytes(const void* src, size_t n, void* dst, size_t npad, hipStream_t st) {
+  if (npad == 0) return hipSuccess;
+  if (!dst || n > npad || (n > 0 && !src)) return hipErrorInvalidValue;
+  const long long blocks = ((long long)npad + 255) / 256;
+  if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(copy_pad_bytes_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                     static_cast<const uint8_t*>(src), (long long)n, static_cast<uint8_t*>(dst), (long long)npad);
+  return hipGetLastError();
+}
+
 hipError_t launch_copy_words(const void* src, void* dst, size_t bytes, hipStream_t st) {
   if (bytes == 0) return hipSuccess;
   if (bytes & 3) return hipErrorInvalidValue;
@@ -459,5 +479,8 @@ hipError_t tlk_launch_split_i8x4(const float* X, int ldx, int M, int K, uint8_t*
 }
 hipError_t tlk_launch_copy_words(const void* src, void* dst, size_t bytes, hipStream_t st) {
   return tl::launch_copy_words(src, dst, bytes, st);
+}
+hipError_t tlk_launch_copy_pad_bytes(const void* src, size_t n, void* dst, size_t npad, hipStream_t st) {
+  return tl::launch_copy_pad_bytes(src, n, dst, npad, st);
 }
 }  // extern "C"

@@ -66,6 +66,9 @@ hipError_t tlk_launch_unpack_tiles(const uint8_t* tiles, int rows, int cols, int
 hipError_t tlk_launch_split_i8x4(const float* X, int ldx, int M, int K, uint8_t* tiles, int* xe, hipStream_t st);
 // 4-byte-word copy by a kernel (bytes % 4 == 0), e.g. from mapped pinned host memory
 hipError_t tlk_launch_copy_words(const void* src, void* dst, size_t bytes, hipStream_t st);
+// dst[0, npad) = src[0, n) followed by zeros, by a kernel (src null when n == 0):
+// padding that stays a kernel node when the caller captures the stream
+hipError_t tlk_launch_copy_pad_bytes(const void* src, size_t n, void* dst, size_t npad, hipStream_t st);
 // one streaming read of `bytes` (a multiple of 16, 16-byte aligned) by grid
 // work-groups of 256 lanes with u (4 or 8) 16-byte loads in flight each
 // (stream.hip): the read floor of a launch that moves those bytes
@@ -276,6 +279,7 @@ hipError_t launch_argmax_keys(const uint64_t* keys, int n, int32_t* token, float
 hipError_t launch_split_i8x4(const float* X, int ldx, int M, int K, uint8_t* tiles, int* xe, hipStream_t st);
 hipError_t launch_stream_read(const void* p, size_t bytes, int grid, int u, uint32_t* sink, hipStream_t st);
 hipError_t launch_copy_words(const void* src, void* dst, size_t bytes, hipStream_t st);
+hipError_t launch_copy_pad_bytes(const void* src, size_t n, void* dst, size_t npad, hipStream_t st);
 
 int attn_chunks(int max_seq);
 int attn_chunk_size(int max_seq);
