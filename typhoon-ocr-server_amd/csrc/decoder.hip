@@ -22,6 +22,8 @@
 //
 // KV cache: per layer and kv head [max_seq][128] fp32 (head-first, as the
 // reference's kv_cache.c), K and V in separate arrays.
+#include <atomic>
+
 #include "tl_common.h"
 #include "tl_kernels.h"
 
@@ -244,6 +246,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const int* __restrict_
   if (tid == 0) s_last = __hip_atomic_fetch_add(a.count + h, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nc - 1;
   __syncthreads();
   if (!s_last) return;
+  // the merger's acquire: the chunks' partials are read after the counter
+  // showed them all arrived (agent scope; once per kv head and token)
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 
   // out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c, M = max_c m_c, in
   // chunk order over rounds of kMergeRound chunks (one round up to 2048
@@ -347,13 +352,16 @@ __global__ __launch_bounds__(1024) void step_end_kernel(const uint64_t* __restri
   }
 }
 
-static int g_attn_t = 0;   // positions per work-group override (tuning), 0 = planner
+// positions per work-group override (tuning), 0 = planner; atomic, since a
+// setter may run while other threads plan launches
+static std::atomic<int> g_attn_t{0};
 
-void attn_set_chunk(int t) { g_attn_t = (t == 32 || t == 64 || t == 128) ? t : 0; }
+void attn_set_chunk(int t) { g_attn_t.store((t == 32 || t == 64 || t == 128) ? t : 0, std::memory_order_relaxed); }
 
 int attn_chunk_size(int max_seq) {
   (void)max_seq;
-  return g_attn_t ? g_attn_t : 64;
+  const int t = g_attn_t.load(std::memory_order_relaxed);
+  return t ? t : 64;
 }
 
 int attn_chunks(int max_seq) { return cdiv(max_seq, 32); }   // records per q head for the smallest chunks

@@ -528,6 +528,9 @@ __global__ __launch_bounds__(256) void flash_prefill_mfma_kernel(const float* __
     if (tid == 0) s_last = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
     __syncthreads();
     if (!s_last) return;
+    // the merger's acquire: the other half is read after the counter showed
+    // it arrived (agent scope; once per split tile)
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (tid == 0) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // combine half 0 and half 1 in that order
     const float* other = part + ((size_t)(qt * nheads + qh) * 2 + (1 - half)) * FPART;

@@ -38,6 +38,8 @@
 //     stores, and resets the counter.  Nothing waits on another work-group.
 // A token whose slice holds Inf or NaN gets NaN outputs (the reference's
 // sums give NaN or +-Inf there).
+#include <atomic>
+
 #include "tl_common.h"
 #include "tl_kernels.h"
 
@@ -301,6 +303,9 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
   if (lane == 0) last = __hip_atomic_fetch_add(a.cnt + gg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.S - 1);
   last = __shfl(last, 0, 64);
   if (!last) return;
+  // the winner's acquire: the other slices' partials are read after the
+  // counter showed them all arrived (agent scope; once per row group)
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   asm volatile("" ::: "memory");
   if (owner) {
 #pragma unroll
@@ -328,10 +333,11 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
 // ---------------------------------------------------------------------------
 // planner and launcher
 // ---------------------------------------------------------------------------
-static int g_rows_force_split = 0;
-static int g_rows_force_groups = 0;
-void rows_set_split(int s) { g_rows_force_split = s > 0 ? s : 0; }
-void rows_set_groups(int r) { g_rows_force_groups = r > 0 ? r : 0; }
+// tuning overrides; atomic, since a setter may run while other threads plan launches
+static std::atomic<int> g_rows_force_split{0};
+static std::atomic<int> g_rows_force_groups{0};
+void rows_set_split(int s) { g_rows_force_split.store(s > 0 ? s : 0, std::memory_order_relaxed); }
+void rows_set_groups(int r) { g_rows_force_groups.store(r > 0 ? r : 0, std::memory_order_relaxed); }
 
 bool rows_supported(const GemmLaunch& L) {
   if (L.M < 1 || L.M > 8 || L.N < 1 || L.K < 1) return false;
@@ -363,7 +369,8 @@ RowsPlan rows_plan(int M, int N, int K) {
   const int mp = M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8));
   const int kmax = min(p.tg == 1 ? (mp <= 2 ? 96 : 64) : 32, 256 / mp);
   int s = cdiv(KB, kmax);
-  if (g_rows_force_split > 0) s = max(s, min(g_rows_force_split, KB));
+  const int force_split = g_rows_force_split.load(std::memory_order_relaxed);
+  if (force_split > 0) s = max(s, min(force_split, KB));
   p.kbs = cdiv(KB, s);
   p.split = cdiv(KB, p.kbs);                // every slice holds >= 1 k-block
   p.nkb = p.kbs <= 16 ? 16 : (p.kbs <= 32 ? 32 : (p.kbs <= 64 ? 64 : 96));
@@ -371,7 +378,8 @@ RowsPlan rows_plan(int M, int N, int K) {
   p.cpt = nch <= 256 ? 1 : (nch <= 512 ? 2 : 4);
   p.r = 1;
   if (p.nkb <= 32) {   // the instances built for R > 1
-    if (g_rows_force_groups > 0) p.r = g_rows_force_groups;
+    const int force_groups = g_rows_force_groups.load(std::memory_order_relaxed);
+    if (force_groups > 0) p.r = force_groups;
     else if (p.tg == 2)
       for (int r = 3; r > 1; r--)
         if (cdiv(NG, r) * p.split >= 256) {
