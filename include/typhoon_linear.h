@@ -110,6 +110,13 @@ int tl_gemv_set_plan(int rows, int u);
  * prefetch 7). */
 int tl_gemm_i8_set_cfg(int cfg);
 
+/* Tuning override of the 16-bit MFMA GEMM (W8A16, M > 16 on the tiled
+ * kernel) for every later call in the process: cfg -1 restores the planner's
+ * tile, 0..2 force 128x192, 64x128 or 32x64 tiles; split 0 restores the
+ * planner's K slices, 1..64 force that many (work-groups per tile, whose fp32
+ * partial sums the last to arrive adds in slice order). */
+int tl_gemm_b16_set_plan(int cfg, int split);
+
 /* Tuning override of the 2..8-row kernel of w8a32_linear (int8 digit planes
  * of the fp32 activations) for every later call in the process: 1..64 K
  * slices per weight row group (at least as many as its LDS and registers

@@ -725,3 +725,42 @@ def test_batch1_padded_paths_capture_into_a_graph(lin, orc, dev, path, K):
         np.testing.assert_array_equal(eager, want)
     del g
     W.close()
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 2048, 2048), (200, 1000, 1000), (256, 4096, 2048)])
+def test_w8a16_k_slices(lin, orc, dev, M, N, K):
+    """The 16-bit GEMM with its K range split over 1..4 work-groups per tile
+    (every tile configuration, forced through tl_gemm_b16_set_plan; uneven
+    slices where the K blocks do not divide): fp32 out within 1e-5 and bf16
+    out within 2e-3 of a float64 product in every row, and a repeated call
+    bit-identical (the last work-group to arrive adds the slices in slice
+    order, whichever it is)."""
+    import torch
+    lib = lin.load_library()
+    rng = np.random.default_rng(M * 3 + N + K)
+    x, w, s = make(rng, M, N, K)
+    W = lin.DeviceWeights.from_codes(w, s)
+    xt = torch.from_numpy(x).to(dev).to(torch.bfloat16)
+    want = (xt.float().cpu().numpy().astype(np.float64) @ w.astype(np.float64).T) * s.astype(np.float64)
+    y32 = torch.empty((M, N), dtype=torch.float32, device=dev)
+    yb = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    try:
+        for cfg in (0, 1, 2):
+            for split in (1, 2, 3, 4):
+                say(f"w8a16 K slices M={M} N={N} K={K} cfg={cfg} split={split}")
+                assert lib.tl_gemm_b16_set_plan(cfg, split) == 0
+                lin.w8a16_linear_dev(xt, W, y32)
+                lin.w8a16_linear_dev(xt, W, yb)
+                torch.cuda.synchronize()
+                first = y32.cpu().numpy().copy()
+                e = row_rel_l2(first, want)
+                assert e.max() <= 1e-5, (cfg, split, int(e.argmax()), float(e.max()))
+                e = row_rel_l2(yb.float().cpu().numpy(), want)
+                assert e.max() <= 2e-3, (cfg, split, int(e.argmax()), float(e.max()))
+                y32.fill_(np.nan)
+                lin.w8a16_linear_dev(xt, W, y32)
+                torch.cuda.synchronize()
+                np.testing.assert_array_equal(y32.cpu().numpy(), first)
+    finally:
+        lib.tl_gemm_b16_set_plan(-1, 0)
+    W.close()

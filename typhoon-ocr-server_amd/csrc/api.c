@@ -595,12 +595,12 @@ done:
 
 static int run_gemm(Workspace* ws, GemmLaunch* L, hipStream_t st) {
   TRY(zero_tile(&L->zero_tile));
-  GemmPlan p;
-  tlk_gemm_plan(L->amode, L->M, L->N, L->K, &p);
-  if (p.split > 1) {
-    TRY(tlh_devbuf_ensure(&ws->part, tlk_gemm_workspace_bytes(L->amode, L->M, L->N, L->K), st));
+  size_t part_bytes = 0, counters = 0;
+  tlk_gemm_needs(L, &part_bytes, &counters);
+  if (part_bytes > 0) {
+    TRY(tlh_devbuf_ensure(&ws->part, part_bytes, st));
     L->part = ws->part.p;
-    TRY(ensure_counters(ws, tlk_gemm_counter_count(L->amode, L->M, L->N, L->K), st, &L->cnt));
+    TRY(ensure_counters(ws, counters, st, &L->cnt));
   }
   HIP_TRY(tlk_launch_gemm(L, st));
   return 0;
@@ -1300,6 +1300,17 @@ static int gemm_i8_set_cfg_impl(int cfg) {
 int tl_gemm_i8_set_cfg(int cfg) {
   tlh_begin();
   return tlh_finish("tl_gemm_i8_set_cfg", gemm_i8_set_cfg_impl(cfg));
+}
+
+static int gemm_b16_set_plan_impl(int cfg, int split) {
+  REQ(cfg >= -1 && cfg <= 2, "cfg must be -1 (planner) or 0..2");
+  REQ(split >= 0 && split <= 64, "split must be 0 (planner) or 1..64");
+  tlk_gemm_b16_set_plan(cfg, split);
+  return 0;
+}
+int tl_gemm_b16_set_plan(int cfg, int split) {
+  tlh_begin();
+  return tlh_finish("tl_gemm_b16_set_plan", gemm_b16_set_plan_impl(cfg, split));
 }
 
 static int stream_read_impl(const void* p, size_t bytes, int grid, int u, uint32_t* sink, void* stream) {

@@ -383,6 +383,46 @@ static hipError_t launch_mode(const GemmArgs& a, int cfg, int blocks, hipStream_
   return hipGetLastError();
 }
 
+// which kernel launch_gemm runs for L
+enum GemmKernel { GK_SMALL, GK_I8, GK_B16, GK_GENERIC };
+static GemmKernel gemm_choice(const GemmLaunch& L) {
+  // up to 16 token rows always stream the weights once; more rows too while N
+  // is small (N <= 4096: the tiled kernels would leave CUs idle), up to 64
+  // int8 rows and 48 16-bit rows (measured at N = 2048 / 4096: 64 bf16 rows
+  // 14.1 us here against 11.3 us tiled, 48 rows even, 32 rows 8.2 against
+  // 11.4 us; int8 rows faster here up to 64); for wide N the activation
+  // fragments every work-group re-reads cost more than the tiled kernels' reuse,
+  // except up to 32 int8 rows at lm_head width (>= 2048 row groups, four per
+  // work-group share each fragment): the int8 planes of 5-8 fp32 tokens,
+  // 81 -> 70 us for the lm_head at 8 tokens
+  const int small_rows = (L.amode == A_BF16 || L.amode == A_F16) ? 48 : 64;
+  const bool wide_i8 = L.amode == A_I8 && L.M <= 32 && cdiv(L.N, 16) >= 2048;
+  if (gemm_small_supported(L) && (L.M <= 16 || (L.M <= small_rows && cdiv(L.N, 16) <= 256) || wide_i8))
+    return GK_SMALL;
+  if (L.amode == A_I8 && L.M > 16) return GK_I8;
+  if (L.amode != A_I8 && L.M > 16 && gemm_b16_supported(L)) return GK_B16;
+  return GK_GENERIC;
+}
+
+// split work-space of the kernel launch_gemm picks for L: partial-sum bytes
+// and zeroed arrival counters (0 and 0 when it needs none)
+void gemm_needs(const GemmLaunch& L, size_t* part_bytes, size_t* counters) {
+  *part_bytes = 0;
+  *counters = 0;
+  switch (gemm_choice(L)) {
+    case GK_SMALL:
+    case GK_I8: return;
+    case GK_B16: gemm_b16_needs(L.M, L.N, L.K, part_bytes, counters); return;
+    default: break;
+  }
+  GemmPlan p = gemm_plan(L.amode, L.M, L.N, L.K);
+  if (L.force_split > 0) p.split = L.force_split;
+  if (p.split > 1) {
+    *part_bytes = (size_t)p.split * cdiv(L.M, 16) * 16 * (size_t)cdiv(L.N, 16) * 16 * 4;
+    *counters = (size_t)p.ntm * p.ntn;
+  }
+}
+
 hipError_t launch_gemm(const GemmLaunch& L, hipStream_t st) {
   GemmArgs a;
   a.A = L.A;
@@ -410,24 +450,16 @@ hipError_t launch_gemm(const GemmLaunch& L, hipStream_t st) {
   a.ntn = p.ntn;
   a.part = L.part;
   a.cnt = L.cnt;
-  if (p.split > 1 && (!L.part || !L.cnt)) return hipErrorInvalidValue;
   if (L.amode == A_I8 && L.out != OUT_I32 && L.out != OUT_F32_X4 && !L.xs) return hipErrorInvalidValue;
   if (L.out == OUT_F32_X4 && L.amode != A_I8) return hipErrorInvalidValue;
-  // up to 16 token rows always stream the weights once; more rows too while N
-  // is small (N <= 4096: the tiled kernels would leave CUs idle), up to 64
-  // int8 rows and 48 16-bit rows (measured at N = 2048 / 4096: 64 bf16 rows
-  // 14.1 us here against 11.3 us tiled, 48 rows even, 32 rows 8.2 against
-  // 11.4 us; int8 rows faster here up to 64); for wide N the activation
-  // fragments every work-group re-reads cost more than the tiled kernels' reuse,
-  // except up to 32 int8 rows at lm_head width (>= 2048 row groups, four per
-  // work-group share each fragment): the int8 planes of 5-8 fp32 tokens,
-  // 81 -> 70 us for the lm_head at 8 tokens
-  const int small_rows = (L.amode == A_BF16 || L.amode == A_F16) ? 48 : 64;
-  const bool wide_i8 = L.amode == A_I8 && L.M <= 32 && cdiv(L.N, 16) >= 2048;
-  if (gemm_small_supported(L) && (L.M <= 16 || (L.M <= small_rows && cdiv(L.N, 16) <= 256) || wide_i8))
-    return launch_gemm_small(L, st);
-  if (L.amode == A_I8 && L.M > 16) return launch_gemm_i8(L, st);
-  if (L.amode != A_I8 && L.M > 16 && gemm_b16_supported(L)) return launch_gemm_b16(L, st);
+  switch (gemm_choice(L)) {
+    case GK_SMALL: return launch_gemm_small(L, st);
+    case GK_I8: return launch_gemm_i8(L, st);
+    case GK_B16: return launch_gemm_b16(L, st);
+    default: break;
+  }
+  // the generic kernel's K split needs the work-space gemm_needs reports
+  if (p.split > 1 && (!L.part || !L.cnt)) return hipErrorInvalidValue;
   switch (L.amode) {
     case A_I8: return launch_mode<A_I8>(a, p.cfg, p.blocks, st);
     case A_BF16: return launch_mode<A_BF16>(a, p.cfg, p.blocks, st);
@@ -449,4 +481,8 @@ size_t tlk_gemm_workspace_bytes(int amode, int M, int N, int K) {
 }
 size_t tlk_gemm_counter_count(int amode, int M, int N, int K) { return tl::gemm_counter_count(amode, M, N, K); }
 hipError_t tlk_launch_gemm(const GemmLaunch* L, hipStream_t st) { return tl::launch_gemm(*L, st); }
+void tlk_gemm_needs(const GemmLaunch* L, size_t* part_bytes, size_t* counters) {
+  tl::gemm_needs(*L, part_bytes, counters);
+}
+void tlk_gemm_b16_set_plan(int cfg, int split) { tl::gemm_b16_set_plan(cfg, split); }
 }  // extern "C"

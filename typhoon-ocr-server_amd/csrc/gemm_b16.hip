@@ -18,6 +18,7 @@
 // stay int8 in LDS and are widened to bf16/fp16 in registers after the read.
 // Lanes whose row is past M or whose k is past K copy 16 bytes of zeros.
 #include <algorithm>
+#include <atomic>
 
 #include "tl_common.h"
 #include "tl_kernels.h"
@@ -38,6 +39,9 @@ struct GemmB16Args {
   int ntm, ntn;
   int ep, out;
   const uint8_t* zero_tile;
+  int S;                 // K slices per tile (work-groups per tile)
+  float* part;           // S > 1: fp32 partial tiles [tiles][S][MT*16 x NT*16]
+  uint32_t* cnt;         // S > 1: zeroed arrival counters [tiles]
 };
 
 __device__ inline v8bf as_bf(uint4 u) { return __builtin_bit_cast(v8bf, u); }
@@ -104,9 +108,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wv / WN, wn = wv % WN;
 
+  // work-group b: K slice b / ntiles of tile b % ntiles; with ntiles a
+  // multiple of 8 the tiles are grouped per XCD (b % 8) as ntiles / 8
+  // consecutive tile indices
   const int ntiles = a.ntm * a.ntn;
-  int t = blockIdx.x;
-  if (ntiles % 8 == 0) t = (blockIdx.x % 8) * (ntiles / 8) + blockIdx.x / 8;
+  const int ks = blockIdx.x / ntiles;
+  const int bt = blockIdx.x - ks * ntiles;
+  int t = bt;
+  if (ntiles % 8 == 0) t = (bt % 8) * (ntiles / 8) + bt / 8;
   const int tn = t / a.ntm, tm = t - (t / a.ntm) * a.ntm;
   const int mg0 = tm * MT, ng0 = tn * NT;
 
@@ -114,7 +123,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
   const uint4* Z4 = reinterpret_cast<const uint4*>(a.zero_tile);   // any 16 zero bytes
   const char* Xb = static_cast<const char*>(a.X);
   const int KB = a.KB;
-  const int nst = KB;
+  const int kb0 = (ks * KB) / a.S;                     // this work-group's K blocks [kb0, kb0 + nst)
+  const int nst = ((ks + 1) * KB) / a.S - kb0;
 
   // per copy: source for stage 0 and its advance per stage
   const char* qsrc[PW];
@@ -141,9 +151,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
   }
   const size_t bstride = (size_t)a.NG * 1024;   // bytes between K blocks of the weights
   // Every call issues exactly PW copies, so the explicit vmcnt waits in `step`
-  // count exactly: stages past the end of K re-read the last K block into a
-  // buffer that no step reads again.  (Skipping those copies would let the
-  // last NST-2 steps' waits return before their own stage had landed.)
+  // count exactly: stages past the end of the work-group's K range re-read its
+  // last K block into a buffer that no step reads again.  (Skipping those
+  // copies would let the last NST-2 steps' waits return before their own
+  // stage had landed; waiting for every copy there instead measured 7% slower
+  // at M = 64..256.)
   // K a multiple of 64 (no piece past K): each copy is a per-lane byte offset
   // from a uniform per-stage base (rows past M read row M - 1; their outputs
   // are never stored)
@@ -153,7 +165,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
   for (int p = 0; p < PW; p++)
     qvo[p] = (uint32_t)(qsrc[p] - (qkoff[p] >= 0 ? Xb : reinterpret_cast<const char*>(a.Bt)));
   auto issue = [&](int st, uint4* buf) {
-    const int sc = min(st, nst - 1);
+    const int sc = kb0 + min(st, nst - 1);
     const uint32_t base = lds_addr(buf);
     if constexpr (kfull) {
       const char* sa = Xb + (size_t)sc * 64 * ESZ;
@@ -175,7 +187,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
     }
   };
 
-  // epilogue operands (transposed accumulators: lane holds row m, cols n..n+3)
+  // prologue: stages 0 .. NST-1 in flight first
+#pragma unroll
+  for (int b = 0; b < NST; b++) issue(b, ring[b]);
+  // epilogue operands (transposed accumulators: lane holds row m, cols
+  // n..n+3), loaded behind the first copies: the stage waits below then
+  // also cover them (loads complete in issue order, so the extra loads only
+  // make the first waits stricter), and the loop's last wait leaves them done
   const int mrow = lane & 15;
   const int ncol = (lane >> 4) * 4;
   float e_ws[FN][4], e_b[FN][4];
@@ -187,7 +205,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
       e_ws[j][r] = a.ws[n];
       e_b[j][r] = a.bias ? a.bias[n] : 0.0f;
     }
-  wait_vm<0>();
 
   v4f acc[FM][FN];
 #pragma unroll
@@ -254,9 +271,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // prologue: stages 0 .. NST-1 in flight, stage 0's fragments read
-#pragma unroll
-  for (int b = 0; b < NST; b++) issue(b, ring[b]);
+  // stage 0 landed (and the epilogue operands), its fragments read
   wait_vm<PW * (NST - 1)>();
   stage_barrier();
   read_frags(ring[0], 0);
@@ -267,6 +282,62 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
     for (int b = 0; b < NST; b++) step(st + b, ring[b], ring[(b + 1) % NST], b & 1);
   }
   wait_vm<0>();   // no copy may still be landing in LDS when the work-group exits
+
+  if (a.S > 1) {
+    // K slices: every work-group of the tile stores its fp32 sums, waits for
+    // the stores' acknowledgement and counts in; the last to arrive adds the
+    // S slices in slice order (its own from registers, the same sums and
+    // order whichever work-group merges), then runs the epilogue below
+    constexpr int TF = MT * 16 * NT * 16;
+    float* mine = a.part + ((size_t)bt * a.S + ks) * TF;
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++) st_agent4(mine + (((wv * FM + i) * FN + j) * 64 + lane) * 4, acc[i][j]);
+    __shared__ int s_last;
+    asm volatile("" ::: "memory");
+    wait_vm<0>();                               // this thread's partial stores are acknowledged
+    asm volatile("" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(a.cnt + bt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.S - 1);
+    __syncthreads();
+    if (!s_last) return;
+    // the merger's acquire: the slices are read after the counter showed
+    // them all arrived (agent scope, once per tile: it invalidates this
+    // CU's caches, so the plain 16-byte loads below fetch what the stores
+    // wrote through).  All S slices come from memory, this work-group's own
+    // too (the values it stored), one slice's loads in flight at a time and
+    // added in slice order.
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // QB slices' loads are in flight together (indices past S re-read the
+    // last slice and are not added)
+    constexpr int QB = FM * FN <= 2 ? 8 : (FM * FN <= 8 ? 4 : 1);
+    const float* slices = a.part + (size_t)bt * a.S * TF;
+    for (int q0 = 0; q0 < a.S; q0 += QB) {
+      v4f p[QB][FM][FN];
+#pragma unroll
+      for (int u = 0; u < QB; u++)
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+          for (int j = 0; j < FN; j++)
+            p[u][i][j] = *reinterpret_cast<const v4f*>(slices + (size_t)min(q0 + u, a.S - 1) * TF +
+                                                      (((wv * FM + i) * FN + j) * 64 + lane) * 4);
+#pragma unroll
+      for (int u = 0; u < QB; u++) {
+        if (q0 + u >= a.S) break;
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+          for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+              acc[i][j][r] = q0 + u == 0 ? p[u][i][j][r] : __fadd_rn(acc[i][j][r], p[u][i][j][r]);
+      }
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(a.cnt + bt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 
   const bool vec_ok = ((a.ldy & 3) == 0) &&
                       ((((uintptr_t)a.Y) & (a.out == OUT_F32 ? 15 : 7)) == 0);
@@ -327,22 +398,67 @@ static void b16_cfg(int cfg, int& mt, int& nt) {
   nt = (cfg == 0) ? 12 : (cfg == 1 ? 8 : 4);
 }
 
-// the configuration whose tile count best fills 256 CUs (measured best over
-// the W8A16 sweep)
-static int b16_pick_cfg(int MG, int NG) {
-  int best = 0;
-  double best_eff = -1.0;
-  for (int cfg : {0, 1, 2}) {
-    int mt, nt;
-    b16_cfg(cfg, mt, nt);
-    const int tiles = cdiv(MG, mt) * cdiv(NG, nt);
-    const double eff = (double)tiles / (cdiv(tiles, 256) * 256);
-    if (eff > best_eff + 1e-9) {
-      best_eff = eff;
-      best = cfg;
+// Plan: tile configuration and K slices, from the measured W8A16 sweep
+// (M = 64 .. 1024, N = 2048 .. 12288, K = 2048, every configuration and
+// 1..8 slices): the 32 x 64 tiles while they number at most 512 (two
+// work-groups of 64 KiB share a CU), else the 64 x 128 tiles while they fit
+// one wave of 256 CUs, else the 128 x 192 tiles while they do, else the
+// configuration whose tile count best fills 256 CUs.  The loop is bound by
+// the latency of its stage copies rather than by bytes, so K slices pay only
+// where the tiles are few: at most 64 tiles are split until 256 work-groups
+// run (M = 64, N = 2048: 11.4 -> 10.5 us); with more tiles the slices' store,
+// arrival and reload cost more than they save.
+static std::atomic<int> g_b16_force_cfg{-1};
+static std::atomic<int> g_b16_force_split{0};
+void gemm_b16_set_plan(int cfg, int split) {
+  g_b16_force_cfg.store(cfg >= 0 && cfg <= 2 ? cfg : -1, std::memory_order_relaxed);
+  g_b16_force_split.store(split > 0 ? split : 0, std::memory_order_relaxed);
+}
+
+static int b16_tiles(int cfg, int MG, int NG) {
+  int mt, nt;
+  b16_cfg(cfg, mt, nt);
+  return cdiv(MG, mt) * cdiv(NG, nt);
+}
+
+static void b16_plan(int MG, int NG, int KB, int& cfg_out, int& split_out) {
+  int best;
+  if (b16_tiles(2, MG, NG) <= 512) best = 2;
+  else if (b16_tiles(1, MG, NG) <= 256) best = 1;
+  else if (b16_tiles(0, MG, NG) <= 256) best = 0;
+  else {
+    best = 0;
+    double best_eff = -1.0;
+    for (int cfg : {0, 1, 2}) {
+      const int tiles = b16_tiles(cfg, MG, NG);
+      const double eff = (double)tiles / (cdiv(tiles, 256) * 256);
+      if (eff > best_eff + 1e-9) {
+        best_eff = eff;
+        best = cfg;
+      }
     }
   }
-  return best;
+  const int tiles = b16_tiles(best, MG, NG);
+  int sp = 1;
+  if (tiles <= 64) sp = std::min(std::max(1, 256 / tiles), std::max(1, KB / 8));
+  sp = std::min(sp, 4);
+  const int fc = g_b16_force_cfg.load(std::memory_order_relaxed);
+  const int fs = g_b16_force_split.load(std::memory_order_relaxed);
+  if (fc >= 0) best = fc;
+  if (fs > 0) sp = std::min(fs, std::max(1, KB));
+  cfg_out = best;
+  split_out = sp;
+}
+
+// partial-sum bytes and arrival counters the launch of this shape needs
+void gemm_b16_needs(int M, int N, int K, size_t* part_bytes, size_t* counters) {
+  int cfg, sp, mt, nt;
+  const int MG = cdiv(M, 16), NG = cdiv(N, 16);
+  b16_plan(MG, NG, cdiv(K, 64), cfg, sp);
+  b16_cfg(cfg, mt, nt);
+  const size_t tiles = (size_t)cdiv(MG, mt) * cdiv(NG, nt);
+  *part_bytes = sp > 1 ? tiles * sp * (size_t)(256 * mt * nt) * sizeof(float) : 0;
+  *counters = sp > 1 ? tiles : 0;
 }
 
 template <int AMODE, bool KF>
@@ -378,12 +494,19 @@ hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st) {
   a.ep = L.ep;
   a.out = L.out;
   a.zero_tile = L.zero_tile;
-  const int best = b16_pick_cfg(a.MG, a.NG);
+  int best, sp;
+  b16_plan(a.MG, a.NG, a.KB, best, sp);
   int mt, nt;
   b16_cfg(best, mt, nt);
   a.ntm = cdiv(a.MG, mt);
   a.ntn = cdiv(a.NG, nt);
-  const int blocks = a.ntm * a.ntn;
+  a.S = sp;
+  a.part = static_cast<float*>(L.part);
+  a.cnt = L.cnt;
+  if (sp > 1 && (!a.part || !a.cnt)) return hipErrorInvalidValue;
+  const long long blocks_ll = (long long)a.ntm * a.ntn * sp;
+  if (blocks_ll > 0x7fffffffLL) return hipErrorInvalidValue;
+  const int blocks = (int)blocks_ll;
   const bool kf = (L.K % 64) == 0;
   const dim3 grid(blocks), block(256);
   if (L.amode == A_BF16) {

@@ -510,6 +510,16 @@ __device__ __forceinline__ float ld_agent(const float* p) {
 __device__ __forceinline__ void st_agent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// 16 bytes with the same device-scope write-through (sc1) the agent-scope
+// atomic store above gets, in one vector store: a wave's 64 lanes at
+// consecutive 16-byte slots write whole lines instead of 4-byte pieces.  Not
+// counted by the compiler's own waits: callers wait with wait_vm<0>().  A
+// store of more than 8 bytes needs one wait state before a VALU instruction
+// may overwrite its data registers; the compiler inserts it for its own
+// stores but cannot see into this one, so the s_nop is part of it.
+__device__ __forceinline__ void st_agent4(float* p, v4f v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
+}
 
 // One 1 KiB tile global -> LDS: lane l's 16 bytes land at lds_base + 16 l.
 // Issued as volatile asm with a memory clobber so the compiler neither moves

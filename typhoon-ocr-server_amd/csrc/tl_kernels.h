@@ -237,7 +237,13 @@ size_t tlk_gemm_counter_count(int amode, int M, int N, int K);
 // every GEMM shape: the small-M, int8 LDS-staged, 16-bit LDS-staged or
 // generic MFMA kernel
 hipError_t tlk_launch_gemm(const GemmLaunch* L, hipStream_t st);
+// split work-space of the kernel tlk_launch_gemm picks for *L: partial-sum
+// bytes (L->part) and zeroed arrival counters (L->cnt); 0 when none
+void tlk_gemm_needs(const GemmLaunch* L, size_t* part_bytes, size_t* counters);
 void tlk_gemm_i8_set_cfg(int cfg);   // tuning override of the int8 GEMM (-1 = planner)
+// tuning override of the 16-bit GEMM: tile configuration 0..2 (-1 = planner)
+// and K slices (0 = planner)
+void tlk_gemm_b16_set_plan(int cfg, int split);
 
 // ---- 2..8 rows of fp32 activations as int8 digit planes (rows.hip): amode
 //      A_F32X3; fp32 sums of w * x, y = 2^e fl(t * ws) summed over K slices,
@@ -329,6 +335,9 @@ void gemm_i8_set_cfg(int cfg);
 // when X rows are 16-byte aligned pieces
 bool gemm_b16_supported(const GemmLaunch& L);
 hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st);
+void gemm_b16_needs(int M, int N, int K, size_t* part_bytes, size_t* counters);
+void gemm_b16_set_plan(int cfg, int split);
+void gemm_needs(const GemmLaunch& L, size_t* part_bytes, size_t* counters);
 // M <= 16 rows (gemm_small.hip): GEMV-shaped MFMA kernel
 bool gemm_small_supported(const GemmLaunch& L);
 hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st);
