@@ -134,6 +134,13 @@ int tl_rows_set_groups(int groups);
  * int8 digit rows; 0 on the bf16 / fp16 MFMA small-batch kernel. */
 int tl_w8a16_set_gemv(int on);
 
+/* Tuning switch of w8a32_linear at batch 2 for every later call in the
+ * process: on the GEMV's weight stream with the two token rows as eight int8
+ * digit rows for K > 4096 (1, the default), for every K (2), or never (0:
+ * the digit-row MFMA kernel of batches 2..8, the same arithmetic at one K
+ * slice). */
+int tl_w8a32_set_gemv2(int on);
+
 /* Measurement aid, no counterpart in the reference: one streaming read of
  * `bytes` device bytes (a multiple of 16, p 16-byte aligned) by `grid`
  * work-groups with u (4 or 8) 16-byte loads in flight per lane, the loads

@@ -611,6 +611,7 @@ static int run_gemm(Workspace* ws, GemmLaunch* L, hipStream_t st) {
 /* tuning switches; atomic, since a setter may run while other threads call */
 static atomic_bool g_rows_off = false;
 static atomic_bool g_gemv_w8a16_off = false;   /* W8A16 batch 1 on the bf16 / fp16 MFMA kernel instead */
+static atomic_int g_gemv_rows2 = 1;             /* W8A32 batch 2 on the GEMV: 0 never, 1 K > 4096, 2 any K */
 
 static int run_rows(Workspace* ws, GemmLaunch* L, hipStream_t st, bool* done) {
   *done = false;
@@ -663,6 +664,27 @@ static int op_w8a32_ws(Workspace* ws, const float* X, const tl_weights* W, const
   L.K = W->cols;
   L.ep = EP_SCALE;
   L.out = OUT_F32;
+  /* 2 token rows with K > 4096: the batch-1 GEMV's weight stream with the
+   * two rows as eight int8 digit rows (the arithmetic of the digit-row kernel
+   * below at one K slice, so the same bits), every weight read once for both.
+   * Each weight dword meets 8 code rows from LDS, so below K = 4096, where
+   * the digit-row kernel's per-work-group activation split is short, that
+   * kernel is faster (2048x2048: 3.97 against 4.07 us, 4096x2048: 4.68
+   * against 5.61 us); at 2048x6144 this is (7.04 against 7.81 us). */
+  const int rows2 = atomic_load_explicit(&g_gemv_rows2, memory_order_relaxed);
+  if (batch == 2 && (rows2 == 2 || (rows2 == 1 && W->cols > 4096)) && tlk_gemv_fused_xv(W->cols) > 0) {
+    GemvLaunch G = tlk_gemv_launch_init();
+    G.x = X;
+    G.wt = W->tiles;
+    G.ws = W->scales;
+    G.bias = bias;
+    G.y = Y;
+    G.N = W->rows;
+    G.K = W->cols;
+    G.epi = EPI_W8A32_ROWS2;
+    HIP_TRY(tlk_launch_gemv_i8(&G, st));
+    return 0;
+  }
   /* 2..8 token rows over a weight of fewer than 32768 rows: int8 digit planes
    * of the fp32 rows, made inside the one launch (rows.hip; every work-group
    * splits its activation slice, which an lm_head-wide grid repeats too
@@ -1290,6 +1312,16 @@ static int w8a16_set_gemv_impl(int on) {
 int tl_w8a16_set_gemv(int on) {
   tlh_begin();
   return tlh_finish("tl_w8a16_set_gemv", w8a16_set_gemv_impl(on));
+}
+
+static int w8a32_set_gemv2_impl(int on) {
+  REQ(on >= 0 && on <= 2, "on must be 0, 1 or 2");
+  atomic_store_explicit(&g_gemv_rows2, on, memory_order_relaxed);
+  return 0;
+}
+int tl_w8a32_set_gemv2(int on) {
+  tlh_begin();
+  return tlh_finish("tl_w8a32_set_gemv2", w8a32_set_gemv2_impl(on));
 }
 
 static int gemm_i8_set_cfg_impl(int cfg) {

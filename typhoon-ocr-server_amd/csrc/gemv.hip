@@ -272,7 +272,12 @@ __device__ __forceinline__ float gemv_x1(const float* x, int xt, int k) {
 // e, q = x 2^(30-e) truncated), each weight dword meets all four through
 // v_dot4, and y = fma(2^(e-6) t, ws, bias) with t the digit sums' Horner
 // combination: fp32-accurate products (w8a16_linear batch 1,
-// kernel/w8a16_kernel.c:90-182) on the GEMV's weight stream.
+// kernel/w8a16_kernel.c:90-182) on the GEMV's weight stream.  PL == 2 takes
+// two fp32 token rows (x [2][K]) as eight digit rows, four per token with the
+// token's own e, and stores y[t][n] = 2^(e_t - 6) fl(t_t ws) (+ bias as its
+// own rounding): w8a32_linear at batch 2 (kernel/w8a32_kernel.c:297-350,
+// fp32 semantics) on the weight stream of batch 1, one weight read for both
+// tokens.
 template <int XV, int U, int RH, int PL>
 __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint8_t* wt, const float* ws,
                                                       float* y, int N, int K, int NG, int KB, int flags,
@@ -300,10 +305,11 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
   a.NG = NG;
   a.epi = (flags >> 2) & 7;
   a.x_vec = flags & 3;
-  constexpr int NP = PL ? 4 : 1;        // code rows: the activation codes, or its 4 digit rows
-  const int xt = PL ? (flags >> 8) & 3 : 0;
+  constexpr int NTOK = PL == 2 ? 2 : 1;  // token rows of x
+  constexpr int NP = PL ? 4 * NTOK : 1;  // code rows: the activation codes, or 4 digit rows per token
+  const int xt = PL == 1 ? (flags >> 8) & 3 : 0;
   __shared__ uint4 s_codes[XV > 0 ? XV * 64 * NP : 1];
-  __shared__ uint32_t s_mx[4];
+  __shared__ uint32_t s_mx[4 * NTOK];
   __shared__ float s_tail[4];
   __shared__ int s_red[NP][RH * 4 * SL];
 
@@ -333,12 +339,17 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
   // x is read before the first weight batch is issued, so the wait for x
   // never waits for weights
   float4 xv[XV > 0 ? XV : 1];
+  float4 xv2[PL == 2 ? XV : 1];          // the second token row (PL == 2)
   float4 nwv[XV > 0 ? XV : 1];
   const bool norm = ((flags >> 6) & 3) != NORM_NONE;   // x is a hidden row to normalise first
   if constexpr (XV > 0) {
     if (a.x_vec == 2) {
 #pragma unroll
       for (int i = 0; i < XV; i++) xv[i] = gemv_x4(a.x, xt, 4 * (threadIdx.x + 256 * i));
+      if constexpr (PL == 2) {
+#pragma unroll
+        for (int i = 0; i < XV; i++) xv2[i] = *reinterpret_cast<const float4*>(a.x + K + 4 * (threadIdx.x + 256 * i));
+      }
       if (norm) {
 #pragma unroll
         for (int i = 0; i < XV; i++)
@@ -355,6 +366,11 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
         v.z = (k0 + 2 < K) ? gemv_x1(a.x, xt, k0 + 2) : 0.f;
         v.w = (k0 + 3 < K) ? gemv_x1(a.x, xt, k0 + 3) : 0.f;
         xv[i] = v;
+        if constexpr (PL == 2) {
+          const float* x1 = a.x + K;
+          xv2[i] = make_float4((k0 < K) ? x1[k0] : 0.f, (k0 + 1 < K) ? x1[k0 + 1] : 0.f,
+                               (k0 + 2 < K) ? x1[k0 + 2] : 0.f, (k0 + 3 < K) ? x1[k0 + 3] : 0.f);
+        }
       }
     }
   }
@@ -366,31 +382,41 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
   const float bv = a.bias ? a.bias[nr] : 0.0f;
 
   float xs;
-  int px = 0;                            // plane mode: the row's absmax exponent, or kXeNonFinite
+  int px[NTOK];                          // plane mode: each row's absmax exponent, or kXeNonFinite
+#pragma unroll
+  for (int t = 0; t < NTOK; t++) px[t] = 0;
   if constexpr (PL) {
     // ---- digit rows of x (every element: no scalar tail in this mode) ------
-    uint32_t mx = 0;
 #pragma unroll
-    for (int i = 0; i < XV; i++) {
-      const uint32_t m01 = max(abs_bits(xv[i].x), abs_bits(xv[i].y));
-      const uint32_t m23 = max(abs_bits(xv[i].z), abs_bits(xv[i].w));
-      mx = max(mx, max(m01, m23));
+    for (int t = 0; t < NTOK; t++) {
+      uint32_t mx = 0;
+#pragma unroll
+      for (int i = 0; i < XV; i++) {
+        const float4 v = t == 0 ? xv[i] : xv2[i];
+        const uint32_t m01 = max(abs_bits(v.x), abs_bits(v.y));
+        const uint32_t m23 = max(abs_bits(v.z), abs_bits(v.w));
+        mx = max(mx, max(m01, m23));
+      }
+      mx = wave_umax(mx);
+      if (lane == 0) s_mx[4 * t + wv] = mx;
     }
-    mx = wave_umax(mx);
-    if (lane == 0) s_mx[wv] = mx;
     __syncthreads();
-    const uint32_t m = max(max(s_mx[0], s_mx[1]), max(s_mx[2], s_mx[3]));
-    int ex = 0;
-    if (m < 0x7f800000u && m != 0) (void)frexpf(__uint_as_float(m), &ex);
-    px = m < 0x7f800000u ? ex : kXeNonFinite;
     uint32_t* sc = reinterpret_cast<uint32_t*>(s_codes);
 #pragma unroll
-    for (int i = 0; i < XV; i++) {
-      uint32_t d[4];
-      digit_planes(digit_word(xv[i].x, 30 - ex), digit_word(xv[i].y, 30 - ex), digit_word(xv[i].z, 30 - ex),
-                   digit_word(xv[i].w, 30 - ex), d);
+    for (int t = 0; t < NTOK; t++) {
+      const uint32_t m = max(max(s_mx[4 * t], s_mx[4 * t + 1]), max(s_mx[4 * t + 2], s_mx[4 * t + 3]));
+      int ex = 0;
+      if (m < 0x7f800000u && m != 0) (void)frexpf(__uint_as_float(m), &ex);
+      px[t] = m < 0x7f800000u ? ex : kXeNonFinite;
 #pragma unroll
-      for (int p = 0; p < 4; p++) sc[p * XV * 256 + threadIdx.x + 256 * i] = d[p];
+      for (int i = 0; i < XV; i++) {
+        const float4 v = t == 0 ? xv[i] : xv2[i];
+        uint32_t d[4];
+        digit_planes(digit_word(v.x, 30 - ex), digit_word(v.y, 30 - ex), digit_word(v.z, 30 - ex),
+                     digit_word(v.w, 30 - ex), d);
+#pragma unroll
+        for (int p = 0; p < 4; p++) sc[(4 * t + p) * XV * 256 + threadIdx.x + 256 * i] = d[p];
+      }
     }
     xs = 1.0f;
     __syncthreads();
@@ -515,10 +541,20 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
     }
     const int tot = tots[0];
     const int n = row0 + lane;
-    if constexpr (PL) {
+    if constexpr (PL == 2) {
+      if (n < a.N) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          const float sum = digits_sum(tots[4 * t], tots[4 * t + 1], tots[4 * t + 2], tots[4 * t + 3]);
+          float v = px[t] == kXeNonFinite ? __builtin_nanf("") : ldexpf(__fmul_rn(sum, wsv), px[t] - 6);
+          if (a.bias) v = __fadd_rn(v, bv);
+          a.y[(size_t)t * a.N + n] = v;
+        }
+      }
+    } else if constexpr (PL == 1) {
       if (n < a.N) {
         const float t = digits_sum(tots[0], tots[1], tots[2], tots[3]);
-        const float v = px == kXeNonFinite ? __builtin_nanf("") : __fmaf_rn(ldexpf(t, px - 6), wsv, bv);
+        const float v = px[0] == kXeNonFinite ? __builtin_nanf("") : __fmaf_rn(ldexpf(t, px[0] - 6), wsv, bv);
         const int out = (flags >> 10) & 3;
         if (out == OUT_F32) {
           a.y[n] = v;
@@ -699,6 +735,19 @@ hipError_t launch_gemv_i8(const GemvLaunch& L, hipStream_t st) {
       }
   }
   const int xv = L.x ? gemv_fused_xv(L.K) : 0;
+  if (L.epi == EPI_W8A32_ROWS2) {
+    // two fp32 token rows as eight digit rows: fused x only, no RMSNorm
+    if (!L.x || xv == 0 || L.norm != NORM_NONE || L.x_type != 0 || L.out != OUT_F32) return hipErrorInvalidValue;
+    if (L.K == 1024 * xv && (((uintptr_t)L.x) & 15) == 0) a.x_vec = 2;
+    switch (xv) {
+      case 2: return launch_xv<2, 2>(a, p, st);
+      case 4: return launch_xv<4, 2>(a, p, st);
+      case 6: return launch_xv<6, 2>(a, p, st);
+      case 8: return launch_xv<8, 2>(a, p, st);
+      case 16: return launch_xv<16, 2>(a, p, st);
+      default: return hipErrorInvalidValue;
+    }
+  }
   if (L.epi == EPI_W8A16) {
     // digit-plane mode: fused x only, no RMSNorm; y of type L.out
     if (!L.x || xv == 0 || L.norm != NORM_NONE || L.x_type < 0 || L.x_type > 2) return hipErrorInvalidValue;

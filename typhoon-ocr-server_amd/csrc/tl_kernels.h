@@ -33,7 +33,12 @@ static inline int tlk_cdiv(int a, int b) { return (a + b - 1) / b; }
 // y[8b + r] = fl(silu(gate) * up) with the reference's fast-exp silu
 // EPI_W8A16: fp32-semantics products of a bf16 / fp16 / fp32 x (x_type) as
 // four int8 digit rows, y = fma(sum, ws, bias) stored as `out`
-enum { EPI_W8A32 = 0, EPI_W8A8 = 1, EPI_ACC = 2, EPI_ARGMAX = 3, EPI_SWIGLU = 4, EPI_W8A16 = 5 };
+// EPI_W8A32_ROWS2: two fp32 token rows (x [2][K], contiguous) as four int8
+// digit rows each; y[t][n] = 2^(e_t - 6) fl(sum * ws) (+ bias as its own
+// rounding), y [2][N]: the arithmetic of the digit-row kernel (rows.hip) at
+// one K slice
+enum { EPI_W8A32 = 0, EPI_W8A8 = 1, EPI_ACC = 2, EPI_ARGMAX = 3, EPI_SWIGLU = 4, EPI_W8A16 = 5,
+       EPI_W8A32_ROWS2 = 6 };
 // GEMV x prologues: the numpy final RMSNorm (decoder.py:444-446) or the
 // decoder's RMSNorm (kernel/ops.c:22-56, estimate-based rsqrt)
 enum { NORM_NONE = 0, NORM_NUMPY = 1, NORM_DECODER = 2 };

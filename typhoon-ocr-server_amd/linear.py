@@ -45,6 +45,7 @@ SIGNATURES = {
     "tl_rows_set_split": (_int, [_int]),
     "tl_rows_set_groups": (_int, [_int]),
     "tl_w8a16_set_gemv": (_int, [_int]),
+    "tl_w8a32_set_gemv2": (_int, [_int]),
     "tl_attn_set_chunk": (_int, [_int]),
     "tl_prefill_set_fused_quant": (_int, [_int]),
     "tl_stream_read_dev": (_int, [_vp, ctypes.c_size_t, _int, _int, _vp, _vp]),
