@@ -343,40 +343,46 @@ def bench_single_gemv(lin, torch, dev, stream, N=6144, K=2048, reps=10):
             "timing": "graph of one launch per weight copy, replayed; HIP events; per-launch average"}
 
 
-def bench_w8a8_prefill(lin, torch, dev, reps=20):
+def bench_w8a8_prefill(lin, torch, dev):
+    """W8A8 prefill GEMMs at M = 1024 (N = 6144, K = 2048 and N = 2048, K =
+    6144), weights rotating over >= 512 MB of copies, graph-replayed calls:
+    the whole call (per-token quantization into int8 tiles + the int8 MFMA
+    GEMM, tl_w8a8_linear_f32_dev), and its two halves timed on their own
+    (tl_w8a8_quantize_tiles_dev; tl_w8a8_linear_tiles_dev, the GEMM alone on
+    codes quantized once)."""
+    lib = lin.load_library()
     out = {}
-    tot_ops, tot_t = 0.0, 0.0
+    tot_ops, tot_t, tot_g = 0.0, 0.0, 0.0
     for (N, K) in [(6144, 2048), (2048, 6144)]:
         M = 1024
-        copies = max(2, int(np.ceil(512e6 / (N * K))))      # rotate > 512 MB of weights
-        Ws = []
-        for c in range(copies):
-            w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev)
-            s = torch.rand(N, device=dev) * 0.018 + 0.002
-            Ws.append(lin.DeviceWeights.from_codes(w, s))
+        Ws = rotating(lin, torch, dev, N, K, min_bytes=512e6)
         x = torch.randn((M, K), device=dev)
         y = torch.empty((M, N), device=dev)
-        st = torch.cuda.current_stream()
-        for i in range(3):
-            lin.w8a8_linear_f32_dev(x, Ws[i % copies], y, stream=st)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(st)
-        for i in range(reps):
-            lin.w8a8_linear_f32_dev(x, Ws[i % copies], y, stream=st)
-        e1.record(st)
-        torch.cuda.synchronize()
-        t = e0.elapsed_time(e1) * 1e-3 / reps
+        tiles = torch.empty(lib.tl_w8a8_tiles_bytes(M, K), dtype=torch.uint8, device=dev)
+        scales = torch.empty(-(-M // 16) * 16, dtype=torch.float32, device=dev)
+        t = time_graph(torch, lambda i, st: lin.w8a8_linear_f32_dev(x, Ws[i], y, stream=st), len(Ws))
+        tq = time_graph(torch, lambda i, st: lin.w8a8_quantize_tiles_dev(x, tiles, scales, stream=st), 1)
+        lin.w8a8_quantize_tiles_dev(x, tiles, scales)
+        tg = time_graph(torch, lambda i, st: lin.w8a8_linear_tiles_dev(tiles, scales, Ws[i], y, stream=st), len(Ws))
         ops = 2.0 * M * N * K
+        qbytes = M * K * 4 + M * K + M * 4
         out[f"M{M}_N{N}_K{K}"] = {"us": round(t * 1e6, 2), "tops": round(ops / t / 1e12, 1),
-                                   "frac_int8_peak": round(ops / t / 1e12 / INT8_PEAK_TOPS, 4)}
+                                   "frac_int8_peak": round(ops / t / 1e12 / INT8_PEAK_TOPS, 4),
+                                   "gemm_us": round(tg * 1e6, 2),
+                                   "gemm_frac_int8_peak": round(ops / tg / 1e12 / INT8_PEAK_TOPS, 4),
+                                   "quantize_us": round(tq * 1e6, 2),
+                                   "quantize_GBps": round(qbytes / tq / 1e9, 1)}
         tot_ops += ops
         tot_t += t
+        tot_g += tg
         for W in Ws:
             W.close()
     out["tops"] = round(tot_ops / tot_t / 1e12, 1)
     out["frac_int8_peak"] = round(tot_ops / tot_t / 1e12 / INT8_PEAK_TOPS, 4)
-    out["includes"] = "per-token activation quantization kernel + int8 MFMA GEMM, fp32 in/out"
+    out["gemm_frac_int8_peak"] = round(tot_ops / tot_g / 1e12 / INT8_PEAK_TOPS, 4)
+    out["includes"] = ("us / frac_int8_peak: per-token activation quantization kernel + int8 MFMA GEMM, fp32 "
+                       "in/out; gemm_us: the GEMM alone on tiled codes; quantize_us: the quantization alone "
+                       "(fp32 rows read, int8 tiles and scales written); graph-replayed calls")
     return out
 
 
@@ -746,6 +752,32 @@ def bench_decode_rows(lin, torch, dev):
     return out
 
 
+REFERENCE_W8A32_ROWS = [("q_proj", 2048, 2048, 1), ("k_proj", 256, 2048, 1), ("v_proj", 256, 2048, 1),
+                        ("o_proj", 2048, 2048, 1), ("gate_proj", 6144, 2048, 1), ("up_proj", 6144, 2048, 1),
+                        ("down_proj", 2048, 6144, 1), ("q_proj", 2048, 2048, 32), ("gate_proj", 6144, 2048, 32),
+                        ("down_proj", 2048, 6144, 32)]
+
+
+def bench_reference_w8a32_rows(lin, torch, dev):
+    """The reference benchmark's own W8A32 rows (bench_flops.py:257-268: the
+    separate decode projections at batch 1, and q, gate and down at batch 32),
+    graph-replayed over >= 600 MB of rotating weights; GFLOPS = 2 M N K / t
+    as the reference reports them, and HBM GB/s of the rows' bytes."""
+    out = {}
+    for (name, N, K, M) in REFERENCE_W8A32_ROWS:
+        Ws = rotating(lin, torch, dev, N, K)
+        x = torch.randn((M, K), device=dev)
+        y = torch.empty((M, N), device=dev)
+        t = time_graph(torch, lambda i, st: lin.w8a32_linear_dev(x, Ws[i], y, stream=st), len(Ws))
+        b = N * K + 4 * N + 4 * M * K + 4 * M * N
+        out[f"{name}_{N}x{K}_batch{M}"] = {"us": round(t * 1e6, 2), "GFLOPS": round(2.0 * M * N * K / t / 1e9, 1),
+                                          "GBps": round(b / t / 1e9, 1),
+                                          "frac_hbm": round(b / t / 1e9 / HBM_PEAK_GBS, 4)}
+        for W in Ws:
+            W.close()
+    return out
+
+
 def bench_w8a16_sweep(lin, torch, dev):
     """W8A16 sweep: bf16 X [M, 2048], int8 W [N, 2048], bf16 out; graph-replayed
     calls (time_graph)."""
@@ -1097,7 +1129,7 @@ def main():
     log("single decode GEMV 6144x2048 over 41 weight copies")
     single = bench_single_gemv(lin, torch, dev, stream)
 
-    prefill = rows = sweep = pre32 = host = None
+    prefill = rows = ref_rows = sweep = pre32 = host = None
     if not args.quick:
         log("host-pointer ABI (PCIe-inclusive)")
         host = bench_host_abi(lin)
@@ -1106,6 +1138,8 @@ def main():
         prefill = bench_w8a8_prefill(lin, torch, dev)
         log("W8A32 decode rows M=1..8")
         rows = bench_decode_rows(lin, torch, dev)
+        log("W8A32: the reference benchmark's rows (batch 1 and 32)")
+        ref_rows = bench_reference_w8a32_rows(lin, torch, dev)
         log("W8A16 sweep")
         sweep = bench_w8a16_sweep(lin, torch, dev)
         log("W8A32 prefill (fp32 semantics)")
@@ -1148,6 +1182,7 @@ def main():
         "decoder_greedy": dec,
         "w8a8_prefill": prefill,
         "w8a32_decode_rows": rows,
+        "w8a32_reference_rows": ref_rows,
         "w8a16_sweep": sweep,
         "w8a32_prefill": pre32,
         "host_abi": host,

@@ -219,6 +219,22 @@ int tl_w8a8_linear_dev(const int8_t *x_int8, const float *x_scales, const tl_wei
  * then the int8 MFMA GEMM with the fp32 epilogue. */
 int tl_w8a8_linear_f32_dev(const float *X, const tl_weights *W, const float *bias, float *Y,
                            int batch, void *stream);
+
+/* The two halves of tl_w8a8_linear_f32_dev at batch > 1, for callers that
+ * quantize once and reuse the codes, or time the GEMM alone (no reference
+ * counterpart: the reference's w8a8_quantize_activations / w8a8_linear,
+ * w8a8_kernel.c:109-114, :259-275, on row-major codes):
+ * tl_w8a8_quantize_tiles_dev writes the per-token int8 codes of X [batch][K]
+ * in the library's 16x64 activation tile layout (tl_w8a8_tiles_bytes bytes)
+ * and the token scales (ceil(batch/16)*16 floats of room); the codes are
+ * those of w8a8_quantize_activations.  tl_w8a8_linear_tiles_dev runs the
+ * int8 MFMA GEMM on them with the fp32 epilogue fl(fl(fl(acc) ws) xs)
+ * (+ bias as its own rounding). */
+size_t tl_w8a8_tiles_bytes(int batch, int K);
+int tl_w8a8_quantize_tiles_dev(const float *X, int batch, int K, uint8_t *x_tiles, float *x_scales,
+                               void *stream);
+int tl_w8a8_linear_tiles_dev(const uint8_t *x_tiles, const float *x_scales, const tl_weights *W,
+                             const float *bias, float *Y, int batch, void *stream);
 /* W8A16: X bf16 or fp16 [batch x K], Y fp32, bf16 or fp16 [batch x N]. */
 int tl_w8a16_linear_dev(const void *X, int x_type, const tl_weights *W, const float *bias,
                         void *Y, int y_type, int batch, void *stream);

@@ -814,3 +814,32 @@ def test_w8a16_k_slices(lin, orc, dev, M, N, K):
     finally:
         lib.tl_gemm_b16_set_plan(-1, 0)
     W.close()
+
+
+@pytest.mark.parametrize("M,N,K", [(1024, 6144, 2048), (1024, 2048, 6144), (300, 1000, 1000)])
+def test_w8a8_quantize_tiles_then_gemm(lin, orc, dev, M, N, K):
+    """The two halves of tl_w8a8_linear_f32_dev (per-token codes into the
+    activation tile layout, then the GEMM on them) give its outputs bit for
+    bit, bias included; the token scales are the oracle's
+    w8a8_quantize_activations scales."""
+    import torch
+    say(f"w8a8 quantize tiles + GEMM M={M} N={N} K={K}")
+    lib = lin.load_library()
+    rng = np.random.default_rng(M + N + K + 88)
+    x, w, s = make(rng, M, N, K)
+    b = rng.standard_normal(N).astype(F)
+    W = lin.DeviceWeights.from_codes(w, s)
+    xd = torch.from_numpy(x).to(dev)
+    bd = torch.from_numpy(b).to(dev)
+    tiles = torch.empty(lib.tl_w8a8_tiles_bytes(M, K), dtype=torch.uint8, device=dev)
+    scales = torch.empty(-(-M // 16) * 16, dtype=torch.float32, device=dev)
+    y_full = torch.empty((M, N), dtype=torch.float32, device=dev)
+    y_split = torch.empty((M, N), dtype=torch.float32, device=dev)
+    lin.w8a8_linear_f32_dev(xd, W, y_full, bias=bd)
+    lin.w8a8_quantize_tiles_dev(xd, tiles, scales)
+    lin.w8a8_linear_tiles_dev(tiles, scales, W, y_split, bias=bd)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y_split.cpu().numpy(), y_full.cpu().numpy())
+    _, xs = orc.quantize_rows(x)
+    np.testing.assert_array_equal(scales.cpu().numpy()[:M], xs)
+    W.close()

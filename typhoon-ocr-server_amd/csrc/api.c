@@ -915,14 +915,15 @@ int tlh_linear_w8a32_planes(const uint8_t* tiles, const int* xe, const tl_weight
   WS_CALL(W->dev, st, linear_w8a32_planes_ws(ws_, tiles, xe, W, Y, batch, st));
 }
 
-static int linear_w8a8_tiles_ws(Workspace* ws, const uint8_t* tiles, const float* xs, const tl_weights* W, float* Y, int batch,
-                          hipStream_t st) {
+static int linear_w8a8_tiles_ws(Workspace* ws, const uint8_t* tiles, const float* xs, const tl_weights* W,
+                                const float* bias, float* Y, int batch, hipStream_t st) {
   GemmLaunch L = tlk_gemm_launch_init();
   L.amode = A_I8;
   L.A = tiles;
   L.Bt = W->tiles;
   L.ws = W->scales;
   L.xs = xs;
+  L.bias = bias;
   L.Y = Y;
   L.ldy = W->rows;
   L.M = batch;
@@ -934,7 +935,7 @@ static int linear_w8a8_tiles_ws(Workspace* ws, const uint8_t* tiles, const float
 
 int tlh_linear_w8a8_tiles(const uint8_t* tiles, const float* xs, const tl_weights* W, float* Y, int batch,
                           hipStream_t st) {
-  WS_CALL(W->dev, st, linear_w8a8_tiles_ws(ws_, tiles, xs, W, Y, batch, st));
+  WS_CALL(W->dev, st, linear_w8a8_tiles_ws(ws_, tiles, xs, W, NULL, Y, batch, st));
 }
 
 /* Quantizes rows of host fp32 on the GPU and returns codes and scales to the
@@ -1518,6 +1519,40 @@ int tl_w8a8_linear_f32_dev(const float* X, const tl_weights* W, const float* bia
                            void* stream) {
   tlh_begin();
   return tlh_finish("tl_w8a8_linear_f32_dev", w8a8_linear_f32_dev_impl(X, W, bias, Y, batch, stream));
+}
+
+/* the two halves of tl_w8a8_linear_f32_dev at batch > 1 */
+size_t tl_w8a8_tiles_bytes(int batch, int K) {
+  if (batch < 1 || K < 1) return 0;
+  return (size_t)tlk_cdiv(batch, 16) * 16 * (size_t)tlk_cdiv(K, 64) * 64;
+}
+
+static int w8a8_quantize_tiles_impl(const float* X, int batch, int K, uint8_t* x_tiles, float* x_scales,
+                                    void* stream) {
+  REQ(X && x_tiles && x_scales && batch >= 1 && K >= 1, "bad arguments");
+  hipStream_t st = (hipStream_t)stream;
+  const bool by_rows = (K == 1024 || K == 2048 || K == 4096 || K == 6144) && (((uintptr_t)X) & 15) == 0;
+  if (by_rows) HIP_TRY(tlk_launch_quantize_rows_by_row(X, batch, K, x_tiles, x_scales, st));
+  else HIP_TRY(tlk_launch_quantize_rows_tiled(X, batch, K, x_tiles, x_scales, true, st));
+  return 0;
+}
+int tl_w8a8_quantize_tiles_dev(const float* X, int batch, int K, uint8_t* x_tiles, float* x_scales, void* stream) {
+  tlh_begin();
+  return tlh_finish("tl_w8a8_quantize_tiles_dev", w8a8_quantize_tiles_impl(X, batch, K, x_tiles, x_scales, stream));
+}
+
+static int w8a8_linear_tiles_impl(const uint8_t* x_tiles, const float* x_scales, const tl_weights* W,
+                                  const float* bias, float* Y, int batch, void* stream) {
+  TRY(tlh_check_weights(W));
+  REQ(x_tiles && x_scales && Y && batch >= 1, "bad arguments");
+  hipStream_t st = (hipStream_t)stream;
+  WS_CALL(W->dev, st, linear_w8a8_tiles_ws(ws_, x_tiles, x_scales, W, bias, Y, batch, st));
+}
+int tl_w8a8_linear_tiles_dev(const uint8_t* x_tiles, const float* x_scales, const tl_weights* W, const float* bias,
+                             float* Y, int batch, void* stream) {
+  tlh_begin();
+  return tlh_finish("tl_w8a8_linear_tiles_dev",
+                    w8a8_linear_tiles_impl(x_tiles, x_scales, W, bias, Y, batch, stream));
 }
 
 static int w8a16_linear_dev_impl(const void* X, int x_type, const tl_weights* W, const float* bias, void* Y,

@@ -95,6 +95,9 @@ SIGNATURES = {
     "tl_quantize_rows_dev": (_int, [_vp, _vp, _vp, _int, _int, _int, _vp]),
     "tl_w8a8_linear_dev": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _vp]),
     "tl_w8a8_linear_f32_dev": (_int, [_vp, _vp, _vp, _vp, _int, _vp]),
+    "tl_w8a8_tiles_bytes": (ctypes.c_size_t, [_int, _int]),
+    "tl_w8a8_quantize_tiles_dev": (_int, [_vp, _int, _int, _vp, _vp, _vp]),
+    "tl_w8a8_linear_tiles_dev": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _vp]),
     "tl_w8a16_linear_dev": (_int, [_vp, _int, _vp, _vp, _vp, _int, _int, _vp]),
     "tl_w8a32_gemv_acc_dev": (_int, [_vp, _vp, _vp, _vp, _vp]),
     "tl_w8a8_gemm_acc_dev": (_int, [_vp, _vp, _vp, _int, _vp]),
@@ -334,6 +337,23 @@ def w8a8_linear_f32_dev(x, W: DeviceWeights, y, bias=None, stream=None):
     lib = load_library()
     _rc(lib, lib.tl_w8a8_linear_f32_dev(x.data_ptr(), W.handle, _ptr(bias), y.data_ptr(), x.shape[0],
                                         _stream(stream)), "tl_w8a8_linear_f32_dev")
+
+
+def w8a8_quantize_tiles_dev(x, tiles, scales, stream=None):
+    """Per-token int8 codes of fp32 x [M, K] into the activation tile layout
+    (tiles: uint8 tensor of tl_w8a8_tiles_bytes(M, K) bytes; scales: fp32
+    tensor of ceil(M / 16) * 16)."""
+    lib = load_library()
+    M, K = x.shape
+    _rc(lib, lib.tl_w8a8_quantize_tiles_dev(x.data_ptr(), M, K, tiles.data_ptr(), scales.data_ptr(),
+                                            _stream(stream)), "tl_w8a8_quantize_tiles_dev")
+
+
+def w8a8_linear_tiles_dev(tiles, scales, W: DeviceWeights, y, bias=None, stream=None):
+    """The W8A8 GEMM on tiled activation codes (w8a8_quantize_tiles_dev)."""
+    lib = load_library()
+    _rc(lib, lib.tl_w8a8_linear_tiles_dev(tiles.data_ptr(), scales.data_ptr(), W.handle, _ptr(bias),
+                                          y.data_ptr(), y.shape[0], _stream(stream)), "tl_w8a8_linear_tiles_dev")
 
 
 def w8a8_linear_dev(x_q, x_scales, W: DeviceWeights, y, bias=None, stream=None):
