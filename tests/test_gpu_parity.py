@@ -249,7 +249,9 @@ def test_registry_detects_in_place_update(lin, orc):
 @pytest.mark.parametrize("M,N,K", [(2, 2048, 2048), (4, 6144, 2048), (8, 2048, 6144), (3, 100, 70),
                                    (17, 512, 2048), (64, 1024, 2048), (200, 4096, 2048),
                                    # the row-wise plane split's other widths (K = 1024 NV)
-                                   (40, 300, 1024), (70, 256, 4096), (33, 130, 6144)])
+                                   (40, 300, 1024), (70, 256, 4096), (33, 130, 6144),
+                                   # long K at 9..32 tokens: the planes, not the three-term split
+                                   (16, 2048, 6144), (32, 2048, 6144), (24, 2048, 4096), (12, 1000, 6144)])
 def test_w8a32_batch_fp32(lin, orc, M, N, K):
     say(f"w8a32 batch M={M} N={N} K={K}")
     rng = np.random.default_rng(M * 13 + N + K)

@@ -695,12 +695,15 @@ static int op_w8a32_ws(Workspace* ws, const float* X, const tl_weights* W, const
     TRY(run_rows(ws, &L, st, &done));
     if (done) return 0;
   }
-  if ((batch <= 16 && W->NG < 2048) || (batch <= 32 && W->NG <= 256)) {
-    /* a few token rows over a narrow weight: the small-M kernel splits the
-     * fp32 rows into three bf16 terms as it loads them (one launch; a
-     * separate plane split costs more than it saves at these sizes: at
-     * N <= 4096, 24-32 tokens 13.7-15.1 us here against 16.6-17.0 us on the
-     * planes, which win from 48 tokens) */
+  if ((batch <= 16 && W->NG < 2048 && W->cols <= 4096) || (batch <= 32 && W->NG <= 256 && W->cols <= 2048)) {
+    /* a few token rows over a narrow weight with a short K: the small-M kernel
+     * splits the fp32 rows into three bf16 terms as it loads them (one launch,
+     * where a separate plane split costs more than it saves: 2048x2048 at 17
+     * tokens 12.8 us here against 14.0 us on the planes, even at 24-32).  Every
+     * work-group re-reads all the token rows, which a long K makes the cost:
+     * 2048x6144 at 9 / 16 / 32 tokens 16.3 / 19.2 / 33.3 us here against
+     * 13.8 / 15.6 / 28.2 us on the planes, 2048x4096 at 17-32 tokens 22.7-25.8
+     * against 19.4-21.7 us */
     return run_gemm(ws, &L, st);
   }
   /* fp32 rows as four int8 planes each (x = 2^e (q0 + q1/254 + q2/254^2 +
