@@ -110,6 +110,12 @@ int tl_gemv_set_plan(int rows, int u);
  * prefetch 7). */
 int tl_gemm_i8_set_cfg(int cfg);
 
+/* Tuning override of the same GEMM's K slices for every later call in the
+ * process: 0 restores the planner (slices where a shape has fewer than 128
+ * tiles), 1..64 force that many work-groups per tile (on the LDS-staged
+ * kernel), whose exact int32 partial sums the last to arrive adds. */
+int tl_gemm_i8_set_split(int split);
+
 /* Tuning override of the 16-bit MFMA GEMM (W8A16, M > 16 on the tiled
  * kernel) for every later call in the process: cfg -1 restores the planner's
  * tile, 0..2 force 128x192, 64x128 or 32x64 tiles; split 0 restores the

@@ -251,7 +251,10 @@ def test_registry_detects_in_place_update(lin, orc):
                                    # the row-wise plane split's other widths (K = 1024 NV)
                                    (40, 300, 1024), (70, 256, 4096), (33, 130, 6144),
                                    # long K at 9..32 tokens: the planes, not the three-term split
-                                   (16, 2048, 6144), (32, 2048, 6144), (24, 2048, 4096), (12, 1000, 6144)])
+                                   (16, 2048, 6144), (32, 2048, 6144), (24, 2048, 4096), (12, 1000, 6144),
+                                   # K 4096 or > 8192 weight rows at 9..16 tokens: the planes too;
+                                   # 17..64 tokens at K >= 4096: K slices on the planes GEMM
+                                   (9, 2048, 4096), (12, 9000, 2048), (20, 2048, 6144), (48, 3072, 4096)])
 def test_w8a32_batch_fp32(lin, orc, M, N, K):
     say(f"w8a32 batch M={M} N={N} K={K}")
     rng = np.random.default_rng(M * 13 + N + K)
@@ -534,12 +537,15 @@ def test_w8a8_gemm(lin, orc, dev, M, N, K):
     W.close()
 
 
-@pytest.mark.parametrize("M,N,K", [(80, 130, 300), (100, 2048, 6144), (300, 1000, 1000), (1024, 6144, 2048)])
+@pytest.mark.parametrize("M,N,K", [(80, 130, 300), (100, 2048, 6144), (300, 1000, 1000), (1024, 6144, 2048),
+                                   (128, 2048, 2048)])
 def test_w8a8_gemm_configs_bit_exact(lin, orc, dev, M, N, K):
     """Every int8 MFMA GEMM configuration (both LDS-staged layouts and the
     register-loaded weight variants with each prefetch depth) gives the exact
     int32 accumulators and the exact fp32 epilogue, on ragged shapes (M, N, K
-    off the tile sizes, K shorter than the prefetch distance) and full size."""
+    off the tile sizes, K shorter than the prefetch distance) and full size;
+    so do K ranges split over 2..8 work-groups per tile (the planner's own
+    split included), called twice each."""
     import torch
     rng = np.random.default_rng(M + N + K)
     x, w, s = make(rng, M, N, K)
@@ -549,19 +555,24 @@ def test_w8a8_gemm_configs_bit_exact(lin, orc, dev, M, N, K):
     W = lin.DeviceWeights.from_codes(w, s)
     xqd, xd = torch.from_numpy(xq).to(dev), torch.from_numpy(x).to(dev)
     lib = lin.load_library()
+    runs = [(cfg, 1) for cfg in range(8)]                       # every kernel unsplit
+    runs += [(-1, sp) for sp in (0, 2, 3, 5, 8)] + [(cfg, 3) for cfg in (0, 1, 2)]   # K slices
     try:
-        for cfg in range(8):
-            say(f"w8a8 gemm cfg={cfg} M={M} N={N} K={K}")
+        for cfg, split in runs:
+            say(f"w8a8 gemm cfg={cfg} split={split} M={M} N={N} K={K}")
             assert lib.tl_gemm_i8_set_cfg(cfg) == 0
-            acc = torch.full((M, N), -7, dtype=torch.int32, device=dev)
-            lin.gemm_acc_dev(xqd, W, acc)
-            y = torch.empty((M, N), dtype=torch.float32, device=dev)
-            lin.w8a8_linear_f32_dev(xd, W, y)
-            torch.cuda.synchronize()
-            np.testing.assert_array_equal(acc.cpu().numpy(), want)
-            np.testing.assert_array_equal(y.cpu().numpy(), want_y)
+            assert lib.tl_gemm_i8_set_split(split) == 0
+            for rep in range(2):                 # twice: the arrival counters are back at zero
+                acc = torch.full((M, N), -7, dtype=torch.int32, device=dev)
+                lin.gemm_acc_dev(xqd, W, acc)
+                y = torch.empty((M, N), dtype=torch.float32, device=dev)
+                lin.w8a8_linear_f32_dev(xd, W, y)
+                torch.cuda.synchronize()
+                np.testing.assert_array_equal(acc.cpu().numpy(), want)
+                np.testing.assert_array_equal(y.cpu().numpy(), want_y)
     finally:
         lib.tl_gemm_i8_set_cfg(-1)
+        lib.tl_gemm_i8_set_split(0)
     W.close()
 
 

@@ -695,15 +695,16 @@ static int op_w8a32_ws(Workspace* ws, const float* X, const tl_weights* W, const
     TRY(run_rows(ws, &L, st, &done));
     if (done) return 0;
   }
-  if ((batch <= 16 && W->NG < 2048 && W->cols <= 4096) || (batch <= 32 && W->NG <= 256 && W->cols <= 2048)) {
+  if (W->cols <= 2048 && ((batch <= 16 && W->NG < 512) || (batch <= 32 && W->NG <= 256))) {
     /* a few token rows over a narrow weight with a short K: the small-M kernel
      * splits the fp32 rows into three bf16 terms as it loads them (one launch,
-     * where a separate plane split costs more than it saves: 2048x2048 at 17
-     * tokens 12.8 us here against 14.0 us on the planes, even at 24-32).  Every
-     * work-group re-reads all the token rows, which a long K makes the cost:
-     * 2048x6144 at 9 / 16 / 32 tokens 16.3 / 19.2 / 33.3 us here against
-     * 13.8 / 15.6 / 28.2 us on the planes, 2048x4096 at 17-32 tokens 22.7-25.8
-     * against 19.4-21.7 us */
+     * where a separate plane split costs more than it saves: 2048x2048 at 9 /
+     * 16 / 17 tokens 7.2 / 8.7 / 12.8 us here against 8.5 / 9.5 / 14.2 us on
+     * the planes, 6144x2048 at 9 / 16 tokens 10.9 / 14.3 against 15.1 / 15.7).
+     * Every work-group re-reads all the token rows, which a long K or many
+     * weight rows make the cost: 2048x4096 at 9 / 16 tokens 11.9 / 14.4 us here
+     * against 11.1 / 12.6 us on the planes, 12288x2048 at 16 tokens 20.6
+     * against 15.9 us, 2048x6144 at 32 tokens 33.3 against 19.7 us */
     return run_gemm(ws, &L, st);
   }
   /* fp32 rows as four int8 planes each (x = 2^e (q0 + q1/254 + q2/254^2 +
@@ -1336,6 +1337,16 @@ static int gemm_i8_set_cfg_impl(int cfg) {
 int tl_gemm_i8_set_cfg(int cfg) {
   tlh_begin();
   return tlh_finish("tl_gemm_i8_set_cfg", gemm_i8_set_cfg_impl(cfg));
+}
+
+static int gemm_i8_set_split_impl(int split) {
+  REQ(split >= 0 && split <= 64, "split must be 0 (planner) or 1..64");
+  tlk_gemm_i8_set_split(split);
+  return 0;
+}
+int tl_gemm_i8_set_split(int split) {
+  tlh_begin();
+  return tlh_finish("tl_gemm_i8_set_split", gemm_i8_set_split_impl(split));
 }
 
 static int gemm_b16_set_plan_impl(int cfg, int split) {

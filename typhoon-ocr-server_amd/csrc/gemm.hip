@@ -410,8 +410,8 @@ void gemm_needs(const GemmLaunch& L, size_t* part_bytes, size_t* counters) {
   *part_bytes = 0;
   *counters = 0;
   switch (gemm_choice(L)) {
-    case GK_SMALL:
-    case GK_I8: return;
+    case GK_SMALL: return;
+    case GK_I8: gemm_i8_needs(L.M, L.N, L.K, part_bytes, counters); return;
     case GK_B16: gemm_b16_needs(L.M, L.N, L.K, part_bytes, counters); return;
     default: break;
   }

@@ -21,6 +21,9 @@
 // that the work-groups placed on one XCD (dispatch is round-robin over the 8
 // XCDs) share a band of B columns and all of A, which then stays in that
 // XCD's 4 MB L2.
+#include <algorithm>
+#include <atomic>
+
 #include "tl_common.h"
 #include "tl_kernels.h"
 
@@ -39,6 +42,9 @@ struct GemmI8Args {
   int ntm, ntn;         // work-group tiles along M and N
   int out;
   const uint8_t* zero_tile;  // 1 KiB of zeros (source of k-blocks past K)
+  int S;                // K slices per tile (LDS-staged kernel; 1 elsewhere)
+  int32_t* part;        // S > 1: int32 partial tiles [tiles][S][16 MT x 16 NT]
+  uint32_t* cnt;        // S > 1: zeroed arrival counters [tiles]
 };
 
 // Work-group -> tile.  Dispatch is round-robin over the 8 XCDs: work-group b
@@ -125,15 +131,20 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds_kernel(GemmI8Args a)
   const int wm = wv / WN, wn = wv % WN;
 
   // XCD-aware tile order: work-group b runs on XCD b % 8; the work-groups of
-  // one XCD walk M fastest within a band of N tiles.
+  // one XCD walk M fastest within a band of N tiles.  With K slices,
+  // work-group b takes slice b / tiles of tile b % tiles.
+  const int ntiles = a.ntm * a.ntn;
+  const int ks = blockIdx.x / ntiles;
+  const int bt = blockIdx.x - ks * ntiles;
   int tm, tn;
-  tile_of(blockIdx.x, a.ntm, a.ntn, tm, tn);
+  tile_of(bt, a.ntm, a.ntn, tm, tn);
   const int mg0 = tm * MT, ng0 = tn * NT;
 
   const uint4* A4 = reinterpret_cast<const uint4*>(a.At) + lane;
   const uint4* B4 = reinterpret_cast<const uint4*>(a.Bt) + lane;
   const uint4* Z4 = reinterpret_cast<const uint4*>(a.zero_tile) + lane;
-  const int KB = a.KB;
+  const int kb0 = (ks * a.KB) / a.S;                  // this work-group's k-blocks [kb0, kb0 + KB)
+  const int KB = ((ks + 1) * a.KB) / a.S - kb0;
   const int nst = cdiv(KB, KT);
 
   // Copy source of each tile this wave copies, fixed except for the K offset:
@@ -150,11 +161,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds_kernel(GemmI8Args a)
     qlds[p] = (uint32_t)q * 1024u;
     if (q < TA) {
       const int mg = min(mg0 + q / KT, a.MG - 1);
-      qsrc[p] = A4 + ((size_t)qk[p] * a.MG + mg) * 64;
+      qsrc[p] = A4 + ((size_t)(kb0 + qk[p]) * a.MG + mg) * 64;
       qstride[p] = (size_t)KT * a.MG * 64;
     } else {
       const int ng = min(ng0 + (q - TA) / KT, a.NG - 1);
-      qsrc[p] = B4 + ((size_t)qk[p] * a.NG + ng) * 64;
+      qsrc[p] = B4 + ((size_t)(kb0 + qk[p]) * a.NG + ng) * 64;
       qstride[p] = (size_t)KT * a.NG * 64;
     }
   }
@@ -269,6 +280,57 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds_kernel(GemmI8Args a)
   }
 
   wait_vm<0>();   // no copy may still be landing in LDS when the work-group exits
+
+  if (a.S > 1) {
+    // K slices: every work-group of the tile stores its int32 sums (16-byte
+    // write-through stores), waits for their acknowledgement and counts in;
+    // the last to arrive adds the S slices (exact integer sums, so any order
+    // gives the same bits; slice order here) and runs the epilogue below
+    constexpr int TF = MT * 16 * NT * 16;
+    int32_t* mine = a.part + ((size_t)bt * a.S + ks) * TF;
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+        st_agent4(reinterpret_cast<float*>(mine) + (((wv * FM + i) * FN + j) * 64 + lane) * 4,
+                  __builtin_bit_cast(v4f, acc[i][j]));
+    __shared__ int s_last;
+    asm volatile("" ::: "memory");
+    wait_vm<0>();                               // this thread's partial stores are acknowledged
+    asm volatile("" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(a.cnt + bt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.S - 1);
+    __syncthreads();
+    if (!s_last) return;
+    // the merger's acquire: the slices are read after the counter showed them
+    // all arrived (agent scope, once per tile; plain 16-byte loads after it)
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    constexpr int QB = FM * FN <= 8 ? 4 : (FM * FN <= 16 ? 2 : 1);   // slices in flight together
+    const int32_t* slices = a.part + (size_t)bt * a.S * TF;
+    for (int q0 = 0; q0 < a.S; q0 += QB) {
+      v4i pv[QB][FM][FN];
+#pragma unroll
+      for (int u = 0; u < QB; u++)
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+          for (int j = 0; j < FN; j++)
+            pv[u][i][j] = *reinterpret_cast<const v4i*>(slices + (size_t)min(q0 + u, a.S - 1) * TF +
+                                                        (((wv * FM + i) * FN + j) * 64 + lane) * 4);
+#pragma unroll
+      for (int u = 0; u < QB; u++) {
+        if (q0 + u >= a.S) break;
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+          for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[i][j][r] = q0 + u == 0 ? pv[u][i][j][r] : acc[i][j][r] + pv[u][i][j][r];
+      }
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(a.cnt + bt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 
   // epilogue: y = fl(fl(fl(acc) * ws[n]) * xs[m]) (+ bias[n]); 16-byte
   // streaming stores when the 4 columns are inside N and the row is 16-byte
@@ -537,11 +599,15 @@ static void i8_cfg(int cfg, int& mt, int& nt) {
   else { mt = 8; nt = 8; }
 }
 
-static int g_i8_force_cfg = -1;
-void gemm_i8_set_cfg(int cfg) { g_i8_force_cfg = cfg; }
+// tuning overrides; atomic, since a setter may run while other threads plan launches
+static std::atomic<int> g_i8_force_cfg{-1};
+static std::atomic<int> g_i8_force_split{0};
+void gemm_i8_set_cfg(int cfg) { g_i8_force_cfg.store(cfg, std::memory_order_relaxed); }
+void gemm_i8_set_split(int s) { g_i8_force_split.store(s > 0 ? s : 0, std::memory_order_relaxed); }
 
 int gemm_i8_pick_cfg(int M, int N, int K) {
-  if (g_i8_force_cfg >= 0) return g_i8_force_cfg;
+  const int force = g_i8_force_cfg.load(std::memory_order_relaxed);
+  if (force >= 0) return force;
   (void)K;
   // 2048 rows and more (the 4 x 1200 plane rows of a 1200-token fp32 batch):
   // many tiles per CU, where the deepest weight prefetch on 64 x 128 tiles
@@ -571,6 +637,42 @@ int gemm_i8_pick_cfg(int M, int N, int K) {
   return best;
 }
 
+// Plan: configuration and K slices.  With fewer than 128 tiles (a few
+// hundred rows over a narrow N: the int8 planes of 17..64 fp32 tokens, small
+// W8A8 batches) and K >= 4096, the K range of every tile is split over up to
+// 4 work-groups on the LDS-staged kernel (its configuration of the same
+// tile); slices keep at least 16 k-blocks.  The merge costs three dependent
+// memory round trips (partials stored, arrival counted, partials read back),
+// about 3 us: at K = 2048 every split measured slower than none, at K = 4096
+// and 6144 a split of 4 (3 from 64 tiles up, 2 from 96) was the fastest or
+// within 3 % of it (2048 x 6144 at 128 plane rows: 28.5 -> 19.7 us).  The
+// int32 partial sums are exact, so the result is the same bits for every split.
+static void gemm_i8_plan(int M, int N, int K, int& cfg, int& split) {
+  cfg = gemm_i8_pick_cfg(M, N, K);
+  int mt, nt;
+  i8_cfg(cfg, mt, nt);
+  const int tiles = cdiv(cdiv(M, 16), mt) * cdiv(cdiv(N, 16), nt);
+  const int KB = cdiv(K, 64);
+  split = 1;
+  if (tiles < 128 && KB >= 64) split = std::min(std::min(4, 256 / tiles), KB / 16);
+  const int fs = g_i8_force_split.load(std::memory_order_relaxed);
+  if (fs > 0) split = std::min(fs, KB);
+  if (split > 1) {              // the LDS-staged kernel of the same tile
+    if (cfg == 3 || cfg == 4 || cfg == 5) cfg = 0;
+    else if (cfg == 6) cfg = 1;
+    else if (cfg == 7) cfg = 2;
+  }
+}
+
+void gemm_i8_needs(int M, int N, int K, size_t* part_bytes, size_t* counters) {
+  int cfg, sp, mt, nt;
+  gemm_i8_plan(M, N, K, cfg, sp);
+  i8_cfg(cfg, mt, nt);
+  const size_t tiles = (size_t)cdiv(cdiv(M, 16), mt) * cdiv(cdiv(N, 16), nt);
+  *part_bytes = sp > 1 ? tiles * sp * (size_t)(256 * mt * nt) * sizeof(int32_t) : 0;
+  *counters = sp > 1 ? tiles : 0;
+}
+
 hipError_t launch_gemm_i8(const GemmLaunch& L, hipStream_t st) {
   GemmI8Args a;
   a.At = static_cast<const uint8_t*>(L.A);
@@ -592,12 +694,19 @@ hipError_t launch_gemm_i8(const GemmLaunch& L, hipStream_t st) {
   if (L.out == OUT_F32_X4 && (!L.xe || L.M % 4 != 0)) return hipErrorInvalidValue;
   if (L.out != OUT_I32 && L.out != OUT_F32_X4 && !L.xs) return hipErrorInvalidValue;
   if (!L.zero_tile) return hipErrorInvalidValue;
-  const int cfg = gemm_i8_pick_cfg(L.M, L.N, L.K);
+  int cfg, sp;
+  gemm_i8_plan(L.M, L.N, L.K, cfg, sp);
   int mt, nt;
   i8_cfg(cfg, mt, nt);
   a.ntm = cdiv(a.MG, mt);
   a.ntn = cdiv(a.NG, nt);
-  const int blocks = a.ntm * a.ntn;
+  a.S = sp;
+  a.part = static_cast<int32_t*>(L.part);
+  a.cnt = L.cnt;
+  if (sp > 1 && (!a.part || !a.cnt || cfg > 2)) return hipErrorInvalidValue;
+  const long long blocks_ll = (long long)a.ntm * a.ntn * sp;
+  if (blocks_ll > 0x7fffffffLL) return hipErrorInvalidValue;
+  const int blocks = (int)blocks_ll;
   switch (cfg) {
     case 0: hipLaunchKernelGGL((gemm_i8_lds_kernel<8, 12, 1, 4, 2, 2>), dim3(blocks), dim3(256), 0, st, a); break;
     case 1: hipLaunchKernelGGL((gemm_i8_lds_kernel<4, 8, 1, 8, 2, 2>), dim3(blocks), dim3(256), 0, st, a); break;
@@ -614,3 +723,4 @@ hipError_t launch_gemm_i8(const GemmLaunch& L, hipStream_t st) {
 }  // namespace tl
 
 extern "C" void tlk_gemm_i8_set_cfg(int cfg) { tl::gemm_i8_set_cfg(cfg); }
+extern "C" void tlk_gemm_i8_set_split(int s) { tl::gemm_i8_set_split(s); }

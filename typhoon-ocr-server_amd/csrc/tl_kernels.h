@@ -246,6 +246,7 @@ hipError_t tlk_launch_gemm(const GemmLaunch* L, hipStream_t st);
 // bytes (L->part) and zeroed arrival counters (L->cnt); 0 when none
 void tlk_gemm_needs(const GemmLaunch* L, size_t* part_bytes, size_t* counters);
 void tlk_gemm_i8_set_cfg(int cfg);   // tuning override of the int8 GEMM (-1 = planner)
+void tlk_gemm_i8_set_split(int s);   // tuning override of its K slices (0 = planner)
 // tuning override of the 16-bit GEMM: tile configuration 0..2 (-1 = planner)
 // and K slices (0 = planner)
 void tlk_gemm_b16_set_plan(int cfg, int split);
@@ -335,6 +336,8 @@ hipError_t launch_gemm(const GemmLaunch& L, hipStream_t st);
 hipError_t launch_gemm_i8(const GemmLaunch& L, hipStream_t st);
 int gemm_i8_pick_cfg(int M, int N, int K);
 void gemm_i8_set_cfg(int cfg);
+void gemm_i8_set_split(int s);
+void gemm_i8_needs(int M, int N, int K, size_t* part_bytes, size_t* counters);
 
 // LDS-staged 16-bit MFMA GEMM (gemm_b16.hip): A_BF16 / A_F16, used for M > 16
 // when X rows are 16-byte aligned pieces

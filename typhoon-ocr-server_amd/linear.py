@@ -41,6 +41,7 @@ SIGNATURES = {
     "tl_device_count": (_int, []),
     "tl_gemv_set_plan": (_int, [_int, _int]),
     "tl_gemm_i8_set_cfg": (_int, [_int]),
+    "tl_gemm_i8_set_split": (_int, [_int]),
     "tl_gemm_b16_set_plan": (_int, [_int, _int]),
     "tl_rows_set_split": (_int, [_int]),
     "tl_rows_set_groups": (_int, [_int]),
