@@ -140,11 +140,13 @@ int tl_rows_set_groups(int groups);
  * int8 digit rows; 0 on the bf16 / fp16 MFMA small-batch kernel. */
 int tl_w8a16_set_gemv(int on);
 
-/* Tuning switch of w8a32_linear at batch 2 for every later call in the
- * process: on the GEMV's weight stream with the two token rows as eight int8
- * digit rows for K > 4096 (1, the default), for every K (2), or never (0:
- * the digit-row MFMA kernel of batches 2..8, the same arithmetic at one K
- * slice). */
+/* Tuning switch of w8a32_linear at batch 2..4 for every later call in the
+ * process: on the GEMV's weight stream with four int8 digit rows per token
+ * where measured faster (1, the default: batch 2 at every shape, 3..4 below
+ * 32768 weight rows, K <= 8192), wherever the kernel takes the shape (2:
+ * batch 2 up to K = 16384, 3..4 up to K = 8192), or never (0: the digit-row
+ * MFMA kernel of batches 2..8 or the planes GEMM, the same arithmetic as the
+ * former at one K slice). */
 int tl_w8a32_set_gemv2(int on);
 
 /* Measurement aid, no counterpart in the reference: one streaming read of

@@ -396,49 +396,64 @@ def test_rows_digit_planes_k_slices(lin, orc, M, N, K):
         lib.tl_w8a32_set_gemv2(1)
 
 
+@pytest.mark.parametrize("M", [2, 3, 4])
 @pytest.mark.parametrize("N,K", [(4096, 2048), (2048, 2048), (12288, 2048), (2048, 6144), (1000, 1000),
                                  (37, 50), (300, 16384)])
-def test_w8a32_two_rows_on_the_gemv(lin, orc, dev, N, K):
-    """w8a32_linear at batch 2 on the GEMV's weight stream with the two fp32
-    rows as eight int8 digit rows (the default from K > 4096; switched on at
-    every K here): bit-identical to the digit-row kernel at
-    one K slice (the same exponent, digits, sums and epilogue), which is its
-    path at batch 2 with the switch off, and within relative L2 1e-5 of the
-    oracle's fp32 GEMM, bias included; a NaN in one row gives NaN in that
-    row only, an all-zero row gives the bias exactly; the device entry point
+def test_w8a32_token_rows_on_the_gemv(lin, orc, dev, M, N, K):
+    """w8a32_linear at batch 2..4 on the GEMV's weight stream with four int8
+    digit rows per fp32 token (switched on for every shape it takes here):
+    bit-identical to the digit-row kernel at one K slice (the same exponent,
+    digits, sums and epilogue), which is its path with the switch off, and
+    within relative L2 1e-5 of the oracle's fp32 GEMM, bias included (rows of
+    1e-36 and 1e35 magnitude too); a NaN in one row gives NaN in that row
+    only, an all-zero row gives the bias exactly; the device entry point
     gives the same bits."""
     import torch
-    say(f"w8a32 two rows on the GEMV N={N} K={K}")
+    if M > 2 and K > 8192:
+        pytest.skip("3 or 4 token rows run on the GEMV up to K = 8192")
+    say(f"w8a32 {M} token rows on the GEMV N={N} K={K}")
     lib = lin.load_library()
-    rng = np.random.default_rng(N * 7 + K)
-    x, w, s = make(rng, 2, N, K)
+    rng = np.random.default_rng(N * 7 + K + M)
+    x, w, s = make(rng, M, N, K)
     b = rng.standard_normal(N).astype(F)
     want = orc.w8a32_linear(x, w, s, bias=b)
-    assert lib.tl_w8a32_set_gemv2(2) == 0            # the GEMV at every K (by default K > 4096)
+    assert lib.tl_w8a32_set_gemv2(2) == 0            # the GEMV for every shape it takes
     try:
         got = lin.w8a32_linear(x, w, s, bias=b)
         assert rel_l2(got, want) <= 1e-5, rel_l2(got, want)
         xn = x.copy()
-        xn[1, K // 3] = np.nan
+        xn[M - 1, K // 3] = np.nan
         xz = x.copy()
         xz[0] = 0.0
         gn = lin.w8a32_linear(xn, w, s, bias=b)
         gz = lin.w8a32_linear(xz, w, s, bias=b)
-        assert np.isnan(gn[1]).all()
-        np.testing.assert_array_equal(gn[0], got[0])
+        assert np.isnan(gn[M - 1]).all()
+        np.testing.assert_array_equal(gn[:M - 1], got[:M - 1])
         np.testing.assert_array_equal(gz[0], b)
-        np.testing.assert_array_equal(gz[1], got[1])
+        np.testing.assert_array_equal(gz[1:], got[1:])
+        # a row of 1e-36 (a digit scale of about 2^149, past the float range,
+        # taken in two exact steps) and one of 1e35
+        xe = x.copy()
+        xe[0] *= F(1e-36)
+        xe[1] *= F(1e35)
+        ge = lin.w8a32_linear(xe, w, s)
+        we = orc.w8a32_linear(xe, w, s)
+        for r in range(M):
+            assert rel_l2(ge[r], we[r]) <= 1e-5, (r, rel_l2(ge[r], we[r]))
         W = lin.DeviceWeights.from_codes(w, s)
-        y = torch.empty((2, N), dtype=torch.float32, device=dev)
+        y = torch.empty((M, N), dtype=torch.float32, device=dev)
         lin.w8a32_linear_dev(torch.from_numpy(x).to(dev), W, y, bias=torch.from_numpy(b).to(dev))
         torch.cuda.synchronize()
         np.testing.assert_array_equal(y.cpu().numpy(), got)
         W.close()
-        if N < 32768 and K % 4 == 0 and K <= 6144:     # the digit-row kernel's one-slice shapes
+        # the digit-row kernel's one-slice shapes (at most 96 k-blocks a slice
+        # for 2 tokens, 64 for 3..4)
+        if N < 32768 and K % 4 == 0 and -(-K // 64) <= (96 if M <= 2 else 64):
             assert lib.tl_w8a32_set_gemv2(0) == 0
             assert lib.tl_rows_set_split(1) == 0
             np.testing.assert_array_equal(lin.w8a32_linear(x, w, s, bias=b), got)
             np.testing.assert_array_equal(lin.w8a32_linear(xz, w, s, bias=b), gz)
+            np.testing.assert_array_equal(lin.w8a32_linear(xe, w, s), ge)
     finally:
         lib.tl_w8a32_set_gemv2(1)
         lib.tl_rows_set_split(0)

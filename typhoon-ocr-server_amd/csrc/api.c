@@ -611,7 +611,21 @@ static int run_gemm(Workspace* ws, GemmLaunch* L, hipStream_t st) {
 /* tuning switches; atomic, since a setter may run while other threads call */
 static atomic_bool g_rows_off = false;
 static atomic_bool g_gemv_w8a16_off = false;   /* W8A16 batch 1 on the bf16 / fp16 MFMA kernel instead */
-static atomic_int g_gemv_rows2 = 1;             /* W8A32 batch 2 on the GEMV: 0 never, 1 K > 4096, 2 any K */
+static atomic_int g_gemv_rows2 = 1;             /* W8A32 batch 2..4 on the GEMV: 0 never, 1 planner, 2 always */
+
+/* W8A32 batch 2..4 on the GEMV's token-row mode (mode 1 the measured choice,
+ * 2 wherever the kernel takes the shape).  Against the digit-row kernel
+ * (rows.hip) and the planes GEMM (graph-replayed calls over rotating weights):
+ * 2 tokens 2.97-7.11 against 3.92-8.04 us on every decoder shape, lm_head
+ * 48.8 against 54.3 us; 3 / 4 tokens 3.92-8.20 against 4.37-9.57 us on every
+ * decoder shape (down 7.40 / 7.48 against 9.50 / 9.57), while an lm_head-wide
+ * weight (53.6 / 55.8 against 54.4 / 54.7 us) stays on the planes GEMM */
+static bool gemv_rows_ok(const tl_weights* W, int batch, int mode) {
+  const int xv = tlk_gemv_fused_xv(W->cols);
+  if (xv == 0 || (batch > 2 && xv > 8)) return false;
+  if (mode == 2 || batch == 2) return true;
+  return W->NG < 2048;
+}
 
 static int run_rows(Workspace* ws, GemmLaunch* L, hipStream_t st, bool* done) {
   *done = false;
@@ -664,15 +678,11 @@ static int op_w8a32_ws(Workspace* ws, const float* X, const tl_weights* W, const
   L.K = W->cols;
   L.ep = EP_SCALE;
   L.out = OUT_F32;
-  /* 2 token rows with K > 4096: the batch-1 GEMV's weight stream with the
-   * two rows as eight int8 digit rows (the arithmetic of the digit-row kernel
-   * below at one K slice, so the same bits), every weight read once for both.
-   * Each weight dword meets 8 code rows from LDS, so below K = 4096, where
-   * the digit-row kernel's per-work-group activation split is short, that
-   * kernel is faster (2048x2048: 3.97 against 4.07 us, 4096x2048: 4.68
-   * against 5.61 us); at 2048x6144 this is (7.04 against 7.81 us). */
-  const int rows2 = atomic_load_explicit(&g_gemv_rows2, memory_order_relaxed);
-  if (batch == 2 && (rows2 == 2 || (rows2 == 1 && W->cols > 4096)) && tlk_gemv_fused_xv(W->cols) > 0) {
+  /* 2..4 token rows: the batch-1 GEMV's weight stream with four int8 digit
+   * rows per token (the arithmetic of the digit-row kernel below at one K
+   * slice, so the same bits), every weight read once for all of them */
+  const int rows_mode = atomic_load_explicit(&g_gemv_rows2, memory_order_relaxed);
+  if (batch >= 2 && batch <= 4 && rows_mode != 0 && gemv_rows_ok(W, batch, rows_mode)) {
     GemvLaunch G = tlk_gemv_launch_init();
     G.x = X;
     G.wt = W->tiles;
@@ -681,7 +691,8 @@ static int op_w8a32_ws(Workspace* ws, const float* X, const tl_weights* W, const
     G.y = Y;
     G.N = W->rows;
     G.K = W->cols;
-    G.epi = EPI_W8A32_ROWS2;
+    G.epi = EPI_W8A32_ROWS;
+    G.ntok = batch;
     HIP_TRY(tlk_launch_gemv_i8(&G, st));
     return 0;
   }

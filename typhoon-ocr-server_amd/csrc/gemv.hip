@@ -57,6 +57,7 @@ struct GemvArgs {
   int x_vec;           // 2: K == 1024*XV and x aligned to 4 elements (unguarded loads)
   int x_type = 0;      // EPI_W8A16: 0 fp32, 1 bf16, 2 fp16
   int out = OUT_F32;   // EPI_W8A16: output type
+  int ntok = 1;        // EPI_W8A32_ROWS: token rows
 };
 
 __device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, int n, int acc, float xs,
@@ -112,6 +113,48 @@ __device__ __forceinline__ void consume_batch(const uint4 (&b)[U], const uint4 (
       const int d = dot16(b[u], cv[u][p], 0);
       acc[p] += (ws.kb_of(i0 + u) < ws.kb1) ? d : 0;
     }
+}
+
+// Digit-row modes (NP = 4..16 code rows, XV > 0): NM int8 MFMAs per load
+// instruction instead of NP LDS reads and 4 NP v_dot4 per lane.  The weight
+// load is the MFMA's second operand as it stands.  RH == 16: lane l holds
+// tile lane l (row l & 15, 16-byte k slice l >> 4), the operand layout
+// itself; the first operand is code row l & 15 at the lane's own k slice
+// (zero rows from NP up), and C[code row][weight row] is the dot product.
+// RH == 8: lane l holds weight row 8h + (l & 7) at k-block kb + (l >> 5),
+// slice (l >> 3) & 3, while the MFMA pairs lane 16 s + i of the first operand
+// with lane 16 s + j of the second: virtual rows j and j + 8 are the same
+// weight row over the two complementary halves of the k slices.  With code
+// row l & 7 at the lane's own (k-block, slice), C[i][j] with i >> 3 == j >> 3
+// is code row i & 7 times weight row j & 7 over one half, and
+// C[i][j] + C[i + 8][j + 8] the whole dot product (the other entries mix
+// halves and are ignored); 16 code rows take two MFMAs, rows 0-7 and 8-15.
+// K-blocks at or past kb1 (clamped loads) and code rows past NP contribute
+// zero operands, so the int32 sums equal the v_dot4 sums bit for bit.
+template <int RH, int NP>
+constexpr int gemv_nm() { return RH == 16 ? (NP + 15) / 16 : (NP + 7) / 8; }
+
+template <int XV, int U, int RH, int NP>
+__device__ __forceinline__ void consume_batch_mfma(const uint4 (&b)[U], const uint4* s_codes, const WStream<RH>& ws,
+                                                   int i0, int lg, int lane, v4i (&acc)[gemv_nm<RH, NP>()]) {
+  constexpr int NM = gemv_nm<RH, NP>();
+#pragma unroll
+  for (int mm = 0; mm < NM; mm++) {
+    const int crow = RH * mm + (lane & (RH - 1));
+    uint4 cv[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      // unconditional LDS read (clamped row), then a mask: a select around
+      // the load would become a branch
+      const uint4 c = s_codes[min(crow, NP - 1) * XV * 64 + ws.kb_clamped(i0 + u) * 4 + lg];
+      const uint32_t m = (crow < NP && ws.kb_of(i0 + u) < ws.kb1) ? 0xffffffffu : 0u;
+      cv[u] = make_uint4(c.x & m, c.y & m, c.z & m, c.w & m);
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++)
+      acc[mm] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, cv[u]), __builtin_bit_cast(v4i, b[u]),
+                                                      acc[mm], 0, 0, 0);
+  }
 }
 
 template <int XV, int U, int RH>
@@ -265,19 +308,21 @@ __device__ __forceinline__ float gemv_x1(const float* x, int xt, int k) {
 // flags: bits 0-1 x_vec, bits 2-4 epilogue, bit 5 bias present, bits 6-7
 // RMSNorm of x first (NORM_*; K == 1024 XV a power of two, x_vec 2); plane
 // mode (PL, EPI_W8A16): bits 8-9 x type (0 fp32, 1 bf16, 2 fp16), bits 10-11
-// output type (OUT_F32, OUT_BF16, OUT_F16).
+// output type (OUT_F32, OUT_BF16, OUT_F16); token rows (PL >= 2,
+// EPI_W8A32_ROWS): bits 12-14 their number.
 //
 // Plane mode: x (any of the three types, held as fp32) becomes four int8
 // digit rows in LDS (digit_word / digit_planes: the row's absmax exponent
-// e, q = x 2^(30-e) truncated), each weight dword meets all four through
-// v_dot4, and y = fma(2^(e-6) t, ws, bias) with t the digit sums' Horner
-// combination: fp32-accurate products (w8a16_linear batch 1,
-// kernel/w8a16_kernel.c:90-182) on the GEMV's weight stream.  PL == 2 takes
-// two fp32 token rows (x [2][K]) as eight digit rows, four per token with the
-// token's own e, and stores y[t][n] = 2^(e_t - 6) fl(t_t ws) (+ bias as its
-// own rounding): w8a32_linear at batch 2 (kernel/w8a32_kernel.c:297-350,
-// fp32 semantics) on the weight stream of batch 1, one weight read for both
-// tokens.
+// e, q = x 2^(30-e) truncated), every weight load meets them in int8 MFMAs
+// (consume_batch_mfma), and y = fma(2^(e-6) t, ws, bias) with t the digit
+// sums' Horner combination: fp32-accurate products (w8a16_linear batch 1,
+// kernel/w8a16_kernel.c:90-182) on the GEMV's weight stream.  PL == 2 and 4
+// take up to that many fp32 token rows (x [ntok][K]) as four digit rows per
+// token with the token's own e, and store y[t][n] = 2^(e_t - 6) fl(t_t ws)
+// (+ bias as its own rounding): w8a32_linear at batch 2..4
+// (kernel/w8a32_kernel.c:297-350, fp32 semantics) on the weight stream of
+// batch 1, one weight read for every token.  Token slots past ntok repeat
+// the last row; their outputs are not stored.
 template <int XV, int U, int RH, int PL>
 __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint8_t* wt, const float* ws,
                                                       float* y, int N, int K, int NG, int KB, int flags,
@@ -305,13 +350,16 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
   a.NG = NG;
   a.epi = (flags >> 2) & 7;
   a.x_vec = flags & 3;
-  constexpr int NTOK = PL == 2 ? 2 : 1;  // token rows of x
+  constexpr int NTOK = PL >= 2 ? PL : 1; // token slots of x
   constexpr int NP = PL ? 4 * NTOK : 1;  // code rows: the activation codes, or 4 digit rows per token
+  static_assert(NP <= 16, "at most 16 code rows");
   const int xt = PL == 1 ? (flags >> 8) & 3 : 0;
+  const int ntok = PL >= 2 ? (flags >> 12) & 7 : 1;   // token rows of x and y
   __shared__ uint4 s_codes[XV > 0 ? XV * 64 * NP : 1];
   __shared__ uint32_t s_mx[4 * NTOK];
   __shared__ float s_tail[4];
-  __shared__ int s_red[NP][RH * 4 * SL];
+  __shared__ int s_red[PL ? 1 : NP][PL ? 1 : RH * 4 * SL];
+  __shared__ int s_redp[PL ? NP : 1][RH][4];   // digit-row modes: [code row][weight row][wave]
 
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // k slice of this wave
@@ -339,16 +387,20 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
   // x is read before the first weight batch is issued, so the wait for x
   // never waits for weights
   float4 xv[XV > 0 ? XV : 1];
-  float4 xv2[PL == 2 ? XV : 1];          // the second token row (PL == 2)
+  float4 xvt[NTOK > 1 ? NTOK - 1 : 1][XV > 0 ? XV : 1];     // token slots 1.. (PL >= 2)
   float4 nwv[XV > 0 ? XV : 1];
   const bool norm = ((flags >> 6) & 3) != NORM_NONE;   // x is a hidden row to normalise first
   if constexpr (XV > 0) {
     if (a.x_vec == 2) {
 #pragma unroll
       for (int i = 0; i < XV; i++) xv[i] = gemv_x4(a.x, xt, 4 * (threadIdx.x + 256 * i));
-      if constexpr (PL == 2) {
+      if constexpr (NTOK > 1) {
 #pragma unroll
-        for (int i = 0; i < XV; i++) xv2[i] = *reinterpret_cast<const float4*>(a.x + K + 4 * (threadIdx.x + 256 * i));
+        for (int t = 1; t < NTOK; t++) {
+          const float* xr = a.x + (size_t)min(t, ntok - 1) * K;
+#pragma unroll
+          for (int i = 0; i < XV; i++) xvt[t - 1][i] = *reinterpret_cast<const float4*>(xr + 4 * (threadIdx.x + 256 * i));
+        }
       }
       if (norm) {
 #pragma unroll
@@ -366,10 +418,13 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
         v.z = (k0 + 2 < K) ? gemv_x1(a.x, xt, k0 + 2) : 0.f;
         v.w = (k0 + 3 < K) ? gemv_x1(a.x, xt, k0 + 3) : 0.f;
         xv[i] = v;
-        if constexpr (PL == 2) {
-          const float* x1 = a.x + K;
-          xv2[i] = make_float4((k0 < K) ? x1[k0] : 0.f, (k0 + 1 < K) ? x1[k0 + 1] : 0.f,
-                               (k0 + 2 < K) ? x1[k0 + 2] : 0.f, (k0 + 3 < K) ? x1[k0 + 3] : 0.f);
+        if constexpr (NTOK > 1) {
+#pragma unroll
+          for (int t = 1; t < NTOK; t++) {
+            const float* x1 = a.x + (size_t)min(t, ntok - 1) * K;
+            xvt[t - 1][i] = make_float4((k0 < K) ? x1[k0] : 0.f, (k0 + 1 < K) ? x1[k0 + 1] : 0.f,
+                                        (k0 + 2 < K) ? x1[k0 + 2] : 0.f, (k0 + 3 < K) ? x1[k0 + 3] : 0.f);
+          }
         }
       }
     }
@@ -392,7 +447,7 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
       uint32_t mx = 0;
 #pragma unroll
       for (int i = 0; i < XV; i++) {
-        const float4 v = t == 0 ? xv[i] : xv2[i];
+        const float4 v = t == 0 ? xv[i] : xvt[t > 0 ? t - 1 : 0][i];
         const uint32_t m01 = max(abs_bits(v.x), abs_bits(v.y));
         const uint32_t m23 = max(abs_bits(v.z), abs_bits(v.w));
         mx = max(mx, max(m01, m23));
@@ -408,12 +463,12 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
       int ex = 0;
       if (m < 0x7f800000u && m != 0) (void)frexpf(__uint_as_float(m), &ex);
       px[t] = m < 0x7f800000u ? ex : kXeNonFinite;
+      const Pow2 ps = pow2_split(30 - ex);
 #pragma unroll
       for (int i = 0; i < XV; i++) {
-        const float4 v = t == 0 ? xv[i] : xv2[i];
+        const float4 v = t == 0 ? xv[i] : xvt[t > 0 ? t - 1 : 0][i];
         uint32_t d[4];
-        digit_planes(digit_word(v.x, 30 - ex), digit_word(v.y, 30 - ex), digit_word(v.z, 30 - ex),
-                     digit_word(v.w, 30 - ex), d);
+        digit_planes(digit_word(v.x, ps), digit_word(v.y, ps), digit_word(v.z, ps), digit_word(v.w, ps), d);
 #pragma unroll
         for (int p = 0; p < 4; p++) sc[(4 * t + p) * XV * 256 + threadIdx.x + 256 * i] = d[p];
       }
@@ -506,45 +561,98 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
   // Both batches were issued before the prologue.  The loop body is
   // straight-line code that enters and leaves with the 2U loads of b0 and b1
   // outstanding, so the compiler keeps the wait counts exact.
-  int acc[NP];
+  int acc[PL ? 1 : NP];
 #pragma unroll
-  for (int p = 0; p < NP; p++) acc[p] = 0;
+  for (int p = 0; p < (PL ? 1 : NP); p++) acc[p] = 0;
+  constexpr int NM = gemv_nm<RH, NP>();
+  v4i macc[NM];                          // digit-row modes: the MFMA accumulators
+#pragma unroll
+  for (int mm = 0; mm < NM; mm++) macc[mm] = v4i{0, 0, 0, 0};
   int i = 0;
-  for (; i + 2 * U < n_i; i += 2 * U) {
+  if constexpr (PL) {
+    for (; i + 2 * U < n_i; i += 2 * U) {
+      consume_batch_mfma<XV, U, RH, NP>(b0, s_codes, st, i, lg, lane, macc);
+      load_batch<XV, U, RH>(b0, c0, st, cg, i + 2 * U, lg);
+      consume_batch_mfma<XV, U, RH, NP>(b1, s_codes, st, i + U, lg, lane, macc);
+      load_batch<XV, U, RH>(b1, c1, st, cg, i + 3 * U, lg);
+    }
+    consume_batch_mfma<XV, U, RH, NP>(b0, s_codes, st, i, lg, lane, macc);
+    consume_batch_mfma<XV, U, RH, NP>(b1, s_codes, st, i + U, lg, lane, macc);
+  } else {
+    for (; i + 2 * U < n_i; i += 2 * U) {
+      consume_batch<XV, U, RH, NP>(b0, c0, s_codes, st, i, lg, acc);
+      load_batch<XV, U, RH>(b0, c0, st, cg, i + 2 * U, lg);
+      consume_batch<XV, U, RH, NP>(b1, c1, s_codes, st, i + U, lg, acc);
+      load_batch<XV, U, RH>(b1, c1, st, cg, i + 3 * U, lg);
+    }
     consume_batch<XV, U, RH, NP>(b0, c0, s_codes, st, i, lg, acc);
-    load_batch<XV, U, RH>(b0, c0, st, cg, i + 2 * U, lg);
     consume_batch<XV, U, RH, NP>(b1, c1, s_codes, st, i + U, lg, acc);
-    load_batch<XV, U, RH>(b1, c1, st, cg, i + 3 * U, lg);
   }
-  consume_batch<XV, U, RH, NP>(b0, c0, s_codes, st, i, lg, acc);
-  consume_batch<XV, U, RH, NP>(b1, c1, s_codes, st, i + U, lg, acc);
 
   // ---- reduction: row r's 4*SL partials (wave w, lane slot q) at
-  //      s_red[p][r*4*SL + w*SL + q], summed in that order by wave 0 ---------
+  //      s_red[p][r*4*SL + w*SL + q], summed in that order by wave 0; in the
+  //      digit-row modes each wave's C entries go to s_redp[p][row][wave]
+  //      (integer sums: every order gives the same bits) ----------------------
+  if constexpr (PL) {
+    // lane l, register e of MFMA mm holds C[4 (l >> 4) + e][l & 15] of its
+    // code rows RH mm ..
+    const int q = lane >> 4;
 #pragma unroll
-  for (int p = 0; p < NP; p++) s_red[p][r * 4 * SL + wv * SL + slot] = acc[p];
+    for (int mm = 0; mm < NM; mm++) {
+      if constexpr (RH == 8) {
+        v4i other;
+#pragma unroll
+        for (int e = 0; e < 4; e++) other[e] = __shfl(macc[mm][e], (lane + 40) & 63, 64);
+        if ((lane & 8) == 0 && q < 2) {    // lanes 0-7 and 16-23: code rows 8 mm + 4q + e, weight row lane & 7
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int cr = 8 * mm + 4 * q + e;
+            if (cr < NP) s_redp[min(cr, NP - 1)][lane & 7][wv] = macc[mm][e] + other[e];
+          }
+        }
+      } else {                             // code rows 4q + e, weight row lane & 15
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int cr = 4 * q + e;
+          if (cr < NP) s_redp[min(cr, NP - 1)][lane & 15][wv] = macc[mm][e];
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < NP; p++) s_red[p][r * 4 * SL + wv * SL + slot] = acc[p];
+  }
   __syncthreads();
   if (wv != 0) return;
   uint64_t key = 0;
   if (lane < RH) {
     int tots[NP];
+    if constexpr (PL) {
 #pragma unroll
-    for (int pp = 0; pp < NP; pp++) {
-      const int4* p = reinterpret_cast<const int4*>(s_red[pp] + lane * 4 * SL);
-      int t = 0;
-#pragma unroll
-      for (int q = 0; q < SL; q++) {
-        const int4 v = p[q];
-        t += (v.x + v.y) + (v.z + v.w);
+      for (int pp = 0; pp < NP; pp++) {
+        const int4 v = *reinterpret_cast<const int4*>(s_redp[pp][lane]);
+        tots[pp] = (v.x + v.y) + (v.z + v.w);
       }
-      tots[pp] = t;
+    } else {
+#pragma unroll
+      for (int pp = 0; pp < NP; pp++) {
+        const int4* p = reinterpret_cast<const int4*>(s_red[pp] + lane * 4 * SL);
+        int t = 0;
+#pragma unroll
+        for (int q = 0; q < SL; q++) {
+          const int4 v = p[q];
+          t += (v.x + v.y) + (v.z + v.w);
+        }
+        tots[pp] = t;
+      }
     }
     const int tot = tots[0];
     const int n = row0 + lane;
-    if constexpr (PL == 2) {
+    if constexpr (PL >= 2) {
       if (n < a.N) {
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
+        for (int t = 0; t < NTOK; t++) {
+          if (t >= ntok) break;
           const float sum = digits_sum(tots[4 * t], tots[4 * t + 1], tots[4 * t + 2], tots[4 * t + 3]);
           float v = px[t] == kXeNonFinite ? __builtin_nanf("") : ldexpf(__fmul_rn(sum, wsv), px[t] - 6);
           if (a.bias) v = __fadd_rn(v, bv);
@@ -603,7 +711,7 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
 template <int XV, int U, int RH, int PL>
 static void launch_one(const GemvArgs& a, int blocks, hipStream_t st) {
   const int flags = (a.x_vec & 3) | ((a.epi & 7) << 2) | (a.bias ? 32 : 0) | ((a.norm & 3) << 6) |
-                    ((a.x_type & 3) << 8) | ((a.out & 3) << 10);
+                    ((a.x_type & 3) << 8) | ((a.out & 3) << 10) | ((a.ntok & 7) << 12);
   const size_t dyn = a.norm == NORM_NUMPY ? (size_t)(a.K / 128) * kNpNormStride * sizeof(float) : 0;
   hipLaunchKernelGGL((gemv_i8_kernel<XV, U, RH, PL>), dim3(blocks), dim3(256), dyn, st, a.x, a.wt, a.ws, a.y,
                      a.N, a.K, a.NG, a.KB, flags, a.xq, a.xs_in, a.bias, a.acc_out, a.xs_out, a.keys,
@@ -735,16 +843,44 @@ hipError_t launch_gemv_i8(const GemvLaunch& L, hipStream_t st) {
       }
   }
   const int xv = L.x ? gemv_fused_xv(L.K) : 0;
-  if (L.epi == EPI_W8A32_ROWS2) {
-    // two fp32 token rows as eight digit rows: fused x only, no RMSNorm
+  if (L.epi == EPI_W8A32_ROWS && L.ntok > 2 && a.NG >= 256 && g_force_rows == 0) {
+    // 3..4 token rows: every work-group splits all of them into digit rows,
+    // so from 256 row groups up the 16-row work-groups (half as many splits)
+    // are faster: 4096x2048 at 3 / 4 tokens 5.30 / 5.39 -> 4.11 / 4.20 us
+    // (2048-row weights stay faster on 8-row work-groups: 3.92 against 4.00)
+    p.rows = 16;
+    p.blocks = cdiv(L.N, 16);
+    const int n_i = cdiv(cdiv(L.K, 64), 4);
+    p.u = 8;
+    for (int u : {2, 4, 8, 12})
+      if (2 * u >= n_i) {
+        p.u = u;
+        break;
+      }
+    if (g_force_u > 0 && u_ok(16, g_force_u)) p.u = g_force_u;
+  }
+  if (L.epi == EPI_W8A32_ROWS) {
+    // 2..4 fp32 token rows as four digit rows each: fused x only, no RMSNorm;
+    // 3 or 4 rows (16 code rows of XV KiB of LDS each) up to K = 8192
     if (!L.x || xv == 0 || L.norm != NORM_NONE || L.x_type != 0 || L.out != OUT_F32) return hipErrorInvalidValue;
+    if (L.ntok < 2 || L.ntok > 4 || (L.ntok > 2 && xv > 8)) return hipErrorInvalidValue;
+    a.ntok = L.ntok;
     if (L.K == 1024 * xv && (((uintptr_t)L.x) & 15) == 0) a.x_vec = 2;
+    if (L.ntok == 2) {
+      switch (xv) {
+        case 2: return launch_xv<2, 2>(a, p, st);
+        case 4: return launch_xv<4, 2>(a, p, st);
+        case 6: return launch_xv<6, 2>(a, p, st);
+        case 8: return launch_xv<8, 2>(a, p, st);
+        case 16: return launch_xv<16, 2>(a, p, st);
+        default: return hipErrorInvalidValue;
+      }
+    }
     switch (xv) {
-      case 2: return launch_xv<2, 2>(a, p, st);
-      case 4: return launch_xv<4, 2>(a, p, st);
-      case 6: return launch_xv<6, 2>(a, p, st);
-      case 8: return launch_xv<8, 2>(a, p, st);
-      case 16: return launch_xv<16, 2>(a, p, st);
+      case 2: return launch_xv<2, 4>(a, p, st);
+      case 4: return launch_xv<4, 4>(a, p, st);
+      case 6: return launch_xv<6, 4>(a, p, st);
+      case 8: return launch_xv<8, 4>(a, p, st);
       default: return hipErrorInvalidValue;
     }
   }

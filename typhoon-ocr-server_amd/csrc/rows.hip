@@ -184,13 +184,13 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
     const uint32_t mx = s_mx[t];
     int ex = 0;
     if (mx < 0x7f800000u && mx != 0) (void)frexpf(__uint_as_float(mx), &ex);
-    const int sh = 30 - ex;
+    const Pow2 sc = pow2_split(30 - ex);
     uint32_t pl[4][4];                       // [plane][dword]
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const float4 v = xr[j][i];
       uint32_t d[4];
-      digit_planes(digit_word(v.x, sh), digit_word(v.y, sh), digit_word(v.z, sh), digit_word(v.w, sh), d);
+      digit_planes(digit_word(v.x, sc), digit_word(v.y, sc), digit_word(v.z, sc), digit_word(v.w, sc), d);
 #pragma unroll
       for (int p = 0; p < 4; p++) pl[p][i] = d[p];
     }

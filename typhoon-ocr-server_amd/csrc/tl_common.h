@@ -237,14 +237,35 @@ __device__ __forceinline__ uint32_t codes4_rne(float4 v, float inv) {
 // ---------------------------------------------------------------------------
 constexpr int kXeNonFinite = -100000;   // exponent marking a row with Inf / NaN
 
+// 2^s as a float, s in [-126, 127]
+__device__ __forceinline__ float pow2f(int s) { return __uint_as_float((uint32_t)(s + 127) << 23); }
+
+// x 2^sh for sh in [-126, 227] as two multiplications by powers of two,
+// 2^s1 with s1 = min(sh, 100), then 2^(sh - s1).  When the second factor is
+// not 1, |x| 2^100 >= 2^-49 for every nonzero float x, so the first product is
+// exact and the result is rounded at most once, in the second: the value of
+// ldexpf(x, sh) (exact when normal, the same round-to-nearest-even when
+// subnormal).  The per-element conversions use this instead of ldexpf: on
+// gfx950 ldexpf followed by the digit clamp measured several times slower
+// (the two-row GEMV's digit prologue 1.2-2.7 us per launch against 0.1-0.6 us).
+struct Pow2 {
+  float a, b;
+};
+__device__ __forceinline__ Pow2 pow2_split(int sh) {
+  const int s1 = min(sh, 100);
+  return Pow2{pow2f(s1), pow2f(sh - s1)};
+}
+__device__ __forceinline__ float mul_pow2(float x, Pow2 p) { return __fmul_rn(__fmul_rn(x, p.a), p.b); }
+
 // the four int8 planes of 4 values of a row with exponent e (v = x 2^-e
 // exact, |v| < 64): dword p holds plane p of the 4 values, one byte each
 __device__ __forceinline__ void planes4_i8(const float (&v)[4], int e, uint32_t (&code)[4]) {
 #pragma unroll
   for (int p = 0; p < 4; p++) code[p] = 0u;
+  const Pow2 sc = pow2_split(-e);
 #pragma unroll
   for (int q = 0; q < 4; q++) {
-    float r = ldexpf(v[q], -e);
+    float r = mul_pow2(v[q], sc);
     float c = rintf(r);
     const uint32_t b0 = (uint32_t)((int)c & 0xff);
     r = __fsub_rn(r, c);
@@ -298,11 +319,11 @@ __device__ __forceinline__ float planes_scale(float t, float ws, int e) {
 // sum_k w_k x_k = 2^(24 - sh) (a0 + 2^-8 (a1 + 2^-8 (a2 + 2^-8 a3))).
 // ---------------------------------------------------------------------------
 // biased digit word of one activation: (q + 0x808080) with q = x 2^sh
-// truncated toward zero (x 2^sh is exact in fp32, |x 2^sh| < 2^30 for a
-// finite slice; the clamp keeps Inf and NaN, whose token's outputs are NaN
-// anyway, in the int range)
-__device__ __forceinline__ uint32_t digit_word(float x, int sh) {
-  return (uint32_t)(int)__builtin_amdgcn_fmed3f(ldexpf(x, sh), -0x1p30f, 0x1p30f) + 0x808080u;
+// truncated toward zero, sc = pow2_split(sh) (x 2^sh is exact wherever
+// |q| >= 1, and |x 2^sh| < 2^30 for a finite slice; the clamp keeps Inf and
+// NaN, whose token's outputs are NaN anyway, in the int range)
+__device__ __forceinline__ uint32_t digit_word(float x, Pow2 sc) {
+  return (uint32_t)(int)__builtin_amdgcn_fmed3f(mul_pow2(x, sc), -0x1p30f, 0x1p30f) + 0x808080u;
 }
 
 // four biased digit words (k .. k+3) -> the four digit-plane dwords:

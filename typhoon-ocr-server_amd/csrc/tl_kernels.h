@@ -33,12 +33,12 @@ static inline int tlk_cdiv(int a, int b) { return (a + b - 1) / b; }
 // y[8b + r] = fl(silu(gate) * up) with the reference's fast-exp silu
 // EPI_W8A16: fp32-semantics products of a bf16 / fp16 / fp32 x (x_type) as
 // four int8 digit rows, y = fma(sum, ws, bias) stored as `out`
-// EPI_W8A32_ROWS2: two fp32 token rows (x [2][K], contiguous) as four int8
-// digit rows each; y[t][n] = 2^(e_t - 6) fl(sum * ws) (+ bias as its own
-// rounding), y [2][N]: the arithmetic of the digit-row kernel (rows.hip) at
-// one K slice
+// EPI_W8A32_ROWS: 2..4 fp32 token rows (x [ntok][K], contiguous) as four
+// int8 digit rows each; y[t][n] = 2^(e_t - 6) fl(sum * ws) (+ bias as its own
+// rounding), y [ntok][N]: the arithmetic of the digit-row kernel (rows.hip)
+// at one K slice
 enum { EPI_W8A32 = 0, EPI_W8A8 = 1, EPI_ACC = 2, EPI_ARGMAX = 3, EPI_SWIGLU = 4, EPI_W8A16 = 5,
-       EPI_W8A32_ROWS2 = 6 };
+       EPI_W8A32_ROWS = 6 };
 // GEMV x prologues: the numpy final RMSNorm (decoder.py:444-446) or the
 // decoder's RMSNorm (kernel/ops.c:22-56, estimate-based rsqrt)
 enum { NORM_NONE = 0, NORM_NUMPY = 1, NORM_DECODER = 2 };
@@ -188,6 +188,7 @@ typedef struct GemvLaunch {
   int N TLK_DEF(0), K TLK_DEF(0), epi TLK_DEF(EPI_W8A32);
   int x_type TLK_DEF(0);                 // EPI_W8A16: x is 0 fp32, 1 bf16, 2 fp16
   int out TLK_DEF(OUT_F32);              // EPI_W8A16: y is OUT_F32 / OUT_BF16 / OUT_F16
+  int ntok TLK_DEF(1);                   // EPI_W8A32_ROWS: token rows of x and y (2..4)
 } GemvLaunch;
 static inline GemvLaunch tlk_gemv_launch_init(void) {
   GemvLaunch L;
@@ -196,6 +197,7 @@ static inline GemvLaunch tlk_gemv_launch_init(void) {
   L.norm_eps = 1e-6f;
   L.epi = EPI_W8A32;
   L.out = OUT_F32;
+  L.ntok = 1;
   return L;
 }
 void tlk_gemv_plan(int N, int K, GemvPlan* plan);
