@@ -118,7 +118,11 @@ int tl_gemm_i8_set_split(int split);
 
 /* Tuning override of the 16-bit MFMA GEMM (W8A16, M > 16 on the tiled
  * kernel) for every later call in the process: cfg -1 restores the planner's
- * tile, 0..2 force 128x192, 64x128 or 32x64 tiles; split 0 restores the
+ * kernel and tile, 0..2 force 128x192, 64x128 or 32x64 tiles, 3 forces the
+ * streamed small-M kernel (M <= 256, weights read once per work-group of
+ * token rows; with cfg 3 a split of 100 R + 10 TG + U picks its work-group
+ * shape: R, TG in {1, 2, 4} weight / token row groups, U in {2, 4} tiles per
+ * load batch); split 0 restores the
  * planner's K slices, 1..64 force that many (work-groups per tile, whose fp32
  * partial sums the last to arrive adds in slice order). */
 int tl_gemm_b16_set_plan(int cfg, int split);

@@ -844,6 +844,62 @@ def test_w8a16_k_slices(lin, orc, dev, M, N, K):
     W.close()
 
 
+SMALL_B16_SHAPES = [100 * r + 10 * t + u for r in (1, 2, 4) for t in (1, 2, 4) for u in (2, 4)
+                    if u == 2 or t == 1 or r * t <= 8]
+
+
+@pytest.mark.parametrize("M,N,K", [(96, 2048, 2048), (128, 1000, 1000), (200, 2000, 2112), (40, 4096, 2048),
+                                   (17, 300, 192)])
+def test_w8a16_small_kernel_shapes(lin, orc, dev, M, N, K):
+    """W8A16 batches of 17..256 tokens on the streamed small-M kernel (token
+    rows spread over the grid's y extent): the planner's choice and every
+    forced work-group shape (tl_gemm_b16_set_plan(3, 100 R + 10 TG + U)),
+    ragged M, N and K included: fp32 out within 1e-5 and bf16 out within 2e-3
+    of a float64 product in every row, with and without bias; fp16 X with fp16
+    out within 2e-3; a repeated call bit-identical."""
+    import torch
+    lib = lin.load_library()
+    rng = np.random.default_rng(M * 5 + N + K)
+    x, w, s = make(rng, M, N, K)
+    b = rng.standard_normal(N).astype(F)
+    W = lin.DeviceWeights.from_codes(w, s)
+    xt = torch.from_numpy(x).to(dev).to(torch.bfloat16)
+    bd = torch.from_numpy(b).to(dev)
+    want = (xt.float().cpu().numpy().astype(np.float64) @ w.astype(np.float64).T) * s.astype(np.float64)
+    wantb = want + b.astype(np.float64)
+    xh = torch.from_numpy(x.astype(np.float16)).to(dev)
+    wanth = (x.astype(np.float16).astype(np.float64) @ w.astype(np.float64).T) * s.astype(np.float64)
+    y32 = torch.empty((M, N), dtype=torch.float32, device=dev)
+    yb = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    yh = torch.empty((M, N), dtype=torch.float16, device=dev)
+    try:
+        for cfg, code in [(-1, 0), (3, 0)] + [(3, c) for c in SMALL_B16_SHAPES]:
+            say(f"w8a16 small kernel M={M} N={N} K={K} cfg={cfg} shape={code}")
+            assert lib.tl_gemm_b16_set_plan(cfg, code) == 0
+            lin.w8a16_linear_dev(xt, W, y32)
+            lin.w8a16_linear_dev(xt, W, yb)
+            lin.w8a16_linear_dev(xh, W, yh)
+            torch.cuda.synchronize()
+            first = y32.cpu().numpy().copy()
+            e = row_rel_l2(first, want)
+            assert e.max() <= 1e-5, (code, int(e.argmax()), float(e.max()))
+            e = row_rel_l2(yb.float().cpu().numpy(), want)
+            assert e.max() <= 2e-3, (code, int(e.argmax()), float(e.max()))
+            e = row_rel_l2(yh.float().cpu().numpy(), wanth)
+            assert e.max() <= 2e-3, (code, int(e.argmax()), float(e.max()))
+            lin.w8a16_linear_dev(xt, W, y32, bias=bd)
+            torch.cuda.synchronize()
+            e = row_rel_l2(y32.cpu().numpy(), wantb)
+            assert e.max() <= 1e-5, (code, int(e.argmax()), float(e.max()))
+            y32.fill_(np.nan)
+            lin.w8a16_linear_dev(xt, W, y32)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(y32.cpu().numpy(), first)
+    finally:
+        lib.tl_gemm_b16_set_plan(-1, 0)
+    W.close()
+
+
 @pytest.mark.parametrize("M,N,K", [(1024, 6144, 2048), (1024, 2048, 6144), (300, 1000, 1000)])
 def test_w8a8_quantize_tiles_then_gemm(lin, orc, dev, M, N, K):
     """The two halves of tl_w8a8_linear_f32_dev (per-token codes into the

@@ -388,16 +388,27 @@ enum GemmKernel { GK_SMALL, GK_I8, GK_B16, GK_GENERIC };
 static GemmKernel gemm_choice(const GemmLaunch& L) {
   // up to 16 token rows always stream the weights once; more rows too while N
   // is small (N <= 4096: the tiled kernels would leave CUs idle), up to 64
-  // int8 rows and 48 16-bit rows (measured at N = 2048 / 4096: 64 bf16 rows
-  // 14.1 us here against 11.3 us tiled, 48 rows even, 32 rows 8.2 against
-  // 11.4 us; int8 rows faster here up to 64); for wide N the activation
+  // int8 rows; for wide N the activation
   // fragments every work-group re-reads cost more than the tiled kernels' reuse,
   // except up to 32 int8 rows at lm_head width (>= 2048 row groups, four per
   // work-group share each fragment): the int8 planes of 5-8 fp32 tokens,
   // 81 -> 70 us for the lm_head at 8 tokens
-  const int small_rows = (L.amode == A_BF16 || L.amode == A_F16) ? 48 : 64;
-  const bool wide_i8 = L.amode == A_I8 && L.M <= 32 && cdiv(L.N, 16) >= 2048;
-  if (gemm_small_supported(L) && (L.M <= 16 || (L.M <= small_rows && cdiv(L.N, 16) <= 256) || wide_i8))
+  const bool b16 = L.amode == A_BF16 || L.amode == A_F16;
+  if (b16) {   // tuning override: 3 the small-M kernel, 0..2 a tile of the tiled one
+    const int fc = gemm_b16_forced_cfg();
+    if (fc == 3 && gemm_small_supported(L)) return GK_SMALL;
+    if (fc >= 0 && fc <= 2 && L.M > 16 && gemm_b16_supported(L)) return GK_B16;
+  }
+  // 16-bit rows (one token group per work-group, the grid's y extent over the
+  // token rows): up to 128 rows at N <= 2048 and 64 at N <= 4096, measured at
+  // K = 2048 against every tile of the tiled kernel (M = 64 / 96 / 128,
+  // N = 2048: 6.7 / 9.0 / 9.2 us against 10.5 / 11.5 / 11.5; M = 64,
+  // N = 4096: 9.6 against 11.6; at M = 256, or N = 12288 from 32 rows, the
+  // tiled kernel wins: 11.6 against 13.4 us, 12.0 against 14.1)
+  const int ng = cdiv(L.N, 16);
+  const bool b16_small = b16 && ((ng <= 128 && L.M <= 128) || (ng <= 256 && L.M <= 64));
+  const bool wide_i8 = L.amode == A_I8 && L.M <= 32 && ng >= 2048;
+  if (gemm_small_supported(L) && (L.M <= 16 || (!b16 && L.M <= 64 && ng <= 256) || b16_small || wide_i8))
     return GK_SMALL;
   if (L.amode == A_I8 && L.M > 16) return GK_I8;
   if (L.amode != A_I8 && L.M > 16 && gemm_b16_supported(L)) return GK_B16;

@@ -411,9 +411,15 @@ static void b16_cfg(int cfg, int& mt, int& nt) {
 static std::atomic<int> g_b16_force_cfg{-1};
 static std::atomic<int> g_b16_force_split{0};
 void gemm_b16_set_plan(int cfg, int split) {
-  g_b16_force_cfg.store(cfg >= 0 && cfg <= 2 ? cfg : -1, std::memory_order_relaxed);
+  g_b16_force_cfg.store(cfg >= 0 && cfg <= 3 ? cfg : -1, std::memory_order_relaxed);
+  // with cfg 3, split (when > 64) picks the small-M kernel's work-group shape
+  gemm_small_set_b16_shape(cfg == 3 && split > 64 ? split : 0);
+  if (cfg == 3) split = 0;
   g_b16_force_split.store(split > 0 ? split : 0, std::memory_order_relaxed);
 }
+
+// -1 planner, 0..2 a forced tile of this kernel, 3 the streamed small-M kernel
+int gemm_b16_forced_cfg() { return g_b16_force_cfg.load(std::memory_order_relaxed); }
 
 static int b16_tiles(int cfg, int MG, int NG) {
   int mt, nt;
@@ -444,7 +450,7 @@ static void b16_plan(int MG, int NG, int KB, int& cfg_out, int& split_out) {
   sp = std::min(sp, 4);
   const int fc = g_b16_force_cfg.load(std::memory_order_relaxed);
   const int fs = g_b16_force_split.load(std::memory_order_relaxed);
-  if (fc >= 0) best = fc;
+  if (fc >= 0 && fc <= 2) best = fc;
   if (fs > 0) sp = std::min(fs, std::max(1, KB));
   cfg_out = best;
   split_out = sp;

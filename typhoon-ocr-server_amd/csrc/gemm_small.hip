@@ -16,6 +16,9 @@
 //   A_F32X3 fp32 rows split exactly into three bf16 terms (six MFMAs per block)
 // Token rows >= M read row M-1 (their output columns are never stored); K
 // positions >= K are zero in the weight tiles and are zeroed in X as well.
+#include <algorithm>
+#include <atomic>
+
 #include "tl_common.h"
 #include "tl_kernels.h"
 
@@ -172,8 +175,10 @@ __device__ inline acc_small_t<AMODE> mma_x(const WOps<AMODE>& w, const XOps<AMOD
 // R row groups per work-group share every activation fragment (loaded and,
 // for fp32 activations, split into bf16 terms once per k-block), so the
 // activation work per weight byte falls by R for large N.  TG token groups of
-// 16 rows (M <= 16 TG) ride along on every weight tile: the weights are
-// streamed once for all of them.
+// 16 rows ride along on every weight tile: the weights are streamed once for
+// all of them.  Work-group (x, y) takes row groups R x .. R x + R - 1 and
+// token groups TG y .. TG y + TG - 1, so the grid's y extent spreads the
+// token rows over more work-groups where one would re-read all of them.
 template <int AMODE, int U, int R, int TG>
 __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
   using acc_t = acc_small_t<AMODE>;
@@ -182,6 +187,7 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g0 = blockIdx.x * R;                       // first weight row group
+  const int tg0 = blockIdx.y * TG;                     // first token group
   const int kb0 = (wv * a.KB) / 4, kb1 = ((wv + 1) * a.KB) / 4;
   const int n_t = kb1 - kb0;                           // may be 0 when KB < 4
   const int last = max(n_t - 1, 0);
@@ -211,7 +217,7 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
         b[u][r] = make_uint4(w.x, w.y, w.z, w.w);
       }
 #pragma unroll
-      for (int g = 0; g < TG; g++) x[u][g] = load_a<AMODE>(a, min(kb0 + t, a.KB - 1), g, lane);
+      for (int g = 0; g < TG; g++) x[u][g] = load_a<AMODE>(a, min(kb0 + t, a.KB - 1), tg0 + g, lane);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -276,7 +282,7 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
             const int a1 = __shfl_xor(tot[q], 1, 64), a2 = __shfl_xor(tot[q], 2, 64), a3 = __shfl_xor(tot[q], 3, 64);
             y[q] = planes_sum(tot[q], a1, a2, a3);
           }
-          const int m = tg * 16 + (lane & 15);
+          const int m = (tg0 + tg) * 16 + (lane & 15);
           if ((lane & 3) != 0 || m >= a.M) continue;
           const int t = m >> 2;
           const int e = a.xe[t];
@@ -292,12 +298,12 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
       return;
     }
   }
-  // lane holds D[n .. n+3][m]: m = 16 tg + (lane & 15), n = 16 g + 4 (lane >> 4)
+  // lane holds D[n .. n+3][m]: m = 16 (tg0 + tg) + (lane & 15), n = 16 g + 4 (lane >> 4)
 #pragma unroll
   for (int tg = 0; tg < TG; tg++)
 #pragma unroll
   for (int rg = 0; rg < R; rg++) {
-    const int m = tg * 16 + (lane & 15);
+    const int m = (tg0 + tg) * 16 + (lane & 15);
     if (m >= a.M) continue;
     acc_t tot = s_part[rg][tg][0][lane];
 #pragma unroll
@@ -340,7 +346,8 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
 }
 
 bool gemm_small_supported(const GemmLaunch& L) {
-  if (L.M < 1 || L.M > 64) return false;
+  const int max_rows = (L.amode == A_BF16 || L.amode == A_F16) ? 256 : 64;
+  if (L.M < 1 || L.M > max_rows) return false;
   if (L.amode == A_I8) return true;                    // code tiles, any K
   const int epv = (L.amode == A_F32X3) ? 4 : 8;        // elements per 16 bytes
   if (L.K % epv != 0 || L.lda % epv != 0) return false;
@@ -349,9 +356,16 @@ bool gemm_small_supported(const GemmLaunch& L) {
 
 template <int AMODE, int R, int TG>
 static void launch_small_rt(const GemmSmallArgs& a, int u, hipStream_t st) {
-  const dim3 grid(cdiv(a.NG, R)), block(256);
-  if (u == 4) hipLaunchKernelGGL((gemm_small_kernel<AMODE, 4, R, TG>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((gemm_small_kernel<AMODE, 2, R, TG>), grid, block, 0, st, a);
+  const dim3 grid(cdiv(a.NG, R), cdiv(a.MG, TG)), block(256);
+  // batches of 4 tiles exist for one token group, and for 16-bit rows up to
+  // 8 row x token groups per work-group (wider ones pass 512 VGPRs)
+  if constexpr (TG == 1 || ((AMODE == A_BF16 || AMODE == A_F16) && R * TG <= 8)) {
+    if (u == 4) {
+      hipLaunchKernelGGL((gemm_small_kernel<AMODE, 4, R, TG>), grid, block, 0, st, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((gemm_small_kernel<AMODE, 2, R, TG>), grid, block, 0, st, a);
 }
 
 template <int AMODE, int R>
@@ -364,8 +378,14 @@ static void launch_small_r(const GemmSmallArgs& a, int u, int tg, hipStream_t st
 template <int AMODE>
 static void launch_small_mode(const GemmSmallArgs& a, int u, int r, int tg, hipStream_t st) {
   if (r == 4) launch_small_r<AMODE, 4>(a, u, tg, st);
+  else if (r == 2) launch_small_r<AMODE, 2>(a, u, tg, st);
   else launch_small_r<AMODE, 1>(a, u, tg, st);
 }
+
+// tuning override of the 16-bit rows' work-group shape: 100 R + 10 TG + U
+// (R, TG in {1, 2, 4}, U in {2, 4}), 0 = the planner in launch_gemm_small
+static std::atomic<int> g_small_b16_shape{0};
+void gemm_small_set_b16_shape(int code) { g_small_b16_shape.store(code, std::memory_order_relaxed); }
 
 hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st) {
   if (!gemm_small_supported(L)) return hipErrorInvalidValue;
@@ -392,12 +412,39 @@ hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st) {
   const int n_t = cdiv(a.KB, 4);
   // four row groups per work-group once there are work-groups to spare
   // (>= 2048 row groups: the lm_head), else one
-  const int r = a.NG >= 2048 ? 4 : 1;
-  const int tg = a.MG <= 1 ? 1 : (a.MG <= 2 ? 2 : 4);
+  int r = a.NG >= 2048 ? 4 : 1;
+  int tg = a.MG <= 1 ? 1 : (a.MG <= 2 ? 2 : 4);
+  const bool b16 = L.amode == A_BF16 || L.amode == A_F16;
+  int u_force = 0;
+  if (b16 && a.MG >= 2) {
+    // 16-bit rows, 17..256 tokens: one token group per work-group (the token
+    // rows spread over the grid's y extent instead of every work-group
+    // re-reading all of them) and two weight row groups while that still
+    // gives 160+ work-groups, with a wave's whole K quarter in flight at
+    // K = 2048.  Measured over every shape (R, TG, U) at K = 2048: best or
+    // within 2 % of it wherever this kernel beats the tiled one, e.g.
+    // M = 64, N = 2048: 6.7 us against 10.5 (tiled 32 x 64 tiles, 4 K slices)
+    // and 6.8-7.3 us for one row group x all four token groups.
+    r = (long long)cdiv(a.NG, 2) * a.MG >= 160 ? 2 : 1;
+    tg = 1;
+    u_force = n_t >= 8 ? 4 : 2;
+  }
+  if (b16) {
+    const int code = g_small_b16_shape.load(std::memory_order_relaxed);
+    const int cr = code / 100, ct = (code / 10) % 10, cu = code % 10;
+    if ((cr == 1 || cr == 2 || cr == 4) && (ct == 1 || ct == 2 || ct == 4) && (cu == 2 || cu == 4) &&
+        (cu == 2 || ct == 1 || cr * ct <= 8)) {
+      r = cr;
+      tg = ct;
+      u_force = cu;
+    }
+  }
+  if (cdiv(a.MG, tg) > 65535) return hipErrorInvalidValue;
   // batches of 4 tiles only with one token group: more activation fragments
   // in flight push the waves past 256 VGPRs (one wave per SIMD); int8 codes
   // (one 16-byte fragment per tile) also with four row groups
-  const int u = (tg == 1 && n_t >= 8 && (r == 1 || L.amode == A_I8)) ? 4 : 2;
+  int u = (tg == 1 && n_t >= 8 && (r == 1 || L.amode == A_I8)) ? 4 : 2;
+  if (u_force) u = u_force;
   switch (L.amode) {
     case A_I8: launch_small_mode<A_I8>(a, u, r, tg, st); break;
     case A_BF16: launch_small_mode<A_BF16>(a, u, r, tg, st); break;

@@ -347,6 +347,8 @@ bool gemm_b16_supported(const GemmLaunch& L);
 hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st);
 void gemm_b16_needs(int M, int N, int K, size_t* part_bytes, size_t* counters);
 void gemm_b16_set_plan(int cfg, int split);
+int gemm_b16_forced_cfg();
+void gemm_small_set_b16_shape(int code);
 void gemm_needs(const GemmLaunch& L, size_t* part_bytes, size_t* counters);
 // M <= 16 rows (gemm_small.hip): GEMV-shaped MFMA kernel
 bool gemm_small_supported(const GemmLaunch& L);
