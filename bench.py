@@ -907,6 +907,8 @@ def main():
                     help="decode set only (no prefill, sweeps or CPU baseline)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the W8A8 prefill timing (for counter runs)")
+    ap.add_argument("--w8a16-only", action="store_true",
+                    help="only the W8A16 sweep (for counter runs)")
     ap.add_argument("--decoder-layers", type=int, default=28,
                     help="layers of the full-decoder workload (fewer only to profile it)")
     ap.add_argument("--decoder-steps", type=int, default=512,
@@ -942,6 +944,9 @@ def main():
 
     if args.prefill_only:
         print(json.dumps({"w8a8_prefill": bench_w8a8_prefill(lin, torch, dev)}), flush=True)
+        return
+    if args.w8a16_only:
+        print(json.dumps({"w8a16_sweep": bench_w8a16_sweep(lin, torch, dev)}), flush=True)
         return
     if args.decoder_only:
         print(json.dumps({"decoder_greedy": bench_decoder_generate(lin, torch, dev, n_layers=args.decoder_layers,
