@@ -701,7 +701,12 @@ static int op_w8a32_ws(Workspace* ws, const float* X, const tl_weights* W, const
    * splits its activation slice, which an lm_head-wide grid repeats too
    * often: 151936 rows at 2 tokens 60.1 us there against 57.0 us below, at 8
    * tokens 133 against 68 us) */
-  if (batch <= 8 && W->NG < 2048) {
+  /* ... except 5..8 rows with K past 2048 (more than 32 k-blocks), which the
+   * digit-row kernel's LDS takes in several K slices and a merge: there the
+   * planes below are faster (2048x6144 at 5 / 8 tokens 13.8 / 14.7 us against
+   * 11.2 / 11.4 us), unless a slice count is forced for tuning */
+  const bool rows_sliced = batch > 4 && tlk_cdiv(W->cols, 64) > 32 && tlk_rows_forced_split() == 0;
+  if (batch <= 8 && W->NG < 2048 && !rows_sliced) {
     bool done;
     TRY(run_rows(ws, &L, st, &done));
     if (done) return 0;

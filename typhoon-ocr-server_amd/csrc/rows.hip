@@ -468,6 +468,7 @@ void tlk_rows_plan(int M, int N, int K, RowsPlan* plan) { *plan = tl::rows_plan(
 size_t tlk_rows_workspace_bytes(int M, int N, int K) { return tl::rows_workspace_bytes(M, N, K); }
 size_t tlk_rows_counter_count(int N) { return tl::rows_counter_count(N); }
 void tlk_rows_set_split(int s) { tl::rows_set_split(s); }
+int tlk_rows_forced_split(void) { return tl::g_rows_force_split.load(std::memory_order_relaxed); }
 void tlk_rows_set_groups(int r) { tl::rows_set_groups(r); }
 hipError_t tlk_launch_rows(const GemmLaunch* L, hipStream_t st) { return tl::launch_rows(*L, st); }
 }  // extern "C"

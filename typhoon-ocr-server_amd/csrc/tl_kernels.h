@@ -265,6 +265,7 @@ void tlk_rows_plan(int M, int N, int K, RowsPlan* plan);
 size_t tlk_rows_workspace_bytes(int M, int N, int K);   // partials when split > 1
 size_t tlk_rows_counter_count(int N);                   // zeroed arrival counters
 void tlk_rows_set_split(int s);                         // tuning override (0 = planner)
+int tlk_rows_forced_split(void);                        // that override (0 = none)
 void tlk_rows_set_groups(int r);                        // tuning override (0 = planner)
 hipError_t tlk_launch_rows(const GemmLaunch* L, hipStream_t st);
 
