@@ -47,6 +47,27 @@ def bf16_to_f32(b):
     return (b.astype(np.uint32) << 16).view(F)
 
 
+def plant_inf(x, w, r, k_pos=9, k_neg=None):
+    """Row r of x gets +Inf at column k_pos and -Inf at column k_neg (K - 5 by
+    default, another K slice for K > 64), and every seventh weight row a zero
+    code at k_pos: the reference's fp32 sums then give NaN (inf * 0, or
+    infinite terms of both signs), +Inf and -Inf across the outputs."""
+    K = x.shape[1]
+    k_neg = K - 5 if k_neg is None else k_neg
+    x[r, k_pos] = np.inf
+    x[r, k_neg] = -np.inf
+    w[::7, k_pos] = 0
+
+
+def assert_nonfinite_row(got, want, tag=""):
+    """A row holding Inf: NaN exactly where the oracle gives NaN, and the
+    oracle's signed Inf everywhere else (all three occur)."""
+    assert np.isnan(want).any() and np.isposinf(want).any() and np.isneginf(want).any(), tag
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want), err_msg=f"NaN positions {tag}")
+    keep = ~np.isnan(want)
+    np.testing.assert_array_equal(got[keep], want[keep], err_msg=f"signed Inf {tag}")
+
+
 def test_single_hip_runtime(lin):
     """The library and torch must share one HIP runtime in the process."""
     lin.load_library()
@@ -292,8 +313,8 @@ def test_w8a32_planes_special_rows(lin, orc, M, N, K):
     1000x its rms are each within relative L2 1e-5 of the oracle's fp32
     GEMM (the planes hold x to about 2^-32 of the row's absmax, with an exact
     power-of-two scale); a row holding NaN gives NaN in every output, a row
-    holding Inf gives no finite output (the reference's sums give NaN or
-    +-Inf there; here every such output is NaN)."""
+    holding +Inf and -Inf gives the oracle's NaN / +Inf / -Inf output by
+    output."""
     say(f"w8a32 planes special rows M={M} N={N} K={K}")
     rng = np.random.default_rng(M * 3 + N + K)
     x, w, s = make(rng, M, N, K)
@@ -304,7 +325,7 @@ def test_w8a32_planes_special_rows(lin, orc, M, N, K):
         x[3, 17] = F(1000.0) * np.sqrt(np.mean(x[3] ** 2))
     nan_row, inf_row = M - 1, M - 2
     x[nan_row, 5] = np.nan
-    x[inf_row, 9] = np.inf
+    plant_inf(x, w, inf_row)
     b = rng.standard_normal(N).astype(F)
     got = lin.w8a32_linear(x, w, s, bias=b)
     want = orc.w8a32_linear(x, w, s, bias=b)
@@ -312,7 +333,7 @@ def test_w8a32_planes_special_rows(lin, orc, M, N, K):
         if r == nan_row:
             assert np.isnan(got[r]).all()
         elif r == inf_row:
-            assert not np.isfinite(want[r]).any() and np.isnan(got[r]).all()
+            assert_nonfinite_row(got[r], want[r])
         elif r == 0:
             np.testing.assert_array_equal(got[r], b)
         else:
@@ -326,7 +347,8 @@ def test_w8a32_small_batch_special_rows(lin, orc, M, N, K):
     """Small batches on narrow weights (up to 32 tokens, N < 32768) split fp32
     X into three bf16 terms inside the small-M kernel: rows of zeros, of 1e-36
     and of 1e30 magnitude and a 1000x outlier row are within relative L2 1e-5
-    of the oracle; a row holding NaN or Inf gives NaN in every output.  (This
+    of the oracle; a row holding NaN gives NaN in every output, a row holding
+    +Inf and -Inf the oracle's NaN / +Inf / -Inf output by output.  (This
     path sums w * x before the row's weight scale, so activations with an rms
     above about 1e34 would overflow where the reference, which scales every
     weight first, stays finite.)"""
@@ -339,13 +361,15 @@ def test_w8a32_small_batch_special_rows(lin, orc, M, N, K):
     x[3, 17] = F(1000.0) * np.sqrt(np.mean(x[3] ** 2))
     nan_row, inf_row = M - 1, M - 2
     x[nan_row, 5] = np.nan
-    x[inf_row, 9] = np.inf
+    plant_inf(x, w, inf_row)
     b = rng.standard_normal(N).astype(F)
     got = lin.w8a32_linear(x, w, s, bias=b)
     want = orc.w8a32_linear(x, w, s, bias=b)
     for r in range(M):
-        if r in (nan_row, inf_row):
+        if r == nan_row:
             assert not np.isfinite(want[r]).any() and np.isnan(got[r]).all(), r
+        elif r == inf_row:
+            assert_nonfinite_row(got[r], want[r], r)
         elif r == 0:
             np.testing.assert_allclose(got[r], b, rtol=0, atol=0)
         else:
@@ -359,7 +383,9 @@ def test_rows_digit_planes_k_slices(lin, orc, M, N, K):
     every K-slice count: one slice (outputs stored directly) and 2..5 slices
     (partials merged by the row group's last work-group), each within
     relative L2 1e-5 of the oracle's fp32 GEMM, bias included; a row holding
-    NaN gives NaN outputs and leaves the other rows' bits unchanged, and two
+    NaN gives NaN outputs and one holding +Inf and -Inf in different K slices
+    the oracle's NaN / +Inf / -Inf output by output (the slices' partials
+    merge under IEEE addition), leaving the other rows' bits unchanged; two
     calls in a row give the same bits (the arrival counters are back at
     zero); the earlier small-batch kernel (split -1) agrees too.  Work-groups
     of 2 and 3 weight row groups sharing one split of the activations
@@ -369,10 +395,12 @@ def test_rows_digit_planes_k_slices(lin, orc, M, N, K):
     lib = lin.load_library()
     rng = np.random.default_rng(M * 31 + N + K)
     x, w, s = make(rng, M, N, K)
+    xn = x.copy()
+    plant_inf(xn, w, 0)                              # zero codes in w before the oracle runs
+    xn[M - 1, K // 3] = np.nan
     b = rng.standard_normal(N).astype(F)
     want = orc.w8a32_linear(x, w, s, bias=b)
-    xn = x.copy()
-    xn[M - 1, K // 3] = np.nan
+    want_inf = orc.w8a32_linear(xn, w, s, bias=b)[0]
     try:
         assert lib.tl_w8a32_set_gemv2(0) == 0        # 2 rows too on the digit-row kernel
         by_split = {}
@@ -389,7 +417,8 @@ def test_rows_digit_planes_k_slices(lin, orc, M, N, K):
                 by_split.setdefault(split, got)
                 gn = lin.w8a32_linear(xn, w, s, bias=b)
                 assert np.isnan(gn[M - 1]).all(), (groups, split)
-                np.testing.assert_array_equal(gn[:M - 1], got[:M - 1])
+                assert_nonfinite_row(gn[0], want_inf, (groups, split))
+                np.testing.assert_array_equal(gn[1:M - 1], got[1:M - 1])
     finally:
         lib.tl_rows_set_split(0)
         lib.tl_rows_set_groups(0)
@@ -406,7 +435,8 @@ def test_w8a32_token_rows_on_the_gemv(lin, orc, dev, M, N, K):
     digits, sums and epilogue), which is its path with the switch off, and
     within relative L2 1e-5 of the oracle's fp32 GEMM, bias included (rows of
     1e-36 and 1e35 magnitude too); a NaN in one row gives NaN in that row
-    only, an all-zero row gives the bias exactly; the device entry point
+    only, +Inf and -Inf in another the oracle's NaN / +Inf / -Inf output by
+    output, an all-zero row gives the bias exactly; the device entry point
     gives the same bits."""
     import torch
     if M > 2 and K > 8192:
@@ -415,20 +445,23 @@ def test_w8a32_token_rows_on_the_gemv(lin, orc, dev, M, N, K):
     lib = lin.load_library()
     rng = np.random.default_rng(N * 7 + K + M)
     x, w, s = make(rng, M, N, K)
+    xn = x.copy()
+    plant_inf(xn, w, 0, k_neg=K // 2)                # zero codes in w before the oracle runs
+    xn[M - 1, K // 3] = np.nan
     b = rng.standard_normal(N).astype(F)
     want = orc.w8a32_linear(x, w, s, bias=b)
+    want_inf = orc.w8a32_linear(xn, w, s, bias=b)[0]
     assert lib.tl_w8a32_set_gemv2(2) == 0            # the GEMV for every shape it takes
     try:
         got = lin.w8a32_linear(x, w, s, bias=b)
         assert rel_l2(got, want) <= 1e-5, rel_l2(got, want)
-        xn = x.copy()
-        xn[M - 1, K // 3] = np.nan
         xz = x.copy()
         xz[0] = 0.0
         gn = lin.w8a32_linear(xn, w, s, bias=b)
         gz = lin.w8a32_linear(xz, w, s, bias=b)
         assert np.isnan(gn[M - 1]).all()
-        np.testing.assert_array_equal(gn[:M - 1], got[:M - 1])
+        assert_nonfinite_row(gn[0], want_inf)
+        np.testing.assert_array_equal(gn[1:M - 1], got[1:M - 1])
         np.testing.assert_array_equal(gz[0], b)
         np.testing.assert_array_equal(gz[1:], got[1:])
         # a row of 1e-36 (a digit scale of about 2^149, past the float range,
@@ -647,8 +680,9 @@ def test_w8a16_batch1_gemv_digit_rows(lin, orc, dev, N, K):
     (the reference's bf16 dot products) with and without bias, also with the
     bf16 / fp16 MFMA kernel switched in (tl_w8a16_set_gemv(0)) for the same
     inputs; bf16 and fp16 outputs within 2e-3; a zero row gives the bias
-    exactly, a row of 1e-30 magnitude stays within 1e-5, and NaN or Inf in x
-    gives NaN outputs."""
+    exactly, a row of 1e-30 magnitude stays within 1e-5, a NaN in x gives NaN
+    outputs, and +Inf and -Inf in x the oracle's NaN / +Inf / -Inf output by
+    output (on both kernels)."""
     import torch
     say(f"w8a16 batch-1 GEMV N={N} K={K}")
     lib = lin.load_library()
@@ -669,10 +703,19 @@ def test_w8a16_batch1_gemv_digit_rows(lin, orc, dev, N, K):
     np.testing.assert_array_equal(lin.w8a16_linear(z, w, s, bias=b), b[None, :])
     tiny = bf16_bits(x * F(1e-30))
     assert rel_l2(lin.w8a16_linear(tiny, w, s), orc.w8a16_linear(tiny, w, s)) <= 1e-5
-    for bad in (np.nan, np.inf):
-        xx = x.copy()
-        xx[0, K // 2] = bad
-        assert np.isnan(lin.w8a16_linear(bf16_bits(xx), w, s)).all(), bad
+    xx = x.copy()
+    xx[0, K // 2] = np.nan
+    assert np.isnan(lin.w8a16_linear(bf16_bits(xx), w, s)).all()
+    xx = x.copy()
+    wi = w.copy()
+    plant_inf(xx, wi, 0)
+    want_inf = orc.w8a16_linear(bf16_bits(xx), wi, s, bias=b)[0]
+    try:
+        for on in (1, 0):
+            assert lib.tl_w8a16_set_gemv(on) == 0
+            assert_nonfinite_row(lin.w8a16_linear(bf16_bits(xx), wi, s, bias=b)[0], want_inf, on)
+    finally:
+        lib.tl_w8a16_set_gemv(1)
     # device path: bf16 / fp16 x with bf16 / fp16 out
     W = lin.DeviceWeights.from_codes(w, s)
     xt = torch.from_numpy(x).to(dev).to(torch.bfloat16)

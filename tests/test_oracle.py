@@ -274,6 +274,37 @@ def test_w8a16_paths(orc):
         assert np.linalg.norm(y - exact) / np.linalg.norm(exact) < 1e-6
 
 
+def test_nonfinite_rows_closed_form(orc):
+    """A token row holding +Inf at column kp and -Inf at column kn: the
+    reference's fp32 sums of x times the dequantized weights (scales > 0) give,
+    output by output, IEEE's closed form: NaN where a weight code at kp or kn
+    is 0 (inf * 0) or where sign(w[n,kp]) != -sign(w[n,kn]) (inf - inf), else
+    that common sign times Inf; finite terms change nothing.  A NaN anywhere
+    in the row gives NaN everywhere.  Checked on the W8A32 batch branch
+    (dequantize then SGEMM) and the W8A16 bf16 branch at 1 and 3 tokens; a
+    summation that dropped the Inf terms, or took the code's magnitude for its
+    sign, fails it."""
+    rng = np.random.default_rng(17)
+    M, N, K = 3, 96, 264
+    kp, kn = 9, 200
+    x = rng.standard_normal((M, K)).astype(F)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    w[::7, kp] = 0
+    w[3::11, kn] = 0
+    ws = rng.uniform(0.002, 0.02, N).astype(F)
+    x[1, kp], x[1, kn] = np.inf, -np.inf
+    x[2, 40] = np.nan
+    sp, sn = np.sign(w[:, kp].astype(int)), -np.sign(w[:, kn].astype(int))
+    want = np.where((sp == 0) | (sn == 0) | (sp != sn), np.nan, np.where(sp > 0, np.inf, -np.inf))
+    assert np.isnan(want).any() and np.isposinf(want).any() and np.isneginf(want).any()
+    y = orc.w8a32_linear(x, w, ws, bias=rng.standard_normal(N).astype(F))
+    np.testing.assert_array_equal(y[1], want)
+    assert np.isnan(y[2]).all() and np.isfinite(y[0]).all()
+    xb = ((x.view(np.uint32).astype(np.uint64) + 0x7fff + ((x.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
+    np.testing.assert_array_equal(orc.w8a16_linear(xb, w, ws)[1], want)
+    np.testing.assert_array_equal(orc.w8a16_linear(xb[1:2], w, ws)[0], want)
+
+
 def _pairwise_model(x):
     """The summation order the GPU final-RMSNorm kernel uses for K = 128*2^j:
     per 128-block 8 interleaved accumulators, ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)),

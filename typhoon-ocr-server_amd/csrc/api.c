@@ -744,6 +744,8 @@ static int op_w8a32_ws(Workspace* ws, const float* X, const tl_weights* W, const
   P.Bt = W->tiles;
   P.ws = W->scales;
   P.xe = xe;
+  P.xraw = X;       /* outputs of a row holding Inf / NaN are taken from it */
+  P.ldxr = K;
   P.bias = bias;
   P.Y = Y;
   P.ldy = W->rows;

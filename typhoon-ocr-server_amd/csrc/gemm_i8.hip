@@ -35,6 +35,8 @@ struct GemmI8Args {
   const float* ws;      // [N]
   const float* xs;      // [M]
   const int* xe;        // OUT_F32_X4: per-token exponents [M / 4]
+  const float* xraw;    // OUT_F32_X4: the fp32 token rows (null: NaN for a non-finite row)
+  int ldxr;
   const float* bias;    // [N] or null
   void* Y;              // fp32 [M][ldy] or int32 (OUT_I32)
   int ldy;
@@ -107,6 +109,34 @@ __device__ __forceinline__ void planes_epilogue(const GemmI8Args& a, const v4i c
     st_stream(yp, make_float4(y[0], y[1], y[2], y[3]));
   } else {
     for (int r = 0; r < 4 && n + r < a.N; r++) yp[r] = y[r];
+  }
+}
+
+// After planes_epilogue over a lane's FM x FN accumulator tiles (rows m0 + 16i,
+// columns n0 + 16j): the outputs it stored for tokens flagged kXeNonFinite
+// (NaN there) are stored again with the reference's fp32 value, nonfinite_dot
+// over the fp32 row in a.xraw.  One copy per kernel, out of the unrolled
+// epilogue, run only by a lane holding a flagged token; the same lane rewrites
+// the same addresses, so its later store is the one that stays.
+template <int FM, int FN>
+__device__ __forceinline__ void planes_fixup(const GemmI8Args& a, int m0, int n0, int lane) {
+  if ((lane & 3) != 0) return;
+#pragma unroll 1
+  for (int i = 0; i < FM; i++) {
+    const int m = m0 + 16 * i;
+    if (m >= a.M || a.xe[m >> 2] != kXeNonFinite) continue;
+    float* yp = reinterpret_cast<float*>(a.Y) + (size_t)(m >> 2) * a.ldy;
+#pragma unroll 1
+    for (int j = 0; j < FN; j++) {
+#pragma unroll 1
+      for (int r = 0; r < 4; r++) {
+        const int n = n0 + 16 * j + r;
+        if (n >= a.N) break;
+        float y = nonfinite_dot(a.xraw, 0, (size_t)(m >> 2) * a.ldxr, 0, a.K, a.Bt, a.NG, n);
+        if (a.bias) y = __fadd_rn(y, a.bias[n]);
+        yp[n] = y;
+      }
+    }
   }
 }
 
@@ -358,6 +388,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds_kernel(GemmI8Args a)
       for (int j = 0; j < FN; j++)
         planes_epilogue(a, acc[i][j], (mg0 + wm * FM + i) * 16 + mrow, (ng0 + wn * FN + j) * 16 + ncol, e_ws[j],
                         e_b[j], e_xe[i], lane, vec_ok);
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < FM; i++) bad |= e_xe[i] == kXeNonFinite;
+    if (bad && a.xraw) planes_fixup<FM, FN>(a, (mg0 + wm * FM) * 16 + mrow, (ng0 + wn * FN) * 16 + ncol, lane);
     return;
   }
 #pragma unroll
@@ -553,6 +587,10 @@ __global__ __launch_bounds__(256) void gemm_i8_wcol_kernel(GemmI8Args a) {
       for (int j = 0; j < FN; j++)
         planes_epilogue(a, acc[i][j], (mg0 + i) * 16 + mrow, (ng0 + j) * 16 + ncol, e_ws[j], e_b[j], e_xe[i], lane,
                         vec_ok);
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < MT; i++) bad |= e_xe[i] == kXeNonFinite;
+    if (bad && a.xraw) planes_fixup<MT, FN>(a, mg0 * 16 + mrow, ng0 * 16 + ncol, lane);
     return;
   }
 #pragma unroll
@@ -693,6 +731,8 @@ hipError_t launch_gemm_i8(const GemmLaunch& L, hipStream_t st) {
   a.ws = L.ws;
   a.xs = L.xs;
   a.xe = L.xe;
+  a.xraw = L.xraw;
+  a.ldxr = L.ldxr;
   a.bias = L.bias;
   a.Y = L.Y;
   a.ldy = L.ldy;

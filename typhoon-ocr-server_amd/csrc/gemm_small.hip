@@ -33,6 +33,8 @@ struct GemmSmallArgs {
   const float* ws;
   const float* xs;      // per-token scales (A_I8)
   const int* xe;        // OUT_F32_X4: per-token exponents
+  const float* xraw;    // OUT_F32_X4: the fp32 token rows (null: NaN for a non-finite row)
+  int ldxr;
   const float* bias;
   void* Y;
   int ldy;
@@ -295,10 +297,35 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
             reinterpret_cast<float*>(a.Y)[(size_t)t * a.ldy + n] = v;
           }
         }
+      // a token flagged kXeNonFinite got NaN above: the lane stores its
+      // outputs again with the reference's fp32 value (nonfinite_dot over the
+      // fp32 row in a.xraw), one copy out of the unrolled loops, which carry
+      // no flag for it (the token flags are read again here)
+      if (a.xraw && (lane & 3) == 0) {
+#pragma unroll 1
+        for (int tg = 0; tg < TG; tg++) {
+          const int m = (tg0 + tg) * 16 + (lane & 15);
+          if (m >= a.M || a.xe[m >> 2] != kXeNonFinite) continue;
+          const int t = m >> 2;
+#pragma unroll 1
+          for (int rg = 0; rg < R; rg++) {
+            const int n0 = (g0 + rg) * 16 + 4 * (lane >> 4);
+#pragma unroll 1
+            for (int q = 0; q < 4; q++) {
+              const int n = n0 + q;
+              if (n >= a.N) break;
+              float v = nonfinite_dot(a.xraw, 0, (size_t)t * a.ldxr, 0, a.K, a.Bt, a.NG, n);
+              if (a.bias) v = __fadd_rn(v, a.bias[n]);
+              reinterpret_cast<float*>(a.Y)[(size_t)t * a.ldy + n] = v;
+            }
+          }
+        }
+      }
       return;
     }
   }
   // lane holds D[n .. n+3][m]: m = 16 (tg0 + tg) + (lane & 15), n = 16 g + 4 (lane >> 4)
+  int nan_sum = 0;        // A_F32X3: an output of this lane summed to NaN (an int: no lane-mask merges)
 #pragma unroll
   for (int tg = 0; tg < TG; tg++)
 #pragma unroll
@@ -332,6 +359,7 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
           y = __fmul_rn(tot[q], a.ws[n]);
           if (a.bias) y = __fadd_rn(y, a.bias[n]);
         }
+        if constexpr (AMODE == A_F32X3) nan_sum |= (int)(tot[q] != tot[q]);
       }
       if (a.out == OUT_F32) {
         reinterpret_cast<float*>(a.Y)[o] = y;
@@ -340,6 +368,42 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
       } else {
         const _Float16 h = (_Float16)y;
         reinterpret_cast<uint16_t*>(a.Y)[o] = __builtin_bit_cast(uint16_t, h);
+      }
+    }
+  }
+  if constexpr (AMODE == A_F32X3) {
+    // a row holding Inf or NaN sums to NaN above (the bf16 split of an
+    // infinite x makes Inf - Inf): the lane finds those outputs among its own
+    // stores (a NaN read back) and stores them again with the reference's
+    // fp32 value, NaN or +-Inf from x and the weight codes (nonfinite_dot; a
+    // finite row whose terms overflowed finds no Inf and stays NaN), one copy
+    // out of the unrolled loops
+    if (nan_sum) {
+#pragma unroll 1
+      for (int b = 0; b < 4 * R * TG; b++) {
+        const int tg = b / (4 * R), rg = (b >> 2) % R, q = b & 3;
+        const int m = (tg0 + tg) * 16 + (lane & 15);
+        const int n = (g0 + rg) * 16 + 4 * (lane >> 4) + q;
+        if (m >= a.M || n >= a.N) continue;
+        const size_t o = (size_t)m * a.ldy + n;
+        bool was_nan;
+        if (a.out == OUT_F32) {
+          was_nan = __builtin_isnan(reinterpret_cast<const float*>(a.Y)[o]);
+        } else {
+          const uint16_t h = reinterpret_cast<const uint16_t*>(a.Y)[o];
+          was_nan = a.out == OUT_BF16 ? (h & 0x7fff) > 0x7f80 : (h & 0x7fff) > 0x7c00;
+        }
+        if (!was_nan) continue;
+        float y = nonfinite_dot(a.A, 0, (size_t)m * a.lda, 0, a.K, a.Bt, a.NG, n);
+        if (a.bias) y = __fadd_rn(y, a.bias[n]);
+        if (a.out == OUT_F32) {
+          reinterpret_cast<float*>(a.Y)[o] = y;
+        } else if (a.out == OUT_BF16) {
+          reinterpret_cast<uint16_t*>(a.Y)[o] = (uint16_t)f32_to_bf16_rne(y);
+        } else {
+          const _Float16 h = (_Float16)y;
+          reinterpret_cast<uint16_t*>(a.Y)[o] = __builtin_bit_cast(uint16_t, h);
+        }
       }
     }
   }
@@ -396,6 +460,8 @@ hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st) {
   a.ws = L.ws;
   a.xs = L.xs;
   a.xe = L.xe;
+  a.xraw = L.xraw;
+  a.ldxr = L.ldxr;
   a.bias = L.bias;
   a.Y = L.Y;
   a.ldy = L.ldy;

@@ -650,11 +650,22 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
     const int n = row0 + lane;
     if constexpr (PL >= 2) {
       if (n < a.N) {
+        uint32_t bad = 0;
 #pragma unroll
         for (int t = 0; t < NTOK; t++) {
           if (t >= ntok) break;
           const float sum = digits_sum(tots[4 * t], tots[4 * t + 1], tots[4 * t + 2], tots[4 * t + 3]);
+          bad |= (uint32_t)(px[t] == kXeNonFinite) << t;
           float v = px[t] == kXeNonFinite ? __builtin_nanf("") : ldexpf(__fmul_rn(sum, wsv), px[t] - 6);
+          if (a.bias) v = __fadd_rn(v, bv);
+          a.y[(size_t)t * a.N + n] = v;
+        }
+        // a token holding Inf or NaN got NaN: store the reference's fp32 sum
+        // instead (NaN or +-Inf, nonfinite_dot), one copy out of the token loop
+#pragma unroll 1
+        for (int t = 0; bad >> t; t++) {
+          if (!((bad >> t) & 1)) continue;
+          float v = nonfinite_dot(a.x, 0, (size_t)t * K, 0, K, a.wt, a.NG, n);
           if (a.bias) v = __fadd_rn(v, bv);
           a.y[(size_t)t * a.N + n] = v;
         }
@@ -662,7 +673,8 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const float* x, const uint
     } else if constexpr (PL == 1) {
       if (n < a.N) {
         const float t = digits_sum(tots[0], tots[1], tots[2], tots[3]);
-        const float v = px[0] == kXeNonFinite ? __builtin_nanf("") : __fmaf_rn(ldexpf(t, px[0] - 6), wsv, bv);
+        const float v = px[0] == kXeNonFinite ? __fadd_rn(nonfinite_dot(a.x, xt, 0, 0, K, a.wt, a.NG, n), bv)
+                                              : __fmaf_rn(ldexpf(t, px[0] - 6), wsv, bv);
         const int out = (flags >> 10) & 3;
         if (out == OUT_F32) {
           a.y[n] = v;

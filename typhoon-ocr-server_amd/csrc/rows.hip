@@ -36,8 +36,9 @@
 //     acknowledgement and bumps work-group column g's arrival counter; the work-group
 //     that brings it to S adds the S partials in slice order, adds the bias,
 //     stores, and resets the counter.  Nothing waits on another work-group.
-// A token whose slice holds Inf or NaN gets NaN outputs (the reference's
-// sums give NaN or +-Inf there).
+// A token whose slice holds Inf or NaN gets that slice's fp32 sum as the
+// reference gives it, NaN or +-Inf (nonfinite_dot, tl_common.h), which the
+// slices' merge adds like any partial.
 #include <atomic>
 
 #include "tl_common.h"
@@ -89,6 +90,39 @@ __device__ __forceinline__ void store_out(const RowsArgs& a, size_t o, float y) 
   } else {
     const _Float16 h = (_Float16)y;
     reinterpret_cast<uint16_t*>(a.Y)[o] = __builtin_bit_cast(uint16_t, h);
+  }
+}
+
+// After the epilogue: the outputs (slice < 0, one K slice) or slice partials
+// (slice s) a lane stored for tokens whose slice holds Inf or NaN (NaN there)
+// are stored again with the reference's fp32 sum over the slice, NaN or +-Inf
+// (nonfinite_dot).  One copy per kernel, out of the unrolled epilogue; the
+// lane rewrites its own addresses, before its partials are acknowledged.
+template <int AMODE, int R, int TG>
+__device__ __forceinline__ void nonfinite_fixup(const RowsArgs& a, const uint32_t* mx, int gg, int tq, int lane,
+                                                int kb_lo, int nk, int slice) {
+  constexpr int xt = AMODE == A_F32X3 ? 0 : (AMODE == A_BF16 ? 1 : 2);
+  const int k1 = min(64 * (kb_lo + nk), a.K);
+#pragma unroll 1
+  for (int tg = 0; tg < TG; tg++) {
+    const int t = 4 * tg + tq;
+    if (t >= a.M || mx[t] < 0x7f800000u) continue;
+#pragma unroll 1
+    for (int r = 0; r < R; r++) {
+      const int n0 = 16 * (gg * R + r) + 4 * (lane >> 4);
+#pragma unroll 1
+      for (int q = 0; q < 4; q++) {
+        const int n = n0 + q;
+        if (n >= a.N) break;
+        float v = nonfinite_dot(a.X, xt, (size_t)t * a.ldx, 64 * kb_lo, k1, a.Bt, a.NG, n);
+        if (slice < 0) {
+          if (a.bias) v = __fadd_rn(v, a.bias[n]);
+          store_out(a, (size_t)t * a.ldy + n, v);
+        } else {
+          st_agent(a.part + ((size_t)slice * a.M + t) * a.N + n, v);
+        }
+      }
+    }
   }
 }
 
@@ -232,6 +266,7 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
   //      4 tq + p (digit row p of token 4 tg + tq), n0 = 16 g + 4 (lane >> 4)
   const int tq = (lane >> 2) & 3;
   const bool owner = (lane & 3) == 0;
+  bool bad = false;                            // a token of this lane's slice holds Inf or NaN
   float y[R][TG][4];
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -247,6 +282,7 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
       }
       const int t = min(4 * tg + tq, a.M - 1);
       const uint32_t mx = s_mx[t];
+      bad |= mx >= 0x7f800000u;
       int ex = 0;
       if (mx < 0x7f800000u && mx != 0) (void)frexpf(__uint_as_float(mx), &ex);
 #pragma unroll
@@ -278,6 +314,7 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
         }
       }
     }
+    if (bad) nonfinite_fixup<AMODE, R, TG>(a, s_mx, gg, tq, lane, kb_lo, nk, -1);
     return;
   }
 
@@ -295,6 +332,7 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
           if (n0 + q < a.N) st_agent(a.part + ((size_t)s * a.M + t) * a.N + n0 + q, y[r][tg][q]);
       }
     }
+    if (bad) nonfinite_fixup<AMODE, R, TG>(a, s_mx, gg, tq, lane, kb_lo, nk, s);
   }
   asm volatile("" ::: "memory");
   wait_vm<0>();                                // this wave's partial stores are acknowledged

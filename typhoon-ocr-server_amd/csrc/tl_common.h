@@ -237,6 +237,41 @@ __device__ __forceinline__ uint32_t codes4_rne(float4 v, float inv) {
 // ---------------------------------------------------------------------------
 constexpr int kXeNonFinite = -100000;   // exponent marking a row with Inf / NaN
 
+// The fp32 value of sum_k x[k] w[n][k] over k in [k0, k1) for a row slice
+// that holds Inf or NaN, as the reference's fp32 sums give it (X times the
+// dequantized weights, code x scale with scale > 0, kernel/w8a32_kernel.c:
+// 297-350; bf16 x times bf16 codes, w8a16_kernel.c:90-182): NaN when the
+// slice holds a NaN, when an infinite x meets a zero code (inf * 0), or when
+// the infinite terms have both signs; otherwise the infinite terms' common
+// sign times Inf, which no finite term changes.  Partial sums of K slices
+// combine the same way under IEEE addition.  x is fp32 (xt 0), bf16 (1) or
+// fp16 (2) at element offset `off` of x; w is in the 16x64 tile layout with NG
+// row groups.  Called only for rows the kernels flag as non-finite, so it
+// reads the slice element by element.
+__device__ __forceinline__ float nonfinite_dot(const void* x, int xt, size_t off, int k0, int k1,
+                                                               const uint8_t* wt, int NG, int n) {
+  bool pos = false, neg = false;
+  const int g = n >> 4, r = n & 15;
+  for (int k = k0; k < k1; k++) {
+    float v;
+    if (xt == 0) {
+      v = static_cast<const float*>(x)[off + k];
+    } else {
+      const uint16_t h = static_cast<const uint16_t*>(x)[off + k];
+      v = xt == 1 ? __uint_as_float((uint32_t)h << 16) : (float)__builtin_bit_cast(_Float16, h);
+    }
+    if (v != v) return __builtin_nanf("");
+    if (__builtin_fabsf(v) != __builtin_inff()) continue;
+    const int kb = k >> 6, kk = k & 63;
+    const int8_t c = (int8_t)wt[((size_t)kb * NG + g) * 1024 + (size_t)(r + 16 * (kk >> 4)) * 16 + (kk & 15)];
+    if (c == 0) return __builtin_nanf("");
+    if ((v > 0.0f) == (c > 0)) pos = true;
+    else neg = true;
+  }
+  if (pos == neg) return __builtin_nanf("");   // both signs (or, defensively, no Inf found)
+  return pos ? __builtin_inff() : -__builtin_inff();
+}
+
 // 2^s as a float, s in [-126, 127]
 __device__ __forceinline__ float pow2f(int s) { return __uint_as_float((uint32_t)(s + 127) << 23); }
 

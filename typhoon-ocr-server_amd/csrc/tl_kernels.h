@@ -67,7 +67,8 @@ hipError_t tlk_launch_unpack_tiles(const uint8_t* tiles, int rows, int cols, int
 // MG = ceil(4M / 16), k-blocks ceil(K / 64); row 4t + p is plane p of token
 // t) and per-token exponents xe[M]: x = 2^e (q0 + q1/254 + q2/254^2 +
 // q3/254^3) up to 2^-32 of the row's absmax; a row holding Inf or NaN gets
-// xe = kXeNonFinite (tl_common.h; its outputs are NaN)
+// xe = kXeNonFinite (tl_common.h; the GEMM epilogues given the fp32 rows in
+// GemmLaunch.xraw take that row's outputs from them, nonfinite_dot, else NaN)
 hipError_t tlk_launch_split_i8x4(const float* X, int ldx, int M, int K, uint8_t* tiles, int* xe, hipStream_t st);
 // 4-byte-word copy by a kernel (bytes % 4 == 0), e.g. from mapped pinned host memory
 hipError_t tlk_launch_copy_words(const void* src, void* dst, size_t bytes, hipStream_t st);
@@ -229,6 +230,8 @@ typedef struct GemmLaunch {
   int force_split TLK_DEF(0);
   const uint8_t* zero_tile TLK_DEF(nullptr);   // 1 KiB of device zeros (LDS-staged int8 GEMM)
   const int* xe TLK_DEF(nullptr);        // OUT_F32_X4: per-token power-of-two exponents (split_i8x4)
+  const float* xraw TLK_DEF(nullptr);    // OUT_F32_X4: the fp32 token rows [M / 4][ldxr] the planes came
+  int ldxr TLK_DEF(0);                   //   from (outputs of a non-finite row from them); null: NaN
 } GemmLaunch;
 static inline GemmLaunch tlk_gemm_launch_init(void) {
   GemmLaunch L;
