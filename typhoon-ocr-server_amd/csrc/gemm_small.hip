@@ -247,6 +247,27 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
 
   load(b0, x0, 0);
   load(b1, x1, U);
+  // the epilogue's per-column scales (and, for int8 codes, the per-token
+  // exponent or scale), issued behind the first tiles instead of as
+  // dependent loads after the reduction: columns past N read column N-1,
+  // token rows past M row M-1 (neither is stored)
+  float wsv[R][4];
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int q = 0; q < 4; q++) wsv[r][q] = a.ws ? a.ws[min((g0 + r) * 16 + 4 * (lane >> 4) + q, a.N - 1)] : 0.0f;
+  int xev[TG];
+  float xsv[TG];
+#pragma unroll
+  for (int g = 0; g < TG; g++) {
+    const int m = min((tg0 + g) * 16 + (lane & 15), a.M - 1);
+    xev[g] = 0;
+    xsv[g] = 0.0f;
+    if constexpr (AMODE == A_I8) {
+      if (a.out == OUT_F32_X4) xev[g] = a.xe[m >> 2];
+      else if (a.out != OUT_I32) xsv[g] = a.xs[m];
+    }
+  }
   int t = 0;
   for (; t + 2 * U < n_t; t += 2 * U) {
     consume(b0, x0, t);
@@ -262,15 +283,18 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
 #pragma unroll
     for (int g = 0; g < TG; g++) s_part[r][g][wv][lane] = acc[r][g];
   __syncthreads();
-  if (wv != 0) return;
+  // Epilogue: the R x TG (row group, token group) pairs are spread over the
+  // 4 waves, pair TG rg + tg on wave (TG rg + tg) mod 4 (wave-uniform).
   if constexpr (AMODE == A_I8) {
     if (a.out == OUT_F32_X4) {
       // rows 4t .. 4t+3 are the planes of token t: the lane quad 4t .. 4t+3
       // (mod 16) holds them; its first lane combines and stores row t
+      const bool vec = (a.ldy & 3) == 0 && (((uintptr_t)a.Y) & 15) == 0;
 #pragma unroll
       for (int tg = 0; tg < TG; tg++)
 #pragma unroll
         for (int rg = 0; rg < R; rg++) {
+          if ((TG * rg + tg) % 4 != wv) continue;
           acc_t tot = s_part[rg][tg][0][lane];
 #pragma unroll
           for (int w = 1; w < 4; w++) {
@@ -285,16 +309,19 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
             y[q] = planes_sum(tot[q], a1, a2, a3);
           }
           const int m = (tg0 + tg) * 16 + (lane & 15);
-          if ((lane & 3) != 0 || m >= a.M) continue;
-          const int t = m >> 2;
-          const int e = a.xe[t];
           const int n0 = (g0 + rg) * 16 + 4 * (lane >> 4);
+          if ((lane & 3) != 0 || m >= a.M || n0 >= a.N) continue;
+          const int t = m >> 2;
+#pragma unroll
           for (int q = 0; q < 4; q++) {
-            const int n = n0 + q;
-            if (n >= a.N) break;
-            float v = planes_scale(y[q], a.ws[n], e);
-            if (a.bias) v = __fadd_rn(v, a.bias[n]);
-            reinterpret_cast<float*>(a.Y)[(size_t)t * a.ldy + n] = v;
+            y[q] = planes_scale(y[q], wsv[rg][q], xev[tg]);
+            if (a.bias && n0 + q < a.N) y[q] = __fadd_rn(y[q], a.bias[n0 + q]);
+          }
+          float* yp = reinterpret_cast<float*>(a.Y) + (size_t)t * a.ldy + n0;
+          if (vec && n0 + 4 <= a.N) {
+            *reinterpret_cast<float4*>(yp) = make_float4(y[0], y[1], y[2], y[3]);
+          } else {
+            for (int q = 0; q < 4 && n0 + q < a.N; q++) yp[q] = y[q];
           }
         }
       // a token flagged kXeNonFinite got NaN above: the lane stores its
@@ -309,6 +336,7 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
           const int t = m >> 2;
 #pragma unroll 1
           for (int rg = 0; rg < R; rg++) {
+            if ((TG * rg + tg) % 4 != wv) continue;   // another wave's pair
             const int n0 = (g0 + rg) * 16 + 4 * (lane >> 4);
 #pragma unroll 1
             for (int q = 0; q < 4; q++) {
@@ -324,14 +352,20 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
       return;
     }
   }
-  // lane holds D[n .. n+3][m]: m = 16 (tg0 + tg) + (lane & 15), n = 16 g + 4 (lane >> 4)
+  // lane holds D[n .. n+3][m]: m = 16 (tg0 + tg) + (lane & 15), n = 16 g + 4 (lane >> 4);
+  // the 4 consecutive outputs of row m go out as one 16-byte (fp32, int32) or
+  // 8-byte (bf16, fp16) store where the row stride and base allow it
+  const int esz = (a.out == OUT_BF16 || a.out == OUT_F16) ? 2 : 4;
+  const bool vec = (a.ldy & 3) == 0 && (((uintptr_t)a.Y) & (4 * esz - 1)) == 0;
   int nan_sum = 0;        // A_F32X3: an output of this lane summed to NaN (an int: no lane-mask merges)
 #pragma unroll
   for (int tg = 0; tg < TG; tg++)
 #pragma unroll
   for (int rg = 0; rg < R; rg++) {
+    if ((TG * rg + tg) % 4 != wv) continue;
     const int m = (tg0 + tg) * 16 + (lane & 15);
-    if (m >= a.M) continue;
+    const int n0 = (g0 + rg) * 16 + 4 * (lane >> 4);
+    if (m >= a.M || n0 >= a.N) continue;
     acc_t tot = s_part[rg][tg][0][lane];
 #pragma unroll
     for (int w = 1; w < 4; w++) {
@@ -339,35 +373,59 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; q++) tot[q] += p[q];
     }
-    const int n0 = (g0 + rg) * 16 + 4 * (lane >> 4);
-    for (int q = 0; q < 4; q++) {
-      const int n = n0 + q;
-      if (n >= a.N) break;
-      const size_t o = (size_t)m * a.ldy + n;
-      float y;
-      if constexpr (AMODE == A_I8) {
-        if (a.out == OUT_I32) {
-          reinterpret_cast<int32_t*>(a.Y)[o] = tot[q];
-          continue;
+    const bool full = vec && n0 + 4 <= a.N;
+    const size_t o = (size_t)m * a.ldy + n0;
+    if constexpr (AMODE == A_I8) {
+      if (a.out == OUT_I32) {
+        if (full) {
+          *reinterpret_cast<v4i*>(reinterpret_cast<int32_t*>(a.Y) + o) = tot;
+        } else {
+          for (int q = 0; q < 4 && n0 + q < a.N; q++) reinterpret_cast<int32_t*>(a.Y)[o + q] = tot[q];
         }
-        y = __fmul_rn(__fmul_rn((float)tot[q], a.ws[n]), a.xs[m]);
-        if (a.bias) y = __fadd_rn(y, a.bias[n]);
+        continue;
+      }
+    }
+    float y[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int n = min(n0 + q, a.N - 1);
+      if constexpr (AMODE == A_I8) {
+        y[q] = __fmul_rn(__fmul_rn((float)tot[q], wsv[rg][q]), xsv[tg]);
+        if (a.bias) y[q] = __fadd_rn(y[q], a.bias[n]);
       } else {
         if (a.ep == EP_SCALE_FMA) {
-          y = __fmaf_rn(tot[q], a.ws[n], a.bias ? a.bias[n] : 0.0f);
+          y[q] = __fmaf_rn(tot[q], wsv[rg][q], a.bias ? a.bias[n] : 0.0f);
         } else {
-          y = __fmul_rn(tot[q], a.ws[n]);
-          if (a.bias) y = __fadd_rn(y, a.bias[n]);
+          y[q] = __fmul_rn(tot[q], wsv[rg][q]);
+          if (a.bias) y[q] = __fadd_rn(y[q], a.bias[n]);
         }
-        if constexpr (AMODE == A_F32X3) nan_sum |= (int)(tot[q] != tot[q]);
+        if constexpr (AMODE == A_F32X3) nan_sum |= (int)(tot[q] != tot[q] && n0 + q < a.N);
       }
-      if (a.out == OUT_F32) {
-        reinterpret_cast<float*>(a.Y)[o] = y;
-      } else if (a.out == OUT_BF16) {
-        reinterpret_cast<uint16_t*>(a.Y)[o] = (uint16_t)f32_to_bf16_rne(y);
+    }
+    if (a.out == OUT_F32) {
+      float* yp = reinterpret_cast<float*>(a.Y) + o;
+      if (full) {
+        *reinterpret_cast<float4*>(yp) = make_float4(y[0], y[1], y[2], y[3]);
       } else {
-        const _Float16 h = (_Float16)y;
-        reinterpret_cast<uint16_t*>(a.Y)[o] = __builtin_bit_cast(uint16_t, h);
+        for (int q = 0; q < 4 && n0 + q < a.N; q++) yp[q] = y[q];
+      }
+    } else {
+      uint16_t h[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        if (a.out == OUT_BF16) {
+          h[q] = (uint16_t)f32_to_bf16_rne(y[q]);
+        } else {
+          const _Float16 f = (_Float16)y[q];
+          h[q] = __builtin_bit_cast(uint16_t, f);
+        }
+      }
+      uint16_t* yp = reinterpret_cast<uint16_t*>(a.Y) + o;
+      if (full) {
+        *reinterpret_cast<uint2*>(yp) = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16),
+                                                   (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+      } else {
+        for (int q = 0; q < 4 && n0 + q < a.N; q++) yp[q] = h[q];
       }
     }
   }
@@ -382,6 +440,7 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmSmallArgs a) {
 #pragma unroll 1
       for (int b = 0; b < 4 * R * TG; b++) {
         const int tg = b / (4 * R), rg = (b >> 2) % R, q = b & 3;
+        if ((TG * rg + tg) % 4 != wv) continue;   // another wave's pair
         const int m = (tg0 + tg) * 16 + (lane & 15);
         const int n = (g0 + rg) * 16 + 4 * (lane >> 4) + q;
         if (m >= a.M || n >= a.N) continue;
@@ -420,16 +479,22 @@ bool gemm_small_supported(const GemmLaunch& L) {
 
 template <int AMODE, int R, int TG>
 static void launch_small_rt(const GemmSmallArgs& a, int u, hipStream_t st) {
-  const dim3 grid(cdiv(a.NG, R), cdiv(a.MG, TG)), block(256);
-  // batches of 4 tiles exist for one token group, and for 16-bit rows up to
-  // 8 row x token groups per work-group (wider ones pass 512 VGPRs)
-  if constexpr (TG == 1 || ((AMODE == A_BF16 || AMODE == A_F16) && R * TG <= 8)) {
-    if (u == 4) {
-      hipLaunchKernelGGL((gemm_small_kernel<AMODE, 4, R, TG>), grid, block, 0, st, a);
-      return;
+  if constexpr (AMODE == A_F32X3 && R * TG > 8) {
+    // never planned (fp32 rows run here only below 512 weight row groups, one
+    // per work-group); the instance would pass 512 VGPRs
+    launch_small_rt<AMODE, 8 / TG, TG>(a, u, st);
+  } else {
+    const dim3 grid(cdiv(a.NG, R), cdiv(a.MG, TG)), block(256);
+    // batches of 4 tiles exist for one token group, and for 16-bit rows up to
+    // 8 row x token groups per work-group (wider ones pass 512 VGPRs)
+    if constexpr (TG == 1 || ((AMODE == A_BF16 || AMODE == A_F16) && R * TG <= 8)) {
+      if (u == 4) {
+        hipLaunchKernelGGL((gemm_small_kernel<AMODE, 4, R, TG>), grid, block, 0, st, a);
+        return;
+      }
     }
+    hipLaunchKernelGGL((gemm_small_kernel<AMODE, 2, R, TG>), grid, block, 0, st, a);
   }
-  hipLaunchKernelGGL((gemm_small_kernel<AMODE, 2, R, TG>), grid, block, 0, st, a);
 }
 
 template <int AMODE, int R>

@@ -30,12 +30,15 @@
 //     xor spreads a quad's writes over the banks; readers undo it);
 //   * per weight tile: one ds_read_b128 of codes and one MFMA per token
 //     group; the 4 waves' int32 accumulators meet in LDS;
-//   * wave 0 combines each token's four digit sums (lane quads), scales them
-//     (y_s = 2^(e-6) fl(t ws)), and either stores the outputs (S == 1) or
-//     stores its partials with agent-scope atomic stores, waits for their
-//     acknowledgement and bumps work-group column g's arrival counter; the work-group
-//     that brings it to S adds the S partials in slice order, adds the bias,
-//     stores, and resets the counter.  Nothing waits on another work-group.
+//   * the (row group, token group) pairs are spread over the 4 waves; each
+//     combines its pairs' four digit sums per token (lane quads), scales them
+//     (y_s = 2^(e-6) fl(t ws), the scales loaded with the weight tiles), and
+//     either stores the outputs (S == 1, 16 bytes per token and lane quad) or
+//     stores its partials with agent-scope atomic stores and waits for their
+//     acknowledgement; then one thread bumps work-group column g's arrival
+//     counter; the work-group that brings it to S adds the S partials in slice
+//     order, adds the bias, stores, and resets the counter.  Nothing waits on
+//     another work-group.
 // A token whose slice holds Inf or NaN gets that slice's fp32 sum as the
 // reference gives it, NaN or +-Inf (nonfinite_dot, tl_common.h), which the
 // slices' merge adds like any partial.
@@ -100,7 +103,7 @@ __device__ __forceinline__ void store_out(const RowsArgs& a, size_t o, float y) 
 // lane rewrites its own addresses, before its partials are acknowledged.
 template <int AMODE, int R, int TG>
 __device__ __forceinline__ void nonfinite_fixup(const RowsArgs& a, const uint32_t* mx, int gg, int tq, int lane,
-                                                int kb_lo, int nk, int slice) {
+                                                int wv, int kb_lo, int nk, int slice) {
   constexpr int xt = AMODE == A_F32X3 ? 0 : (AMODE == A_BF16 ? 1 : 2);
   const int k1 = min(64 * (kb_lo + nk), a.K);
 #pragma unroll 1
@@ -109,6 +112,7 @@ __device__ __forceinline__ void nonfinite_fixup(const RowsArgs& a, const uint32_
     if (t >= a.M || mx[t] < 0x7f800000u) continue;
 #pragma unroll 1
     for (int r = 0; r < R; r++) {
+      if ((r * TG + tg) % 4 != wv) continue;   // another wave's pair
       const int n0 = 16 * (gg * R + r) + 4 * (lane >> 4);
 #pragma unroll 1
       for (int q = 0; q < 4; q++) {
@@ -183,6 +187,22 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
       typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
       const v4u_t w = __builtin_nontemporal_load(reinterpret_cast<const v4u_t*>(wbase[r] + (size_t)kb * tstride));
       wt[r][i] = make_uint4(w.x, w.y, w.z, w.w);
+    }
+  }
+  // ---- the scales (and bias) of this lane's output columns n0 .. n0+3 of
+  //      every row group, issued after the weight tiles (loads retire in
+  //      issue order, so only the epilogue waits for them) instead of as
+  //      dependent loads inside it (columns past N read column N-1; their
+  //      outputs are never stored)
+  float wsv[R][4], bsv[R][4];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int n0 = 16 * (gg * R + r) + 4 * (lane >> 4);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int n = min(n0 + q, a.N - 1);
+      wsv[r][q] = a.ws[n];
+      bsv[r][q] = a.bias ? a.bias[n] : 0.0f;
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -260,19 +280,22 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
 #pragma unroll
     for (int tg = 0; tg < TG; tg++) s_part[r][tg][wv][lane] = acc[r][tg];
   __syncthreads();
-  if (wv != 0) return;
 
-  // ---- wave 0: lane holds D[n0 .. n0+3][m] of row group g, m = lane & 15 =
-  //      4 tq + p (digit row p of token 4 tg + tq), n0 = 16 g + 4 (lane >> 4)
+  // ---- epilogue: the R x TG (row group, token group) pairs are spread over
+  //      the 4 waves, pair r TG + tg on wave (r TG + tg) mod 4.  A lane holds
+  //      D[n0 .. n0+3][m] of its pair, m = lane & 15 = 4 tq + p (digit row p of
+  //      token 4 tg + tq), n0 = 16 g + 4 (lane >> 4); the quad's first lane
+  //      (p = 0) combines the four digit sums and owns the token's 4 outputs
   const int tq = (lane >> 2) & 3;
   const bool owner = (lane & 3) == 0;
-  bool bad = false;                            // a token of this lane's slice holds Inf or NaN
+  const bool vec = a.out == OUT_F32 && (a.ldy & 3) == 0 && (((uintptr_t)a.Y) & 15) == 0;
+  bool bad = false;                            // a token of this wave's pairs holds Inf or NaN
   float y[R][TG][4];
 #pragma unroll
   for (int r = 0; r < R; r++) {
-    const int n0 = 16 * (gg * R + r) + 4 * (lane >> 4);
 #pragma unroll
     for (int tg = 0; tg < TG; tg++) {
+      if ((r * TG + tg) % 4 != wv) continue;   // wave-uniform
       v4i tot = s_part[r][tg][0][lane];
 #pragma unroll
       for (int w = 1; w < 4; w++) {
@@ -289,8 +312,7 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
       for (int q = 0; q < 4; q++) {
         const int a1 = __shfl_xor(tot[q], 1, 64), a2 = __shfl_xor(tot[q], 2, 64), a3 = __shfl_xor(tot[q], 3, 64);
         const float sum = digits_sum(tot[q], a1, a2, a3);
-        const int n = min(n0 + q, a.N - 1);
-        y[r][tg][q] = mx >= 0x7f800000u ? __builtin_nanf("") : ldexpf(__fmul_rn(sum, a.ws[n]), ex - 6);
+        y[r][tg][q] = mx >= 0x7f800000u ? __builtin_nanf("") : ldexpf(__fmul_rn(sum, wsv[r][q]), ex - 6);
       }
     }
   }
@@ -302,29 +324,36 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
       const int n0 = 16 * (gg * R + r) + 4 * (lane >> 4);
 #pragma unroll
       for (int tg = 0; tg < TG; tg++) {
+        if ((r * TG + tg) % 4 != wv) continue;
         const int t = 4 * tg + tq;
-        if (t >= a.M) continue;
+        if (t >= a.M || n0 >= a.N) continue;
+        float v[4];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const int n = n0 + q;
-          if (n >= a.N) continue;
-          float v = y[r][tg][q];
-          if (a.bias) v = __fadd_rn(v, a.bias[n]);
-          store_out(a, (size_t)t * a.ldy + n, v);
+        for (int q = 0; q < 4; q++) v[q] = a.bias ? __fadd_rn(y[r][tg][q], bsv[r][q]) : y[r][tg][q];
+        if (vec && n0 + 4 <= a.N) {
+          // the 4 outputs of the token as one 16-byte store
+          *reinterpret_cast<float4*>(static_cast<float*>(a.Y) + (size_t)t * a.ldy + n0) =
+              make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; q++)
+            if (n0 + q < a.N) store_out(a, (size_t)t * a.ldy + n0 + q, v[q]);
         }
       }
     }
-    if (bad) nonfinite_fixup<AMODE, R, TG>(a, s_mx, gg, tq, lane, kb_lo, nk, -1);
+    if (bad) nonfinite_fixup<AMODE, R, TG>(a, s_mx, gg, tq, lane, wv, kb_lo, nk, -1);
     return;
   }
 
-  // ---- S > 1: partials, arrival, and the last work-group's merge
+  // ---- S > 1: partials, arrival, and the last work-group's merge (each
+  //      wave merges its own pairs)
   if (owner) {
 #pragma unroll
     for (int r = 0; r < R; r++) {
       const int n0 = 16 * (gg * R + r) + 4 * (lane >> 4);
 #pragma unroll
       for (int tg = 0; tg < TG; tg++) {
+        if ((r * TG + tg) % 4 != wv) continue;
         const int t = 4 * tg + tq;
         if (t >= a.M) continue;
 #pragma unroll
@@ -332,15 +361,17 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
           if (n0 + q < a.N) st_agent(a.part + ((size_t)s * a.M + t) * a.N + n0 + q, y[r][tg][q]);
       }
     }
-    if (bad) nonfinite_fixup<AMODE, R, TG>(a, s_mx, gg, tq, lane, kb_lo, nk, s);
+    if (bad) nonfinite_fixup<AMODE, R, TG>(a, s_mx, gg, tq, lane, wv, kb_lo, nk, s);
   }
   asm volatile("" ::: "memory");
   wait_vm<0>();                                // this wave's partial stores are acknowledged
   asm volatile("" ::: "memory");
-  int last = 0;
-  if (lane == 0) last = __hip_atomic_fetch_add(a.cnt + gg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.S - 1);
-  last = __shfl(last, 0, 64);
-  if (!last) return;
+  __shared__ int s_last;
+  __syncthreads();                             // every wave's partials acknowledged
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add(a.cnt + gg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.S - 1);
+  __syncthreads();
+  if (!s_last) return;
   // the winner's acquire: the other slices' partials are read after the
   // counter showed them all arrived (agent scope; once per row group)
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
@@ -351,6 +382,7 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
       const int n0 = 16 * (gg * R + r) + 4 * (lane >> 4);
 #pragma unroll
       for (int tg = 0; tg < TG; tg++) {
+        if ((r * TG + tg) % 4 != wv) continue;
         const int t = 4 * tg + tq;
         if (t >= a.M) continue;
 #pragma unroll
@@ -359,13 +391,13 @@ __global__ __launch_bounds__(256) void rows_planes_kernel(RowsArgs a) {
           if (n >= a.N) continue;
           float v = ld_agent(a.part + (size_t)t * a.N + n);
           for (int ss = 1; ss < a.S; ss++) v = __fadd_rn(v, ld_agent(a.part + ((size_t)ss * a.M + t) * a.N + n));
-          if (a.bias) v = __fadd_rn(v, a.bias[n]);
+          if (a.bias) v = __fadd_rn(v, bsv[r][q]);
           store_out(a, (size_t)t * a.ldy + n, v);
         }
       }
     }
   }
-  if (lane == 0) __hip_atomic_store(a.cnt + gg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(a.cnt + gg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
