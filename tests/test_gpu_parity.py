@@ -288,12 +288,15 @@ def test_w8a32_batch_fp32(lin, orc, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(3, 32776, 200), (8, 40000, 2048), (16, 33000, 130), (48, 33000, 130),
-                                   (30, 32800, 256), (64, 4100, 512), (20, 700, 2048)])
+                                   (30, 32800, 256), (64, 4100, 512), (20, 700, 2048), (16, 12288, 2048),
+                                   (32, 6144, 2048), (64, 6144, 2048), (24, 12280, 2048)])
 def test_small_m_wide_n(lin, orc, M, N, K):
     """M <= 64 token rows (one to four 16-row token groups per weight tile),
     also over N >= 32768 outputs (the lm_head's regime, where a work-group
-    covers several 16-row weight groups): W8A32 fp32 within 1e-5, W8A16 fp32
-    out within 1e-5, W8A8 within 1e-5."""
+    covers several 16-row weight groups) and on the mid-width weights the
+    small-M kernel takes up to 12288 rows (fp32 rows at 16 tokens, int8 codes
+    at 32 rows; N = 12280 ends in a partial row group): W8A32 fp32 within
+    1e-5, W8A16 fp32 out within 1e-5, W8A8 within 1e-5."""
     say(f"small-M wide-N M={M} N={N} K={K}")
     rng = np.random.default_rng(M * 7 + N + K)
     x, w, s = make(rng, M, N, K)

@@ -711,16 +711,17 @@ static int op_w8a32_ws(Workspace* ws, const float* X, const tl_weights* W, const
     TRY(run_rows(ws, &L, st, &done));
     if (done) return 0;
   }
-  if (W->cols <= 2048 && ((batch <= 16 && W->NG < 512) || (batch <= 32 && W->NG <= 256))) {
-    /* a few token rows over a narrow weight with a short K: the small-M kernel
-     * splits the fp32 rows into three bf16 terms as it loads them (one launch,
-     * where a separate plane split costs more than it saves: 2048x2048 at 9 /
-     * 16 / 17 tokens 7.2 / 8.7 / 12.8 us here against 8.5 / 9.5 / 14.2 us on
-     * the planes, 6144x2048 at 9 / 16 tokens 10.9 / 14.3 against 15.1 / 15.7).
-     * Every work-group re-reads all the token rows, which a long K or many
-     * weight rows make the cost: 2048x4096 at 9 / 16 tokens 11.9 / 14.4 us here
-     * against 11.1 / 12.6 us on the planes, 12288x2048 at 16 tokens 20.6
-     * against 15.9 us, 2048x6144 at 32 tokens 33.3 against 19.7 us */
+  if (W->cols <= 2048 && ((batch <= 16 && W->NG <= 768) || (batch <= 32 && W->NG <= 384))) {
+    /* a few token rows over a weight of up to 12288 rows with a short K: the
+     * small-M kernel splits the fp32 rows into three bf16 terms as it loads
+     * them (one launch, where a separate plane split costs more than it
+     * saves: 2048x2048 at 9 / 16 / 32 tokens 6.9 / 8.6 / 8.6 us; 6144x2048
+     * at 24 / 32 tokens 10.8 / 11.4 us against 14.8 / 15.4 us on the planes,
+     * 12288x2048 at 9 / 16 tokens 10.7 / 11.9 against 15.8 / 16.1).  Every
+     * work-group reads all the token rows of its token group, which more
+     * tokens over many weight rows or a long K make the cost: 12288x2048 at
+     * 24 / 32 tokens 17.9 / 19.9 us here against 15.3 / 16.1 us on the
+     * planes, 2048x4096 at 9 / 16 tokens 11.9 / 14.4 against 11.1 / 12.6 */
     return run_gemm(ws, &L, st);
   }
   /* fp32 rows as four int8 planes each (x = 2^e (q0 + q1/254 + q2/254^2 +

@@ -399,16 +399,22 @@ static GemmKernel gemm_choice(const GemmLaunch& L) {
     if (fc == 3 && gemm_small_supported(L)) return GK_SMALL;
     if (fc >= 0 && fc <= 2 && L.M > 16 && gemm_b16_supported(L)) return GK_B16;
   }
-  // 16-bit rows (one token group per work-group, the grid's y extent over the
-  // token rows): up to 128 rows at N <= 2048 and 64 at N <= 4096, measured at
-  // K = 2048 against every tile of the tiled kernel (M = 64 / 96 / 128,
-  // N = 2048: 6.7 / 9.0 / 9.2 us against 10.5 / 11.5 / 11.5; M = 64,
-  // N = 4096: 9.6 against 11.6; at M = 256, or N = 12288 from 32 rows, the
-  // tiled kernel wins: 11.6 against 13.4 us, 12.0 against 14.1)
+  // 16-bit rows (the grid's y extent over the token groups): up to 256 rows at
+  // N <= 4096 and 64 rows on wider N, measured at K = 2048 against every tile
+  // of the tiled kernel (M = 96 / 128 / 192 / 256, N = 2048: 6.8 / 6.9 / 9.2 /
+  // 9.3 us against 11.5 / 11.5 / 11.6 / 11.8; N = 4096: 9.4 / 9.5 / 14.9 /
+  // 15.0 against 11.8 / 11.9 / 16.1 / 16.2; N = 12288 at 32 / 64 rows 10.3 /
+  // 15.7 against 12.0 / 16.6; from 96 rows there the tiled kernel wins: 20.7
+  // against 25.2 us)
   const int ng = cdiv(L.N, 16);
-  const bool b16_small = b16 && ((ng <= 128 && L.M <= 128) || (ng <= 256 && L.M <= 64));
+  const bool b16_small = b16 && L.M <= 256 && (ng <= 256 || L.M <= 64);
   const bool wide_i8 = L.amode == A_I8 && L.M <= 32 && ng >= 2048;
-  if (gemm_small_supported(L) && (L.M <= 16 || (!b16 && L.M <= 64 && ng <= 256) || b16_small || wide_i8))
+  // int8 codes and fp32 rows: up to 64 rows at N <= 6144 and 32 rows at
+  // N <= 12288 (W8A8 at K = 2048, N = 6144, 24..64 rows: 8.1-11.0 us against
+  // 12.7-13.7 us on the tiled kernel; N = 12288 at 24 / 32 rows 12.1 / 12.4
+  // against 13.4, at 48 / 64 rows 15.4 / 16.3 against 14.2 / 14.4)
+  const bool mid_i8 = !b16 && ((L.M <= 64 && ng <= 384) || (L.M <= 32 && ng <= 768));
+  if (gemm_small_supported(L) && (L.M <= 16 || mid_i8 || b16_small || wide_i8))
     return GK_SMALL;
   if (L.amode == A_I8 && L.M > 16) return GK_I8;
   if (L.amode != A_I8 && L.M > 16 && gemm_b16_supported(L)) return GK_B16;

@@ -547,18 +547,53 @@ hipError_t launch_gemm_small(const GemmLaunch& L, hipStream_t st) {
   int tg = a.MG <= 1 ? 1 : (a.MG <= 2 ? 2 : 4);
   const bool b16 = L.amode == A_BF16 || L.amode == A_F16;
   int u_force = 0;
+  if (!b16) {
+    if (a.NG >= 2048) {
+      // weights far past the caches (the lm_head): every token group rides
+      // on each weight tile, so the tiles are streamed once; four row groups
+      // per work-group, batches of 2 tiles (lm_head planes at 2 tokens 51.2
+      // -> 46.7 us against batches of 4)
+      u_force = 2;
+    } else {
+      // weights within the caches: one token group per work-group (the
+      // grid's y extent over the token groups) and the most row groups that
+      // still leave >= 192 work-groups; batches of 4 tiles for one row group
+      // (and two of int8 codes).  Measured over every shape (R, TG, U) at
+      // K = 2048 / 6144: the best or within 3 % at every point, e.g. W8A32
+      // at 32 tokens, N = 2048: 14.4 -> 8.6 us (all token groups on one
+      // work-group before); W8A8 at 64 rows, N = 2048: 7.7 -> 6.3 us; the
+      // int8 planes of 8 tokens over 2048 x 6144: 10.9 -> 9.0 us
+      tg = 1;
+      r = 1;
+      for (int cr = 4; cr > 1; cr >>= 1)
+        if ((long long)cdiv(a.NG, cr) * a.MG >= 192) {
+          r = cr;
+          break;
+        }
+      u_force = (n_t >= 8 && (r == 1 || (r == 2 && L.amode == A_I8))) ? 4 : 2;
+    }
+  }
   if (b16 && a.MG >= 2) {
-    // 16-bit rows, 17..256 tokens: one token group per work-group (the token
-    // rows spread over the grid's y extent instead of every work-group
-    // re-reading all of them) and two weight row groups while that still
-    // gives 160+ work-groups, with a wave's whole K quarter in flight at
-    // K = 2048.  Measured over every shape (R, TG, U) at K = 2048: best or
-    // within 2 % of it wherever this kernel beats the tiled one, e.g.
-    // M = 64, N = 2048: 6.7 us against 10.5 (tiled 32 x 64 tiles, 4 K slices)
-    // and 6.8-7.3 us for one row group x all four token groups.
-    r = (long long)cdiv(a.NG, 2) * a.MG >= 160 ? 2 : 1;
+    // 16-bit rows, 17..256 tokens: the widest work-group, most weight row
+    // groups R and then most token groups TG (each 4, 2 or 1, TG at most the
+    // token groups there are), that still leaves >= 192 work-groups; batches
+    // of 4 tiles only below 4 (row group, token group) pairs.  Measured over
+    // every shape (R, TG, U) at K = 2048 and M = 32..256, N = 2048 / 4096 /
+    // 12288: the best shape or within 2 % of it at every point, e.g.
+    // M = 256, N = 2048: 4 x 2 groups 9.3 us (1 x 4: 13.3, the tiled kernel
+    // 11.5); M = 64, N = 4096: 4 x 1 groups 7.1 us (2 x 1: 8.7).
+    r = 1;
     tg = 1;
-    u_force = n_t >= 8 ? 4 : 2;
+    bool found = false;
+    for (int cr = 4; cr >= 1 && !found; cr >>= 1)
+      for (int ct = 4; ct >= 1; ct >>= 1)
+        if (ct <= a.MG && (long long)cdiv(a.NG, cr) * cdiv(a.MG, ct) >= 192) {
+          r = cr;
+          tg = ct;
+          found = true;
+          break;
+        }
+    u_force = (r * tg >= 4 || n_t < 8) ? 2 : 4;
   }
   if (b16) {
     const int code = g_small_b16_shape.load(std::memory_order_relaxed);
