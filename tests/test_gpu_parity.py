@@ -851,11 +851,13 @@ def test_batch1_padded_paths_capture_into_a_graph(lin, orc, dev, path, K):
     W.close()
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 2048, 2048), (200, 1000, 1000), (256, 4096, 2048)])
+@pytest.mark.parametrize("M,N,K", [(64, 2048, 2048), (200, 1000, 1000), (200, 1000, 2048), (256, 4096, 2048)])
 def test_w8a16_k_slices(lin, orc, dev, M, N, K):
     """The 16-bit GEMM with its K range split over 1..4 work-groups per tile
-    (every tile configuration, forced through tl_gemm_b16_set_plan; uneven
-    slices where the K blocks do not divide): fp32 out within 1e-5 and bf16
+    (every tile configuration, forced through tl_gemm_b16_set_plan: the
+    LDS-staged kernel's 0..2 and the column-split kernel's 4..8, which K not a
+    multiple of 64 runs on configuration 0's kernel; uneven slices where the
+    K blocks do not divide): fp32 out within 1e-5 and bf16
     out within 2e-3 of a float64 product in every row, and a repeated call
     bit-identical (the last work-group to arrive adds the slices in slice
     order, whichever it is)."""
@@ -869,7 +871,7 @@ def test_w8a16_k_slices(lin, orc, dev, M, N, K):
     y32 = torch.empty((M, N), dtype=torch.float32, device=dev)
     yb = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     try:
-        for cfg in (0, 1, 2):
+        for cfg in (0, 1, 2, 4, 5, 6, 7, 8):
             for split in (1, 2, 3, 4):
                 say(f"w8a16 K slices M={M} N={N} K={K} cfg={cfg} split={split}")
                 assert lib.tl_gemm_b16_set_plan(cfg, split) == 0

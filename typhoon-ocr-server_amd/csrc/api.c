@@ -1369,7 +1369,7 @@ int tl_gemm_i8_set_split(int split) {
 }
 
 static int gemm_b16_set_plan_impl(int cfg, int split) {
-  REQ(cfg >= -1 && cfg <= 3, "cfg must be -1 (planner), 0..2 (tiles) or 3 (small-M kernel)");
+  REQ(cfg >= -1 && cfg <= 8, "cfg must be -1 (planner), 0..2 or 4..8 (tiles) or 3 (small-M kernel)");
   REQ((split >= 0 && split <= 64) || (cfg == 3 && split >= 112 && split <= 444),
       "split must be 0 (planner) or 1..64 (with cfg 3: 0, or the shape code 100 R + 10 TG + U)");
   tlk_gemm_b16_set_plan(cfg, split);

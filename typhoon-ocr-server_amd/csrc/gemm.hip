@@ -397,7 +397,7 @@ static GemmKernel gemm_choice(const GemmLaunch& L) {
   if (b16) {   // tuning override: 3 the small-M kernel, 0..2 a tile of the tiled one
     const int fc = gemm_b16_forced_cfg();
     if (fc == 3 && gemm_small_supported(L)) return GK_SMALL;
-    if (fc >= 0 && fc <= 2 && L.M > 16 && gemm_b16_supported(L)) return GK_B16;
+    if (((fc >= 0 && fc <= 2) || fc >= 4) && L.M > 16 && gemm_b16_supported(L)) return GK_B16;
   }
   // 16-bit rows (the grid's y extent over the token groups): up to 256 rows at
   // N <= 4096 and 64 rows on wider N, measured at K = 2048 against every tile

@@ -9,14 +9,17 @@
 // barrier per 64-wide K stage, transposed accumulators (weights as the MFMA's
 // first operand) so each lane stores 4 consecutive output columns.
 //
-// A copies land directly in MFMA operand layout.  Within a 64-wide K block the
-// int8 weight tile gives lane l row (l & 15) and k = 16 (l >> 4) + 0..15; the
-// bf16 MFMA consumes 8 k per lane, so the block is two MFMAs, half h taking
-// k = 16 (l >> 4) + 8 h + 0..7.  Each A copy therefore reads, for lane l,
-// 8 elements X[row][64 kb + 16 (l >> 4) + 8 h ..] (2 copies per row group and
-// K block), and a wave reads its operand with one ds_read_b128 per copy.  Weight tiles
-// stay int8 in LDS and are widened to bf16/fp16 in registers after the read.
-// Lanes whose row is past M or whose k is past K copy 16 bytes of zeros.
+// Within a 64-wide K block the int8 weight tile gives lane l row (l & 15) and
+// k = 16 (l >> 4) + 0..15; the bf16 MFMA consumes 8 k per lane, so the block
+// is two MFMAs, half h taking k = 16 (l >> 4) + 8 h + 0..7.  X (row-major in
+// memory) is copied a whole 128-byte row segment per 8 lanes into a swizzled
+// row-major LDS tile (xtile_* below: 2 copies per row group and K block), and
+// a wave reads each MFMA operand with one conflict-free ds_read_b128.  (Copies
+// in MFMA operand order, lane l reading 16 bytes of row l & 15, spread every
+// copy over 16 half-used lines: about 10 B/clk per CU against the int8
+// GEMM's 22-38.)  Weight tiles stay int8 and are widened to bf16/fp16 in
+// registers after the read.  Lanes whose row is past M or whose k is past K
+// copy 16 bytes of zeros.
 #include <algorithm>
 #include <atomic>
 
@@ -78,6 +81,136 @@ __device__ inline v4f mfma16(uint4 w, uint4 x, v4f c) {
   else return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(w), as_bf(x), c, 0, 0, 0);
 }
 
+// X tiles in LDS.  A row group's 64-wide K block of X (16 rows x 128 bytes)
+// is two 1 KiB copies, rows 0-7 and 8-15.  Copy half j: lane l fetches row
+// 8 j + (l >> 3), 16-byte chunk (l & 7) ^ (l >> 3) ^ j of the row (so every
+// 8 lanes read one whole 128-byte line of X), and its 16 bytes land at
+// 16 l.  The XOR swizzle spreads the chunks that one MFMA operand read takes
+// from 16 rows (lane l: row l & 15, chunk 2 (l >> 4) + h) over distinct
+// bank groups.  Both functions are per-lane constants.
+__device__ __forceinline__ int xtile_row(int lane, int j) { return 8 * j + (lane >> 3); }
+__device__ __forceinline__ int xtile_chunk(int lane, int j) { return (lane & 7) ^ (lane >> 3) ^ j; }
+// uint4 index, within a row group's two copies, of lane's operand for K half h
+// (X[row lane & 15][16 (lane >> 4) + 8 h .. + 7])
+__device__ __forceinline__ int xtile_frag(int lane, int h) {
+  const int rr = lane & 15, j = rr >> 3, r8 = rr & 7;
+  const int kc = 2 * (lane >> 4) + h;
+  return j * 64 + r8 * 8 + (kc ^ r8 ^ j);
+}
+
+// The end of a tile's work-group: with K slices (a.S > 1) the K-slice merge,
+// then the epilogue (scale, bias, conversion, stores).  acc[i][j] holds row
+// group rg0 + i (lane: row lane & 15) and column group cg0 + j (lane: columns
+// 4 (lane >> 4) .. + 3); slot0 + i is this wave's slot of row i in the
+// partial tile (the slots of the waves of a work-group do not overlap).
+template <int FM, int FN>
+__device__ __forceinline__ void b16_finish(const GemmB16Args& a, v4f (&acc)[FM][FN], int rg0, int cg0, int slot0,
+                                           int bt, int ks, const float (&e_ws)[FN][4], const float (&e_b)[FN][4]) {
+  const int lane = threadIdx.x & 63;
+  const int mrow = lane & 15;
+  const int ncol = (lane >> 4) * 4;
+  if (a.S > 1) {
+    // K slices: every work-group of the tile stores its fp32 sums, waits for
+    // the stores' acknowledgement and counts in; the last to arrive adds the
+    // S slices in slice order (its own from registers, the same sums and
+    // order whichever work-group merges), then runs the epilogue below
+    constexpr int TF = 4 * FM * FN * 256;         // floats per partial tile: 4 waves x FM x FN fragments
+    float* mine = a.part + ((size_t)bt * a.S + ks) * TF;
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++) st_agent4(mine + (((slot0 + i) * FN + j) * 64 + lane) * 4, acc[i][j]);
+    __shared__ int s_last;
+    asm volatile("" ::: "memory");
+    wait_vm<0>();                               // this thread's partial stores are acknowledged
+    asm volatile("" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(a.cnt + bt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.S - 1);
+    __syncthreads();
+    if (!s_last) return;
+    // the merger's acquire: the slices are read after the counter showed
+    // them all arrived (agent scope, once per tile: it invalidates this
+    // CU's caches, so the plain 16-byte loads below fetch what the stores
+    // wrote through).  All S slices come from memory, this work-group's own
+    // too (the values it stored), one slice's loads in flight at a time and
+    // added in slice order.
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // QB slices' loads are in flight together (indices past S re-read the
+    // last slice and are not added)
+    constexpr int QB = FM * FN <= 2 ? 8 : (FM * FN <= 8 ? 4 : 1);
+    const float* slices = a.part + (size_t)bt * a.S * TF;
+    for (int q0 = 0; q0 < a.S; q0 += QB) {
+      v4f p[QB][FM][FN];
+#pragma unroll
+      for (int u = 0; u < QB; u++)
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+          for (int j = 0; j < FN; j++)
+            p[u][i][j] = *reinterpret_cast<const v4f*>(slices + (size_t)min(q0 + u, a.S - 1) * TF +
+                                                      (((slot0 + i) * FN + j) * 64 + lane) * 4);
+#pragma unroll
+      for (int u = 0; u < QB; u++) {
+        if (q0 + u >= a.S) break;
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+          for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+              acc[i][j][r] = q0 + u == 0 ? p[u][i][j][r] : __fadd_rn(acc[i][j][r], p[u][i][j][r]);
+      }
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(a.cnt + bt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  const bool vec_ok = ((a.ldy & 3) == 0) &&
+                      ((((uintptr_t)a.Y) & (a.out == OUT_F32 ? 15 : 7)) == 0);
+#pragma unroll
+  for (int i = 0; i < FM; i++) {
+    const int m = (rg0 + i) * 16 + mrow;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+      const int n = (cg0 + j) * 16 + ncol;
+      if (n >= a.N) continue;
+      float y[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float c = acc[i][j][r];
+        if (a.ep == EP_SCALE_FMA) {
+          y[r] = __fmaf_rn(c, e_ws[j][r], e_b[j][r]);
+        } else {
+          y[r] = __fmul_rn(c, e_ws[j][r]);
+          if (a.bias) y[r] = __fadd_rn(y[r], e_b[j][r]);
+        }
+      }
+      const size_t o = (size_t)m * a.ldy + n;
+      const bool full = vec_ok && n + 4 <= a.N;
+      if (a.out == OUT_F32) {
+        float* yp = reinterpret_cast<float*>(a.Y) + o;
+        if (full) st_stream(yp, make_float4(y[0], y[1], y[2], y[3]));   // streaming, as the int8 GEMM's
+        else for (int r = 0; r < 4 && n + r < a.N; r++) yp[r] = y[r];
+      } else {
+        uint16_t hv[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          if (a.out == OUT_BF16) {
+            hv[r] = (uint16_t)f32_to_bf16_rne(y[r]);
+          } else {
+            const _Float16 h = (_Float16)y[r];
+            hv[r] = __builtin_bit_cast(uint16_t, h);
+          }
+        }
+        uint16_t* yp = reinterpret_cast<uint16_t*>(a.Y) + o;
+        if (full) *reinterpret_cast<uint2*>(yp) = make_uint2(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16));
+        else for (int r = 0; r < 4 && n + r < a.N; r++) yp[r] = hv[r];
+      }
+    }
+  }
+}
+
 // KF: K is a multiple of 64 (every copy a per-lane offset from a uniform
 // per-stage base; the general path masks pieces past K and rows past M)
 template <int AMODE, int MT, int NT, int NST, int WM, int WN, bool KF>
@@ -137,8 +270,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
     qlds[p] = (uint32_t)q * 1024u;
     if (q < TA) {
       const int i = q / AP, j = q % AP;
-      const int row = (mg0 + i) * 16 + (lane & 15);
-      const int koff = 16 * (lane >> 4) + EPC * j;
+      const int row = (mg0 + i) * 16 + xtile_row(lane, j);
+      const int koff = EPC * xtile_chunk(lane, j);
       qrow_ok[p] = row < a.M;
       qkoff[p] = koff;
       qsrc[p] = Xb + ((size_t)min(row, a.M - 1) * a.lda + koff) * ESZ;
@@ -194,7 +327,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
   // n..n+3), loaded behind the first copies: the stage waits below then
   // also cover them (loads complete in issue order, so the extra loads only
   // make the first waits stricter), and the loop's last wait leaves them done
-  const int mrow = lane & 15;
   const int ncol = (lane >> 4) * 4;
   float e_ws[FN][4], e_b[FN][4];
 #pragma unroll
@@ -217,11 +349,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
   // stage's MFMAs): set c holds the stage's A copies of this wave's row
   // groups and its raw int8 weight tiles.
   uint4 fa[2][FM * AP], fb[2][FN];
+  const int xf[AP] = {xtile_frag(lane, 0), xtile_frag(lane, 1)};
   auto read_frags = [&](const uint4* buf, int c) {
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
-      for (int j = 0; j < AP; j++) fa[c][i * AP + j] = buf[((wm * FM + i) * AP + j) * 64 + lane];
+      for (int h = 0; h < AP; h++) fa[c][i * AP + h] = buf[(wm * FM + i) * AP * 64 + xf[h]];
 #pragma unroll
     for (int j = 0; j < FN; j++) fb[c][j] = buf[(TA + wn * FN + j) * 64 + lane];
   };
@@ -283,106 +416,188 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
   }
   wait_vm<0>();   // no copy may still be landing in LDS when the work-group exits
 
-  if (a.S > 1) {
-    // K slices: every work-group of the tile stores its fp32 sums, waits for
-    // the stores' acknowledgement and counts in; the last to arrive adds the
-    // S slices in slice order (its own from registers, the same sums and
-    // order whichever work-group merges), then runs the epilogue below
-    constexpr int TF = MT * 16 * NT * 16;
-    float* mine = a.part + ((size_t)bt * a.S + ks) * TF;
-#pragma unroll
-    for (int i = 0; i < FM; i++)
-#pragma unroll
-      for (int j = 0; j < FN; j++) st_agent4(mine + (((wv * FM + i) * FN + j) * 64 + lane) * 4, acc[i][j]);
-    __shared__ int s_last;
-    asm volatile("" ::: "memory");
-    wait_vm<0>();                               // this thread's partial stores are acknowledged
-    asm volatile("" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0)
-      s_last = __hip_atomic_fetch_add(a.cnt + bt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.S - 1);
-    __syncthreads();
-    if (!s_last) return;
-    // the merger's acquire: the slices are read after the counter showed
-    // them all arrived (agent scope, once per tile: it invalidates this
-    // CU's caches, so the plain 16-byte loads below fetch what the stores
-    // wrote through).  All S slices come from memory, this work-group's own
-    // too (the values it stored), one slice's loads in flight at a time and
-    // added in slice order.
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    // QB slices' loads are in flight together (indices past S re-read the
-    // last slice and are not added)
-    constexpr int QB = FM * FN <= 2 ? 8 : (FM * FN <= 8 ? 4 : 1);
-    const float* slices = a.part + (size_t)bt * a.S * TF;
-    for (int q0 = 0; q0 < a.S; q0 += QB) {
-      v4f p[QB][FM][FN];
-#pragma unroll
-      for (int u = 0; u < QB; u++)
-#pragma unroll
-        for (int i = 0; i < FM; i++)
-#pragma unroll
-          for (int j = 0; j < FN; j++)
-            p[u][i][j] = *reinterpret_cast<const v4f*>(slices + (size_t)min(q0 + u, a.S - 1) * TF +
-                                                      (((wv * FM + i) * FN + j) * 64 + lane) * 4);
-#pragma unroll
-      for (int u = 0; u < QB; u++) {
-        if (q0 + u >= a.S) break;
-#pragma unroll
-        for (int i = 0; i < FM; i++)
-#pragma unroll
-          for (int j = 0; j < FN; j++)
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-              acc[i][j][r] = q0 + u == 0 ? p[u][i][j][r] : __fadd_rn(acc[i][j][r], p[u][i][j][r]);
-      }
-    }
-    if (threadIdx.x == 0) __hip_atomic_store(a.cnt + bt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  b16_finish<FM, FN>(a, acc, mg0 + wm * FM, ng0 + wn * FN, wv * FM, bt, ks, e_ws, e_b);
+}
 
-  const bool vec_ok = ((a.ldy & 3) == 0) &&
-                      ((((uintptr_t)a.Y) & (a.out == OUT_F32 ? 15 : 7)) == 0);
+// One output dword of the widening: int8 elements 2p, 2p + 1 of a lane's 16
+// (dword p / 2, bytes 2 (p % 2), + 1) as two 16-bit values, exact
+template <int AMODE>
+__device__ __forceinline__ uint32_t widen_pair(uint4 w, int p) {
+  const uint32_t d = (p >> 1) == 0 ? w.x : ((p >> 1) == 1 ? w.y : ((p >> 1) == 2 ? w.z : w.w));
+  const int sh = (p & 1) * 16;
+  const float f0 = (float)(int8_t)((d >> sh) & 0xff), f1 = (float)(int8_t)((d >> (sh + 8)) & 0xff);
+  if constexpr (AMODE == A_F16) {
+    const _Float16 h0 = (_Float16)f0, h1 = (_Float16)f1;
+    return (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+  } else {
+    return __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+  }
+}
+__device__ __forceinline__ void set_dword(uint4& u, int c, uint32_t v) {
+  if (c == 0) u.x = v;
+  else if (c == 1) u.y = v;
+  else if (c == 2) u.z = v;
+  else u.w = v;
+}
+
+// Column-split variant: the 4 waves split the tile's N columns (wave w owns
+// weight row groups ng0 + FN w .. + FN - 1) and share its MT row groups of X.
+// Each weight tile is private to one wave, so it goes from global memory
+// straight into that wave's registers (one 16-byte load per lane per tile, in
+// MFMA operand order) and is widened once per work-group; only the shared X
+// tiles pass through the LDS ring (2 MT KiB per stage, so the ring holds D
+// stages in 2 MT D KiB).  Per 64-wide K stage and work-group: 2 MT KiB
+// copied into LDS, 8 MT KiB of fragment reads, 4 FN KiB of register loads,
+// 8 MT FN MFMAs.
+//
+// Pipeline (as the int8 column-split kernel): stage s's copies and loads are
+// issued D steps ahead (weight register set s % (D + 1), LDS buffer s % D).
+// Step s waits for stage s + 1, one barrier makes its X tiles visible and
+// frees buffer s % D, whose copy for stage s + D follows; the MFMAs of stage
+// s run interleaved with the fragment reads of stage s + 1, the issue of
+// stage s + D and the widening of the next weight column, two elements at a
+// time between MFMAs.  Stages past the work-group's K range re-read its last
+// K block (branch-free, so every wait counts exactly); nothing reads what
+// they bring in.  K is a multiple of 64.
+template <int AMODE, int MT, int FN, int D>
+__global__ __launch_bounds__(256) void gemm_b16_wcol_kernel(GemmB16Args a) {
+  constexpr int NW = 4, NT = NW * FN, AP = 2, ESZ = 2;
+  constexpr int TA = MT * AP;          // X copies (1 KiB each) per stage
+  constexpr int PA = TA / NW;          // ... per wave
+  constexpr int NB = D + 1;            // weight register sets
+  constexpr int PS = PA + FN;          // vector memory operations per wave per stage
+  static_assert(TA % NW == 0, "X copies must divide over the waves");
+  static_assert(NB % 2 == 0, "fragment double buffer needs an even unroll");
+  static_assert(PS * (D - 1) < 64, "vmcnt range");
+  __shared__ uint4 sA[D * TA * 64];
+
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+  // work-group b: K slice b / ntiles of tile b % ntiles (XCD-grouped tile
+  // order as the LDS-staged kernel's)
+  const int ntiles = a.ntm * a.ntn;
+  const int ks = blockIdx.x / ntiles;
+  const int bt = blockIdx.x - ks * ntiles;
+  int t = bt;
+  if (ntiles % 8 == 0) t = (bt % 8) * (ntiles / 8) + bt / 8;
+  const int tn = t / a.ntm, tm = t - (t / a.ntm) * a.ntm;
+  const int mg0 = tm * MT, ng0 = tn * NT + wv * FN;
+  const int KB = a.KB;
+  const int kb0 = (ks * KB) / a.S;
+  const int nst = ((ks + 1) * KB) / a.S - kb0;
+
+  // X copies: copy q = wv + NW p is half q % AP of row group q / AP; lane l
+  // reads X[row (l & 15)][64 kb + 16 (l >> 4) + 8 (q % AP) ..] (rows past M
+  // read row M - 1; their outputs are never stored)
+  const char* Xb = static_cast<const char*>(a.X);
+  uint32_t avo[PA];
 #pragma unroll
-  for (int i = 0; i < FM; i++) {
-    const int m = (mg0 + wm * FM + i) * 16 + mrow;
-    if (m >= a.M) continue;
+  for (int p = 0; p < PA; p++) {
+    const int q = wv + NW * p;
+    const int row = min((mg0 + q / AP) * 16 + xtile_row(lane, q % AP), a.M - 1);
+    avo[p] = (uint32_t)(((size_t)row * a.lda + 8 * xtile_chunk(lane, q % AP)) * ESZ);
+  }
+  const uint4* B4 = reinterpret_cast<const uint4*>(a.Bt) + lane;
+  const uint4* bsrc[FN];
+#pragma unroll
+  for (int j = 0; j < FN; j++) bsrc[j] = B4 + (size_t)min(ng0 + j, a.NG - 1) * 64;
+  const size_t bstride = (size_t)a.NG * 64;
+  const uint32_t sbase = lds_addr(sA);
+  constexpr uint32_t SBYTES = TA * 1024;
+
+  uint4 wb[NB][FN];
+  auto copy_a = [&](int st, int p) {
+    const int sc = kb0 + min(st, nst - 1);
+    dma_tile_s(avo[p], Xb + (size_t)sc * 64 * ESZ, sbase + (uint32_t)(st % D) * SBYTES + (uint32_t)(wv + NW * p) * 1024u);
+  };
+  auto load_b = [&](int st, int c, int j) { wb[c][j] = bsrc[j][(size_t)(kb0 + min(st, nst - 1)) * bstride]; };
+
+  // epilogue operands first (older than every copy, so the first wait covers them)
+  const int ncol = (lane >> 4) * 4;
+  float e_ws[FN][4], e_b[FN][4];
+#pragma unroll
+  for (int j = 0; j < FN; j++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int n = min((ng0 + j) * 16 + ncol + r, a.N - 1);
+      e_ws[j][r] = a.ws[n];
+      e_b[j][r] = a.bias ? a.bias[n] : 0.0f;
+    }
+
+  v4f acc[MT][FN];
+#pragma unroll
+  for (int i = 0; i < MT; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  uint4 fa[2][TA];
+  const int xf[AP] = {xtile_frag(lane, 0), xtile_frag(lane, 1)};
+  auto read_frags = [&](int st, int c) {
+    const uint4* buf = sA + (size_t)(st % D) * (TA * 64);
+#pragma unroll
+    for (int i = 0; i < TA; i++) fa[c][i] = buf[(i / AP) * AP * 64 + xf[i % AP]];
+  };
+
+  // prologue: stages 0 .. D-1 in flight, stage 0 visible and its fragments read
+#pragma unroll
+  for (int b = 0; b < D; b++) {
+#pragma unroll
+    for (int p = 0; p < PA; p++) copy_a(b, p);
+#pragma unroll
+    for (int j = 0; j < FN; j++) load_b(b, b, j);
+  }
+  wait_vm<PS * (D - 1)>();
+  stage_barrier();
+  read_frags(0, 0);
+
+  // step s (weight set b = s % NB, fragment set f = s & 1)
+  auto step = [&](int st, int b, int f) {
+    wait_vm<PS * (D - 2)>();   // stage s + 1 landed (this wave's part)
+    wait_lgkm0();              // this wave's reads of stage s are done
+    stage_barrier();           // stage s + 1 visible; buffer s % D free
+    constexpr int NMEM = TA + PS;
+    const int nb = (b + D) % NB;
+    auto mem_op = [&](int q) {
+      if (q < PA) copy_a(st + D, q);
+      else if (q < PS) load_b(st + D, nb, q - PA);
+      else fa[f ^ 1][q - PS] = sA[(size_t)((st + 1) % D) * (TA * 64) + ((q - PS) / AP) * AP * 64 + xf[(q - PS) % AP]];
+    };
+    uint4 wcol[2][2];          // widened weight column j (set j & 1): the two K halves
+#pragma unroll
+    for (int p = 0; p < 8; p++) set_dword(wcol[0][p >> 2], p & 3, widen_pair<AMODE>(wb[b][0], p));
+    __builtin_amdgcn_sched_barrier(0);
+    constexpr int NM = 2 * MT;           // MFMAs per weight column
 #pragma unroll
     for (int j = 0; j < FN; j++) {
-      const int n = (ng0 + wn * FN + j) * 16 + ncol;
-      if (n >= a.N) continue;
-      float y[4];
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const float c = acc[i][j][r];
-        if (a.ep == EP_SCALE_FMA) {
-          y[r] = __fmaf_rn(c, e_ws[j][r], e_b[j][r]);
-        } else {
-          y[r] = __fmul_rn(c, e_ws[j][r]);
-          if (a.bias) y[r] = __fadd_rn(y[r], e_b[j][r]);
-        }
-      }
-      const size_t o = (size_t)m * a.ldy + n;
-      const bool full = vec_ok && n + 4 <= a.N;
-      if (a.out == OUT_F32) {
-        float* yp = reinterpret_cast<float*>(a.Y) + o;
-        if (full) st_stream(yp, make_float4(y[0], y[1], y[2], y[3]));   // streaming, as the int8 GEMM's
-        else for (int r = 0; r < 4 && n + r < a.N; r++) yp[r] = y[r];
-      } else {
-        uint16_t hv[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          if (a.out == OUT_BF16) {
-            hv[r] = (uint16_t)f32_to_bf16_rne(y[r]);
-          } else {
-            const _Float16 h = (_Float16)y[r];
-            hv[r] = __builtin_bit_cast(uint16_t, h);
-          }
-        }
-        uint16_t* yp = reinterpret_cast<uint16_t*>(a.Y) + o;
-        if (full) *reinterpret_cast<uint2*>(yp) = make_uint2(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16));
-        else for (int r = 0; r < 4 && n + r < a.N; r++) yp[r] = hv[r];
+      for (int u = 0; u < NM; u++) {
+        const int h = u / MT, i = u % MT;
+        acc[i][j] = mfma16<AMODE>(wcol[j & 1][h], fa[f][i * AP + h], acc[i][j]);
+        __builtin_amdgcn_sched_barrier(0);
+        const int m = j * NM + u;
+        if (m < NMEM) mem_op(m);
+        // the next column's widening, one output dword per MFMA slot
+        if (j + 1 < FN && u < 8) set_dword(wcol[(j + 1) & 1][u >> 2], u & 3, widen_pair<AMODE>(wb[b][j + 1], u));
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
+#pragma unroll
+    for (int q = FN * NM; q < NMEM; q++) mem_op(q);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  const int kfull = nst - nst % NB;
+  for (int st = 0; st < kfull; st += NB) {
+#pragma unroll
+    for (int b = 0; b < NB; b++) step(st + b, b, b & 1);
   }
+#pragma unroll
+  for (int b = 0; b < NB - 1; b++)
+    if (kfull + b < nst) step(kfull + b, b, b & 1);
+
+  wait_vm<0>();   // no copy may still be landing in LDS when the work-group exits
+
+  b16_finish<MT, FN>(a, acc, mg0, ng0, wv * MT, bt, ks, e_ws, e_b);
 }
 
 // ---------------------------------------------------------------------------
@@ -393,17 +608,29 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
 // cfg 2   32 x  64 tiles, 8-deep ring (64 KiB)
 // The smaller tiles exist for mid-size M (64 < M <= 512) with small N, where
 // the larger ones leave most CUs idle.
+// cfg 4  128 x 192 tiles, column-split (weights to registers), 5-deep X ring (80 KiB)
+// cfg 5  128 x 192 tiles, column-split, 7-deep X ring (112 KiB)
+// cfg 6  128 x 128 tiles, column-split, 7-deep X ring (112 KiB)
+// cfg 7   64 x 192 tiles, column-split, 7-deep X ring (56 KiB)
+// cfg 8   64 x 128 tiles, column-split, 9-deep X ring (72 KiB)
+// (the column-split kernel needs K % 64 == 0; other K run cfg 0's tiles)
 static void b16_cfg(int cfg, int& mt, int& nt) {
+  if (cfg >= 4) {
+    mt = cfg >= 7 ? 4 : 8;
+    nt = (cfg == 6 || cfg == 8) ? 8 : 12;
+    return;
+  }
   mt = (cfg == 0) ? 8 : (cfg == 1 ? 4 : 2);
   nt = (cfg == 0) ? 12 : (cfg == 1 ? 8 : 4);
 }
 
 // Plan: tile configuration and K slices, from the measured W8A16 sweep
 // (M = 64 .. 1024, N = 2048 .. 12288, K = 2048, every configuration and
-// 1..8 slices): the 32 x 64 tiles while they number at most 512 (two
-// work-groups of 64 KiB share a CU), else the 64 x 128 tiles while they fit
-// one wave of 256 CUs, else the 128 x 192 tiles while they do, else the
-// configuration whose tile count best fills 256 CUs.  The loop is bound by
+// 1..8 slices).  K a multiple of 64: the column-split kernel (b16_plan).
+// Other K, the LDS-staged kernel: the 32 x 64 tiles while they number at
+// most 512 (two work-groups of 64 KiB share a CU), else the 64 x 128 tiles
+// while they fit one wave of 256 CUs, else the 128 x 192 tiles while they
+// do, else the configuration whose tile count best fills 256 CUs.  The loop is bound by
 // the latency of its stage copies rather than by bytes, so K slices pay only
 // where the tiles are few: at most 64 tiles are split until 256 work-groups
 // run (M = 64, N = 2048: 11.4 -> 10.5 us); with more tiles the slices' store,
@@ -411,14 +638,15 @@ static void b16_cfg(int cfg, int& mt, int& nt) {
 static std::atomic<int> g_b16_force_cfg{-1};
 static std::atomic<int> g_b16_force_split{0};
 void gemm_b16_set_plan(int cfg, int split) {
-  g_b16_force_cfg.store(cfg >= 0 && cfg <= 3 ? cfg : -1, std::memory_order_relaxed);
+  g_b16_force_cfg.store(cfg >= 0 && cfg <= 8 ? cfg : -1, std::memory_order_relaxed);
   // with cfg 3, split (when > 64) picks the small-M kernel's work-group shape
   gemm_small_set_b16_shape(cfg == 3 && split > 64 ? split : 0);
   if (cfg == 3) split = 0;
   g_b16_force_split.store(split > 0 ? split : 0, std::memory_order_relaxed);
 }
 
-// -1 planner, 0..2 a forced tile of this kernel, 3 the streamed small-M kernel
+// -1 planner, 0..2 and 4..8 a forced tile configuration of this file's
+// kernels, 3 the streamed small-M kernel
 int gemm_b16_forced_cfg() { return g_b16_force_cfg.load(std::memory_order_relaxed); }
 
 static int b16_tiles(int cfg, int MG, int NG) {
@@ -427,9 +655,26 @@ static int b16_tiles(int cfg, int MG, int NG) {
   return cdiv(MG, mt) * cdiv(NG, nt);
 }
 
-static void b16_plan(int MG, int NG, int KB, int& cfg_out, int& split_out) {
+static void b16_plan(int MG, int NG, int KB, bool kf, int& cfg_out, int& split_out) {
   int best;
-  if (b16_tiles(2, MG, NG) <= 512) best = 2;
+  if (kf) {
+    // column-split kernel: the configuration of least estimated time, rounds
+    // of 256 work-groups times the measured time of one work-group at
+    // K = 2048 (one per CU, bound by its per-CU load rate: 64 x 128 tiles
+    // 16.0 us, 64 x 192 20.5, 128 x 128 23.3, 128 x 192 30.3; MI355X sweep of
+    // M = 64..1024, N = 2048..12288, every configuration)
+    static const int kc[4] = {8, 7, 6, 4};
+    static const float kt[4] = {16.0f, 20.5f, 23.3f, 30.3f};
+    best = 8;
+    float tbest = 3.0e38f;
+    for (int c = 0; c < 4; c++) {
+      const float t = (float)cdiv(b16_tiles(kc[c], MG, NG), 256) * kt[c];
+      if (t < tbest) {
+        tbest = t;
+        best = kc[c];
+      }
+    }
+  } else if (b16_tiles(2, MG, NG) <= 512) best = 2;
   else if (b16_tiles(1, MG, NG) <= 256) best = 1;
   else if (b16_tiles(0, MG, NG) <= 256) best = 0;
   else {
@@ -450,25 +695,56 @@ static void b16_plan(int MG, int NG, int KB, int& cfg_out, int& split_out) {
   sp = std::min(sp, 4);
   const int fc = g_b16_force_cfg.load(std::memory_order_relaxed);
   const int fs = g_b16_force_split.load(std::memory_order_relaxed);
-  if (fc >= 0 && fc <= 2) best = fc;
+  if ((fc >= 0 && fc <= 2) || fc >= 4) best = fc;
+  if (best >= 4 && !kf) best = 0;   // the column-split kernel needs K % 64 == 0
   if (fs > 0) sp = std::min(fs, std::max(1, KB));
   cfg_out = best;
   split_out = sp;
 }
 
-// partial-sum bytes and arrival counters the launch of this shape needs
+// partial-sum bytes and arrival counters the launch of this shape needs (the
+// larger of the two plans: whether the launch takes the K-multiple-of-64 path
+// also depends on the row stride, which is not known here)
 void gemm_b16_needs(int M, int N, int K, size_t* part_bytes, size_t* counters) {
-  int cfg, sp, mt, nt;
   const int MG = cdiv(M, 16), NG = cdiv(N, 16);
-  b16_plan(MG, NG, cdiv(K, 64), cfg, sp);
-  b16_cfg(cfg, mt, nt);
-  const size_t tiles = (size_t)cdiv(MG, mt) * cdiv(NG, nt);
-  *part_bytes = sp > 1 ? tiles * sp * (size_t)(256 * mt * nt) * sizeof(float) : 0;
-  *counters = sp > 1 ? tiles : 0;
+  *part_bytes = 0;
+  *counters = 0;
+  for (int kf = 0; kf < 2; kf++) {
+    int cfg, sp, mt, nt;
+    b16_plan(MG, NG, cdiv(K, 64), kf != 0 && K % 64 == 0, cfg, sp);
+    b16_cfg(cfg, mt, nt);
+    const size_t tiles = (size_t)cdiv(MG, mt) * cdiv(NG, nt);
+    if (sp > 1) {
+      *part_bytes = std::max(*part_bytes, tiles * sp * (size_t)(256 * mt * nt) * sizeof(float));
+      *counters = std::max(*counters, tiles);
+    }
+  }
 }
 
 template <int AMODE, bool KF>
 static void launch_b16(const GemmB16Args& a, int cfg, dim3 grid, dim3 block, hipStream_t st) {
+  if constexpr (KF) {
+    if (cfg == 4) {
+      hipLaunchKernelGGL((gemm_b16_wcol_kernel<AMODE, 8, 3, 5>), grid, block, 0, st, a);
+      return;
+    }
+    if (cfg == 5) {
+      hipLaunchKernelGGL((gemm_b16_wcol_kernel<AMODE, 8, 3, 7>), grid, block, 0, st, a);
+      return;
+    }
+    if (cfg == 6) {
+      hipLaunchKernelGGL((gemm_b16_wcol_kernel<AMODE, 8, 2, 7>), grid, block, 0, st, a);
+      return;
+    }
+    if (cfg == 7) {
+      hipLaunchKernelGGL((gemm_b16_wcol_kernel<AMODE, 4, 3, 7>), grid, block, 0, st, a);
+      return;
+    }
+    if (cfg == 8) {
+      hipLaunchKernelGGL((gemm_b16_wcol_kernel<AMODE, 4, 2, 9>), grid, block, 0, st, a);
+      return;
+    }
+  }
   if (cfg == 0) hipLaunchKernelGGL((gemm_b16_lds_kernel<AMODE, 8, 12, 4, 2, 2, KF>), grid, block, 0, st, a);
   else if (cfg == 1) hipLaunchKernelGGL((gemm_b16_lds_kernel<AMODE, 4, 8, 8, 2, 2, KF>), grid, block, 0, st, a);
   else hipLaunchKernelGGL((gemm_b16_lds_kernel<AMODE, 2, 4, 8, 2, 2, KF>), grid, block, 0, st, a);
@@ -501,7 +777,10 @@ hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st) {
   a.out = L.out;
   a.zero_tile = L.zero_tile;
   int best, sp;
-  b16_plan(a.MG, a.NG, a.KB, best, sp);
+  // K a multiple of 64, and every X byte offset fits the copies' 32-bit
+  // per-lane offsets (else the general path, with 64-bit addresses)
+  const bool kf = (L.K % 64) == 0 && (size_t)L.M * (size_t)L.lda * 2 < ((size_t)1 << 32);
+  b16_plan(a.MG, a.NG, a.KB, kf, best, sp);
   int mt, nt;
   b16_cfg(best, mt, nt);
   a.ntm = cdiv(a.MG, mt);
@@ -513,7 +792,6 @@ hipError_t launch_gemm_b16(const GemmLaunch& L, hipStream_t st) {
   const long long blocks_ll = (long long)a.ntm * a.ntn * sp;
   if (blocks_ll > 0x7fffffffLL) return hipErrorInvalidValue;
   const int blocks = (int)blocks_ll;
-  const bool kf = (L.K % 64) == 0;
   const dim3 grid(blocks), block(256);
   if (L.amode == A_BF16) {
     if (kf) launch_b16<A_BF16, true>(a, best, grid, block, st);
