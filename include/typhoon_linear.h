@@ -118,7 +118,10 @@ int tl_gemm_i8_set_split(int split);
 
 /* Tuning override of the 16-bit MFMA GEMM (W8A16, M > 16 on the tiled
  * kernel) for every later call in the process: cfg -1 restores the planner's
- * kernel and tile, 0..2 force 128x192, 64x128 or 32x64 tiles, 3 forces the
+ * kernel and tile, 0..2 force 128x192, 64x128 or 32x64 tiles of the
+ * LDS-staged kernel, 4..8 the column-split kernel's 128x192 (5- or 7-deep
+ * ring), 128x128, 64x192 or 64x128 tiles (K a multiple of 64; other K run
+ * cfg 0), 3 forces the
  * streamed small-M kernel (M <= 256, weights read once per work-group of
  * token rows; with cfg 3 a split of 100 R + 10 TG + U picks its work-group
  * shape: R, TG in {1, 2, 4} weight / token row groups, U in {2, 4} tiles per

@@ -612,7 +612,9 @@ __global__ __launch_bounds__(256) void gemm_b16_wcol_kernel(GemmB16Args a) {
 // cfg 5  128 x 192 tiles, column-split, 7-deep X ring (112 KiB)
 // cfg 6  128 x 128 tiles, column-split, 7-deep X ring (112 KiB)
 // cfg 7   64 x 192 tiles, column-split, 7-deep X ring (56 KiB)
-// cfg 8   64 x 128 tiles, column-split, 9-deep X ring (72 KiB)
+// cfg 8   64 x 128 tiles, column-split, 9-deep X ring (72 KiB; two work-groups
+//         share a CU.  11- and 13-deep rings measured no faster with one
+//         work-group per CU and 20-35% slower where a CU runs several)
 // (the column-split kernel needs K % 64 == 0; other K run cfg 0's tiles)
 static void b16_cfg(int cfg, int& mt, int& nt) {
   if (cfg >= 4) {
