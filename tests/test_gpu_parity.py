@@ -896,6 +896,32 @@ SMALL_B16_SHAPES = [100 * r + 10 * t + u for r in (1, 2, 4) for t in (1, 2, 4) f
                     if u == 2 or t == 1 or r * t <= 8]
 
 
+def test_w8a16_rows_past_32bit_offsets(lin, orc, dev):
+    """X of more than 4 GiB (2^20 + 40 rows of 2048 bf16): the tiled kernels'
+    copies address X with 32-bit per-lane offsets from a per-stage base, so
+    such X takes the general path with 64-bit addresses.  The first and the
+    last rows (past 2^32 bytes) within 1e-5 of a float64 product."""
+    import torch
+    M, N, K = (1 << 20) + 40, 48, 2048
+    say(f"w8a16 rows past 32-bit offsets M={M} N={N} K={K}")
+    rng = np.random.default_rng(77)
+    _, w, s = make(rng, 1, N, K)
+    W = lin.DeviceWeights.from_codes(w, s)
+    xt = torch.randn((M, K), device=dev, dtype=torch.float32, generator=torch.Generator(device=dev).manual_seed(5)
+                     ).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    lin.w8a16_linear_dev(xt, W, y)
+    torch.cuda.synchronize()
+    for sl in (slice(0, 40), slice(M - 40, M)):
+        xs = xt[sl].float().cpu().numpy().astype(np.float64)
+        want = (xs @ w.astype(np.float64).T) * s.astype(np.float64)
+        e = row_rel_l2(y[sl].cpu().numpy(), want)
+        assert e.max() <= 1e-5, (sl, int(e.argmax()), float(e.max()))
+    del xt, y
+    torch.cuda.empty_cache()
+    W.close()
+
+
 @pytest.mark.parametrize("M,N,K", [(96, 2048, 2048), (128, 1000, 1000), (200, 2000, 2112), (40, 4096, 2048),
                                    (17, 300, 192)])
 def test_w8a16_small_kernel_shapes(lin, orc, dev, M, N, K):
