@@ -289,9 +289,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_b16_lds_kernel(GemmB16Args 
   // copies would let the last NST-2 steps' waits return before their own
   // stage had landed; waiting for every copy there instead measured 7% slower
   // at M = 64..256.)
-  // K a multiple of 64 (no piece past K): each copy is a per-lane byte offset
-  // from a uniform per-stage base (rows past M read row M - 1; their outputs
-  // are never stored)
+  // K a multiple of 64 (no piece past K) and X under 4 GiB (the launcher's
+  // condition for KF): each copy is a 32-bit per-lane byte offset from a
+  // uniform per-stage base (rows past M read row M - 1; their outputs are
+  // never stored)
   constexpr bool kfull = KF;
   uint32_t qvo[PW];
 #pragma unroll
@@ -487,8 +488,8 @@ __global__ __launch_bounds__(256) void gemm_b16_wcol_kernel(GemmB16Args a) {
   const int kb0 = (ks * KB) / a.S;
   const int nst = ((ks + 1) * KB) / a.S - kb0;
 
-  // X copies: copy q = wv + NW p is half q % AP of row group q / AP; lane l
-  // reads X[row (l & 15)][64 kb + 16 (l >> 4) + 8 (q % AP) ..] (rows past M
+  // X copies: copy q = wv + NW p holds rows 8 (q % AP) .. + 7 of row group
+  // q / AP in the swizzled layout of xtile_row / xtile_chunk (rows past M
   // read row M - 1; their outputs are never stored)
   const char* Xb = static_cast<const char*>(a.X);
   uint32_t avo[PA];
