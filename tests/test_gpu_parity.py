@@ -753,8 +753,8 @@ def test_w8a16_bf16_fp16(lin, orc, dev, M, N):
     (the reference's w8a16_gemm: X widened exactly, W dequantized, SGEMM;
     w8a16_kernel.c:187-216): bf16 X with bf16 out and fp16 X with fp16 out
     within relative L2 2e-3 in every row, bf16 X with fp32 out within 1e-5 in
-    every row.  At M = 1024 x N = 12288 that is every M tile of the LDS-staged
-    GEMM in its XCD-grouped launch order."""
+    every row.  At M = 1024 x N = 12288 that is every M tile of the
+    column-split GEMM in its XCD-grouped launch order."""
     import torch
     K = 2048
     say(f"w8a16 bf16/fp16/fp32-out M={M} N={N} K={K}, all rows")
